@@ -1,0 +1,417 @@
+"""Benchmark of the MI355X linear hot path of MingTTS.
+
+Headline step: one decode step of the backbone linears -- 24 Qwen2-0.5B layers x {qkv
+1152x896 + bias, o 896x896 (+= residual), gate|up 2 x 4864x896 with SiLU*mul, down
+896x4864 (+= residual)} at M = 2 rows (the CFG cond/uncond pair), fp16 weights ~
+N(0, 0.02^2), fp32 activations ~ N(0, 1), run as ONE persistent launch of the linear
+sequence (96 dependent linears).  ``value`` is the step's achieved HBM rate in GB/s
+(algorithmic bytes / step time), inputs resident in HBM.
+
+Also measured in the same run (extra keys of the JSON line): the single GEMV
+(4864 x 896, fp16, from a rotated >= 1 GiB weight pool), the same decode step as 96
+separate launches, the prefill GEMM stack at M = 64 / 256 / 512 (MFMA TFLOPS), batch-2
+decode attention over fp16 caches, the DiT head MLP, and the CPU baseline (the oracle's
+vectorised restatement of the reference CPU loop on a bounded sample of the step).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ming-tts_amd"))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+H, QKV, INTER, LAYERS = 896, 1152, 4864, 24
+METRIC = "decode-step linear µs + achieved HBM GB/s (% of 8 TB/s); prefill MFMA TFLOPS"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def ensure_built() -> None:
+    import mingtts
+    if not os.path.exists(mingtts.LIB_PATH):
+        log("library not built; building")
+        import __graft_entry__
+        __graft_entry__.build()
+
+
+class Events:
+    """HIP events on torch's current stream (the stream every launch below uses)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def start(self):
+        self.a.record()
+
+    def stop_ms(self) -> float:
+        self.b.record()
+        self.b.synchronize()
+        return self.a.elapsed_time(self.b)
+
+
+def make_layers(torch, dev, layers=LAYERS, seed=0):
+    """Distinct per-layer fp16 weights ~ N(0, 0.02^2): 715.6 MB for 24 layers (> the 256 MB
+    Infinity Cache, so every step streams from HBM).  Synthetic, generated on the device."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def w(*shape):
+        return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * 0.02).half()
+
+    return [dict(qkv=w(QKV, H), qkv_b=w(QKV), o=w(H, H), gate=w(INTER, H), up=w(INTER, H), down=w(H, INTER))
+            for _ in range(layers)]
+
+
+def decode_ops(mt, ws, M, resid, qkv, mlp):
+    ops = []
+    for p in ws:
+        ops.append(mt.op(resid, p["qkv"], qkv, M, bias=p["qkv_b"]))
+        ops.append(mt.op(qkv, p["o"], resid, M, flags=mt.GemvFlags.accumulate, ldx=QKV))
+        ops.append(mt.op(resid, p["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=p["up"]))
+        ops.append(mt.op(mlp, p["down"], resid, M, flags=mt.GemvFlags.accumulate))
+    return ops
+
+
+def shape_bytes(M, N, K, f, xsize=4) -> int:
+    """Algorithmic bytes of one linear: 16-bit weights (x2 gated) + bias + x read + fp32 y
+    write (+ y read when accumulating)."""
+    wb = 2 * N * K * (2 if f & 8 else 1) + (2 * N if f & 1 else 0)
+    return wb + xsize * M * K + 4 * M * N * (2 if f & 2 else 1)
+
+
+def op_bytes(o, xsize=4) -> int:
+    return shape_bytes(o.p.M, o.p.N, o.p.K, o.p.flags, xsize)
+
+
+def op_flops(o) -> int:
+    return 2 * o.p.M * o.p.N * o.p.K * (2 if o.p.flags & 8 else 1)
+
+
+def bench_decode_seq(torch, mt, dev, ws, steps, warmup, M=2):
+    resid = torch.randn(M, H, device=dev)
+    qkv = torch.zeros(M, QKV, device=dev)
+    mlp = torch.zeros(M, INTER, device=dev)
+    x0 = resid.clone()
+    ops = decode_ops(mt, ws, M, resid, qkv, mlp)
+    seq = mt.Seq(ops)
+    ev = Events(torch)
+    for _ in range(warmup):
+        resid.copy_(x0)
+        seq.run()
+    torch.cuda.synchronize()
+    # Each step starts from the same residual (a device copy, outside the timed launches).
+    times = []
+    for _ in range(steps):
+        resid.copy_(x0)
+        ev.start()
+        seq.run()
+        times.append(ev.stop_ms())
+    seq.check()
+    nbytes = sum(op_bytes(o) for o in ops)
+    flops = sum(op_flops(o) for o in ops)
+    res = dict(groups=seq.groups, bytes=nbytes, flops=flops, times_ms=times, ops=len(ops))
+    seq.close()
+    return res
+
+
+def bench_decode_per_op(torch, mt, dev, ws, steps, M=2):
+    resid = torch.randn(M, H, device=dev)
+    qkv = torch.zeros(M, QKV, device=dev)
+    mlp = torch.zeros(M, INTER, device=dev)
+    ops = decode_ops(mt, ws, M, resid, qkv, mlp)
+    L = mt.load()
+    s = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        for o in ops:
+            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
+            if rc:
+                raise RuntimeError(mt.last_error())
+
+    step()
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    times = []
+    for _ in range(steps):
+        ev.start()
+        step()
+        times.append(ev.stop_ms())
+    return dict(times_ms=times)
+
+
+def bench_gemv_single(torch, mt, dev, reps=200, M=1):
+    """4864 x 896 fp16 GEMV, each dispatch reading a fresh slice of a >= 1 GiB pool."""
+    N, K = 4864, 896
+    per = N * K
+    copies = (1 << 30) // (per * 2) + 1
+    pool = (torch.randn(copies, N, K, device=dev) * 0.02).half()
+    x = torch.randn(M, K, device=dev).half()
+    y = torch.zeros(M, N, device=dev)
+    L = mt.load()
+    s = torch.cuda.current_stream().cuda_stream
+    p = mt.GemvParams(M, N, K, K, N, 0, 0.0)
+    for i in range(copies):
+        L.mt_linear(x.data_ptr(), mt.F16, pool[i].data_ptr(), None, mt.F16, None, y.data_ptr(), p, s)
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    ev.start()
+    for i in range(reps):
+        rc = L.mt_linear(x.data_ptr(), mt.F16, pool[i % copies].data_ptr(), None, mt.F16, None, y.data_ptr(), p, s)
+        if rc:
+            raise RuntimeError(mt.last_error())
+    ms = ev.stop_ms()
+    nbytes = 2 * N * K + 2 * M * K + 4 * M * N
+    us = ms * 1e3 / reps
+    del pool
+    return dict(M=M, us_per_dispatch=us, gbs=nbytes / (us * 1e-6) / 1e9, bytes=nbytes, pool_copies=copies)
+
+
+def bench_prefill(torch, mt, dev, ws, M, reps=3):
+    """The 24-layer backbone GEMMs at M rows, fp16 activations, fp32 outputs: 96 launches."""
+    x = torch.randn(M, H, device=dev).half()
+    xi = torch.randn(M, INTER, device=dev).half()
+    yq = torch.zeros(M, QKV, device=dev)
+    yh = torch.zeros(M, H, device=dev)
+    ym = torch.zeros(M, INTER, device=dev)
+    ops = []
+    for p in ws:
+        ops.append(mt.op(x, p["qkv"], yq, M, bias=p["qkv_b"]))
+        ops.append(mt.op(x, p["o"], yh, M, flags=mt.GemvFlags.accumulate))
+        ops.append(mt.op(x, p["gate"], ym, M, flags=mt.GemvFlags.siluGate, w2=p["up"]))
+        ops.append(mt.op(xi, p["down"], yh, M, flags=mt.GemvFlags.accumulate))
+    L = mt.load()
+    s = torch.cuda.current_stream().cuda_stream
+
+    def stack():
+        for o in ops:
+            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
+            if rc:
+                raise RuntimeError(mt.last_error())
+
+    stack()
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    best = None
+    for _ in range(reps):
+        ev.start()
+        stack()
+        ms = ev.stop_ms()
+        best = ms if best is None else min(best, ms)
+    flops = sum(op_flops(o) for o in ops)
+    nbytes = sum(op_bytes(o, xsize=2) for o in ops)
+    tflops = flops / (best * 1e-3) / 1e12
+    attainable = min(MFMA_F16_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBS / 1e3)
+    return dict(M=M, us=best * 1e3, tflops=tflops, pct_mfma_peak=100 * tflops / MFMA_F16_PEAK_TFLOPS,
+                pct_attainable=100 * tflops / attainable, gflop=flops / 1e9, mbytes=nbytes / 1e6)
+
+
+def bench_attention(torch, mt, dev, reps=200):
+    """Batch-2 decode attention, 14 q / 2 kv heads, d 64, fp16 caches of 512, lengths ~ U[32, 512]."""
+    import numpy as np
+    B, HQ, HKV, CAP = 2, 14, 2, 512
+    lens = np.random.default_rng(0).integers(32, 513, B).astype(np.int32)
+    kc = torch.randn(B, HKV, CAP, 64, device=dev).half()
+    vc = torch.randn(B, HKV, CAP, 64, device=dev).half()
+    q = torch.randn(B, HQ * 64, device=dev)
+    out = torch.zeros(B, HQ * 64, device=dev)
+    lens_d = torch.from_numpy(lens).to(dev)
+    stride = HKV * CAP * 64
+    mt.attention_decode(q, HQ * 64, B, HQ, HKV, lens_d, 0, kc, vc, CAP, stride, out, HQ * 64)
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    ev.start()
+    for _ in range(reps):
+        mt.attention_decode(q, HQ * 64, B, HQ, HKV, lens_d, 0, kc, vc, CAP, stride, out, HQ * 64)
+    us = ev.stop_ms() * 1e3 / reps
+    nbytes = int(sum(2 * HKV * int(l) * 64 * 2 for l in lens)) + 2 * B * HQ * 64 * 4
+    return dict(us_per_dispatch=us, gbs=nbytes / (us * 1e-6) / 1e9, lens=lens.tolist(), bytes=nbytes)
+
+
+def bench_dit(torch, mt, dev, reps=3):
+    """DiT head MLP (896 -> 3584 GELU -> 896, += residual) at M = 64 and adaLN 896 -> 5376
+    at M = 2, 8 blocks x 10 ODE steps = 240 launches; the 8 blocks' weights repeat across
+    steps (Infinity-Cache resident after the first step)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    blocks = [dict(ff1=(torch.randn(3584, H, generator=g, device=dev) * 0.02).half(),
+                   ff1_b=(torch.randn(3584, generator=g, device=dev) * 0.02).half(),
+                   ff2=(torch.randn(H, 3584, generator=g, device=dev) * 0.02).half(),
+                   ff2_b=(torch.randn(H, generator=g, device=dev) * 0.02).half(),
+                   ada=(torch.randn(6 * H, H, generator=g, device=dev) * 0.02).half(),
+                   ada_b=(torch.randn(6 * H, generator=g, device=dev) * 0.02).half()) for _ in range(8)]
+    x = torch.randn(64, H, device=dev).half()
+    hmid = torch.randn(64, 3584, device=dev).half()
+    t = torch.randn(2, H, device=dev).half()
+    y1 = torch.zeros(64, 3584, device=dev)
+    y2 = torch.zeros(64, H, device=dev)
+    ya = torch.zeros(2, 6 * H, device=dev)
+    ops = []
+    for _ in range(10):
+        for b in blocks:
+            ops.append(mt.op(t, b["ada"], ya, 2, bias=b["ada_b"]))
+            ops.append(mt.op(x, b["ff1"], y1, 64, flags=mt.GemvFlags.gelu, bias=b["ff1_b"]))
+            ops.append(mt.op(hmid, b["ff2"], y2, 64, flags=mt.GemvFlags.accumulate, bias=b["ff2_b"]))
+    L = mt.load()
+    s = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        for o in ops:
+            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
+            if rc:
+                raise RuntimeError(mt.last_error())
+
+    run()
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    best = None
+    for _ in range(reps):
+        ev.start()
+        run()
+        ms = ev.stop_ms()
+        best = ms if best is None else min(best, ms)
+    flops = sum(op_flops(o) for o in ops)
+    return dict(us_10_steps=best * 1e3, tflops=flops / (best * 1e-3) / 1e12, launches=len(ops))
+
+
+def cpu_baseline(torch, ws, target_s=10.0, M=2):
+    """The oracle's vectorised restatement of the reference CPU loop (KernelTests.swift:86-101,
+    K sum split 16 ways, OpenMP over output rows) on the host cores, over the first layers of
+    the same decode step (same shapes, same weights), repeated for about target_s seconds."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    layers = ws[:2]
+    host = [{k: v.cpu().numpy().view(np.uint16) for k, v in p.items()} for p in layers]
+    rng = np.random.default_rng(1)
+    resid0 = rng.standard_normal((M, H)).astype(np.float32)
+    threads = O.max_threads()
+
+    def step():
+        resid = resid0.copy()
+        for p in host:
+            qkv = O.linear_fast(resid, p["qkv"], None, O.F16, p["qkv_b"], None, M, QKV, H, 0, threads)
+            resid = O.linear_fast(np.ascontiguousarray(qkv[:, :H]), p["o"], None, O.F16, None, resid, M, H, H,
+                                  O.ACCUM, threads)
+            mlp = O.linear_fast(resid, p["gate"], p["up"], O.F16, None, None, M, INTER, H, O.SILU_GATE, threads)
+            resid = O.linear_fast(mlp, p["down"], None, O.F16, None, resid, M, H, INTER, O.ACCUM, threads)
+        return resid
+
+    step()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        step()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= target_s or n >= 10000:
+            break
+    per_layer = (shape_bytes(M, QKV, H, 1) + shape_bytes(M, H, H, 2) + shape_bytes(M, INTER, H, 8)
+                 + shape_bytes(M, H, INTER, 2))
+    nbytes = per_layer * len(host)
+    return dict(value=nbytes * n / dt / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"{len(host)} of the 24 decode-step layers (8 linears, M=2, fp16 W) x {n} repeats, "
+                       f"{dt:.1f} s, oracle linear_fast (K sum split 16 ways) with {threads} OpenMP threads",
+                step_ms_extrapolated=1e3 * dt / n * LAYERS / len(host))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["decode", "all"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the linear hot path "
+              "would shard by output features, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        return 2
+    ensure_built()
+    import torch
+    import mingtts as mt
+    mt.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log("generating 24 layers of fp16 weights")
+    ws = make_layers(torch, dev)
+    torch.cuda.synchronize()
+
+    log(f"decode step (persistent sequence): {args.warmup} warmup + {args.steps} timed")
+    d = bench_decode_seq(torch, mt, dev, ws, args.steps, args.warmup)
+    t = sorted(d["times_ms"])
+    mean_ms = sum(t) / len(t)
+    median_ms = t[len(t) // 2]
+    gbs = d["bytes"] / (mean_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0, 0.02^2) fp16 weights, N(0, 1) fp32 activations, generated on the device)",
+        "config": {
+            "workload": "decode step of the Qwen2-0.5B backbone linears: 24 layers x {qkv 1152x896+bias, "
+                        "o 896x896 +=, gate|up 2x4864x896 SiLU*mul, down 896x4864 +=}, M=2 (CFG pair), "
+                        "fp16 W, fp32 activations and outputs, one persistent launch of 96 dependent linears",
+            "layers": LAYERS, "rows": 2, "hidden": H, "intermediate": INTER, "qkv": QKV,
+            "parallelism": "single GPU",
+        },
+        "decode_step_us": round(mean_ms * 1e3, 2),
+        "decode_step_us_median": round(median_ms * 1e3, 2),
+        "decode_step_us_min": round(t[0] * 1e3, 2),
+        "hbm_pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "algorithmic_bytes_per_step": d["bytes"],
+        "seq_workgroups": d["groups"],
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "seq_kernel<2, f16, f32> (one launch per decode step)"},
+    }
+    if args.only == "all":
+        log("decode step as 96 separate launches")
+        p = bench_decode_per_op(torch, mt, dev, ws, max(5, args.steps // 5))
+        line["decode_step_us_per_op_launches"] = round(1e3 * sorted(p["times_ms"])[len(p["times_ms"]) // 2], 2)
+        log("single GEMV 4864x896 from a rotated 1 GiB pool")
+        line["gemv_single"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                               for k, v in bench_gemv_single(torch, mt, dev).items()}
+        line["gemv_single_m2"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                  for k, v in bench_gemv_single(torch, mt, dev, M=2).items()}
+        line["prefill"] = []
+        for M in (64, 256, 512):
+            log(f"prefill stack M={M}")
+            line["prefill"].append({k: (round(v, 3) if isinstance(v, float) else v)
+                                    for k, v in bench_prefill(torch, mt, dev, ws, M).items()})
+        log("decode attention batch 2")
+        line["attention_decode"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                    for k, v in bench_attention(torch, mt, dev).items()}
+        log("DiT head")
+        line["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
+    if not args.no_cpu:
+        log("CPU baseline (oracle, host cores)")
+        cb = cpu_baseline(torch, ws)
+        line["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cb.items()}
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,193 @@
+/*
+ * mingtts_hip.h -- C ABI of the MI355X (gfx950) linear hot path of MingTTS.
+ *
+ * Every entry point takes caller-owned device pointers, enqueues work on the
+ * given HIP stream and returns; the caller synchronises.  No entry point
+ * allocates device memory on the call path except mt_seq_create (once, at plan
+ * time).  Errors are returned, never raised: 0 on success, a negative code
+ * otherwise, with a message in mt_last_error() (thread-local).
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   mt_linear            Encoder.linear            Sources/MingTTS/Engine/Kernels.swift:128-161
+ *   mt_gemv_params       GemvParams                Sources/MingTTS/Engine/Shaders.swift:39
+ *   MT_BIAS .. MT_SILU   GemvFlags                 Sources/MingTTS/Engine/Kernels.swift:21-28
+ *   mt_linear_kernel     Kernels.usesGemm + the    Sources/MingTTS/Engine/Kernels.swift:81-86,
+ *                        scalarRowsMax rule                                         126, 137-151
+ *   mt_set_tuning        Encoder.kSplitOverride /  Sources/MingTTS/Engine/Kernels.swift:98-126
+ *                        columnTilesOverride /
+ *                        scalarRowsMax
+ *   mt_seq_*             QwenForward.dispatches    Sources/MingTTS/Engine/Qwen.swift:72-97
+ *                        encoded on one serial       (each dispatch sees the writes of the
+ *                        compute encoder             ones before it)
+ *   mt_rope_cache        Encoder.ropeCache         Sources/MingTTS/Engine/Kernels.swift:180-191
+ *   mt_attention         Encoder.attention         Sources/MingTTS/Engine/Kernels.swift:193-206
+ *   mt_attention_decode  Encoder.attention over B  Sources/MingTTS/Engine/Kernels.swift:193-206
+ *                        independent caches at
+ *                        M = 1 each
+ *   mt_last_error        MingTTSError text         Sources/MingTTS/Engine/MetalContext.swift:6-26
+ */
+#ifndef MINGTTS_HIP_H
+#define MINGTTS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI-identical to hipStream_t; NULL is the default stream. */
+typedef struct ihipStream_t *mt_stream_t;
+
+/* Return codes. */
+#define MT_OK 0
+#define MT_EHIP (-5)       /* a HIP runtime error; the text is in mt_last_error() */
+#define MT_ENOMEM (-12)
+#define MT_EINVAL (-22)    /* a shape, alignment, dtype or pointer the kernels cannot take */
+#define MT_ENOTSUP (-95)
+
+/* GemvParams, Shaders.swift:39.  y[m, n] = sum_k x[m, k] w[n, k] (+ epilogue).
+ * ldx / ldy are row strides in elements of x / y.  eps is unused by linears. */
+typedef struct mt_gemv_params {
+    uint32_t M, N, K, ldx, ldy, flags;
+    float eps;
+} mt_gemv_params;
+
+/* GemvFlags, Kernels.swift:21-28.  Epilogue order (Shaders.swift:92-103):
+ * v = acc + bias[n]; v = silu(v) * acc2 (SILU_GATE, acc2 = x . w2); v = gelu_tanh(v);
+ * v = silu(v); v += y_old (ACCUM); store. */
+enum {
+    MT_BIAS = 1,
+    MT_ACCUM = 2,
+    MT_GELU = 4,
+    MT_SILU_GATE = 8,
+    MT_SILU = 16
+};
+
+/* Element types.  Weights and bias are 16-bit; activations x may be any of the
+ * three; y is always fp32 (an fp16/bf16 output alone would break 1e-3). */
+typedef enum mt_dtype { MT_F32 = 0, MT_F16 = 1, MT_BF16 = 2 } mt_dtype;
+
+/* Kernel families, as reported by mt_linear_kernel. */
+enum { MT_KERNEL_GEMV = 1, MT_KERNEL_GEMM = 2 };
+
+/*
+ * One linear, Encoder.linear (Kernels.swift:128-161).
+ *   x     [M, ldx] of type xt; rows past M are never read.
+ *   w     [N, K] of type wt, row-major, 16-byte aligned, K % 8 == 0.
+ *   w2    [N, K] gate partner ("up") for MT_SILU_GATE, else NULL.
+ *   bias  [N] of type wt, or NULL.  A non-NULL bias sets MT_BIAS (Kernels.swift:135);
+ *         MT_BIAS with a NULL bias is an error.
+ *   y     [M, ldy] fp32; read first when MT_ACCUM (y may be the residual stream).
+ *         x must not overlap y.
+ * Requirements (else MT_EINVAL): K % 8 == 0; ldx >= K, ldy >= N; x 16-byte aligned
+ * and ldx * sizeof(xt) % 16 == 0; w, w2 16-byte aligned; y 4-byte aligned;
+ * wt in {MT_F16, MT_BF16}.  M == 0 or N == 0 is a no-op.
+ */
+int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt,
+              const void *bias, float *y, mt_gemv_params p, mt_stream_t stream);
+
+/* The kernel family mt_linear picks for a shape (MT_KERNEL_GEMV / MT_KERNEL_GEMM),
+ * the analogue of Kernels.usesGemm and scalarRowsMax. */
+int mt_linear_kernel(uint32_t M, uint32_t N, uint32_t K, mt_dtype xt, mt_dtype wt);
+
+/* Process-wide tuning overrides, the analogue of Encoder.kSplitOverride /
+ * columnTilesOverride / scalarRowsMax (Kernels.swift:98-126).  value < 0 restores
+ * the default.  Returns the previous value, or MT_EINVAL for an unknown key. */
+enum {
+    MT_TUNE_GEMV_ROWS_MAX = 1,   /* M up to this goes to the GEMV family (default 8) */
+    MT_TUNE_GEMV_LANES = 2,      /* lanes per output feature in the GEMV, 8..64 (0 = auto) */
+    MT_TUNE_GEMM_SPLITK = 3,     /* K splits of the MFMA GEMM (0 = auto) */
+    MT_TUNE_SEQ_GROUPS = 4       /* workgroups of the persistent sequence kernel (0 = auto) */
+};
+int mt_set_tuning(int key, int value);
+
+/*
+ * A sequence of linears executed in order, each seeing the writes of the ones
+ * before it -- QwenForward.dispatches on a serial encoder (Qwen.swift:72-97).
+ * mt_seq_create validates every op and uploads the plan once; mt_seq_run runs the
+ * whole sequence as ONE persistent kernel launch (cooperative, one workgroup set
+ * resident for the whole sequence, a device-wide barrier between ops).  Every op
+ * must satisfy mt_linear's requirements with M <= 8.  The pointers in the plan are
+ * fixed; their contents may change between runs.  Runs of one plan must not
+ * overlap in time (the plan's barrier state is shared).
+ */
+typedef struct mt_linear_op {
+    const void *x;
+    const void *w;
+    const void *w2;
+    const void *bias;
+    float *y;
+    mt_gemv_params p;
+    int32_t xt;   /* mt_dtype */
+    int32_t wt;   /* mt_dtype */
+} mt_linear_op;
+
+typedef struct mt_seq mt_seq;
+int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out);
+int mt_seq_run(mt_seq *seq, mt_stream_t stream);
+int mt_seq_destroy(mt_seq *seq);
+/* Workgroups the plan's kernel runs with (after mt_seq_create). */
+int mt_seq_groups(const mt_seq *seq);
+/* Synchronous health check of a plan after its runs completed: MT_EHIP if any device-wide
+ * barrier of a run gave up after its spin bound (co-residency was lost), else MT_OK.
+ * No counterpart in the reference (Metal has no in-kernel grid barrier). */
+int mt_seq_check(mt_seq *seq);
+
+/*
+ * Encoder.ropeCache (Kernels.swift:180-191, Shaders.swift:451-486): NeoX RoPE
+ * (pairs i, i + 32 of each 64-wide head, angle = pos * inv_freq[i]) on the hq query
+ * heads of qkv in place, and the rotated k heads plus the raw v heads appended to
+ * the caches at positions pos0 .. pos0 + M - 1.  qkv rows are [q(hq*64) | k(hkv*64) |
+ * v(hkv*64)] with row stride ldq floats.  Caches are [hkv, cache_len, 64] of type
+ * cache_t (MT_F32 as the reference, or MT_F16).
+ */
+int mt_rope_cache(float *qkv, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv, uint32_t pos0,
+                  void *k_cache, void *v_cache, mt_dtype cache_t, uint32_t cache_len,
+                  const float *inv_freq, mt_stream_t stream);
+
+/*
+ * Batched decode form of mt_rope_cache: B independent sequences, one qkv row each.
+ * Row b is rotated at position pos[b] (a device array of B uint32) and its k / v land
+ * in sequence b's caches (k_cache / v_cache + b * cache_stride elements) at pos[b].
+ * A pos[b] >= cache_len appends nothing (the q heads are still rotated).
+ */
+int mt_rope_cache_decode(float *qkv, uint32_t ldq, uint32_t B, uint32_t hq, uint32_t hkv,
+                         const uint32_t *pos, void *k_cache, void *v_cache, mt_dtype cache_t,
+                         uint32_t cache_len, uint64_t cache_stride, const float *inv_freq,
+                         mt_stream_t stream);
+
+/*
+ * Encoder.attention (Kernels.swift:193-206, Shaders.swift:490-596): causal GQA of
+ * the M query rows at positions pos0 .. pos0 + M - 1 over the cache, keys
+ * [max(0, pos + 1 - window), pos] (window 0 = unlimited), scores scaled by `scale`,
+ * max-subtracted softmax, out = sum p v.  q rows hold hq heads of 64 (stride ldq),
+ * out rows stride ldo.  pos0 + M <= cache_len <= 4096.
+ */
+int mt_attention(const float *q, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv,
+                 uint32_t pos0, uint32_t window, const void *k_cache, const void *v_cache,
+                 mt_dtype cache_t, uint32_t cache_len, float *out, uint32_t ldo, float scale,
+                 mt_stream_t stream);
+
+/*
+ * Batched decode attention: B independent sequences, one query row each (the CFG
+ * cond/uncond pair at B = 2).  Sequence b attends over its own cache (k_cache +
+ * b * cache_stride elements, layout [hkv, cache_len, 64]) at keys
+ * [max(0, len_b - window), len_b), len_b = lens[b] (a device array of B uint32,
+ * 1 <= len_b <= cache_len).  q / out rows b at stride ldq / ldo.
+ */
+int mt_attention_decode(const float *q, uint32_t ldq, uint32_t B, uint32_t hq, uint32_t hkv,
+                        const uint32_t *lens, uint32_t window, const void *k_cache,
+                        const void *v_cache, mt_dtype cache_t, uint32_t cache_len,
+                        uint64_t cache_stride, float *out, uint32_t ldo, float scale,
+                        mt_stream_t stream);
+
+/* Text of the last error on this thread ("" if none). */
+const char *mt_last_error(void);
+/* Library version string. */
+const char *mt_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINGTTS_HIP_H */

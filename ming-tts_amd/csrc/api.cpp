@@ -1,0 +1,258 @@
+// The C ABI (include/mingtts_hip.h): argument validation, kernel choice, error text.
+//
+// Validation happens before any HIP call, so a rejected call touches no device state
+// and works without a GPU (the CPU tests rely on that).  Shape errors that the reference
+// turns into preconditionFailure (Kernels.swift:105, 147) are returned as MT_EINVAL.
+#include <errno.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+#include <vector>
+
+#include "mingtts_hip.h"
+#include "mt_internal.hpp"
+
+namespace mt {
+
+
+namespace {
+thread_local char g_err[512] = "";
+Tuning g_tuning;
+
+size_t dtype_size(int t) { return t == DT_F32 ? 4 : 2; }
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+const char *dtype_name(int t) { return t == DT_F32 ? "f32" : t == DT_F16 ? "f16" : t == DT_BF16 ? "bf16" : "?"; }
+}  // namespace
+
+Tuning &tuning() { return g_tuning; }
+
+int set_error(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(MT_EHIP, "%s launch: %s", what, hipGetErrorString(e));
+    return MT_OK;
+}
+
+// Checks one linear's arguments; fills `a` (with the bias flag set from the pointer,
+// Kernels.swift:135).  Returns MT_OK or MT_EINVAL with the reason.
+static int validate_linear(const char *who, const void *x, int xt, const void *w, const void *w2, int wt,
+                           const void *bias, float *y, const mt_gemv_params &p, LinearArgs &a) {
+    if (xt != DT_F32 && xt != DT_F16 && xt != DT_BF16)
+        return set_error(MT_EINVAL, "%s: unknown activation dtype %d", who, xt);
+    if (wt != DT_F16 && wt != DT_BF16)
+        return set_error(MT_EINVAL, "%s: weights must be f16 or bf16, got %s", who, dtype_name(wt));
+    const uint32_t known = MT_BIAS | MT_ACCUM | MT_GELU | MT_SILU_GATE | MT_SILU;
+    if (p.flags & ~known) return set_error(MT_EINVAL, "%s: unknown flag bits 0x%x", who, p.flags & ~known);
+    uint32_t flags = p.flags;
+    if (bias) flags |= MT_BIAS;
+    if ((flags & MT_BIAS) && !bias) return set_error(MT_EINVAL, "%s: MT_BIAS without a bias pointer", who);
+    if ((flags & MT_SILU_GATE) && !w2) return set_error(MT_EINVAL, "%s: MT_SILU_GATE without w2", who);
+    if (p.M && p.N) {
+        if (!x || !w || !y) return set_error(MT_EINVAL, "%s: null x, w or y", who);
+        if (p.K == 0 || p.K % 8) return set_error(MT_EINVAL, "%s: K must be a positive multiple of 8, got %u", who, p.K);
+        if (p.ldx < p.K) return set_error(MT_EINVAL, "%s: ldx %u < K %u", who, p.ldx, p.K);
+        if (p.ldy < p.N) return set_error(MT_EINVAL, "%s: ldy %u < N %u", who, p.ldy, p.N);
+        if (!aligned(x, 16) || (static_cast<size_t>(p.ldx) * dtype_size(xt)) % 16)
+            return set_error(MT_EINVAL, "%s: x must be 16-byte aligned with 16-byte row stride", who);
+        if (!aligned(w, 16) || (w2 && (flags & MT_SILU_GATE) && !aligned(w2, 16)))
+            return set_error(MT_EINVAL, "%s: w / w2 must be 16-byte aligned", who);
+        if (!aligned(y, 4)) return set_error(MT_EINVAL, "%s: y must be 4-byte aligned", who);
+        if (bias && !aligned(bias, 2)) return set_error(MT_EINVAL, "%s: bias must be 2-byte aligned", who);
+        // x must not overlap y (y may be read-modify-written under MT_ACCUM).
+        const char *xb = static_cast<const char *>(x);
+        const char *xe = xb + (static_cast<size_t>(p.M - 1) * p.ldx + p.K) * dtype_size(xt);
+        const char *yb = reinterpret_cast<const char *>(y);
+        const char *ye = yb + (static_cast<size_t>(p.M - 1) * p.ldy + p.N) * 4;
+        if (xb < ye && yb < xe) return set_error(MT_EINVAL, "%s: x overlaps y", who);
+    }
+    a.x = x;
+    a.w = static_cast<const uint16_t *>(w);
+    a.w2 = static_cast<const uint16_t *>((flags & MT_SILU_GATE) ? w2 : w);
+    a.bias = static_cast<const uint16_t *>(bias);
+    a.y = y;
+    a.M = p.M;
+    a.N = p.N;
+    a.K = p.K;
+    a.ldx = p.ldx;
+    a.ldy = p.ldy;
+    a.flags = flags;
+    return MT_OK;
+}
+
+static int kernel_for(uint32_t M) { return static_cast<int>(M) <= g_tuning.gemv_rows_max ? MT_KERNEL_GEMV : MT_KERNEL_GEMM; }
+
+}  // namespace mt
+
+using namespace mt;
+
+extern "C" {
+
+const char *mt_last_error(void) { return g_err; }
+
+const char *mt_version(void) { return "mingtts_hip 0.1.0 gfx950"; }
+
+int mt_linear_kernel(uint32_t M, uint32_t N, uint32_t K, mt_dtype xt, mt_dtype wt) {
+    (void)N; (void)K; (void)xt; (void)wt;
+    return kernel_for(M);
+}
+
+int mt_set_tuning(int key, int value) {
+    int *slot = nullptr;
+    int def = 0;
+    switch (key) {
+        case MT_TUNE_GEMV_ROWS_MAX: slot = &g_tuning.gemv_rows_max; def = 8; break;
+        case MT_TUNE_GEMV_LANES: slot = &g_tuning.gemv_lanes; def = 0; break;
+        case MT_TUNE_GEMM_SPLITK: slot = &g_tuning.gemm_splitk; def = 0; break;
+        case MT_TUNE_SEQ_GROUPS: slot = &g_tuning.seq_groups; def = 0; break;
+        default: return set_error(MT_EINVAL, "mt_set_tuning: unknown key %d", key);
+    }
+    if (key == MT_TUNE_GEMV_ROWS_MAX && value > 8)
+        return set_error(MT_EINVAL, "mt_set_tuning: the GEMV takes at most 8 rows per block, got %d", value);
+    const int old = *slot;
+    *slot = value < 0 ? def : value;
+    return old;
+}
+
+int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt, const void *bias,
+              float *y, mt_gemv_params p, mt_stream_t stream) {
+    LinearArgs a;
+    int rc = validate_linear("mt_linear", x, xt, w, w2, wt, bias, y, p, a);
+    if (rc) return rc;
+    if (p.M == 0 || p.N == 0) return MT_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (kernel_for(p.M) == MT_KERNEL_GEMV) return launch_gemv(a, xt, wt, s, g_tuning.gemv_lanes);
+    return launch_gemm(a, xt, wt, s, g_tuning.gemm_splitk);
+}
+
+int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
+    if (!out) return set_error(MT_EINVAL, "mt_seq_create: null out");
+    *out = nullptr;
+    if (n_ops && !ops) return set_error(MT_EINVAL, "mt_seq_create: null ops");
+    std::vector<SeqOp> dev(n_ops);
+    int wt = -1, xt = -1;
+    uint32_t max_m = 1;
+    for (uint32_t i = 0; i < n_ops; i++) {
+        const mt_linear_op &o = ops[i];
+        char who[48];
+        snprintf(who, sizeof(who), "mt_seq_create: op %u", i);
+        LinearArgs a;
+        int rc = validate_linear(who, o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, a);
+        if (rc) return rc;
+        if (o.p.M == 0 || o.p.N == 0) return set_error(MT_EINVAL, "%s: empty op", who);
+        if (o.p.M > 8) return set_error(MT_EINVAL, "%s: a sequence takes M <= 8, got %u", who, o.p.M);
+        if (wt < 0) { wt = o.wt; xt = o.xt; }
+        if (o.wt != wt || o.xt != xt)
+            return set_error(MT_EINVAL, "%s: every op of a sequence must share the weight and activation types", who);
+        if (o.p.M > max_m) max_m = o.p.M;
+        SeqOp &d = dev[i];
+        d.x = a.x; d.w = a.w; d.w2 = a.w2; d.bias = a.bias; d.y = a.y;
+        d.M = a.M; d.N = a.N; d.K = a.K; d.ldx = a.ldx; d.ldy = a.ldy; d.flags = a.flags;
+        d.lanes_log2 = gemv_lanes_log2(a.K, g_tuning.gemv_lanes);
+        d.pad = 0;
+    }
+    const int mr = max_m <= 1 ? 1 : max_m <= 2 ? 2 : max_m <= 4 ? 4 : 8;
+    SeqPlan *plan = nullptr;
+    int rc = seq_create(dev.data(), n_ops, mr, wt < 0 ? DT_F16 : wt, xt < 0 ? DT_F32 : xt, &plan);
+    if (rc) return rc;
+    *out = reinterpret_cast<mt_seq *>(plan);
+    return MT_OK;
+}
+
+int mt_seq_run(mt_seq *seq, mt_stream_t stream) {
+    if (!seq) return set_error(MT_EINVAL, "mt_seq_run: null plan");
+    return seq_run(reinterpret_cast<SeqPlan *>(seq), reinterpret_cast<hipStream_t>(stream));
+}
+
+int mt_seq_check(mt_seq *seq) {
+    if (!seq) return set_error(MT_EINVAL, "mt_seq_check: null plan");
+    return seq_check(reinterpret_cast<SeqPlan *>(seq));
+}
+
+int mt_seq_destroy(mt_seq *seq) {
+    seq_destroy(reinterpret_cast<SeqPlan *>(seq));
+    return MT_OK;
+}
+
+int mt_seq_groups(const mt_seq *seq) {
+    if (!seq) return set_error(MT_EINVAL, "mt_seq_groups: null plan");
+    return seq_groups(reinterpret_cast<const SeqPlan *>(seq));
+}
+
+// Shared checks of the rope / attention entry points.
+static int validate_heads(const char *who, uint32_t hq, uint32_t hkv, int ct, uint32_t cache_len) {
+    if (hq == 0 || hkv == 0 || hq % hkv) return set_error(MT_EINVAL, "%s: hq %u must be a positive multiple of hkv %u", who, hq, hkv);
+    if (ct != DT_F32 && ct != DT_F16) return set_error(MT_EINVAL, "%s: cache dtype must be f32 or f16", who);
+    if (cache_len == 0 || cache_len > 4096) return set_error(MT_EINVAL, "%s: cache_len %u outside 1..4096", who, cache_len);
+    return MT_OK;
+}
+
+int mt_rope_cache(float *qkv, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv, uint32_t pos0, void *k_cache,
+                  void *v_cache, mt_dtype cache_t, uint32_t cache_len, const float *inv_freq, mt_stream_t stream) {
+    int rc = validate_heads("mt_rope_cache", hq, hkv, cache_t, cache_len);
+    if (rc) return rc;
+    if (M == 0) return MT_OK;
+    if (!qkv || !k_cache || !v_cache || !inv_freq) return set_error(MT_EINVAL, "mt_rope_cache: null pointer");
+    if (ldq < (hq + 2 * hkv) * 64) return set_error(MT_EINVAL, "mt_rope_cache: ldq %u < (hq + 2 hkv) * 64", ldq);
+    if (static_cast<uint64_t>(pos0) + M > cache_len)
+        return set_error(MT_EINVAL, "mt_rope_cache: positions %u..%u past cache_len %u", pos0, pos0 + M - 1, cache_len);
+    return launch_rope_cache(qkv, ldq, M, hq, hkv, pos0, nullptr, k_cache, v_cache, cache_t, cache_len, 0, inv_freq,
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+int mt_rope_cache_decode(float *qkv, uint32_t ldq, uint32_t B, uint32_t hq, uint32_t hkv, const uint32_t *pos,
+                         void *k_cache, void *v_cache, mt_dtype cache_t, uint32_t cache_len, uint64_t cache_stride,
+                         const float *inv_freq, mt_stream_t stream) {
+    int rc = validate_heads("mt_rope_cache_decode", hq, hkv, cache_t, cache_len);
+    if (rc) return rc;
+    if (B == 0) return MT_OK;
+    if (!qkv || !pos || !k_cache || !v_cache || !inv_freq) return set_error(MT_EINVAL, "mt_rope_cache_decode: null pointer");
+    if (ldq < (hq + 2 * hkv) * 64) return set_error(MT_EINVAL, "mt_rope_cache_decode: ldq %u < (hq + 2 hkv) * 64", ldq);
+    if (B > 1 && cache_stride < static_cast<uint64_t>(hkv) * cache_len * 64)
+        return set_error(MT_EINVAL, "mt_rope_cache_decode: cache_stride smaller than one cache");
+    return launch_rope_cache(qkv, ldq, B, hq, hkv, 0, pos, k_cache, v_cache, cache_t, cache_len, cache_stride,
+                             inv_freq, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mt_attention(const float *q, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv, uint32_t pos0, uint32_t window,
+                 const void *k_cache, const void *v_cache, mt_dtype cache_t, uint32_t cache_len, float *out,
+                 uint32_t ldo, float scale, mt_stream_t stream) {
+    int rc = validate_heads("mt_attention", hq, hkv, cache_t, cache_len);
+    if (rc) return rc;
+    if (M == 0) return MT_OK;
+    if (!q || !k_cache || !v_cache || !out) return set_error(MT_EINVAL, "mt_attention: null pointer");
+    if (ldq < hq * 64 || ldo < hq * 64) return set_error(MT_EINVAL, "mt_attention: ldq / ldo < hq * 64");
+    if (!aligned(q, 16) || ldq % 4 || !aligned(out, 16) || ldo % 4)
+        return set_error(MT_EINVAL, "mt_attention: q / out must be 16-byte aligned with 16-byte row strides");
+    if (static_cast<uint64_t>(pos0) + M > cache_len)
+        return set_error(MT_EINVAL, "mt_attention: positions %u..%u past cache_len %u", pos0, pos0 + M - 1, cache_len);
+    return launch_attention(q, ldq, M, hq, hkv, pos0, nullptr, window, k_cache, v_cache, cache_t, cache_len, 0, out,
+                            ldo, scale, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mt_attention_decode(const float *q, uint32_t ldq, uint32_t B, uint32_t hq, uint32_t hkv, const uint32_t *lens,
+                        uint32_t window, const void *k_cache, const void *v_cache, mt_dtype cache_t,
+                        uint32_t cache_len, uint64_t cache_stride, float *out, uint32_t ldo, float scale,
+                        mt_stream_t stream) {
+    int rc = validate_heads("mt_attention_decode", hq, hkv, cache_t, cache_len);
+    if (rc) return rc;
+    if (B == 0) return MT_OK;
+    if (!q || !lens || !k_cache || !v_cache || !out) return set_error(MT_EINVAL, "mt_attention_decode: null pointer");
+    if (ldq < hq * 64 || ldo < hq * 64) return set_error(MT_EINVAL, "mt_attention_decode: ldq / ldo < hq * 64");
+    if (!aligned(q, 16) || ldq % 4 || !aligned(out, 16) || ldo % 4)
+        return set_error(MT_EINVAL, "mt_attention_decode: q / out must be 16-byte aligned with 16-byte row strides");
+    if (B > 1 && cache_stride < static_cast<uint64_t>(hkv) * cache_len * 64)
+        return set_error(MT_EINVAL, "mt_attention_decode: cache_stride smaller than one cache");
+    return launch_attention(q, ldq, B, hq, hkv, 0, lens, window, k_cache, v_cache, cache_t, cache_len, cache_stride,
+                            out, ldo, scale, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

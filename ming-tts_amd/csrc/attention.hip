@@ -1,0 +1,233 @@
+// NeoX RoPE + KV-cache append, and causal GQA attention over the cache.
+//
+// Reference kernels replaced: rope_cache (Shaders.swift:451-486) and attention_cache<SPLIT>
+// (Shaders.swift:490-596).  Same arithmetic (fp32 scores, scale after the q.k dot,
+// max-subtracted softmax, fp32 p.v), caches of fp32 (reference) or fp16 (decode config).
+//
+// Attention layout on gfx950: one 256-thread workgroup per (query row, head) item.
+//   - scores: groups of 8 lanes own one key (lane r of a group reads dims 8r..8r+7, so a
+//     wave reads 8 whole key rows per load instruction), 32 keys per pass, the 8 partial
+//     dots meet by shuffles; scores land in LDS (at most 4096 keys);
+//   - softmax: block max and block sum through LDS;
+//   - p.v: 16 lanes cover the 64 dims of one V row (4 dims each, one coalesced row per
+//     16 lanes), 16 key phases per workgroup, partial sums meet in LDS in a fixed order.
+// Batched decode (mt_attention_decode) is the same kernel with a per-row cache base and
+// the row's query position read from a device array.
+#include "mt_device.hpp"
+#include "mt_internal.hpp"
+#include "mingtts_hip.h"
+
+namespace mt {
+
+namespace {
+
+constexpr int ATT_THREADS = 256;
+constexpr int ATT_MAXKEYS = 4096;
+
+template <int CT>
+__device__ __forceinline__ void load8(const void *base, size_t off, float *o) {
+    if constexpr (CT == DT_F32) {
+        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + off);
+        const float4 a = p[0], b = p[1];
+        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+        o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+    } else {
+        const uint4 v = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + off);
+        unpack8<CT>(v, o);
+    }
+}
+
+template <int CT>
+__device__ __forceinline__ float4 load4(const void *base, size_t off) {
+    if constexpr (CT == DT_F32) {
+        return *reinterpret_cast<const float4 *>(static_cast<const float *>(base) + off);
+    } else {
+        const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(base) + off);
+        return make_float4(dec_lo<CT>(v.x), dec_hi<CT>(v.x), dec_lo<CT>(v.y), dec_hi<CT>(v.y));
+    }
+}
+
+template <int CT>
+__device__ __forceinline__ void store1(void *base, size_t off, float v) {
+    if constexpr (CT == DT_F32) static_cast<float *>(base)[off] = v;
+    else static_cast<_Float16 *>(base)[off] = static_cast<_Float16>(v);
+}
+
+// Grid (ceil(slots / 2), rows); 64 threads: lane & 31 is the rotation pair, lane >> 5 picks
+// one of two head slots.  Slots: hq query heads, hkv key heads, hkv value heads.
+template <int CT>
+__global__ __launch_bounds__(64) void rope_cache_kernel(float *qkv, uint32_t ldq, uint32_t hq, uint32_t hkv,
+                                                        uint32_t pos0, const uint32_t *pos_arr, void *kc,
+                                                        void *vc, uint32_t cache_len, uint64_t cache_stride,
+                                                        const float *inv_freq) {
+    const uint32_t i = threadIdx.x & 31;
+    const uint32_t slot = blockIdx.x * 2 + (threadIdx.x >> 5);
+    const uint32_t m = blockIdx.y;
+    if (slot >= hq + 2 * hkv) return;
+    const uint32_t pos = pos_arr ? pos_arr[m] : pos0 + m;
+    const uint64_t cbase = pos_arr ? static_cast<uint64_t>(m) * cache_stride : 0;
+    float *row = qkv + static_cast<size_t>(m) * ldq + static_cast<size_t>(slot) * 64;
+    // A device-side position past the cache (only possible through pos_arr, which the host
+    // cannot see) appends nothing; the query heads are still rotated.
+    if (slot >= hq && pos >= cache_len) return;
+    if (slot >= hq + hkv) {
+        const size_t dst = cbase + (static_cast<size_t>(slot - hq - hkv) * cache_len + pos) * 64;
+        store1<CT>(vc, dst + i, row[i]);
+        store1<CT>(vc, dst + i + 32, row[i + 32]);
+        return;
+    }
+    const float angle = static_cast<float>(pos) * inv_freq[i];
+    const float c = cosf(angle), s = sinf(angle);
+    const float x0 = row[i], x1 = row[i + 32];
+    const float r0 = x0 * c - x1 * s;
+    const float r1 = x1 * c + x0 * s;
+    if (slot < hq) {
+        row[i] = r0;
+        row[i + 32] = r1;
+    } else {
+        const size_t dst = cbase + (static_cast<size_t>(slot - hq) * cache_len + pos) * 64;
+        store1<CT>(kc, dst + i, r0);
+        store1<CT>(kc, dst + i + 32, r1);
+    }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <int CT>
+__global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, uint32_t ldq, uint32_t hq,
+                                                                uint32_t hkv, uint32_t pos0, const uint32_t *lens,
+                                                                uint32_t window, const void *kc, const void *vc,
+                                                                uint32_t cache_len, uint64_t cache_stride,
+                                                                float *out, uint32_t ldo, float scale) {
+    __shared__ float sc[ATT_MAXKEYS];
+    __shared__ float red[ATT_THREADS / 64];
+    __shared__ float4 part[16][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t m = blockIdx.x / hq, h = blockIdx.x % hq;
+    const uint32_t kvh = h / (hq / hkv);
+    // Device-side lengths are clamped to the cache; a zero length attends to nothing and
+    // writes zeros.
+    const uint32_t len = lens ? min(lens[m], cache_len) : pos0 + m + 1;
+    const uint64_t cbase = lens ? static_cast<uint64_t>(m) * cache_stride : 0;
+    const uint32_t jEnd = len;
+    const uint32_t jStart = (window > 0 && jEnd > window) ? jEnd - window : 0;
+    const int nk = static_cast<int>(jEnd - jStart);
+    const size_t kvbase = cbase + (static_cast<size_t>(kvh) * cache_len + jStart) * 64;
+
+    // Scores.
+    const int r = tid & 7;
+    float qf[8];
+    {
+        const float4 *qp = reinterpret_cast<const float4 *>(q + static_cast<size_t>(m) * ldq + h * 64 + 8 * r);
+        const float4 a = qp[0], b = qp[1];
+        qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
+        qf[4] = b.x; qf[5] = b.y; qf[6] = b.z; qf[7] = b.w;
+    }
+    float mx = -INFINITY;
+    for (int t = tid >> 3; t < nk; t += ATT_THREADS / 8) {
+        float kf[8];
+        load8<CT>(kc, kvbase + static_cast<size_t>(t) * 64 + 8 * r, kf);
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) s = fmaf(qf[e], kf[e], s);
+        s += __shfl_xor(s, 4, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 1, 64);
+        s *= scale;
+        if (r == 0) sc[t] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+
+    // Softmax numerators and their sum.
+    float sum = 0.0f;
+    for (int t = tid; t < nk; t += ATT_THREADS) {
+        const float e = expf(sc[t] - mx);
+        sc[t] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+
+    // p . v: 16 lanes per V row (4 dims each), 16 key phases.
+    const int d4 = tid & 15, ks = tid >> 4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int t = ks;
+    for (; t + 48 < nk; t += 64) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = load4<CT>(vc, kvbase + static_cast<size_t>(t + 16 * u) * 64 + 4 * d4);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float p = sc[t + 16 * u];
+            acc.x = fmaf(p, v[u].x, acc.x);
+            acc.y = fmaf(p, v[u].y, acc.y);
+            acc.z = fmaf(p, v[u].z, acc.z);
+            acc.w = fmaf(p, v[u].w, acc.w);
+        }
+    }
+    for (; t < nk; t += 16) {
+        const float4 v = load4<CT>(vc, kvbase + static_cast<size_t>(t) * 64 + 4 * d4);
+        const float p = sc[t];
+        acc.x = fmaf(p, v.x, acc.x);
+        acc.y = fmaf(p, v.y, acc.y);
+        acc.z = fmaf(p, v.z, acc.z);
+        acc.w = fmaf(p, v.w, acc.w);
+    }
+    part[ks][d4] = acc;
+    __syncthreads();
+    if (tid < 16) {
+        float4 o = part[0][tid];
+        for (int k = 1; k < 16; k++) {
+            const float4 pp = part[k][tid];
+            o.x += pp.x; o.y += pp.y; o.z += pp.z; o.w += pp.w;
+        }
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        float4 res = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        *reinterpret_cast<float4 *>(out + static_cast<size_t>(m) * ldo + h * 64 + 4 * tid) = res;
+    }
+}
+
+}  // namespace
+
+int launch_rope_cache(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
+                      const uint32_t *pos_arr, void *kc, void *vc, int ct, uint32_t cache_len,
+                      uint64_t cache_stride, const float *inv_freq, hipStream_t stream) {
+    dim3 grid((hq + 2 * hkv + 1) / 2, rows);
+    if (ct == DT_F32)
+        hipLaunchKernelGGL(rope_cache_kernel<DT_F32>, grid, dim3(64), 0, stream, qkv, ldq, hq, hkv, pos0, pos_arr,
+                           kc, vc, cache_len, cache_stride, inv_freq);
+    else
+        hipLaunchKernelGGL(rope_cache_kernel<DT_F16>, grid, dim3(64), 0, stream, qkv, ldq, hq, hkv, pos0, pos_arr,
+                           kc, vc, cache_len, cache_stride, inv_freq);
+    return check_launch("rope_cache");
+}
+
+int launch_attention(const float *q, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
+                     const uint32_t *lens, uint32_t window, const void *kc, const void *vc, int ct,
+                     uint32_t cache_len, uint64_t cache_stride, float *out, uint32_t ldo, float scale,
+                     hipStream_t stream) {
+    dim3 grid(rows * hq);
+    if (ct == DT_F32)
+        hipLaunchKernelGGL(attention_kernel<DT_F32>, grid, dim3(ATT_THREADS), 0, stream, q, ldq, hq, hkv, pos0, lens,
+                           window, kc, vc, cache_len, cache_stride, out, ldo, scale);
+    else
+        hipLaunchKernelGGL(attention_kernel<DT_F16>, grid, dim3(ATT_THREADS), 0, stream, q, ldq, hq, hkv, pos0, lens,
+                           window, kc, vc, cache_len, cache_stride, out, ldo, scale);
+    return check_launch("attention");
+}
+
+}  // namespace mt

@@ -1,0 +1,88 @@
+// Standalone decode GEMV launches of mt_linear (M up to 8 rows per row block).
+//
+// Reference kernel replaced: gemv_kernel<MR> (Shaders.swift:47-108) and, for 3..8 rows,
+// gemm8_kernel (Shaders.swift:188-283).  One wave64 holds 64 / L output features; the
+// workgroup is 256 threads, or fewer when that leaves the grid short of workgroups.
+#include "gemv_core.hpp"
+#include "mt_internal.hpp"
+
+namespace mt {
+
+template <int MR, int WT, int XT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a, int lanes_log2) {
+    const int L = 1 << lanes_log2;
+    const int groups = static_cast<int>(blockDim.x) >> lanes_log2;
+    const int g = static_cast<int>(threadIdx.x) >> lanes_log2;
+    const int j = static_cast<int>(threadIdx.x) & (L - 1);
+    const uint32_t n = blockIdx.x * groups + g;
+    if (n >= a.N) return;  // the whole lane group leaves together; no block barrier follows
+    const uint32_t row0 = blockIdx.y * MR;
+    const int rows = min(MR, static_cast<int>(a.M - row0));
+    gemv_feature<MR, WT, XT, GATED, 4>(a, n, row0, rows, L, j);
+}
+
+namespace {
+
+typedef void (*gemv_fn)(LinearArgs, int);
+
+template <int MR, int WT, int XT>
+gemv_fn pick_gated(bool gated) {
+    return gated ? gemv_kernel<MR, WT, XT, true> : gemv_kernel<MR, WT, XT, false>;
+}
+
+template <int MR, int WT>
+gemv_fn pick_x(int xt, bool gated) {
+    switch (xt) {
+        case DT_F32: return pick_gated<MR, WT, DT_F32>(gated);
+        case DT_F16: return pick_gated<MR, WT, DT_F16>(gated);
+        default: return pick_gated<MR, WT, DT_BF16>(gated);
+    }
+}
+
+template <int MR>
+gemv_fn pick_w(int wt, int xt, bool gated) {
+    return wt == DT_BF16 ? pick_x<MR, DT_BF16>(xt, gated) : pick_x<MR, DT_F16>(xt, gated);
+}
+
+gemv_fn pick(int mr, int wt, int xt, bool gated) {
+    switch (mr) {
+        case 1: return pick_w<1>(wt, xt, gated);
+        case 2: return pick_w<2>(wt, xt, gated);
+        case 4: return pick_w<4>(wt, xt, gated);
+        default: return pick_w<8>(wt, xt, gated);
+    }
+}
+
+}  // namespace
+
+int gemv_lanes_log2(uint32_t K, int override_lanes) {
+    if (override_lanes >= 8 && override_lanes <= 64) {
+        int l2 = 3;
+        while ((1 << l2) < override_lanes) l2++;
+        return l2;
+    }
+    // About eight 16-byte chunks per lane: K = 896 -> 16 lanes (7 chunks each),
+    // K = 4864 -> 64 lanes (9.5), K = 1024 -> 16 (8), K = 4096 -> 64 (8).
+    const uint32_t kc = K / 8;
+    int l2 = 3;
+    while ((1u << l2) < 64u && (1u << l2) * 8u < kc) l2++;
+    return l2;
+}
+
+int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes) {
+    const bool gated = (a.flags & F_SILU_GATE) != 0;
+    const int mr = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : 8;
+    const int l2 = gemv_lanes_log2(a.K, override_lanes);
+    const int L = 1 << l2;
+    // 256 threads per workgroup unless that leaves fewer than 512 workgroups; never below
+    // one wave (64 threads).
+    int threads = 256;
+    while (threads > 64 && (a.N + (threads / L) - 1) / (threads / L) < 512) threads >>= 1;
+    const int per_group = threads / L;
+    dim3 grid((a.N + per_group - 1) / per_group, (a.M + mr - 1) / mr);
+    gemv_fn fn = pick(mr, wt, xt, gated);
+    hipLaunchKernelGGL(fn, grid, dim3(threads), 0, stream, a, l2);
+    return check_launch("gemv");
+}
+
+}  // namespace mt

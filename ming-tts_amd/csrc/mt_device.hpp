@@ -1,0 +1,83 @@
+// Device helpers shared by the gfx950 kernels: 16-bit decode, the linear epilogue,
+// wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mt {
+
+enum : uint32_t { F_BIAS = 1, F_ACCUM = 2, F_GELU = 4, F_SILU_GATE = 8, F_SILU = 16 };
+enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+struct LinearArgs {
+    const void *x;
+    const uint16_t *w;
+    const uint16_t *w2;
+    const uint16_t *bias;
+    float *y;
+    uint32_t M, N, K, ldx, ldy, flags;
+};
+
+// bf16 is the top half of an fp32 (Shaders.swift:12).
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+__device__ __forceinline__ float f16_lo(uint32_t v) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFFu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t v) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
+template <int T>
+__device__ __forceinline__ float dec_lo(uint32_t v) {
+    if constexpr (T == DT_BF16) return bf16_lo(v); else return f16_lo(v);
+}
+template <int T>
+__device__ __forceinline__ float dec_hi(uint32_t v) {
+    if constexpr (T == DT_BF16) return bf16_hi(v); else return f16_hi(v);
+}
+
+// Eight 16-bit values of type T, packed little-endian in a uint4, to fp32.
+template <int T>
+__device__ __forceinline__ void unpack8(const uint4 v, float *o) {
+    o[0] = dec_lo<T>(v.x); o[1] = dec_hi<T>(v.x);
+    o[2] = dec_lo<T>(v.y); o[3] = dec_hi<T>(v.y);
+    o[4] = dec_lo<T>(v.z); o[5] = dec_hi<T>(v.z);
+    o[6] = dec_lo<T>(v.w); o[7] = dec_hi<T>(v.w);
+}
+
+template <int T>
+__device__ __forceinline__ float dec1(uint16_t v) {
+    if constexpr (T == DT_BF16) return __uint_as_float((uint32_t)v << 16);
+    else return (float)__builtin_bit_cast(_Float16, v);
+}
+
+// Clamped tanh-GELU and SiLU, the reference's epilogue activations (Shaders.swift:21-29).
+// tanh(15) is already 1 in fp32, so the clamp changes no representable result.
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float k = 0.7978845608028654f;
+    float u = k * (x + 0.044715f * x * x * x);
+    u = fminf(fmaxf(u, -15.0f), 15.0f);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// The epilogue in the reference order (Shaders.swift:92-103): bias, SiLU-gate, GELU, SiLU,
+// then accumulate into the old output.  yp is the output element's address.
+__device__ __forceinline__ float epilogue(float acc, float acc2, float b, uint32_t flags) {
+    float v = acc + b;
+    if (flags & F_SILU_GATE) v = silu(v) * acc2;
+    if (flags & F_GELU) v = gelu_tanh(v);
+    if (flags & F_SILU) v = silu(v);
+    return v;
+}
+
+// Sum over aligned groups of `width` lanes (a power of two <= 64) of a wave64; every
+// lane of a group ends with the group sum.
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace mt

@@ -1,0 +1,282 @@
+"""Python binding of libmingtts_hip.so (the gfx950 linear hot path of MingTTS).
+
+The library is the product; this module only loads it with ctypes and forwards
+device pointers.  It raises if the library is missing: there is no CPU fallback.
+
+The classes ``Linear``, ``ActView``, ``GemvFlags`` and ``Encoder`` mirror the
+reference's operator layer (Sources/MingTTS/Engine/Kernels.swift:7-44, 128-206) so
+callers and tests read like the reference's own: ``Encoder.linear(x, rows, linear, y,
+flags, gate)`` forwards to ``mt_linear`` with the same argument meaning.  Tensors are
+torch device tensors (plumbing for memory and streams only).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "csrc", "libmingtts_hip.so"))
+
+F32, F16, BF16 = 0, 1, 2
+OK, EHIP, ENOMEM, EINVAL, ENOTSUP = 0, -5, -12, -22, -95
+KERNEL_GEMV, KERNEL_GEMM = 1, 2
+TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS = 1, 2, 3, 4
+
+# Every symbol include/mingtts_hip.h declares.
+EXPORTS = (
+    "mt_linear", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create", "mt_seq_run",
+    "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
+    "mt_attention", "mt_attention_decode", "mt_last_error", "mt_version",
+)
+
+
+class GemvFlags:
+    """GemvFlags, Kernels.swift:21-28."""
+    bias = 1
+    accumulate = 2
+    gelu = 4
+    siluGate = 8
+    silu = 16
+
+
+class MingTTSError(RuntimeError):
+    """An error code returned by the library, with mt_last_error()'s text."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class GemvParams(ctypes.Structure):
+    """mt_gemv_params == GemvParams (Shaders.swift:39)."""
+    _fields_ = [("M", ctypes.c_uint32), ("N", ctypes.c_uint32), ("K", ctypes.c_uint32),
+                ("ldx", ctypes.c_uint32), ("ldy", ctypes.c_uint32), ("flags", ctypes.c_uint32),
+                ("eps", ctypes.c_float)]
+
+
+class LinearOp(ctypes.Structure):
+    """mt_linear_op: one op of a persistent sequence."""
+    _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("w2", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p), ("p", GemvParams),
+                ("xt", ctypes.c_int32), ("wt", ctypes.c_int32)]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads libmingtts_hip.so (raises if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"libmingtts_hip.so is not built at {path}; run __graft_entry__.build()")
+    L = ctypes.CDLL(path)
+    vp, u32, u64, i32, f32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
+    L.mt_linear.argtypes = [vp, i32, vp, vp, i32, vp, vp, GemvParams, vp]
+    L.mt_linear.restype = i32
+    L.mt_linear_kernel.argtypes = [u32, u32, u32, i32, i32]
+    L.mt_linear_kernel.restype = i32
+    L.mt_set_tuning.argtypes = [i32, i32]
+    L.mt_set_tuning.restype = i32
+    L.mt_seq_create.argtypes = [ctypes.POINTER(LinearOp), u32, ctypes.POINTER(vp)]
+    L.mt_seq_create.restype = i32
+    L.mt_seq_run.argtypes = [vp, vp]
+    L.mt_seq_run.restype = i32
+    L.mt_seq_destroy.argtypes = [vp]
+    L.mt_seq_destroy.restype = i32
+    L.mt_seq_groups.argtypes = [vp]
+    L.mt_seq_groups.restype = i32
+    L.mt_seq_check.argtypes = [vp]
+    L.mt_seq_check.restype = i32
+    L.mt_rope_cache.argtypes = [vp, u32, u32, u32, u32, u32, vp, vp, i32, u32, vp, vp]
+    L.mt_rope_cache.restype = i32
+    L.mt_rope_cache_decode.argtypes = [vp, u32, u32, u32, u32, vp, vp, vp, i32, u32, u64, vp, vp]
+    L.mt_rope_cache_decode.restype = i32
+    L.mt_attention.argtypes = [vp, u32, u32, u32, u32, u32, u32, vp, vp, i32, u32, vp, u32, f32, vp]
+    L.mt_attention.restype = i32
+    L.mt_attention_decode.argtypes = [vp, u32, u32, u32, u32, vp, u32, vp, vp, i32, u32, u64, vp, u32, f32, vp]
+    L.mt_attention_decode.restype = i32
+    L.mt_last_error.argtypes = []
+    L.mt_last_error.restype = ctypes.c_char_p
+    L.mt_version.argtypes = []
+    L.mt_version.restype = ctypes.c_char_p
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return load().mt_last_error().decode()
+
+
+def check(rc: int) -> int:
+    if rc < 0:
+        raise MingTTSError(rc, last_error())
+    return rc
+
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def dtype_code(t) -> int:
+    import torch
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[t.dtype]
+
+
+# ------------------------------------------------------------ raw calls --
+
+def linear_raw(x, xt, w, w2, wt, bias, y, M, N, K, ldx, ldy, flags, stream=None) -> int:
+    """mt_linear on raw pointers / tensors; returns the raw return code."""
+    p = GemvParams(M, N, K, ldx, ldy, flags, 0.0)
+    return load().mt_linear(_ptr(x), xt, _ptr(w), _ptr(w2), wt, _ptr(bias), _ptr(y), p, _stream(stream))
+
+
+def linear(x, w, y, M=None, flags=0, w2=None, bias=None, ldx=None, ldy=None, stream=None) -> None:
+    """y[:M] (op)= x[:M] @ w.T with the epilogue in ``flags``; torch tensors, w: [N, K]."""
+    N, K = w.shape
+    M = x.shape[0] if M is None else M
+    ldx = x.stride(0) if ldx is None else ldx
+    ldy = y.stride(0) if ldy is None else ldy
+    check(linear_raw(x, dtype_code(x), w, w2, dtype_code(w), bias, y, M, N, K, ldx, ldy, flags, stream))
+
+
+def linear_kernel(M, N, K, xt=F32, wt=BF16) -> int:
+    return load().mt_linear_kernel(M, N, K, xt, wt)
+
+
+def set_tuning(key: int, value: int) -> int:
+    return check(load().mt_set_tuning(key, value))
+
+
+class Seq:
+    """A persistent linear sequence plan (mt_seq_*)."""
+
+    def __init__(self, ops: Sequence[LinearOp]):
+        arr = (LinearOp * len(ops))(*ops)
+        h = ctypes.c_void_p()
+        check(load().mt_seq_create(arr, len(ops), ctypes.byref(h)))
+        self.handle = h
+        self.n_ops = len(ops)
+
+    def run(self, stream=None) -> None:
+        check(load().mt_seq_run(self.handle, _stream(stream)))
+
+    def check(self) -> None:
+        check(load().mt_seq_check(self.handle))
+
+    @property
+    def groups(self) -> int:
+        return check(load().mt_seq_groups(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            load().mt_seq_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def op(x, w, y, M, flags=0, w2=None, bias=None, ldx=None, ldy=None, xt=None, wt=None) -> LinearOp:
+    """An mt_linear_op over torch tensors (w: [N, K])."""
+    N, K = w.shape
+    if bias is not None:
+        flags |= GemvFlags.bias
+    return LinearOp(_ptr(x), _ptr(w), _ptr(w2), _ptr(bias), _ptr(y),
+                    GemvParams(M, N, K, x.stride(0) if ldx is None else ldx, y.stride(0) if ldy is None else ldy,
+                               flags, 0.0),
+                    dtype_code(x) if xt is None else xt, dtype_code(w) if wt is None else wt)
+
+
+def rope_cache(qkv, ldq, M, hq, hkv, pos0, kc, vc, cache_len, inv_freq, stream=None) -> None:
+    check(load().mt_rope_cache(_ptr(qkv), ldq, M, hq, hkv, pos0, _ptr(kc), _ptr(vc), dtype_code(kc), cache_len,
+                               _ptr(inv_freq), _stream(stream)))
+
+
+def rope_cache_decode(qkv, ldq, B, hq, hkv, pos, kc, vc, cache_len, cache_stride, inv_freq, stream=None) -> None:
+    check(load().mt_rope_cache_decode(_ptr(qkv), ldq, B, hq, hkv, _ptr(pos), _ptr(kc), _ptr(vc), dtype_code(kc),
+                                      cache_len, cache_stride, _ptr(inv_freq), _stream(stream)))
+
+
+def attention(q, ldq, M, hq, hkv, pos0, window, kc, vc, cache_len, out, ldo, scale=0.125, stream=None) -> None:
+    check(load().mt_attention(_ptr(q), ldq, M, hq, hkv, pos0, window, _ptr(kc), _ptr(vc), dtype_code(kc),
+                              cache_len, _ptr(out), ldo, scale, _stream(stream)))
+
+
+def attention_decode(q, ldq, B, hq, hkv, lens, window, kc, vc, cache_len, cache_stride, out, ldo, scale=0.125,
+                     stream=None) -> None:
+    check(load().mt_attention_decode(_ptr(q), ldq, B, hq, hkv, _ptr(lens), window, _ptr(kc), _ptr(vc),
+                                     dtype_code(kc), cache_len, cache_stride, _ptr(out), ldo, scale,
+                                     _stream(stream)))
+
+
+# ------------------------------------------- mirror of the reference types --
+
+@dataclass
+class GPUTensor:
+    """GPUTensor (Kernels.swift:7-11): a tensor at an element offset of a buffer."""
+    buffer: object
+    offset: int = 0
+
+    def ptr(self) -> int:
+        return self.buffer.data_ptr() + self.offset * self.buffer.element_size()
+
+
+@dataclass
+class Linear:
+    """Linear (Kernels.swift:13-19): y = x W^T (+ bias), w [n, k] row-major."""
+    w: GPUTensor
+    bias: Optional[GPUTensor]
+    n: int
+    k: int
+
+
+@dataclass
+class ActView:
+    """ActView (Kernels.swift:30-44): a view of rows at an element offset, stride ``ld``."""
+    buffer: object
+    offset: int = 0
+    ld: int = 0
+
+    def row(self, r: int) -> "ActView":
+        return ActView(self.buffer, self.offset + r * self.ld, self.ld)
+
+    def column(self, c: int) -> "ActView":
+        return ActView(self.buffer, self.offset + c, self.ld)
+
+    def ptr(self) -> int:
+        return self.buffer.data_ptr() + self.offset * self.buffer.element_size()
+
+
+class Encoder:
+    """The reference's Encoder (Kernels.swift:89-206) over the C ABI, on one stream."""
+
+    def __init__(self, stream=None):
+        self.stream = stream
+
+    def linear(self, x: ActView, rows: int, linear: Linear, y: ActView, flags: int = 0,
+               gate: Optional[GPUTensor] = None) -> None:
+        """Encoder.linear (Kernels.swift:132-161)."""
+        wt = dtype_code(linear.w.buffer)
+        check(linear_raw(x.ptr(), dtype_code(x.buffer), linear.w.ptr(), gate.ptr() if gate else None, wt,
+                         linear.bias.ptr() if linear.bias else None, y.ptr(), rows, linear.n, linear.k, x.ld, y.ld,
+                         flags, self.stream))

@@ -1,0 +1,283 @@
+"""CPU oracle for the MingTTS linear hot path.
+
+TEST INFRASTRUCTURE, NOT PRODUCT CODE.  Only ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker (or as the timed CPU baseline).  The HIP library never calls it.
+
+Contents (reference paths relative to the reference checkout):
+
+* ``LCG`` -- the known-answer-test RNG of Tests/MingTTSTests/KernelTests.swift:21-28.
+* ``round16`` / ``decode16`` -- bf16 rounding of KernelTests.swift:30-36, and IEEE fp16.
+* ``gaussian`` -- SplitMix64 + Box-Muller of Sources/MingTTS/Engine/Engine.swift:432-453.
+* ``linear_f32`` -- the reference CPU loop of one linear, KernelTests.swift:86-101, with
+  the kernels' epilogue order (Sources/MingTTS/Engine/Shaders.swift:21-29, 92-103).
+* ``linear_f64`` -- fp64 recomputation on the same rounded inputs (the precision gate).
+* ``linear_fast`` -- the same linear with a 16-way split K sum (timed CPU baseline).
+* ``rope_neox`` / ``attention_f64`` -- NeoX RoPE and causal GQA attention over a cache,
+  restating Shaders.swift:451-596 and the CPU reference of KernelTests.swift:207-268.
+* ``gemv_case`` -- regenerates the reference's linear known-answer tests bit for bit
+  (KernelTests.swift:72-103).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import numpy as np
+
+F32, F16, BF16 = 0, 1, 2
+BIAS, ACCUM, GELU, SILU_GATE, SILU = 1, 2, 4, 8, 16
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """The compiled oracle (oracle/libmt_oracle.so, built by ``make -C oracle``)."""
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "libmt_oracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle library missing: {path} (run make -C oracle)")
+        L = ctypes.CDLL(path)
+        vp, i64, i32, u32, u64, f32 = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                       ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float)
+        L.mto_lcg_fill.argtypes = [u64, vp, i64, f32]
+        L.mto_lcg_fill.restype = u64
+        L.mto_gaussian_fill.argtypes = [u64, vp, i64, f32]
+        L.mto_gaussian_fill.restype = None
+        L.mto_bf16_bits.argtypes = [f32]
+        L.mto_bf16_bits.restype = ctypes.c_uint16
+        L.mto_f16_bits.argtypes = [f32]
+        L.mto_f16_bits.restype = ctypes.c_uint16
+        L.mto_round16.argtypes = [vp, i64, i32, vp, vp]
+        L.mto_round16.restype = None
+        L.mto_decode16.argtypes = [vp, i64, i32, vp]
+        L.mto_decode16.restype = None
+        sig = [vp, i64, vp, vp, i32, vp, vp, vp, i64, i32, i32, i32, u32, i32]
+        L.mto_linear_f32.argtypes = sig
+        L.mto_linear_f32.restype = i32
+        L.mto_linear_fast.argtypes = sig
+        L.mto_linear_fast.restype = i32
+        L.mto_linear_f64.argtypes = [vp, i64, vp, vp, i32, vp, vp, i64, vp, i64, i32, i32, i32, u32, i32]
+        L.mto_linear_f64.restype = i32
+        L.mto_max_threads.argtypes = []
+        L.mto_max_threads.restype = i32
+        _LIB = L
+    return _LIB
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- RNGs --
+
+class LCG:
+    """KernelTests.swift:21-28: uniforms in [-1, 1) from a 64-bit LCG, fp32 arithmetic."""
+
+    def __init__(self, state: int):
+        self.state = state & 0xFFFFFFFFFFFFFFFF
+
+    def floats(self, n: int, scale: float = 1.0) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        self.state = lib().mto_lcg_fill(self.state, _p(out), n, scale)
+        return out
+
+
+def gaussian(seed: int, n: int, scale: float = 1.0) -> np.ndarray:
+    """Engine.swift:432-453: standard normals (times ``scale``) from SplitMix64 + Box-Muller."""
+    out = np.empty(n, np.float32)
+    lib().mto_gaussian_fill(seed & 0xFFFFFFFFFFFFFFFF, _p(out), n, scale)
+    return out
+
+
+# ------------------------------------------------------------ rounding --
+
+def round16(x: np.ndarray, dtype: int) -> tuple[np.ndarray, np.ndarray]:
+    """Round fp32 values to bf16 (KernelTests.swift:30-36) or fp16 (IEEE RNE).
+
+    Returns (uint16 bits, the rounded values as fp32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    bits = np.empty(x.shape, np.uint16)
+    rounded = np.empty(x.shape, np.float32)
+    lib().mto_round16(_p(x), x.size, dtype, _p(bits), _p(rounded))
+    return bits, rounded
+
+
+def decode16(bits: np.ndarray, dtype: int) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().mto_decode16(_p(bits), bits.size, dtype, _p(out))
+    return out
+
+
+# -------------------------------------------------------------- linear --
+
+def _linear_args(x, w, w2, bias, y0, M, N, K):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint16)
+    w2 = None if w2 is None else np.ascontiguousarray(w2, np.uint16)
+    bias = None if bias is None else np.ascontiguousarray(bias, np.uint16)
+    y0 = None if y0 is None else np.ascontiguousarray(y0, np.float32)
+    assert x.size >= M * K and w.size >= N * K
+    return x, w, w2, bias, y0
+
+
+def linear_f32(x, w, w2, wt, bias, y0, M, N, K, flags, threads=0) -> np.ndarray:
+    """The reference CPU loop (KernelTests.swift:86-101): fp32, natural K order.
+
+    x: fp32 [M, K] (rounded values if the kernel reads 16-bit x); w, w2: uint16 [N, K];
+    bias: uint16 [N] or None (passing a bias sets BIAS, as Kernels.swift:135 does);
+    y0: fp32 [M, N] read under ACCUM.  Returns fp32 [M, N]."""
+    x, w, w2, bias, y0 = _linear_args(x, w, w2, bias, y0, M, N, K)
+    if bias is not None:
+        flags |= BIAS
+    y = np.empty((M, N), np.float32)
+    rc = lib().mto_linear_f32(_p(x), K, _p(w), _p(w2), wt, _p(bias), _p(y0), _p(y), N, M, N, K, flags, threads)
+    assert rc == 0, rc
+    return y
+
+
+def linear_fast(x, w, w2, wt, bias, y0, M, N, K, flags, threads=0) -> np.ndarray:
+    """linear_f32 with the K sum split 16 ways (vectorised); the timed CPU baseline."""
+    x, w, w2, bias, y0 = _linear_args(x, w, w2, bias, y0, M, N, K)
+    if bias is not None:
+        flags |= BIAS
+    y = np.empty((M, N), np.float32)
+    rc = lib().mto_linear_fast(_p(x), K, _p(w), _p(w2), wt, _p(bias), _p(y0), _p(y), N, M, N, K, flags, threads)
+    assert rc == 0, rc
+    return y
+
+
+def linear_f64(x, w, w2, wt, bias, y0, M, N, K, flags, threads=0) -> np.ndarray:
+    """fp64 recomputation of the linear on the same inputs; returns float64 [M, N]."""
+    x, w, w2, bias, y0 = _linear_args(x, w, w2, bias, y0, M, N, K)
+    if bias is not None:
+        flags |= BIAS
+    y = np.empty((M, N), np.float64)
+    rc = lib().mto_linear_f64(_p(x), K, _p(w), _p(w2), wt, _p(bias), _p(y0), N, _p(y), N, M, N, K, flags, threads)
+    assert rc == 0, rc
+    return y
+
+
+def max_threads() -> int:
+    return lib().mto_max_threads()
+
+
+# ---------------------------------------------------------- tolerances --
+
+def kat_atol(k: int) -> float:
+    """Per-element absolute tolerance of the reference's linear tests (KernelTests.swift:102)."""
+    return 2e-4 * math.sqrt(k) / 30
+
+
+def worst_violation(got: np.ndarray, want: np.ndarray, atol: float, rtol: float = 1e-4):
+    """assertClose of KernelTests.swift:58-68: the element with the largest |d| - tol.
+
+    Returns (excess, index, got, want); excess <= 0 means every element passed."""
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    assert got.shape == want.shape
+    d = np.abs(got - want)
+    tol = atol + rtol * np.abs(want)
+    ex = d - tol
+    ex = np.where(np.isnan(ex), np.inf, ex)
+    i = int(np.argmax(ex))
+    return float(ex[i]), i, float(got[i]), float(want[i])
+
+
+def normwise_rel_err(got: np.ndarray, want64: np.ndarray) -> float:
+    """max |y - y_hat| / max |y_hat|, the 1e-3 precision gate against fp64."""
+    got = np.asarray(got, np.float64)
+    want64 = np.asarray(want64, np.float64)
+    den = float(np.max(np.abs(want64))) if want64.size else 0.0
+    num = float(np.max(np.abs(got - want64))) if want64.size else 0.0
+    if not np.all(np.isfinite(got)):
+        return float("inf")
+    return num / den if den > 0 else num
+
+
+# ----------------------------------------------------- known answers --
+
+def gemv_case(m: int, n: int, k: int, flags: int, bias: bool, x_scale: float = 1.0, wt: int = BF16) -> dict:
+    """Inputs and expected output of KernelTests.gemvCase (KernelTests.swift:72-103).
+
+    Draw order from one LCG seeded m*1000 + n*7 + k: x (m*k, scale x_scale), w (n*k, 0.1),
+    w2 (n*k, 0.1), b (n), y0 (m*n).  Weights and bias are rounded to ``wt`` (the reference
+    uses bf16); x stays fp32.  ``x`` carries 8 extra NaN rows the kernel must never read."""
+    rng = LCG(m * 1000 + n * 7 + k)
+    x = rng.floats(m * k, x_scale)
+    w = rng.floats(n * k, 0.1)
+    w2 = rng.floats(n * k, 0.1)
+    b = rng.floats(n)
+    y0 = rng.floats(m * n)
+    wb, _ = round16(w, wt)
+    w2b, _ = round16(w2, wt)
+    bb, _ = round16(b, wt)
+    xs = np.concatenate([x, np.full(8 * k, np.nan, np.float32)]).reshape(m + 8, k)
+    gated = bool(flags & SILU_GATE)
+    want = linear_f32(xs[:m], wb.reshape(n, k), w2b.reshape(n, k) if gated else None, wt,
+                      bb if bias else None, y0.reshape(m, n), m, n, k, flags)
+    return dict(m=m, n=n, k=k, flags=flags | (BIAS if bias else 0), x=xs, w=wb.reshape(n, k),
+                w2=w2b.reshape(n, k), bias=bb if bias else None, y0=y0.reshape(m, n), want=want, wt=wt)
+
+
+# Linear known-answer cases of the reference (KernelTests.swift:127-183), (m, n, k, flags, bias, xScale).
+KAT_GEMV_SHAPES = [  # testGemvShapes, KernelTests.swift:127-137
+    (1, 1152, 896, 0, True, 1.0), (2, 2, 896, 0, True, 1.0), (4, 896, 4864, ACCUM, False, 1.0),
+    (6, 4096, 1024, GELU, True, 1.0), (3, 64, 1024, 0, True, 1.0), (21, 300, 896, 0, False, 1.0),
+    (4, 3530, 896, 0, True, 1.0), (1, 896, 64, 0, True, 1.0), (8, 2, 896, 0, True, 1.0),
+]
+KAT_GEMM8_TILES = [  # testGemm8ColumnTiles, KernelTests.swift:142-160
+    (6, 1024, 1024, GELU, True, 1.0), (4, 896, 896, SILU_GATE, False, 1.0), (3, 1152, 896, ACCUM, False, 1.0),
+    (6, 1024, 4096, ACCUM, False, 1.0), (4, 896, 4864, ACCUM, False, 1.0),
+]
+KAT_GEMM_PREFILL = [  # testGemmPrefillShapes, KernelTests.swift:164-172
+    (174, 1152, 896, 0, True, 1.0), (40, 896, 4864, ACCUM, False, 1.0), (33, 4864, 896, SILU_GATE, False, 1.0),
+    (16, 64, 32, GELU, True, 1.0), (65, 128, 64, SILU, True, 1.0),
+]
+KAT_LARGE_INPUTS = [  # testGemvGeluLargeInputs, KernelTests.swift:175-178
+    (6, 256, 1024, GELU, True, 8.0), (1, 256, 896, SILU, False, 8.0),
+]
+KAT_SILU_GATE = [  # testGemvSiluGate, KernelTests.swift:180-183
+    (1, 4864, 896, SILU_GATE, False, 1.0), (5, 256, 896, SILU_GATE, False, 1.0),
+]
+KAT_ALL = KAT_GEMV_SHAPES + KAT_GEMM8_TILES + KAT_GEMM_PREFILL + KAT_LARGE_INPUTS + KAT_SILU_GATE
+
+
+# ------------------------------------------------- rope and attention --
+
+def inv_freq(theta: float = 1e6, dim: int = 64) -> np.ndarray:
+    """1 / theta^(2i / dim) in fp32 as the reference builds it (Qwen.swift:60)."""
+    i = np.arange(dim // 2, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(theta), np.float32(2.0) * i / np.float32(dim))).astype(np.float32)
+
+
+def rope_neox(v: np.ndarray, pos, invf: np.ndarray) -> np.ndarray:
+    """NeoX rotation of 64-wide heads, pairs (i, i + 32), angle pos * inv_freq[i]
+    (Shaders.swift:472-478; KernelTests.swift:207-217), in fp64.  v: [..., 64]."""
+    v = np.asarray(v, np.float64)
+    a = np.asarray(pos, np.float64)[..., None] * invf.astype(np.float64)
+    c, s = np.cos(a), np.sin(a)
+    x0, x1 = v[..., :32], v[..., 32:]
+    return np.concatenate([x0 * c - x1 * s, x1 * c + x0 * s], axis=-1)
+
+
+def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, qpos: int, window: int, scale: float) -> np.ndarray:
+    """Causal attention of one query row (hq heads of 64) over keys [start, qpos] of a
+    cache k, v: [hkv, >= qpos + 1, 64]; start = max(0, qpos + 1 - window) (window 0 =
+    all); GQA kv head = h // (hq // hkv) (Shaders.swift:511-520).  fp64.  Returns [hq, 64]."""
+    hq = q.shape[0]
+    hkv = k.shape[0]
+    start = qpos + 1 - window if (window > 0 and qpos + 1 > window) else 0
+    out = np.zeros((hq, 64), np.float64)
+    for h in range(hq):
+        kvh = h // (hq // hkv)
+        kk = k[kvh, start:qpos + 1].astype(np.float64)
+        vv = v[kvh, start:qpos + 1].astype(np.float64)
+        s = kk @ q[h].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ vv
+    return out

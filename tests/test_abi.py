@@ -1,0 +1,124 @@
+"""The C ABI without a GPU: the library loads, exports every symbol the header declares,
+and rejects bad arguments with MT_EINVAL before touching the device (the reference turns
+the same shape violations into preconditionFailure, Kernels.swift:105, 147)."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import mingtts as mt
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mingtts_hip.h")
+
+ALIGNED = 1 << 20          # fake 16-byte-aligned "device" addresses: never dereferenced,
+W_ADDR = 2 << 20           # every call below fails validation before any HIP call
+Y_ADDR = 8 << 20
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert header_functions() == sorted(mt.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    mt.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", mt.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (mt_[a-z0-9_]+)$", out, flags=re.M))
+    missing = set(header_functions()) - exported
+    assert not missing, missing
+    assert mt.load().mt_version().decode().startswith("mingtts_hip")
+
+
+def lin(M=2, N=64, K=64, ldx=None, ldy=None, flags=0, x=ALIGNED, w=W_ADDR, w2=None, bias=None, y=Y_ADDR,
+        xt=mt.F32, wt=mt.F16):
+    return mt.linear_raw(x, xt, w, w2, wt, bias, y, M, N, K, K if ldx is None else ldx, N if ldy is None else ldy,
+                         flags, stream=0)
+
+
+@pytest.mark.parametrize("kwargs,needle", [
+    (dict(K=60, ldx=64), "multiple of 8"),
+    (dict(K=0), "multiple of 8"),
+    (dict(ldx=32), "ldx"),
+    (dict(ldy=32), "ldy"),
+    (dict(wt=mt.F32), "weights must be f16 or bf16"),
+    (dict(xt=7), "activation dtype"),
+    (dict(flags=mt.GemvFlags.bias), "MT_BIAS without a bias"),
+    (dict(flags=mt.GemvFlags.siluGate), "without w2"),
+    (dict(flags=64), "unknown flag"),
+    (dict(x=ALIGNED + 4), "16-byte aligned"),
+    (dict(ldx=66, K=64), "16-byte"),
+    (dict(w=W_ADDR + 8), "w / w2"),
+    (dict(flags=mt.GemvFlags.siluGate, w2=W_ADDR + 8), "w / w2"),
+    (dict(y=Y_ADDR + 2), "y must be"),
+    (dict(x=None), "null"),
+    (dict(y=ALIGNED + 64), "overlaps"),
+])
+def test_linear_rejects_bad_arguments(kwargs, needle):
+    rc = lin(**kwargs)
+    assert rc == mt.EINVAL
+    assert needle in mt.last_error()
+
+
+def test_empty_linear_is_a_no_op():
+    assert lin(M=0) == mt.OK
+    assert lin(N=0) == mt.OK
+
+
+def test_kernel_choice_and_tuning_round_trip():
+    """The analogue of Kernels.usesGemm / scalarRowsMax (KernelTests.swift:155-157, 165-166)."""
+    assert mt.linear_kernel(1, 1152, 896) == mt.KERNEL_GEMV
+    assert mt.linear_kernel(8, 2, 896) == mt.KERNEL_GEMV
+    assert mt.linear_kernel(174, 1152, 896) == mt.KERNEL_GEMM
+    assert mt.linear_kernel(16, 64, 32) == mt.KERNEL_GEMM
+    old = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, 2)
+    try:
+        assert mt.linear_kernel(3, 1152, 896) == mt.KERNEL_GEMM
+    finally:
+        mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old)
+    assert mt.linear_kernel(3, 1152, 896) == mt.KERNEL_GEMV
+    assert mt.load().mt_set_tuning(99, 0) == mt.EINVAL
+    assert mt.load().mt_set_tuning(mt.TUNE_GEMV_ROWS_MAX, 9) == mt.EINVAL
+
+
+def test_seq_create_validates_every_op_before_the_device():
+    import ctypes
+    ok = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(2, 64, 64, 64, 64, 0, 0.0), mt.F32, mt.F16)
+    bad_m = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(9, 64, 64, 64, 64, 0, 0.0), mt.F32, mt.F16)
+    bad_t = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(2, 64, 64, 64, 64, 0, 0.0), mt.F16, mt.F16)
+    bad_k = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(2, 64, 60, 64, 64, 0, 0.0), mt.F32, mt.F16)
+    L = mt.load()
+    h = ctypes.c_void_p()
+    for ops, needle in (([ok, bad_m], "op 1: a sequence takes M <= 8"), ([ok, bad_t], "share the weight"),
+                        ([bad_k], "op 0: K must")):
+        arr = (mt.LinearOp * len(ops))(*ops)
+        assert L.mt_seq_create(arr, len(ops), ctypes.byref(h)) == mt.EINVAL
+        assert needle in mt.last_error()
+    assert L.mt_seq_create(None, 1, ctypes.byref(h)) == mt.EINVAL
+    assert L.mt_seq_run(None, None) == mt.EINVAL
+
+
+def test_rope_and_attention_reject_bad_arguments():
+    L = mt.load()
+    A = ALIGNED
+    # hq not a multiple of hkv
+    assert L.mt_attention(A, 1152, 1, 14, 3, 0, 0, A, A, mt.F32, 512, A, 896, 0.125, None) == mt.EINVAL
+    # positions past the cache
+    assert L.mt_attention(A, 1152, 4, 14, 2, 510, 0, A, A, mt.F32, 512, A, 896, 0.125, None) == mt.EINVAL
+    assert "past cache_len" in mt.last_error()
+    # cache too long for the score buffer
+    assert L.mt_attention(A, 1152, 1, 14, 2, 0, 0, A, A, mt.F32, 5000, A, 896, 0.125, None) == mt.EINVAL
+    # bf16 caches are not supported
+    assert L.mt_attention_decode(A, 1152, 2, 14, 2, A, 0, A, A, mt.BF16, 512, 65536, A, 896, 0.125, None) == mt.EINVAL
+    # overlapping per-sequence caches
+    assert L.mt_attention_decode(A, 1152, 2, 14, 2, A, 0, A, A, mt.F16, 512, 100, A, 896, 0.125, None) == mt.EINVAL
+    assert L.mt_rope_cache(A, 896, 1, 14, 2, 0, A, A, mt.F32, 512, A, None) == mt.EINVAL   # ldq too small
+    assert L.mt_rope_cache(A, 1152, 2, 14, 2, 511, A, A, mt.F32, 512, A, None) == mt.EINVAL
+    assert L.mt_rope_cache_decode(A, 1152, 2, 14, 2, None, A, A, mt.F16, 512, 65536, A, None) == mt.EINVAL
+    assert L.mt_attention(A, 1152, 0, 14, 2, 0, 0, A, A, mt.F32, 512, A, 896, 0.125, None) == mt.OK  # empty

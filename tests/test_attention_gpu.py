@@ -1,0 +1,115 @@
+"""mt_rope_cache / mt_attention on the GPU against the fp64 oracle: the reference's attention
+known-answer tests (KernelTests.swift:219-278, restated bit for bit) and the batch-2 decode
+configuration (fp16 caches, lengths ~ U[32, 512], RoPE base 1e6)."""
+import numpy as np
+import pytest
+import torch
+
+import mingtts as mt
+import oracle as O
+from _gpu_util import say
+
+pytestmark = pytest.mark.gpu
+HQ, HKV, LD, CAP = 14, 2, (14 + 2 * 2) * 64, 512
+
+
+def _kat(t0, m, window, device):
+    """KernelTests.attentionCase: prefill t0 rows then m decode rows, fp32 cache."""
+    rng = O.LCG(t0 * 31 + m + window)
+    total = t0 + m
+    qkv = rng.floats((total + 8) * LD).reshape(total + 8, LD)
+    invf = O.inv_freq(1e6)
+    qkv_d = torch.from_numpy(qkv.copy()).to(device)
+    kc = torch.zeros(HKV, CAP, 64, device=device)
+    vc = torch.zeros(HKV, CAP, 64, device=device)
+    out = torch.zeros(total, HQ * 64, device=device)
+    invf_d = torch.from_numpy(invf).to(device)
+    for pos0, rows in ((0, t0), (t0, m)):
+        if rows == 0:
+            continue
+        view = qkv_d[pos0:]
+        mt.rope_cache(view, LD, rows, HQ, HKV, pos0, kc, vc, CAP, invf_d)
+        mt.attention(view, LD, rows, HQ, HKV, pos0, window, kc, vc, CAP, out[pos0:], HQ * 64, 0.125)
+    torch.cuda.synchronize()
+    # CPU: rotate every k and q in fp64, attend over the full sequence.
+    ks = np.stack([O.rope_neox(qkv[:total, (HQ + h) * 64:(HQ + h + 1) * 64], np.arange(total), invf)
+                   for h in range(HKV)])
+    vs = np.stack([qkv[:total, (HQ + HKV + h) * 64:(HQ + HKV + h + 1) * 64] for h in range(HKV)])
+    want = np.zeros((total, HQ, 64))
+    for pos in range(total):
+        q = O.rope_neox(qkv[pos, :HQ * 64].reshape(HQ, 64), pos, invf)
+        want[pos] = O.attention_f64(q, ks, vs, pos, window, 0.125)
+    return out.cpu().numpy().reshape(total, HQ, 64), want, kc.cpu().numpy(), ks
+
+
+@pytest.mark.parametrize("t0,m,window", [(37, 1, 0), (130, 4, 0), (100, 4, 64), (20, 4, 64)])
+def test_reference_attention_kats(gpu, t0, m, window):
+    say(f"attention kat t0={t0} m={m} window={window}")
+    got, want, kc, ks = _kat(t0, m, window, gpu)
+    # atol 2e-5 as the reference (KernelTests.swift:267), rtol 1e-4 (assertClose default)
+    ex, i, g, w = O.worst_violation(got, want, 2e-5)
+    assert ex <= 0, f"index {i} got {g} want {w}"
+    np.testing.assert_allclose(kc[:, :t0 + m], ks, atol=2e-6, rtol=1e-5)
+
+
+def test_batched_decode_fp16_cache(gpu):
+    """Batch 2 (CFG pair) decode over 512-position fp16 caches, lengths drawn from U[32, 512],
+    RoPE base 1e6: rope + append the new row at len - 1, then attention over [0, len)."""
+    B = 2
+    rs = np.random.default_rng(2024)
+    lens = rs.integers(32, 513, B).astype(np.uint32)
+    invf = O.inv_freq(1e6)
+    z = O.gaussian(4, B * HKV * CAP * 64 * 2 + B * LD)
+    kc0 = z[:B * HKV * CAP * 64].reshape(B, HKV, CAP, 64).astype(np.float16)
+    vc0 = z[B * HKV * CAP * 64:2 * B * HKV * CAP * 64].reshape(B, HKV, CAP, 64).astype(np.float16)
+    qkv = z[2 * B * HKV * CAP * 64:].reshape(B, LD).copy()
+    kc = torch.from_numpy(kc0.copy()).to(gpu)
+    vc = torch.from_numpy(vc0.copy()).to(gpu)
+    qkv_d = torch.from_numpy(qkv.copy()).to(gpu)
+    pos_d = torch.from_numpy((lens - 1).astype(np.int32)).to(gpu)
+    lens_d = torch.from_numpy(lens.astype(np.int32)).to(gpu)
+    out = torch.zeros(B, HQ * 64, device=gpu)
+    say(f"batched decode lens={lens.tolist()}")
+    stride = HKV * CAP * 64
+    mt.rope_cache_decode(qkv_d, LD, B, HQ, HKV, pos_d, kc, vc, CAP, stride, torch.from_numpy(invf).to(gpu))
+    mt.attention_decode(qkv_d, LD, B, HQ, HKV, lens_d, 0, kc, vc, CAP, stride, out, HQ * 64, 0.125)
+    torch.cuda.synchronize()
+    kcg = kc.cpu().numpy().astype(np.float64)
+    vcg = vc.cpu().numpy().astype(np.float64)
+    got = out.cpu().numpy().reshape(B, HQ, 64)
+    for b in range(B):
+        p = int(lens[b]) - 1
+        knew = O.rope_neox(qkv[b, HQ * 64:(HQ + HKV) * 64].reshape(HKV, 64), p, invf)
+        np.testing.assert_allclose(kcg[b, :, p], knew, rtol=2e-3, atol=2e-3)      # fp16 storage
+        np.testing.assert_array_equal(vcg[b, :, p], qkv[b, (HQ + HKV) * 64:].reshape(HKV, 64).astype(np.float16))
+        # untouched positions keep the old cache
+        np.testing.assert_array_equal(kcg[b, :, :p], kc0[b, :, :p].astype(np.float64))
+        q = O.rope_neox(qkv[b, :HQ * 64].reshape(HQ, 64), p, invf)
+        want = O.attention_f64(q, kcg[b], vcg[b], p, 0, 0.125)    # on the stored fp16 values
+        ex, i, g, w = O.worst_violation(got[b], want, 2e-5)
+        assert ex <= 0, f"b={b} index {i} got {g} want {w}"
+
+
+def test_decode_window_and_length_edges(gpu):
+    """Length 1 (a single key), a window shorter than the length, and a length equal to the cache."""
+    B = 3
+    lens = np.array([1, 300, 512], np.uint32)
+    z = O.gaussian(9, B * HKV * CAP * 64 * 2 + B * HQ * 64)
+    kc0 = z[:B * HKV * CAP * 64].reshape(B, HKV, CAP, 64)
+    vc0 = z[B * HKV * CAP * 64:2 * B * HKV * CAP * 64].reshape(B, HKV, CAP, 64)
+    q = z[2 * B * HKV * CAP * 64:].reshape(B, HQ * 64)
+    kc = torch.from_numpy(kc0.copy()).to(gpu)
+    vc = torch.from_numpy(vc0.copy()).to(gpu)
+    qd = torch.from_numpy(q.copy()).to(gpu)
+    lens_d = torch.from_numpy(lens.astype(np.int32)).to(gpu)
+    out = torch.zeros(B, HQ * 64, device=gpu)
+    for window in (0, 65):
+        say(f"decode edges window={window}")
+        mt.attention_decode(qd, HQ * 64, B, HQ, HKV, lens_d, window, kc, vc, CAP, HKV * CAP * 64, out, HQ * 64,
+                            0.125)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(B, HQ, 64)
+        for b in range(B):
+            want = O.attention_f64(q[b].reshape(HQ, 64), kc0[b], vc0[b], int(lens[b]) - 1, window, 0.125)
+            ex, i, g, w = O.worst_violation(got[b], want, 2e-5)
+            assert ex <= 0, f"window {window} b={b} index {i} got {g} want {w}"

@@ -1,0 +1,143 @@
+"""The persistent linear sequence (mt_seq_*) on the GPU: the decode step's chain of backbone
+linears (Qwen.swift:85-91 per layer) against an fp64 oracle chain, against the same ops
+issued one mt_linear at a time (bit for bit), across re-runs and workgroup counts."""
+import numpy as np
+import pytest
+import torch
+
+import mingtts as mt
+import oracle as O
+from _gpu_util import dev16, say
+
+pytestmark = pytest.mark.gpu
+
+H, QKV, INTER = 896, 1152, 4864
+
+
+def make_stack(layers: int, M: int, seed: int, device):
+    """Per-layer fp16 weights ~ N(0, 0.02^2) (qkv with bias, o, gate, up, down), seeded per
+    layer from the SplitMix64 normal stream, plus the activation buffers of the chain."""
+    ws = []
+    for l in range(layers):
+        n = QKV * H + QKV + H * H + 2 * INTER * H + H * INTER
+        z = O.gaussian(seed * 1000 + l, n, 0.02)
+        bits, _ = O.round16(z, O.F16)
+        o = 0
+        parts = {}
+        for name, size, shape in (("qkv", QKV * H, (QKV, H)), ("qkv_b", QKV, (QKV,)), ("o", H * H, (H, H)),
+                                  ("gate", INTER * H, (INTER, H)), ("up", INTER * H, (INTER, H)),
+                                  ("down", H * INTER, (H, INTER))):
+            parts[name] = bits[o:o + size].reshape(shape)
+            o += size
+        parts["dev"] = {k: dev16(v, O.F16, device) for k, v in parts.items()}
+        ws.append(parts)
+    x0 = O.gaussian(seed + 7, M * H)
+    return ws, x0.reshape(M, H)
+
+
+def chain_ops(ws, M, resid, qkv, mlp):
+    """The decode chain: qkv = resid Wqkv^T + b; resid += qkv[:, :896] Wo^T (the attention
+    output stand-in); mlp = silu(resid Wg^T) * (resid Wu^T); resid += mlp Wd^T."""
+    ops = []
+    for p in ws:
+        d = p["dev"]
+        ops.append(mt.op(resid, d["qkv"], qkv, M, bias=d["qkv_b"]))
+        ops.append(mt.op(qkv, d["o"], resid, M, flags=mt.GemvFlags.accumulate, ldx=QKV))
+        ops.append(mt.op(resid, d["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=d["up"]))
+        ops.append(mt.op(mlp, d["down"], resid, M, flags=mt.GemvFlags.accumulate))
+    return ops
+
+
+def oracle_chain(ws, x0, M):
+    """The same chain in fp64 per op, activations stored as fp32 between ops (as on the GPU)."""
+    resid = x0.astype(np.float32).copy()
+    qkv = mlp = None
+    for p in ws:
+        qkv = O.linear_f64(resid, p["qkv"], None, O.F16, p["qkv_b"], None, M, QKV, H, 0).astype(np.float32)
+        resid = O.linear_f64(np.ascontiguousarray(qkv[:, :H]), p["o"], None, O.F16, None, resid, M, H, H,
+                             O.ACCUM).astype(np.float32)
+        mlp = O.linear_f64(resid, p["gate"], p["up"], O.F16, None, None, M, INTER, H,
+                           O.SILU_GATE).astype(np.float32)
+        resid = O.linear_f64(mlp, p["down"], None, O.F16, None, resid, M, H, INTER, O.ACCUM).astype(np.float32)
+    return resid, qkv, mlp
+
+
+def buffers(M, x0, device):
+    resid = torch.from_numpy(x0.copy()).to(device)
+    qkv = torch.zeros(M, QKV, device=device)
+    mlp = torch.zeros(M, INTER, device=device)
+    return resid, qkv, mlp
+
+
+@pytest.mark.parametrize("layers,M", [(4, 2), (24, 2), (3, 1), (2, 5)])
+def test_decode_chain_matches_fp64_oracle(gpu, layers, M):
+    say(f"seq chain layers={layers} M={M}")
+    ws, x0 = make_stack(layers, M, 11 + M, gpu)
+    resid, qkv, mlp = buffers(M, x0, gpu)
+    seq = mt.Seq(chain_ops(ws, M, resid, qkv, mlp))
+    seq.run()
+    torch.cuda.synchronize()
+    seq.check()
+    want_r, want_q, want_m = oracle_chain(ws, x0, M)
+    for got, want, what in ((resid, want_r, "resid"), (qkv, want_q, "qkv"), (mlp, want_m, "mlp")):
+        g = got.cpu().numpy()
+        assert np.all(np.isfinite(g)), what
+        rel = O.normwise_rel_err(g, want)
+        assert rel <= 1e-3, f"{what}: normwise {rel:.3g}"
+    seq.close()
+
+
+def test_seq_equals_per_op_launches_bit_for_bit(gpu):
+    """Same per-feature lane split and reduction order, so the persistent kernel and 16
+    separate mt_linear launches agree exactly; re-runs and other workgroup counts too."""
+    layers, M = 4, 2
+    say("seq vs per-op")
+    ws, x0 = make_stack(layers, M, 5, gpu)
+    resid, qkv, mlp = buffers(M, x0, gpu)
+    ops = chain_ops(ws, M, resid, qkv, mlp)
+    for o in ops:
+        rc = mt.linear_raw(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p.M, o.p.N, o.p.K, o.p.ldx, o.p.ldy,
+                           o.p.flags, None)
+        assert rc == 0, mt.last_error()
+    torch.cuda.synchronize()
+    ref = resid.cpu().numpy().copy()
+    results = []
+    for groups in (0, 64, 333):
+        old = mt.set_tuning(mt.TUNE_SEQ_GROUPS, groups)
+        try:
+            seq = mt.Seq(ops)
+        finally:
+            mt.set_tuning(mt.TUNE_SEQ_GROUPS, old)
+        say(f"seq groups={seq.groups}")
+        for _ in range(2):   # the barrier counters reset themselves between runs
+            resid.copy_(torch.from_numpy(x0))
+            seq.run()
+            torch.cuda.synchronize()
+            results.append(resid.cpu().numpy().copy())
+        seq.check()
+        seq.close()
+    for r in results:
+        np.testing.assert_array_equal(r, ref)
+
+
+def test_seq_with_bf16_weights_and_fp16_activations(gpu):
+    """A short chain in other dtypes: bf16 W, fp16 x (activations rounded between ops by the
+    caller's buffer type is not possible for an fp32 y, so x here is a fixed fp16 input)."""
+    M, N, K = 2, 512, 256
+    rng = np.random.default_rng(3)
+    wb, _ = O.round16(rng.standard_normal((N, K)).astype(np.float32) * np.float32(0.05), O.BF16)
+    xb, xr = O.round16(rng.standard_normal((M, K)).astype(np.float32), O.F16)
+    w = dev16(wb, O.BF16, gpu)
+    x = dev16(xb, O.F16, gpu)
+    y = torch.zeros(M, N, device=gpu)
+    y2 = torch.zeros(M, N, device=gpu)
+    say("seq bf16/f16")
+    seq = mt.Seq([mt.op(x, w, y, M), mt.op(x, w, y2, M, flags=mt.GemvFlags.gelu)])
+    seq.run()
+    torch.cuda.synchronize()
+    seq.check()
+    want = O.linear_f64(xr, wb, None, O.BF16, None, None, M, N, K, 0)
+    want2 = O.linear_f64(xr, wb, None, O.BF16, None, None, M, N, K, O.GELU)
+    assert O.normwise_rel_err(y.cpu().numpy(), want) <= 1e-5
+    assert O.normwise_rel_err(y2.cpu().numpy(), want2) <= 1e-5
+    seq.close()
