@@ -70,16 +70,21 @@ def make_layers(torch, dev, layers=LAYERS, seed=0):
     def w(*shape):
         return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * 0.02).half()
 
-    return [dict(qkv=w(QKV, H), qkv_b=w(QKV), o=w(H, H), gate=w(INTER, H), up=w(INTER, H), down=w(H, INTER))
-            for _ in range(layers)]
+    def gain(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=dev, dtype=torch.float32)).half()
+
+    return [dict(qkv=w(QKV, H), qkv_b=w(QKV), o=w(H, H), gate=w(INTER, H), up=w(INTER, H), down=w(H, INTER),
+                 norm1=gain(H), norm2=gain(H)) for _ in range(layers)]
 
 
 def decode_ops(mt, ws, M, resid, qkv, mlp):
+    """One layer's linears (Qwen.swift:84-91) with the two RMSNorms fused into qkv and gate|up;
+    the attention output is stood in for by the q part of qkv (attention is timed apart)."""
     ops = []
     for p in ws:
-        ops.append(mt.op(resid, p["qkv"], qkv, M, bias=p["qkv_b"]))
+        ops.append(mt.op(resid, p["qkv"], qkv, M, bias=p["qkv_b"], norm=p["norm1"]))
         ops.append(mt.op(qkv, p["o"], resid, M, flags=mt.GemvFlags.accumulate, ldx=QKV))
-        ops.append(mt.op(resid, p["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=p["up"]))
+        ops.append(mt.op(resid, p["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=p["up"], norm=p["norm2"]))
         ops.append(mt.op(mlp, p["down"], resid, M, flags=mt.GemvFlags.accumulate))
     return ops
 
@@ -92,7 +97,8 @@ def shape_bytes(M, N, K, f, xsize=4) -> int:
 
 
 def op_bytes(o, xsize=4) -> int:
-    return shape_bytes(o.p.M, o.p.N, o.p.K, o.p.flags, xsize)
+    """shape_bytes plus the RMSNorm gain ([K] fp16) when the op has one."""
+    return shape_bytes(o.p.M, o.p.N, o.p.K, o.p.flags, xsize) + (2 * o.p.K if o.norm else 0)
 
 
 def op_flops(o) -> int:
@@ -136,7 +142,10 @@ def bench_decode_per_op(torch, mt, dev, ws, steps, M=2):
 
     def step():
         for o in ops:
-            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
+            if o.norm:
+                rc = L.mt_linear_rmsnorm(o.x, o.xt, o.norm, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
+            else:
+                rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
             if rc:
                 raise RuntimeError(mt.last_error())
 
@@ -298,13 +307,20 @@ def cpu_baseline(torch, ws, target_s=10.0, M=2):
     resid0 = rng.standard_normal((M, H)).astype(np.float32)
     threads = O.max_threads()
 
+    gains = [(O.decode16(p["norm1"], O.F16), O.decode16(p["norm2"], O.F16)) for p in host]
+
+    def norm(x, g):
+        return (x * (np.float32(1.0) / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + np.float32(1e-6))) * g
+                ).astype(np.float32)
+
     def step():
         resid = resid0.copy()
-        for p in host:
-            qkv = O.linear_fast(resid, p["qkv"], None, O.F16, p["qkv_b"], None, M, QKV, H, 0, threads)
+        for p, (g1, g2) in zip(host, gains):
+            qkv = O.linear_fast(norm(resid, g1), p["qkv"], None, O.F16, p["qkv_b"], None, M, QKV, H, 0, threads)
             resid = O.linear_fast(np.ascontiguousarray(qkv[:, :H]), p["o"], None, O.F16, None, resid, M, H, H,
                                   O.ACCUM, threads)
-            mlp = O.linear_fast(resid, p["gate"], p["up"], O.F16, None, None, M, INTER, H, O.SILU_GATE, threads)
+            mlp = O.linear_fast(norm(resid, g2), p["gate"], p["up"], O.F16, None, None, M, INTER, H, O.SILU_GATE,
+                                threads)
             resid = O.linear_fast(mlp, p["down"], None, O.F16, None, resid, M, H, INTER, O.ACCUM, threads)
         return resid
 
@@ -368,9 +384,10 @@ def main() -> int:
         "dtype": "f16",
         "data": "synthetic (seeded N(0, 0.02^2) fp16 weights, N(0, 1) fp32 activations, generated on the device)",
         "config": {
-            "workload": "decode step of the Qwen2-0.5B backbone linears: 24 layers x {qkv 1152x896+bias, "
-                        "o 896x896 +=, gate|up 2x4864x896 SiLU*mul, down 896x4864 +=}, M=2 (CFG pair), "
-                        "fp16 W, fp32 activations and outputs, one persistent launch of 96 dependent linears",
+            "workload": "decode step of the Qwen2-0.5B backbone linears: 24 layers x {rmsnorm+qkv 1152x896+bias, "
+                        "o 896x896 +=, rmsnorm+gate|up 2x4864x896 SiLU*mul, down 896x4864 +=}, M=2 (CFG pair), "
+                        "fp16 W, fp32 activations and outputs, one persistent launch of 96 dependent linears "
+                        "(RMSNorm fused into the qkv and gate|up prologues)",
             "layers": LAYERS, "rows": 2, "hidden": H, "intermediate": INTER, "qkv": QKV,
             "parallelism": "single GPU",
         },

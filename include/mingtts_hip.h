@@ -86,6 +86,16 @@ enum { MT_KERNEL_GEMV = 1, MT_KERNEL_GEMM = 2 };
 int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt,
               const void *bias, float *y, mt_gemv_params p, mt_stream_t stream);
 
+/*
+ * RMSNorm fused into a linear's prologue: the reference's Encoder.rmsnorm into a scratch
+ * row followed by Encoder.linear on it (Kernels.swift:163-171 then 132-161, as Qwen.swift:84-85
+ * and 89-90 issue them), computed as one pass:
+ *   x'[m, k] = x[m, k] * rsqrt(mean_k x[m, k]^2 + p.eps) * norm[k];   y = linear(x')
+ * norm is [K] of type wt, 16-byte aligned.  Everything else is as mt_linear.
+ */
+int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *w, const void *w2,
+                      mt_dtype wt, const void *bias, float *y, mt_gemv_params p, mt_stream_t stream);
+
 /* The kernel family mt_linear picks for a shape (MT_KERNEL_GEMV / MT_KERNEL_GEMM),
  * the analogue of Kernels.usesGemm and scalarRowsMax. */
 int mt_linear_kernel(uint32_t M, uint32_t N, uint32_t K, mt_dtype xt, mt_dtype wt);
@@ -116,6 +126,7 @@ typedef struct mt_linear_op {
     const void *w;
     const void *w2;
     const void *bias;
+    const void *norm;   /* RMSNorm gain as in mt_linear_rmsnorm (eps = p.eps), or NULL */
     float *y;
     mt_gemv_params p;
     int32_t xt;   /* mt_dtype */

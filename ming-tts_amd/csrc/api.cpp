@@ -45,7 +45,8 @@ int check_launch(const char *what) {
 // Checks one linear's arguments; fills `a` (with the bias flag set from the pointer,
 // Kernels.swift:135).  Returns MT_OK or MT_EINVAL with the reason.
 static int validate_linear(const char *who, const void *x, int xt, const void *w, const void *w2, int wt,
-                           const void *bias, float *y, const mt_gemv_params &p, LinearArgs &a) {
+                           const void *bias, const void *norm, float *y, const mt_gemv_params &p,
+                           LinearArgs &a) {
     if (xt != DT_F32 && xt != DT_F16 && xt != DT_BF16)
         return set_error(MT_EINVAL, "%s: unknown activation dtype %d", who, xt);
     if (wt != DT_F16 && wt != DT_BF16)
@@ -67,6 +68,8 @@ static int validate_linear(const char *who, const void *x, int xt, const void *w
             return set_error(MT_EINVAL, "%s: w / w2 must be 16-byte aligned", who);
         if (!aligned(y, 4)) return set_error(MT_EINVAL, "%s: y must be 4-byte aligned", who);
         if (bias && !aligned(bias, 2)) return set_error(MT_EINVAL, "%s: bias must be 2-byte aligned", who);
+        if (norm && !aligned(norm, 16)) return set_error(MT_EINVAL, "%s: norm must be 16-byte aligned", who);
+        if (norm && !(p.eps >= 0.0f)) return set_error(MT_EINVAL, "%s: RMSNorm eps must be >= 0", who);
         // x must not overlap y (y may be read-modify-written under MT_ACCUM).
         const char *xb = static_cast<const char *>(x);
         const char *xe = xb + (static_cast<size_t>(p.M - 1) * p.ldx + p.K) * dtype_size(xt);
@@ -85,6 +88,8 @@ static int validate_linear(const char *who, const void *x, int xt, const void *w
     a.ldx = p.ldx;
     a.ldy = p.ldy;
     a.flags = flags;
+    a.norm = static_cast<const uint16_t *>(norm);
+    a.eps = p.eps;
     return MT_OK;
 }
 
@@ -125,7 +130,19 @@ int mt_set_tuning(int key, int value) {
 int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt, const void *bias,
               float *y, mt_gemv_params p, mt_stream_t stream) {
     LinearArgs a;
-    int rc = validate_linear("mt_linear", x, xt, w, w2, wt, bias, y, p, a);
+    int rc = validate_linear("mt_linear", x, xt, w, w2, wt, bias, nullptr, y, p, a);
+    if (rc) return rc;
+    if (p.M == 0 || p.N == 0) return MT_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (kernel_for(p.M) == MT_KERNEL_GEMV) return launch_gemv(a, xt, wt, s, g_tuning.gemv_lanes);
+    return launch_gemm(a, xt, wt, s, g_tuning.gemm_splitk);
+}
+
+int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *w, const void *w2, mt_dtype wt,
+                      const void *bias, float *y, mt_gemv_params p, mt_stream_t stream) {
+    if (!norm) return set_error(MT_EINVAL, "mt_linear_rmsnorm: null norm");
+    LinearArgs a;
+    int rc = validate_linear("mt_linear_rmsnorm", x, xt, w, w2, wt, bias, norm, y, p, a);
     if (rc) return rc;
     if (p.M == 0 || p.N == 0) return MT_OK;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -145,7 +162,7 @@ int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
         char who[48];
         snprintf(who, sizeof(who), "mt_seq_create: op %u", i);
         LinearArgs a;
-        int rc = validate_linear(who, o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, a);
+        int rc = validate_linear(who, o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.norm, o.y, o.p, a);
         if (rc) return rc;
         if (o.p.M == 0 || o.p.N == 0) return set_error(MT_EINVAL, "%s: empty op", who);
         if (o.p.M > 8) return set_error(MT_EINVAL, "%s: a sequence takes M <= 8, got %u", who, o.p.M);
@@ -154,10 +171,9 @@ int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
             return set_error(MT_EINVAL, "%s: every op of a sequence must share the weight and activation types", who);
         if (o.p.M > max_m) max_m = o.p.M;
         SeqOp &d = dev[i];
-        d.x = a.x; d.w = a.w; d.w2 = a.w2; d.bias = a.bias; d.y = a.y;
-        d.M = a.M; d.N = a.N; d.K = a.K; d.ldx = a.ldx; d.ldy = a.ldy; d.flags = a.flags;
+        d.x = a.x; d.w = a.w; d.w2 = a.w2; d.bias = a.bias; d.y = a.y; d.norm = a.norm;
+        d.M = a.M; d.N = a.N; d.K = a.K; d.ldx = a.ldx; d.ldy = a.ldy; d.flags = a.flags; d.eps = a.eps;
         d.lanes_log2 = gemv_lanes_log2(a.K, g_tuning.gemv_lanes);
-        d.pad = 0;
     }
     const int mr = max_m <= 1 ? 1 : max_m <= 2 ? 2 : max_m <= 4 ? 4 : 8;
     SeqPlan *plan = nullptr;

@@ -10,6 +10,12 @@
 //   - the MR activation rows reuse every weight load (the CFG pair at MR = 2);
 //   - the group's partial sums meet by butterfly shuffles; lane 0 of the group runs the
 //     epilogue and stores MR floats.
+// Fused RMSNorm prologue (NORM): the reference normalises x in its own dispatch
+// (Shaders.swift:414-441: x * rsqrt(mean(x^2) + eps) * g) before qkv and gate|up
+// (Qwen.swift:84-90).  Here the group that streams row n already reads every x chunk, so it
+// also sums x^2 over the row, multiplies x by the gain g on the fly, and applies the
+// per-row scale rsqrt(mean(x^2) + eps) to the finished dot products -- no extra pass over x
+// and no extra launch.
 // Rows of x past M are never read.  The reduction order is fixed, so results are
 // bit-identical from run to run.
 #pragma once
@@ -37,16 +43,17 @@ __device__ __forceinline__ void load_x8(const void *X, size_t off, float *o) {
 __device__ __forceinline__ uint4 as_uint4(u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
 
 // Computes output feature n for rows row0 .. row0 + rows - 1 (rows <= MR) with the calling
-// group of L lanes; j is the lane's index in the group.  Returns nothing: lane j == 0 stores.
-template <int MR, int WT, int XT, bool GATED, int U>
+// group of L lanes; j is the lane's index in the group.  Lane j == 0 stores.
+template <int MR, int WT, int XT, bool GATED, bool NORM, int U>
 __device__ __forceinline__ void gemv_feature(const LinearArgs &a, uint32_t n, uint32_t row0, int rows,
                                              int L, int j) {
     const int KC = static_cast<int>(a.K >> 3);
     const u32x4 *wr = reinterpret_cast<const u32x4 *>(a.w + static_cast<size_t>(n) * a.K);
     const u32x4 *gr = reinterpret_cast<const u32x4 *>((GATED ? a.w2 : a.w) + static_cast<size_t>(n) * a.K);
-    float acc[MR], acc2[MR];
+    const u32x4 *nr = reinterpret_cast<const u32x4 *>(NORM ? a.norm : a.w);
+    float acc[MR], acc2[MR], ss[MR];
 #pragma unroll
-    for (int m = 0; m < MR; m++) { acc[m] = 0.0f; acc2[m] = 0.0f; }
+    for (int m = 0; m < MR; m++) { acc[m] = 0.0f; acc2[m] = 0.0f; ss[m] = 0.0f; }
 
     for (int c0 = j; c0 < KC; c0 += U * L) {
         u32x4 wv[U], gv[U];
@@ -61,14 +68,23 @@ __device__ __forceinline__ void gemv_feature(const LinearArgs &a, uint32_t n, ui
         for (int u = 0; u < U; u++) {
             const int c = c0 + u * L;
             if (c < KC) {
-                float wf[8], gf[8];
+                float wf[8], gf[8], nf[8];
                 unpack8<WT>(as_uint4(wv[u]), wf);
                 if constexpr (GATED) unpack8<WT>(as_uint4(gv[u]), gf);
+                if constexpr (NORM) unpack8<WT>(as_uint4(nr[c]), nf);
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
                     if (m < rows) {
                         float xf[8];
                         load_x8<XT>(a.x, static_cast<size_t>(row0 + m) * a.ldx + static_cast<size_t>(c) * 8, xf);
+                        if constexpr (NORM) {
+                            float q = ss[m];
+#pragma unroll
+                            for (int e = 0; e < 8; e++) q = fmaf(xf[e], xf[e], q);
+                            ss[m] = q;
+#pragma unroll
+                            for (int e = 0; e < 8; e++) xf[e] *= nf[e];
+                        }
                         float s = acc[m];
 #pragma unroll
                         for (int e = 0; e < 8; e++) s = fmaf(xf[e], wf[e], s);
@@ -88,6 +104,11 @@ __device__ __forceinline__ void gemv_feature(const LinearArgs &a, uint32_t n, ui
     for (int m = 0; m < MR; m++) {
         acc[m] = group_sum(acc[m], L);
         if constexpr (GATED) acc2[m] = group_sum(acc2[m], L);
+        if constexpr (NORM) {
+            const float scale = 1.0f / sqrtf(group_sum(ss[m], L) / static_cast<float>(a.K) + a.eps);
+            acc[m] *= scale;
+            acc2[m] *= scale;
+        }
     }
     if (j == 0) {
         const float b = (a.flags & F_BIAS) ? dec1<WT>(a.bias[n]) : 0.0f;

@@ -13,10 +13,14 @@
 //     two MFMAs per step, and x is represented to 2^-22 (fp16) / 2^-17 (bf16) relative,
 //     so the result keeps the reference's fp32-activation accuracy.
 //   - SiLU-gate accumulates W and W2 tiles against the same activation fragments.
+//   - Fused RMSNorm prologue (NORM): x is multiplied by the gain while it is staged (then
+//     always split, so x * g is never rounded to 16 bits alone), each row's sum of squares
+//     is accumulated from the same loads, and the epilogue scales by rsqrt(mean(x^2) + eps).
 //   - Rows past M, weight rows past N and k past K are zero-filled in LDS, never read.
 // MFMA 32x32x16 operand layout (wave64): lane l holds A[l % 32][8 (l / 32) .. + 7] and
 // B[8 (l / 32) .. + 7][l % 32]; the 16 accumulators of lane l are
-// D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32], r = 0..15.  A GPU test pins this layout.
+// D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32], r = 0..15.  Any other layout would scramble
+// the output, which the GEMM parity tests would catch on every shape.
 #include "mt_device.hpp"
 #include "mt_internal.hpp"
 
@@ -60,14 +64,17 @@ __device__ __forceinline__ void split2(float x0, float x1, uint32_t &hi, uint32_
     lo = round16<T>(r0) | (round16<T>(r1) << 16);
 }
 
-template <int WT, int XT, bool GATED>
+template <int WT, int XT, bool GATED, bool NORM>
 __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
-    constexpr bool SPLIT = (XT != WT);
+    constexpr bool SPLIT = (XT != WT) || NORM;
     constexpr int XP = SPLIT ? 2 : 1;
     constexpr int WP = GATED ? 2 : 1;
-    constexpr int XCH = (XT == DT_F32) ? 4 : 2;  // 16-byte x chunks per thread per slice
+    constexpr bool XF32 = (XT == DT_F32);
+    constexpr int XCH = XF32 ? 4 : 2;          // 16-byte x chunks per thread per slice
+    constexpr int XROW = XF32 ? 16 : 8;        // threads sharing one x row in a slice
     __shared__ __attribute__((aligned(16))) uint16_t xs[XP][BM * LDK];
     __shared__ __attribute__((aligned(16))) uint16_t ws[WP][BN * LDK];
+    __shared__ float row_scale[NORM ? BM : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
@@ -77,8 +84,11 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
     f32x16 acc, acc2;
 #pragma unroll
     for (int r = 0; r < 16; r++) { acc[r] = 0.0f; acc2[r] = 0.0f; }
+    float ss[XCH];
+#pragma unroll
+    for (int i = 0; i < XCH; i++) ss[i] = 0.0f;
 
-    u32x4g wreg[2], w2reg[2], xreg[XCH];
+    u32x4g wreg[2], w2reg[2], xreg[XCH], greg[XCH];
 
     auto fetch = [&](uint32_t k0) {
 #pragma unroll
@@ -97,19 +107,28 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const int q = tid + i * NT;
-            u32x4g v = {0u, 0u, 0u, 0u};
-            if constexpr (XT == DT_F32) {
+            u32x4g v = {0u, 0u, 0u, 0u}, g = {0u, 0u, 0u, 0u};
+            if constexpr (XF32) {
                 const int r = q >> 4, c4 = q & 15;
                 const uint32_t m = m0 + r, k = k0 + c4 * 4;
-                if (m < M && k < K)
+                if (m < M && k < K) {
                     v = *reinterpret_cast<const u32x4g *>(static_cast<const float *>(a.x) + static_cast<size_t>(m) * a.ldx + k);
+                    if constexpr (NORM) {
+                        const u32x2g g2 = *reinterpret_cast<const u32x2g *>(a.norm + k);
+                        g.x = g2.x;
+                        g.y = g2.y;
+                    }
+                }
             } else {
                 const int r = q >> 3, kc = q & 7;
                 const uint32_t m = m0 + r, k = k0 + kc * 8;
-                if (m < M && k < K)
+                if (m < M && k < K) {
                     v = *reinterpret_cast<const u32x4g *>(static_cast<const uint16_t *>(a.x) + static_cast<size_t>(m) * a.ldx + k);
+                    if constexpr (NORM) g = *reinterpret_cast<const u32x4g *>(a.norm + k);
+                }
             }
             xreg[i] = v;
+            if constexpr (NORM) greg[i] = g;
         }
     };
 
@@ -124,11 +143,21 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
         for (int i = 0; i < XCH; i++) {
             const int q = tid + i * NT;
             const u32x4g v = xreg[i];
-            if constexpr (XT == DT_F32) {
+            if constexpr (XF32) {
                 const int r = q >> 4, c4 = q & 15;
+                float xf[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+                if constexpr (NORM) {
+                    const u32x4g g = greg[i];
+                    const float gf[4] = {dec_lo<WT>(g.x), dec_hi<WT>(g.x), dec_lo<WT>(g.y), dec_hi<WT>(g.y)};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        ss[i] = fmaf(xf[e], xf[e], ss[i]);
+                        xf[e] *= gf[e];
+                    }
+                }
                 uint32_t h0, l0, h1, l1;
-                split2<WT>(__uint_as_float(v.x), __uint_as_float(v.y), h0, l0);
-                split2<WT>(__uint_as_float(v.z), __uint_as_float(v.w), h1, l1);
+                split2<WT>(xf[0], xf[1], h0, l0);
+                split2<WT>(xf[2], xf[3], h1, l1);
                 const u32x2g hi = {h0, h1}, lo = {l0, l1};
                 *reinterpret_cast<u32x2g *>(&xs[0][r * LDK + c4 * 4]) = hi;
                 *reinterpret_cast<u32x2g *>(&xs[XP - 1][r * LDK + c4 * 4]) = lo;
@@ -136,12 +165,18 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
                 const int r = q >> 3, kc = q & 7;
                 *reinterpret_cast<u32x4g *>(&xs[0][r * LDK + kc * 8]) = v;
             } else {
-                // 16-bit activations of the other type: widen, then split.
+                // 16-bit activations of the other type, or normalised: widen, then split.
                 const int r = q >> 3, kc = q & 7;
                 u32x4g hi, lo;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float x0 = dec_lo<XT>(v[e]), x1 = dec_hi<XT>(v[e]);
+                    float x0 = dec_lo<XT>(v[e]), x1 = dec_hi<XT>(v[e]);
+                    if constexpr (NORM) {
+                        ss[i] = fmaf(x0, x0, ss[i]);
+                        ss[i] = fmaf(x1, x1, ss[i]);
+                        x0 *= dec_lo<WT>(greg[i][e]);
+                        x1 *= dec_hi<WT>(greg[i][e]);
+                    }
                     uint32_t h, l;
                     split2<WT>(x0, x1, h, l);
                     hi[e] = h;
@@ -179,14 +214,32 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
         }
     }
 
+    if constexpr (NORM) {
+        // Row sums of squares: the XROW threads sharing a row are adjacent lanes of one wave.
+#pragma unroll
+        for (int i = 0; i < XCH; i++) {
+            float s = ss[i];
+            for (int off = XROW >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+            const int r = (tid + i * NT) / XROW;
+            if ((tid & (XROW - 1)) == 0) row_scale[r] = 1.0f / sqrtf(s / static_cast<float>(K) + a.eps);
+        }
+        __syncthreads();
+    }
+
     const uint32_t n = n0 + 32 * wn + (lane & 31);
     if (n >= N) return;
     const float bv = (a.flags & F_BIAS) ? dec1<WT>(a.bias[n]) : 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        const uint32_t m = m0 + 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int ml = 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const uint32_t m = m0 + ml;
         if (m < M) {
-            float v = epilogue(acc[r], acc2[r], bv, a.flags);
+            float c = acc[r], c2 = acc2[r];
+            if constexpr (NORM) {
+                c *= row_scale[ml];
+                c2 *= row_scale[ml];
+            }
+            float v = epilogue(c, c2, bv, a.flags);
             float *yp = a.y + static_cast<size_t>(m) * a.ldy + n;
             if (a.flags & F_ACCUM) v += *yp;
             *yp = v;
@@ -197,14 +250,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
 typedef void (*gemm_fn)(LinearArgs);
 
 template <int WT, int XT>
-gemm_fn pick_g(bool gated) { return gated ? gemm_kernel<WT, XT, true> : gemm_kernel<WT, XT, false>; }
+gemm_fn pick_v(bool gated, bool norm) {
+    if (gated) return norm ? gemm_kernel<WT, XT, true, true> : gemm_kernel<WT, XT, true, false>;
+    return norm ? gemm_kernel<WT, XT, false, true> : gemm_kernel<WT, XT, false, false>;
+}
 
 template <int WT>
-gemm_fn pick_x(int xt, bool gated) {
+gemm_fn pick_x(int xt, bool gated, bool norm) {
     switch (xt) {
-        case DT_F32: return pick_g<WT, DT_F32>(gated);
-        case DT_F16: return pick_g<WT, DT_F16>(gated);
-        default: return pick_g<WT, DT_BF16>(gated);
+        case DT_F32: return pick_v<WT, DT_F32>(gated, norm);
+        case DT_F16: return pick_v<WT, DT_F16>(gated, norm);
+        default: return pick_v<WT, DT_BF16>(gated, norm);
     }
 }
 
@@ -212,7 +268,8 @@ gemm_fn pick_x(int xt, bool gated) {
 
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int /*splitk_override*/) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
-    gemm_fn fn = wt == DT_BF16 ? pick_x<DT_BF16>(xt, gated) : pick_x<DT_F16>(xt, gated);
+    const bool norm = a.norm != nullptr;
+    gemm_fn fn = wt == DT_BF16 ? pick_x<DT_BF16>(xt, gated, norm) : pick_x<DT_F16>(xt, gated, norm);
     dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
     hipLaunchKernelGGL(fn, grid, dim3(NT), 0, stream, a);
     return check_launch("gemm");

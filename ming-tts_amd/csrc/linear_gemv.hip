@@ -8,7 +8,7 @@
 
 namespace mt {
 
-template <int MR, int WT, int XT, bool GATED>
+template <int MR, int WT, int XT, bool GATED, bool NORM>
 __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a, int lanes_log2) {
     const int L = 1 << lanes_log2;
     const int groups = static_cast<int>(blockDim.x) >> lanes_log2;
@@ -18,7 +18,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a, int lanes_log2)
     if (n >= a.N) return;  // the whole lane group leaves together; no block barrier follows
     const uint32_t row0 = blockIdx.y * MR;
     const int rows = min(MR, static_cast<int>(a.M - row0));
-    gemv_feature<MR, WT, XT, GATED, 4>(a, n, row0, rows, L, j);
+    gemv_feature<MR, WT, XT, GATED, NORM, 4>(a, n, row0, rows, L, j);
 }
 
 namespace {
@@ -26,30 +26,31 @@ namespace {
 typedef void (*gemv_fn)(LinearArgs, int);
 
 template <int MR, int WT, int XT>
-gemv_fn pick_gated(bool gated) {
-    return gated ? gemv_kernel<MR, WT, XT, true> : gemv_kernel<MR, WT, XT, false>;
+gemv_fn pick_variant(bool gated, bool norm) {
+    if (gated) return norm ? gemv_kernel<MR, WT, XT, true, true> : gemv_kernel<MR, WT, XT, true, false>;
+    return norm ? gemv_kernel<MR, WT, XT, false, true> : gemv_kernel<MR, WT, XT, false, false>;
 }
 
 template <int MR, int WT>
-gemv_fn pick_x(int xt, bool gated) {
+gemv_fn pick_x(int xt, bool gated, bool norm) {
     switch (xt) {
-        case DT_F32: return pick_gated<MR, WT, DT_F32>(gated);
-        case DT_F16: return pick_gated<MR, WT, DT_F16>(gated);
-        default: return pick_gated<MR, WT, DT_BF16>(gated);
+        case DT_F32: return pick_variant<MR, WT, DT_F32>(gated, norm);
+        case DT_F16: return pick_variant<MR, WT, DT_F16>(gated, norm);
+        default: return pick_variant<MR, WT, DT_BF16>(gated, norm);
     }
 }
 
 template <int MR>
-gemv_fn pick_w(int wt, int xt, bool gated) {
-    return wt == DT_BF16 ? pick_x<MR, DT_BF16>(xt, gated) : pick_x<MR, DT_F16>(xt, gated);
+gemv_fn pick_w(int wt, int xt, bool gated, bool norm) {
+    return wt == DT_BF16 ? pick_x<MR, DT_BF16>(xt, gated, norm) : pick_x<MR, DT_F16>(xt, gated, norm);
 }
 
-gemv_fn pick(int mr, int wt, int xt, bool gated) {
+gemv_fn pick(int mr, int wt, int xt, bool gated, bool norm) {
     switch (mr) {
-        case 1: return pick_w<1>(wt, xt, gated);
-        case 2: return pick_w<2>(wt, xt, gated);
-        case 4: return pick_w<4>(wt, xt, gated);
-        default: return pick_w<8>(wt, xt, gated);
+        case 1: return pick_w<1>(wt, xt, gated, norm);
+        case 2: return pick_w<2>(wt, xt, gated, norm);
+        case 4: return pick_w<4>(wt, xt, gated, norm);
+        default: return pick_w<8>(wt, xt, gated, norm);
     }
 }
 
@@ -71,6 +72,7 @@ int gemv_lanes_log2(uint32_t K, int override_lanes) {
 
 int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
+    const bool norm = a.norm != nullptr;
     const int mr = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : 8;
     const int l2 = gemv_lanes_log2(a.K, override_lanes);
     const int L = 1 << l2;
@@ -80,7 +82,7 @@ int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int ove
     while (threads > 64 && (a.N + (threads / L) - 1) / (threads / L) < 512) threads >>= 1;
     const int per_group = threads / L;
     dim3 grid((a.N + per_group - 1) / per_group, (a.M + mr - 1) / mr);
-    gemv_fn fn = pick(mr, wt, xt, gated);
+    gemv_fn fn = pick(mr, wt, xt, gated, norm);
     hipLaunchKernelGGL(fn, grid, dim3(threads), 0, stream, a, l2);
     return check_launch("gemv");
 }

@@ -62,17 +62,22 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
     bool abandoned = false;
     for (uint32_t i = 0; i < n_ops; i++) {
         const SeqOp o = ops[i];
-        const LinearArgs a{o.x, o.w, o.w2, o.bias, o.y, o.M, o.N, o.K, o.ldx, o.ldy, o.flags};
+        const LinearArgs a{o.x, o.w, o.w2, o.bias, o.y, o.M, o.N, o.K, o.ldx, o.ldy, o.flags, o.norm, o.eps};
         const int l2 = o.lanes_log2, L = 1 << l2;
         const int groups = SEQ_THREADS >> l2;
         const int grp = static_cast<int>(threadIdx.x) >> l2, j = static_cast<int>(threadIdx.x) & (L - 1);
         const uint32_t r0 = static_cast<uint32_t>(static_cast<uint64_t>(g) * o.N / G);
         const uint32_t r1 = static_cast<uint32_t>(static_cast<uint64_t>(g + 1) * o.N / G);
         const int rows = static_cast<int>(o.M);
-        if (o.flags & F_SILU_GATE) {
-            for (uint32_t n = r0 + grp; n < r1; n += groups) gemv_feature<MR, WT, XT, true, 4>(a, n, 0, rows, L, j);
+        const bool gated = (o.flags & F_SILU_GATE) != 0, norm = o.norm != nullptr;
+        if (gated && norm) {
+            for (uint32_t n = r0 + grp; n < r1; n += groups) gemv_feature<MR, WT, XT, true, true, 4>(a, n, 0, rows, L, j);
+        } else if (gated) {
+            for (uint32_t n = r0 + grp; n < r1; n += groups) gemv_feature<MR, WT, XT, true, false, 4>(a, n, 0, rows, L, j);
+        } else if (norm) {
+            for (uint32_t n = r0 + grp; n < r1; n += groups) gemv_feature<MR, WT, XT, false, true, 4>(a, n, 0, rows, L, j);
         } else {
-            for (uint32_t n = r0 + grp; n < r1; n += groups) gemv_feature<MR, WT, XT, false, 4>(a, n, 0, rows, L, j);
+            for (uint32_t n = r0 + grp; n < r1; n += groups) gemv_feature<MR, WT, XT, false, false, 4>(a, n, 0, rows, L, j);
         }
         if (i + 1 < n_ops) grid_barrier(sync, (i + 1) * G, abandoned);
     }

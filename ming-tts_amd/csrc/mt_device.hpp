@@ -17,6 +17,8 @@ struct LinearArgs {
     const uint16_t *bias;
     float *y;
     uint32_t M, N, K, ldx, ldy, flags;
+    const uint16_t *norm;  // RMSNorm gain [K] (type of w) applied to x first, or null
+    float eps;             // RMSNorm epsilon
 };
 
 // bf16 is the top half of an fp32 (Shaders.swift:12).

@@ -29,9 +29,10 @@ struct SeqOp {
     const uint16_t *w2;
     const uint16_t *bias;
     float *y;
+    const uint16_t *norm;
     uint32_t M, N, K, ldx, ldy, flags;
+    float eps;
     int32_t lanes_log2;
-    int32_t pad;
 };
 struct SeqPlan;
 int seq_create(const SeqOp *ops, uint32_t n_ops, int mr, int wt, int xt, SeqPlan **out);

@@ -26,7 +26,7 @@ TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS = 1, 2, 3
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
-    "mt_linear", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create", "mt_seq_run",
+    "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_last_error", "mt_version",
 )
@@ -59,8 +59,8 @@ class GemvParams(ctypes.Structure):
 class LinearOp(ctypes.Structure):
     """mt_linear_op: one op of a persistent sequence."""
     _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("w2", ctypes.c_void_p),
-                ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p), ("p", GemvParams),
-                ("xt", ctypes.c_int32), ("wt", ctypes.c_int32)]
+                ("bias", ctypes.c_void_p), ("norm", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("p", GemvParams), ("xt", ctypes.c_int32), ("wt", ctypes.c_int32)]
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -77,6 +77,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     vp, u32, u64, i32, f32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
     L.mt_linear.argtypes = [vp, i32, vp, vp, i32, vp, vp, GemvParams, vp]
     L.mt_linear.restype = i32
+    L.mt_linear_rmsnorm.argtypes = [vp, i32, vp, vp, vp, i32, vp, vp, GemvParams, vp]
+    L.mt_linear_rmsnorm.restype = i32
     L.mt_linear_kernel.argtypes = [u32, u32, u32, i32, i32]
     L.mt_linear_kernel.restype = i32
     L.mt_set_tuning.argtypes = [i32, i32]
@@ -147,13 +149,26 @@ def linear_raw(x, xt, w, w2, wt, bias, y, M, N, K, ldx, ldy, flags, stream=None)
     return load().mt_linear(_ptr(x), xt, _ptr(w), _ptr(w2), wt, _ptr(bias), _ptr(y), p, _stream(stream))
 
 
-def linear(x, w, y, M=None, flags=0, w2=None, bias=None, ldx=None, ldy=None, stream=None) -> None:
-    """y[:M] (op)= x[:M] @ w.T with the epilogue in ``flags``; torch tensors, w: [N, K]."""
+def linear_rmsnorm_raw(x, xt, norm, w, w2, wt, bias, y, M, N, K, ldx, ldy, flags, eps=1e-6, stream=None) -> int:
+    """mt_linear_rmsnorm on raw pointers / tensors; returns the raw return code."""
+    p = GemvParams(M, N, K, ldx, ldy, flags, eps)
+    return load().mt_linear_rmsnorm(_ptr(x), xt, _ptr(norm), _ptr(w), _ptr(w2), wt, _ptr(bias), _ptr(y), p,
+                                    _stream(stream))
+
+
+def linear(x, w, y, M=None, flags=0, w2=None, bias=None, ldx=None, ldy=None, norm=None, eps=1e-6,
+           stream=None) -> None:
+    """y[:M] (op)= x[:M] @ w.T with the epilogue in ``flags``; torch tensors, w: [N, K].
+    With ``norm`` (gain [K]) x is RMS-normalised first (mt_linear_rmsnorm)."""
     N, K = w.shape
     M = x.shape[0] if M is None else M
     ldx = x.stride(0) if ldx is None else ldx
     ldy = y.stride(0) if ldy is None else ldy
-    check(linear_raw(x, dtype_code(x), w, w2, dtype_code(w), bias, y, M, N, K, ldx, ldy, flags, stream))
+    if norm is not None:
+        check(linear_rmsnorm_raw(x, dtype_code(x), norm, w, w2, dtype_code(w), bias, y, M, N, K, ldx, ldy, flags,
+                                 eps, stream))
+    else:
+        check(linear_raw(x, dtype_code(x), w, w2, dtype_code(w), bias, y, M, N, K, ldx, ldy, flags, stream))
 
 
 def linear_kernel(M, N, K, xt=F32, wt=BF16) -> int:
@@ -196,14 +211,15 @@ class Seq:
             pass
 
 
-def op(x, w, y, M, flags=0, w2=None, bias=None, ldx=None, ldy=None, xt=None, wt=None) -> LinearOp:
-    """An mt_linear_op over torch tensors (w: [N, K])."""
+def op(x, w, y, M, flags=0, w2=None, bias=None, ldx=None, ldy=None, xt=None, wt=None, norm=None,
+       eps=1e-6) -> LinearOp:
+    """An mt_linear_op over torch tensors (w: [N, K]); ``norm`` fuses an RMSNorm prologue."""
     N, K = w.shape
     if bias is not None:
         flags |= GemvFlags.bias
-    return LinearOp(_ptr(x), _ptr(w), _ptr(w2), _ptr(bias), _ptr(y),
+    return LinearOp(_ptr(x), _ptr(w), _ptr(w2), _ptr(bias), _ptr(norm), _ptr(y),
                     GemvParams(M, N, K, x.stride(0) if ldx is None else ldx, y.stride(0) if ldy is None else ldy,
-                               flags, 0.0),
+                               flags, eps if norm is not None else 0.0),
                     dtype_code(x) if xt is None else xt, dtype_code(w) if wt is None else wt)
 
 

@@ -166,6 +166,54 @@ def max_threads() -> int:
     return lib().mto_max_threads()
 
 
+def _gelu64(v: np.ndarray) -> np.ndarray:
+    u = np.clip(0.7978845608028654 * (v + 0.044715 * v ** 3), -15.0, 15.0)
+    return 0.5 * v * (1.0 + np.tanh(u))
+
+
+def linear_np64(x64, w, w2, wt, bias, y0, flags) -> np.ndarray:
+    """The linear in fp64 from numpy's matmul (x64: float [M, K] in any precision, w / w2 /
+    bias as 16-bit storage), epilogue in the reference order.  Used where x is itself an
+    fp64 intermediate (the RMSNorm prologue)."""
+    x64 = np.asarray(x64, np.float64)
+    acc = x64 @ decode16(w, wt).astype(np.float64).T
+    v = acc + (decode16(bias, wt).astype(np.float64) if bias is not None else 0.0)
+    if flags & SILU_GATE:
+        acc2 = x64 @ decode16(w2, wt).astype(np.float64).T
+        v = v / (1.0 + np.exp(-v)) * acc2
+    if flags & GELU:
+        v = _gelu64(v)
+    if flags & SILU:
+        v = v / (1.0 + np.exp(-v))
+    if flags & ACCUM:
+        v = v + np.asarray(y0, np.float64)
+    return v
+
+
+def rmsnorm_f64(x, g, wt, eps: float = 1e-6) -> np.ndarray:
+    """RMSNorm of rows, x * rsqrt(mean(x^2) + eps) * g (Shaders.swift:414-441;
+    KernelTests.swift:187-203), in fp64.  g: 16-bit storage of type wt."""
+    x64 = np.asarray(x, np.float64)
+    s = 1.0 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + np.float64(np.float32(eps)))
+    return x64 * s * decode16(g, wt).astype(np.float64)
+
+
+def rmsnorm_f32(x, g, wt, eps: float = 1e-6) -> np.ndarray:
+    """The reference's CPU RMSNorm loop (KernelTests.swift:193-199): fp32 sum of squares in
+    natural order, s = 1 / sqrt(ss / k + eps), y = x * s * g, all fp32."""
+    x = np.asarray(x, np.float32)
+    gf = decode16(g, wt)
+    out = np.empty_like(x)
+    k = x.shape[-1]
+    for r in range(x.shape[0]):
+        ss = np.float32(0.0)
+        for v in x[r]:
+            ss = np.float32(ss + v * v)
+        s = np.float32(1.0) / np.sqrt(np.float32(ss / np.float32(k) + np.float32(eps)))
+        out[r] = x[r] * s * gf
+    return out
+
+
 # ---------------------------------------------------------- tolerances --
 
 def kat_atol(k: int) -> float:
@@ -255,11 +303,16 @@ def inv_freq(theta: float = 1e6, dim: int = 64) -> np.ndarray:
     return (np.float32(1.0) / np.power(np.float32(theta), np.float32(2.0) * i / np.float32(dim))).astype(np.float32)
 
 
-def rope_neox(v: np.ndarray, pos, invf: np.ndarray) -> np.ndarray:
+def rope_neox(v: np.ndarray, pos, invf: np.ndarray, fp32_angle: bool = True) -> np.ndarray:
     """NeoX rotation of 64-wide heads, pairs (i, i + 32), angle pos * inv_freq[i]
-    (Shaders.swift:472-478; KernelTests.swift:207-217), in fp64.  v: [..., 64]."""
+    (Shaders.swift:472-478; KernelTests.swift:207-217).  The angle is formed in fp32 as the
+    reference forms it (``float(pos) * invFreq[i]``); cos, sin and the rotation are fp64.
+    v: [..., 64]."""
     v = np.asarray(v, np.float64)
-    a = np.asarray(pos, np.float64)[..., None] * invf.astype(np.float64)
+    if fp32_angle:
+        a = (np.asarray(pos, np.float32)[..., None] * invf.astype(np.float32)).astype(np.float64)
+    else:
+        a = np.asarray(pos, np.float64)[..., None] * invf.astype(np.float64)
     c, s = np.cos(a), np.sin(a)
     x0, x1 = v[..., :32], v[..., 32:]
     return np.concatenate([x0 * c - x1 * s, x1 * c + x0 * s], axis=-1)

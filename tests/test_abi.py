@@ -71,6 +71,17 @@ def test_empty_linear_is_a_no_op():
     assert lin(N=0) == mt.OK
 
 
+def test_linear_rmsnorm_rejects_bad_arguments():
+    def call(norm=W_ADDR, eps=1e-6, K=64):
+        return mt.linear_rmsnorm_raw(ALIGNED, mt.F32, norm, W_ADDR, None, mt.F16, None, Y_ADDR, 2, 64, K, 64, 64, 0,
+                                     eps, stream=0)
+    assert call(norm=None) == mt.EINVAL and "null norm" in mt.last_error()
+    assert call(norm=W_ADDR + 2) == mt.EINVAL and "norm must be 16-byte" in mt.last_error()
+    assert call(eps=-1e-3) == mt.EINVAL and "eps" in mt.last_error()
+    assert call(eps=float("nan")) == mt.EINVAL
+    assert call(K=12) == mt.EINVAL
+
+
 def test_kernel_choice_and_tuning_round_trip():
     """The analogue of Kernels.usesGemm / scalarRowsMax (KernelTests.swift:155-157, 165-166)."""
     assert mt.linear_kernel(1, 1152, 896) == mt.KERNEL_GEMV
@@ -89,14 +100,17 @@ def test_kernel_choice_and_tuning_round_trip():
 
 def test_seq_create_validates_every_op_before_the_device():
     import ctypes
-    ok = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(2, 64, 64, 64, 64, 0, 0.0), mt.F32, mt.F16)
-    bad_m = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(9, 64, 64, 64, 64, 0, 0.0), mt.F32, mt.F16)
-    bad_t = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(2, 64, 64, 64, 64, 0, 0.0), mt.F16, mt.F16)
-    bad_k = mt.LinearOp(ALIGNED, W_ADDR, None, None, Y_ADDR, mt.GemvParams(2, 64, 60, 64, 64, 0, 0.0), mt.F32, mt.F16)
+    def op(M=2, K=64, xt=mt.F32, norm=None, eps=0.0):
+        return mt.LinearOp(ALIGNED, W_ADDR, None, None, norm, Y_ADDR, mt.GemvParams(M, 64, K, 64, 64, 0, eps), xt, mt.F16)
+
+    ok, bad_m, bad_t, bad_k = op(), op(M=9), op(xt=mt.F16), op(K=60)
+    bad_norm = op(norm=W_ADDR + 8)
+    bad_eps = op(norm=W_ADDR, eps=-1.0)
     L = mt.load()
     h = ctypes.c_void_p()
     for ops, needle in (([ok, bad_m], "op 1: a sequence takes M <= 8"), ([ok, bad_t], "share the weight"),
-                        ([bad_k], "op 0: K must")):
+                        ([bad_k], "op 0: K must"), ([bad_norm], "norm must be 16-byte"),
+                        ([ok, ok, bad_eps], "op 2: RMSNorm eps")):
         arr = (mt.LinearOp * len(ops))(*ops)
         assert L.mt_seq_create(arr, len(ops), ctypes.byref(h)) == mt.EINVAL
         assert needle in mt.last_error()

@@ -199,6 +199,56 @@ def test_strided_views_and_edges(gpu):
         np.testing.assert_array_equal(got[:, N:], y0[:, N:])   # columns past N untouched
 
 
+@pytest.mark.parametrize("rows_max", [8, 0], ids=["gemv", "gemm"])
+def test_reference_rmsnorm_kat_through_identity_weights(gpu, rows_max):
+    """KernelTests.testRMSNorm (KernelTests.swift:187-203) through the fused prologue: with
+    W = I (exact in bf16) the linear returns the normalised rows themselves."""
+    rows, k = 5, 896
+    rng = O.LCG(3)
+    x = rng.floats(rows * k, 3.0).reshape(rows, k)
+    gb, _ = O.round16(rng.floats(k), O.BF16)
+    eye, _ = O.round16(np.eye(k, dtype=np.float32), O.BF16)
+    want = O.rmsnorm_f32(x, gb, O.BF16)
+    x_d = torch.from_numpy(np.concatenate([x, np.full((8, k), np.nan, np.float32)])).to(gpu)
+    y_d = torch.zeros(rows, k, device=gpu)
+    old = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, rows_max)
+    try:
+        say(f"rmsnorm kat rows_max={rows_max}")
+        mt.linear(x_d, dev16(eye, O.BF16, gpu), y_d, M=rows, norm=dev16(gb, O.BF16, gpu), eps=1e-6)
+        torch.cuda.synchronize()
+    finally:
+        mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old)
+    ex, i, g, w = O.worst_violation(y_d.cpu().numpy(), want, 1e-5)   # atol 1e-5 as the reference
+    assert ex <= 0, f"index {i} got {g} want {w}"
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 64, 174])
+@pytest.mark.parametrize("layer", [BACKBONE[0], BACKBONE[2]], ids=["qkv", "gate|up"])
+@pytest.mark.parametrize("xt", [O.F32, O.F16], ids=["xf32", "xf16"])
+def test_fused_rmsnorm_prologue(gpu, M, layer, xt):
+    """rmsnorm then linear (Qwen.swift:84-85, 89-90) as one pass, against the fp64 composition
+    and against the reference's two fp32 loops (norm, then linear on the stored fp32 row)."""
+    label, N, K, flags, bias, gated = layer
+    c = _baseline_case(4000 + M + N, M, N, K, flags, bias, gated)
+    x = c["x"] * np.float32(5.0)       # off-unit scale: the norm must actually rescale
+    gbits, _ = O.round16(1.0 + 0.1 * O.gaussian(4100 + N, K), O.F16)
+    x_d, xu = dev_x(x, xt, gpu)
+    y_d = torch.from_numpy(c["y0"].copy()).to(gpu)
+    say(f"fused rmsnorm {label} M={M} x{xt}")
+    rc = mt.linear_rmsnorm_raw(x_d, xt, dev16(gbits, O.F16, gpu), dev16(c["w"], O.F16, gpu),
+                               dev16(c["w2"], O.F16, gpu) if gated else None, O.F16,
+                               dev16(c["bias"], O.F16, gpu) if c["bias"] is not None else None, y_d,
+                               M, N, K, K, N, flags, 1e-6, None)
+    assert rc == 0, mt.last_error()
+    torch.cuda.synchronize()
+    got = y_d.cpu().numpy()
+    want64 = O.linear_np64(O.rmsnorm_f64(xu, gbits, O.F16), c["w"], c["w2"] if gated else None, O.F16,
+                           c["bias"], c["y0"], c["flags"])
+    normed32 = O.rmsnorm_f32(xu, gbits, O.F16)
+    want32 = O.linear_f32(normed32, c["w"], c["w2"] if gated else None, O.F16, c["bias"], c["y0"], M, N, K, c["flags"])
+    assert_linear_parity(got, want32, want64, K, f"fused rmsnorm {label} M={M}")
+
+
 def test_encoder_mirror_reads_like_the_reference(gpu):
     """Encoder.linear with Linear / ActView / GPUTensor (Kernels.swift:7-44, 132-161)."""
     c = O.gemv_case(2, 2, 896, 0, True)

@@ -160,6 +160,28 @@ def test_linear_f64_matches_library_routines(flags, wt):
         np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("flags", FLAG_SETS)
+def test_linear_np64_agrees_with_linear_f64(flags):
+    M, N, K = 3, 40, 96
+    x, wb, w, w2b, w2, bb, b, y0 = _random_linear(300 + flags, M, N, K, O.BF16, x_scale=3.0)
+    gw2 = w2b if flags & O.SILU_GATE else None
+    np.testing.assert_allclose(O.linear_np64(x, wb, gw2, O.BF16, bb, y0, flags | O.BIAS),
+                               O.linear_f64(x, wb, gw2, O.BF16, bb, y0, M, N, K, flags), rtol=1e-12, atol=1e-12)
+
+
+def test_rmsnorm_matches_torch_rms_norm():
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((5, 896)) * 3).astype(np.float32)
+    gb, g = O.round16(rng.standard_normal(896).astype(np.float32), O.BF16)
+    want = F.rms_norm(torch.from_numpy(x.astype(np.float64)), (896,), torch.from_numpy(g.astype(np.float64)),
+                      eps=float(np.float32(1e-6))).numpy()
+    np.testing.assert_allclose(O.rmsnorm_f64(x, gb, O.BF16), want, rtol=1e-12, atol=1e-12)
+    # the fp32 reference loop sits within fp32 rounding of it
+    np.testing.assert_allclose(O.rmsnorm_f32(x, gb, O.BF16), want, rtol=2e-6, atol=1e-6)
+    # scale invariance: rmsnorm(c x) == rmsnorm(x) up to eps
+    np.testing.assert_allclose(O.rmsnorm_f64(x * 4, gb, O.BF16, 0.0), O.rmsnorm_f64(x, gb, O.BF16, 0.0), rtol=1e-12)
+
+
 def test_linear_f64_brute_force_tiny():
     """2 x 3 x 8 against explicit triple loops over the decoded weights."""
     M, N, K = 2, 3, 8
@@ -299,9 +321,12 @@ def test_inv_freq_and_rope_invariants():
         r = O.rope_neox(q, p, invf)
         np.testing.assert_allclose(np.linalg.norm(r, axis=-1), np.linalg.norm(q, axis=-1), rtol=1e-12)
     # relative position: <R(a) q, R(b) k> depends on b - a only (pairs (i, i+32) rotate together)
-    d1 = np.sum(O.rope_neox(q, 10, invf) * O.rope_neox(k, 13, invf), -1)
-    d2 = np.sum(O.rope_neox(q, 100, invf) * O.rope_neox(k, 103, invf), -1)
+    d1 = np.sum(O.rope_neox(q, 10, invf, False) * O.rope_neox(k, 13, invf, False), -1)
+    d2 = np.sum(O.rope_neox(q, 100, invf, False) * O.rope_neox(k, 103, invf, False), -1)
     np.testing.assert_allclose(d1, d2, rtol=1e-9)
+    # the fp32 angle (the reference's) is within one fp32 rounding of the exact angle
+    r32, r64 = O.rope_neox(q, 511, invf), O.rope_neox(q, 511, invf, False)
+    assert np.max(np.abs(r32 - r64)) <= 511 * 2.0 ** -24 * np.max(np.abs(q)) * 2
     # pairing is (i, i+32): a vector living only in dims {0, 32} stays there
     e = np.zeros(64)
     e[0] = 1.0

@@ -15,8 +15,8 @@ H, QKV, INTER = 896, 1152, 4864
 
 
 def make_stack(layers: int, M: int, seed: int, device):
-    """Per-layer fp16 weights ~ N(0, 0.02^2) (qkv with bias, o, gate, up, down), seeded per
-    layer from the SplitMix64 normal stream, plus the activation buffers of the chain."""
+    """Per-layer fp16 weights ~ N(0, 0.02^2) (qkv with bias, o, gate, up, down) and RMSNorm
+    gains ~ 1 + N(0, 0.1^2), seeded per layer from the SplitMix64 normal stream."""
     ws = []
     for l in range(layers):
         n = QKV * H + QKV + H * H + 2 * INTER * H + H * INTER
@@ -29,6 +29,9 @@ def make_stack(layers: int, M: int, seed: int, device):
                                   ("down", H * INTER, (H, INTER))):
             parts[name] = bits[o:o + size].reshape(shape)
             o += size
+        gains = 1.0 + O.gaussian(seed * 1000 + 500 + l, 2 * H, 0.1)
+        parts["norm1"], _ = O.round16(gains[:H], O.F16)
+        parts["norm2"], _ = O.round16(gains[H:], O.F16)
         parts["dev"] = {k: dev16(v, O.F16, device) for k, v in parts.items()}
         ws.append(parts)
     x0 = O.gaussian(seed + 7, M * H)
@@ -36,14 +39,15 @@ def make_stack(layers: int, M: int, seed: int, device):
 
 
 def chain_ops(ws, M, resid, qkv, mlp):
-    """The decode chain: qkv = resid Wqkv^T + b; resid += qkv[:, :896] Wo^T (the attention
-    output stand-in); mlp = silu(resid Wg^T) * (resid Wu^T); resid += mlp Wd^T."""
+    """The decode chain of one Qwen layer's linears (Qwen.swift:84-91) with the RMSNorms fused:
+    qkv = rmsnorm(resid; g1) Wqkv^T + b; resid += qkv[:, :896] Wo^T (the attention output
+    stand-in); mlp = silu(n Wg^T) * (n Wu^T) with n = rmsnorm(resid; g2); resid += mlp Wd^T."""
     ops = []
     for p in ws:
         d = p["dev"]
-        ops.append(mt.op(resid, d["qkv"], qkv, M, bias=d["qkv_b"]))
+        ops.append(mt.op(resid, d["qkv"], qkv, M, bias=d["qkv_b"], norm=d["norm1"]))
         ops.append(mt.op(qkv, d["o"], resid, M, flags=mt.GemvFlags.accumulate, ldx=QKV))
-        ops.append(mt.op(resid, d["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=d["up"]))
+        ops.append(mt.op(resid, d["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=d["up"], norm=d["norm2"]))
         ops.append(mt.op(mlp, d["down"], resid, M, flags=mt.GemvFlags.accumulate))
     return ops
 
@@ -53,11 +57,12 @@ def oracle_chain(ws, x0, M):
     resid = x0.astype(np.float32).copy()
     qkv = mlp = None
     for p in ws:
-        qkv = O.linear_f64(resid, p["qkv"], None, O.F16, p["qkv_b"], None, M, QKV, H, 0).astype(np.float32)
+        qkv = O.linear_np64(O.rmsnorm_f64(resid, p["norm1"], O.F16), p["qkv"], None, O.F16, p["qkv_b"], None,
+                            0).astype(np.float32)
         resid = O.linear_f64(np.ascontiguousarray(qkv[:, :H]), p["o"], None, O.F16, None, resid, M, H, H,
                              O.ACCUM).astype(np.float32)
-        mlp = O.linear_f64(resid, p["gate"], p["up"], O.F16, None, None, M, INTER, H,
-                           O.SILU_GATE).astype(np.float32)
+        mlp = O.linear_np64(O.rmsnorm_f64(resid, p["norm2"], O.F16), p["gate"], p["up"], O.F16, None, None,
+                            O.SILU_GATE).astype(np.float32)
         resid = O.linear_f64(mlp, p["down"], None, O.F16, None, resid, M, H, INTER, O.ACCUM).astype(np.float32)
     return resid, qkv, mlp
 
@@ -96,8 +101,12 @@ def test_seq_equals_per_op_launches_bit_for_bit(gpu):
     resid, qkv, mlp = buffers(M, x0, gpu)
     ops = chain_ops(ws, M, resid, qkv, mlp)
     for o in ops:
-        rc = mt.linear_raw(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p.M, o.p.N, o.p.K, o.p.ldx, o.p.ldy,
-                           o.p.flags, None)
+        if o.norm:
+            rc = mt.linear_rmsnorm_raw(o.x, o.xt, o.norm, o.w, o.w2, o.wt, o.bias, o.y, o.p.M, o.p.N, o.p.K,
+                                       o.p.ldx, o.p.ldy, o.p.flags, o.p.eps, None)
+        else:
+            rc = mt.linear_raw(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p.M, o.p.N, o.p.K, o.p.ldx, o.p.ldy,
+                               o.p.flags, None)
         assert rc == 0, mt.last_error()
     torch.cuda.synchronize()
     ref = resid.cpu().numpy().copy()
