@@ -112,14 +112,24 @@ enum {
 int mt_set_tuning(int key, int value);
 
 /*
- * A sequence of linears executed in order, each seeing the writes of the ones
- * before it -- QwenForward.dispatches on a serial encoder (Qwen.swift:72-97).
- * mt_seq_create validates every op and uploads the plan once; mt_seq_run runs the
- * whole sequence as ONE persistent kernel launch (cooperative, one workgroup set
- * resident for the whole sequence, a device-wide barrier between ops).  Every op
- * must satisfy mt_linear's requirements with M <= 8.  The pointers in the plan are
- * fixed; their contents may change between runs.  Runs of one plan must not
- * overlap in time (the plan's barrier state is shared).
+ * A sequence of linears with the result of executing them in order, each seeing the
+ * writes of the ones before it -- QwenForward.dispatches on a serial encoder
+ * (Qwen.swift:72-97).  mt_seq_create validates every op, compiles the list into a
+ * dataflow plan and uploads it once; mt_seq_run runs the whole sequence as ONE
+ * persistent cooperative kernel launch in which ops hand activations to each other
+ * through plan-owned tagged buffers (no device-wide barriers).
+ * Requirements, beyond mt_linear's for every op: 1 <= M <= 8; M * K <= 12288; K <= 6144;
+ * one weight type for all ops; an op that reads (as x, or as the old y of MT_ACCUM) a
+ * region an earlier op wrote must view it with that op's row stride and within its
+ * columns; a later write must cover an earlier write of the same region whole; an op
+ * may overwrite a region an earlier op read from its buffer only if every workgroup
+ * provably finished that earlier op (the later op consumes all of a full-width output
+ * in between).  Anything else returns MT_ENOTSUP.
+ * User buffers are read where nothing earlier in the sequence wrote them and are left
+ * holding the last value written to each region; intermediate values of a region that
+ * is written again later never reach the user buffer.  The plan keeps the pointers;
+ * the memory behind them may change between runs.  Runs of one plan must not overlap
+ * in time.
  */
 typedef struct mt_linear_op {
     const void *x;

@@ -154,9 +154,6 @@ int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
     if (!out) return set_error(MT_EINVAL, "mt_seq_create: null out");
     *out = nullptr;
     if (n_ops && !ops) return set_error(MT_EINVAL, "mt_seq_create: null ops");
-    std::vector<SeqOp> dev(n_ops);
-    int wt = -1, xt = -1;
-    uint32_t max_m = 1;
     for (uint32_t i = 0; i < n_ops; i++) {
         const mt_linear_op &o = ops[i];
         char who[48];
@@ -166,18 +163,24 @@ int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
         if (rc) return rc;
         if (o.p.M == 0 || o.p.N == 0) return set_error(MT_EINVAL, "%s: empty op", who);
         if (o.p.M > 8) return set_error(MT_EINVAL, "%s: a sequence takes M <= 8, got %u", who, o.p.M);
-        if (wt < 0) { wt = o.wt; xt = o.xt; }
-        if (o.wt != wt || o.xt != xt)
-            return set_error(MT_EINVAL, "%s: every op of a sequence must share the weight and activation types", who);
-        if (o.p.M > max_m) max_m = o.p.M;
-        SeqOp &d = dev[i];
-        d.x = a.x; d.w = a.w; d.w2 = a.w2; d.bias = a.bias; d.y = a.y; d.norm = a.norm;
-        d.M = a.M; d.N = a.N; d.K = a.K; d.ldx = a.ldx; d.ldy = a.ldy; d.flags = a.flags; d.eps = a.eps;
-        d.lanes_log2 = gemv_lanes_log2(a.K, g_tuning.gemv_lanes);
     }
-    const int mr = max_m <= 1 ? 1 : max_m <= 2 ? 2 : max_m <= 4 ? 4 : 8;
+    // Plan once with the expected workgroup count before touching the device, so a sequence
+    // the dataflow form cannot take is rejected without a GPU; re-plan if the device differs.
+    std::vector<SeqOp> dev;
+    int mr = 1, wt = DT_F16;
+    const int guess = g_tuning.seq_groups > 0 ? g_tuning.seq_groups : 256;
+    int rc = seq_plan(ops, n_ops, guess, dev, mr, wt);
+    if (rc) return rc;
+    if (n_ops == 0) return set_error(MT_EINVAL, "mt_seq_create: empty sequence");
+    int groups = 0;
+    rc = seq_limits(&groups);
+    if (rc) return rc;
+    if (groups != guess) {
+        rc = seq_plan(ops, n_ops, groups, dev, mr, wt);
+        if (rc) return rc;
+    }
     SeqPlan *plan = nullptr;
-    int rc = seq_create(dev.data(), n_ops, mr, wt < 0 ? DT_F16 : wt, xt < 0 ? DT_F32 : xt, &plan);
+    rc = seq_create(dev.data(), n_ops, mr, wt, groups, &plan);
     if (rc) return rc;
     *out = reinterpret_cast<mt_seq *>(plan);
     return MT_OK;

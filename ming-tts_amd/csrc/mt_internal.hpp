@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
+#include "mingtts_hip.h"
 #include "mt_device.hpp"
 
 namespace mt {
@@ -22,20 +25,42 @@ struct Tuning {
 };
 Tuning &tuning();
 
-// One op of a persistent linear sequence, as the kernel reads it.
+// One op of a persistent linear sequence, as the kernel reads it.  Activations produced
+// inside the sequence travel through the plan's tagged buffers (fp32 words whose lowest
+// mantissa bit carries the run's parity, one per output element); user buffers are read
+// only where nothing in the sequence wrote them before, and written only by the last op
+// that writes each region.
 struct SeqOp {
-    const void *x;
+    const void *x;          // external x (when xsrc < 0), element type xt
     const uint16_t *w;
     const uint16_t *w2;
     const uint16_t *bias;
-    float *y;
     const uint16_t *norm;
+    float *y;               // user output (written only when final != 0)
+    uint32_t *tag;          // this op's tagged output [M][N]
     uint32_t M, N, K, ldx, ldy, flags;
     float eps;
-    int32_t lanes_log2;
+    int32_t xsrc;           // op producing x, or -1
+    uint32_t xcol;          // column of x[.][0] in that op's output
+    int32_t ysrc;           // op producing y's old value (accumulate), or -1 (read y)
+    uint32_t ycol;
+    int32_t xt;             // element type of an external x
+    int32_t final_out;      // nonzero: this op's output is the last write of its region
+    int32_t pad;
 };
 struct SeqPlan;
-int seq_create(const SeqOp *ops, uint32_t n_ops, int mr, int wt, int xt, SeqPlan **out);
+// Limits of the persistent sequence kernel: threads per workgroup, 16-byte weight chunks a
+// lane holds across a wait, fp32 activations a workgroup stages in LDS.
+constexpr int SEQ_THREADS_N = 512;
+constexpr int SEQ_CHMAX = 12;      // 16-byte weight chunks per thread per op (held in registers)
+constexpr int SEQ_XLDS = 12288;    // staged activations per LDS buffer (two alternate): M * K
+constexpr int SEQ_PART = 9216;     // partial dot products per op per workgroup: M * chunks
+constexpr int SEQ_RMAX = 64;       // output features per workgroup per op
+// Workgroup count of the persistent kernel on the current device.
+int seq_limits(int *groups);
+// Dataflow plan of a serial op list for `groups` workgroups (host only; no HIP calls).
+int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &mr, int &wt);
+int seq_create(SeqOp *ops, uint32_t n_ops, int mr, int wt, int groups, SeqPlan **out);
 int seq_run(SeqPlan *p, hipStream_t stream);
 int seq_check(SeqPlan *p);
 void seq_destroy(SeqPlan *p);

@@ -1,0 +1,180 @@
+// Plan compiler of mt_seq_create: turns a list of linears (serial-encoder semantics, as
+// QwenForward.dispatches issues them, Qwen.swift:72-97) into the dataflow form the
+// persistent kernel runs.
+//
+// For every op it resolves
+//   - where x comes from: the tagged output of the latest earlier op that wrote x's region
+//     (with the column offset of x inside that output), or the user buffer if nothing
+//     earlier wrote it;
+//   - where the old y of an accumulate comes from, the same way;
+//   - whether the op is the last writer of its output region (only that op writes the
+//     user buffer);
+// and it checks the hazards the dataflow execution could reorder:
+//   - a region read at another layout than it was written (not representable) -> ENOTSUP;
+//   - a final write to a region an earlier op read from the user buffer, unless every
+//     workgroup has provably finished that earlier op (write-after-read) -> ENOTSUP.
+// Overlap between two views with the same row stride is decided element-exactly (column
+// slices of one buffer do not conflict); views with different strides are compared as
+// byte ranges (conservatively).
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "mingtts_hip.h"
+#include "mt_internal.hpp"
+
+namespace mt {
+
+namespace {
+
+struct View {
+    const char *base;
+    uint64_t ld;     // row stride, bytes
+    uint64_t width;  // bytes per row
+    uint64_t rows;
+    uint64_t begin() const { return reinterpret_cast<uint64_t>(base); }
+    uint64_t end() const { return begin() + (rows - 1) * ld + width; }
+};
+
+// Do the element sets of a and b intersect?
+bool overlap(const View &a, const View &b) {
+    if (a.end() <= b.begin() || b.end() <= a.begin()) return false;
+    if (a.ld != b.ld || a.width > a.ld || b.width > b.ld) return true;  // conservative
+    const View &lo = a.begin() <= b.begin() ? a : b;
+    const View &hi = a.begin() <= b.begin() ? b : a;
+    const uint64_t ld = a.ld, diff = hi.begin() - lo.begin();
+    const uint64_t q = diff / ld, col = diff % ld;
+    // hi's row r lies at lo's row r + q, columns [col, col + hi.width) (possibly wrapping
+    // into row r + q + 1 when col + hi.width > ld).
+    for (uint64_t r = 0; r < hi.rows; r++) {
+        const uint64_t lr = r + q;
+        if (lr < lo.rows && col < lo.width) return true;
+        if (col + hi.width > ld && lr + 1 < lo.rows && (col + hi.width - ld) > 0) return true;
+        if (lr >= lo.rows) break;
+    }
+    return false;
+}
+
+// If `in` (fp32 elements) sits inside `out` at one column offset with the same row stride
+// and no more rows, returns true and the column offset (elements).
+bool covered(const View &in, const View &out, uint32_t &col) {
+    if (in.ld != out.ld || in.begin() < out.begin()) return false;
+    const uint64_t d = in.begin() - out.begin();
+    if (d % 4 || d >= out.ld) return false;
+    if (d + in.width > out.width || in.rows > out.rows) return false;
+    col = static_cast<uint32_t>(d / 4);
+    return true;
+}
+
+}  // namespace
+
+int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &mr, int &wt) {
+    out.assign(n, SeqOp{});
+    std::vector<View> xv(n), yv(n);
+    std::vector<int> done_before(n, -1);
+    uint32_t max_m = 1;
+    wt = -1;
+    for (uint32_t i = 0; i < n; i++) {
+        const mt_linear_op &o = ops[i];
+        const mt_gemv_params &p = o.p;
+        SeqOp &d = out[i];
+        const size_t xs = o.xt == MT_F32 ? 4 : 2;
+        xv[i] = View{static_cast<const char *>(o.x), static_cast<uint64_t>(p.ldx) * xs, static_cast<uint64_t>(p.K) * xs, p.M};
+        yv[i] = View{reinterpret_cast<const char *>(o.y), static_cast<uint64_t>(p.ldy) * 4, static_cast<uint64_t>(p.N) * 4, p.M};
+        if (wt < 0) wt = o.wt;
+        if (o.wt != wt) return set_error(MT_EINVAL, "mt_seq_create: op %u: every op of a sequence must share the weight type", i);
+        if (p.M > max_m) max_m = p.M;
+        if (static_cast<uint64_t>(p.M) * p.K > static_cast<uint64_t>(SEQ_XLDS))
+            return set_error(MT_EINVAL, "mt_seq_create: op %u: M*K = %u exceeds the %d activations a workgroup stages",
+                             i, p.M * p.K, SEQ_XLDS);
+        // One workgroup's share of the op: ceil(N / G) features, each K / 8 chunks (twice
+        // with the gate partner); every chunk is one thread's, held in registers.
+        const uint64_t rows = (static_cast<uint64_t>(p.N) + groups - 1) / groups;
+        const uint64_t chunks = rows * (p.K / 8) * ((p.flags & MT_SILU_GATE) ? 2 : 1);
+        if (rows > static_cast<uint64_t>(SEQ_RMAX) || chunks > static_cast<uint64_t>(SEQ_CHMAX) * SEQ_THREADS_N ||
+            chunks * p.M > static_cast<uint64_t>(SEQ_PART))
+            return set_error(MT_ENOTSUP,
+                             "mt_seq_create: op %u: a workgroup's share (%llu features, %llu weight chunks at M = %u) "
+                             "exceeds the sequence kernel's limits (%d, %d, %d partials)",
+                             i, static_cast<unsigned long long>(rows), static_cast<unsigned long long>(chunks), p.M,
+                             SEQ_RMAX, SEQ_CHMAX * SEQ_THREADS_N, SEQ_PART);
+
+        // x: latest earlier writer.
+        d.xsrc = -1;
+        for (int j = static_cast<int>(i) - 1; j >= 0; j--) {
+            if (!overlap(xv[i], yv[j])) continue;
+            uint32_t col = 0;
+            if (o.xt != MT_F32 || !covered(xv[i], yv[j], col))
+                return set_error(MT_ENOTSUP, "mt_seq_create: op %u reads x from op %d's output at another layout", i, j);
+            d.xsrc = j;
+            d.xcol = col;
+            break;
+        }
+        // old y of an accumulate: latest earlier writer.
+        d.ysrc = -1;
+        if (p.flags & MT_ACCUM) {
+            for (int j = static_cast<int>(i) - 1; j >= 0; j--) {
+                if (!overlap(yv[i], yv[j])) continue;
+                uint32_t col = 0;
+                if (!covered(yv[i], yv[j], col))
+                    return set_error(MT_ENOTSUP, "mt_seq_create: op %u accumulates into op %d's output at another layout", i, j);
+                d.ysrc = j;
+                d.ycol = col;
+                break;
+            }
+        }
+        // every workgroup has finished op done_before[i] before op i computes
+        int db = -1;
+        if (d.xsrc >= 0) {
+            db = std::max(db, done_before[d.xsrc]);
+            const mt_linear_op &src = ops[d.xsrc];
+            // x spans all of the producer's features and each workgroup owns at least one
+            if (d.xcol == 0 && p.K == src.p.N && src.p.N >= static_cast<uint32_t>(groups)) db = std::max(db, d.xsrc);
+        }
+        if (d.ysrc >= 0) db = std::max(db, done_before[d.ysrc]);
+        done_before[i] = db;
+
+        d.x = o.x;
+        d.xt = o.xt;
+        d.ldx = p.ldx;
+        d.w = static_cast<const uint16_t *>(o.w);
+        d.w2 = static_cast<const uint16_t *>((p.flags & MT_SILU_GATE) ? o.w2 : o.w);
+        d.bias = static_cast<const uint16_t *>(o.bias);
+        d.norm = static_cast<const uint16_t *>(o.norm);
+        d.y = o.y;
+        d.ldy = p.ldy;
+        d.M = p.M;
+        d.N = p.N;
+        d.K = p.K;
+        d.flags = p.flags | (o.bias ? MT_BIAS : 0);
+        d.eps = p.eps;
+    }
+    // final writers and write-after-read
+    for (uint32_t i = 0; i < n; i++) {
+        out[i].final_out = 1;
+        for (uint32_t k = i + 1; k < n; k++) {
+            if (!overlap(yv[k], yv[i])) continue;
+            uint32_t col = 0;
+            if (!covered(yv[i], yv[k], col))
+                return set_error(MT_ENOTSUP, "mt_seq_create: op %u partly overwrites op %u's output", k, i);
+            out[i].final_out = 0;
+            break;
+        }
+        if (!out[i].final_out) continue;
+        for (uint32_t e = 0; e < i; e++) {
+            const bool reads_x = out[e].xsrc < 0 && overlap(xv[e], yv[i]);
+            const bool reads_y = (ops[e].p.flags & MT_ACCUM) && out[e].ysrc < 0 && e != i && overlap(yv[e], yv[i]);
+            if ((reads_x || reads_y) && static_cast<int>(e) > done_before[i])
+                return set_error(MT_ENOTSUP,
+                                 "mt_seq_create: op %u writes a region op %u read from the user buffer, and not every "
+                                 "workgroup is known to be past op %u",
+                                 i, e, e);
+        }
+    }
+    mr = max_m <= 1 ? 1 : max_m <= 2 ? 2 : max_m <= 4 ? 4 : 8;
+    return MT_OK;
+}
+
+}  // namespace mt

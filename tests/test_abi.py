@@ -100,10 +100,10 @@ def test_kernel_choice_and_tuning_round_trip():
 
 def test_seq_create_validates_every_op_before_the_device():
     import ctypes
-    def op(M=2, K=64, xt=mt.F32, norm=None, eps=0.0):
-        return mt.LinearOp(ALIGNED, W_ADDR, None, None, norm, Y_ADDR, mt.GemvParams(M, 64, K, 64, 64, 0, eps), xt, mt.F16)
+    def op(M=2, K=64, wt=mt.F16, norm=None, eps=0.0):
+        return mt.LinearOp(ALIGNED, W_ADDR, None, None, norm, Y_ADDR, mt.GemvParams(M, 64, K, 64, 64, 0, eps), mt.F32, wt)
 
-    ok, bad_m, bad_t, bad_k = op(), op(M=9), op(xt=mt.F16), op(K=60)
+    ok, bad_m, bad_t, bad_k = op(), op(M=9), op(wt=mt.BF16), op(K=60)
     bad_norm = op(norm=W_ADDR + 8)
     bad_eps = op(norm=W_ADDR, eps=-1.0)
     L = mt.load()
@@ -116,6 +116,31 @@ def test_seq_create_validates_every_op_before_the_device():
         assert needle in mt.last_error()
     assert L.mt_seq_create(None, 1, ctypes.byref(h)) == mt.EINVAL
     assert L.mt_seq_run(None, None) == mt.EINVAL
+
+
+def test_seq_plan_refuses_what_dataflow_cannot_order():
+    """The plan compiler runs before any device call: layouts it cannot map and hazards it
+    cannot prove ordered are refused with MT_ENOTSUP."""
+    import ctypes
+    L = mt.load()
+    h = ctypes.c_void_p()
+    A, B, C, D = 1 << 20, 2 << 20, 3 << 20, 4 << 20
+    W = 8 << 20
+
+    def op(x, y, ldx=64, ldy=64, K=64, N=64, M=2, flags=0):
+        return mt.LinearOp(x, W, None, None, None, y, mt.GemvParams(M, N, K, ldx, ldy, flags, 0.0), mt.F32, mt.F16)
+
+    cases = [
+        ([op(A, B), op(B, C, ldx=32, K=32)], "another layout"),                 # B read at stride 32, written at 64
+        ([op(A, B, ldy=128), op(C, B + 128, ldy=128)], "partly overwrites"),    # columns 32..95 over 0..63
+        ([op(A, B), op(D, A)], "read from the user buffer"),                    # A overwritten, no dependency
+        ([op(A, B), op(B, C), op(B, C, flags=mt.GemvFlags.accumulate, ldy=32, N=32)],
+         "accumulates into op 1's output at another layout"),
+    ]
+    for ops, needle in cases:
+        arr = (mt.LinearOp * len(ops))(*ops)
+        assert L.mt_seq_create(arr, len(ops), ctypes.byref(h)) == mt.ENOTSUP, needle
+        assert needle in mt.last_error(), mt.last_error()
 
 
 def test_rope_and_attention_reject_bad_arguments():
