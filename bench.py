@@ -32,6 +32,23 @@ H, QKV, INTER, LAYERS = 896, 1152, 4864, 24
 METRIC = "decode-step linear µs + achieved HBM GB/s (% of 8 TB/s); prefill MFMA TFLOPS"
 
 
+PROFILE = os.path.join(ROOT, "profiles", "seq_kernel_decode_24L_M2.md")
+
+
+def measured_traffic(path: str = PROFILE):
+    """HBM bytes per launch of the decode kernel from its committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled against a 1 GiB copy): the line
+    ``traffic_per_launch_bytes: N``.  None when the summary is absent."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_per_launch_bytes:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -106,24 +123,27 @@ def op_flops(o) -> int:
 
 
 def bench_decode_seq(torch, mt, dev, ws, steps, warmup, M=2):
+    """Each step resets the residual (a device copy outside the timed bracket), then runs the
+    sequence between two HIP events on the launch stream.  All steps are queued without host
+    synchronisation, so each bracket holds the kernel and its dispatch only."""
     resid = torch.randn(M, H, device=dev)
     qkv = torch.zeros(M, QKV, device=dev)
     mlp = torch.zeros(M, INTER, device=dev)
     x0 = resid.clone()
     ops = decode_ops(mt, ws, M, resid, qkv, mlp)
     seq = mt.Seq(ops)
-    ev = Events(torch)
     for _ in range(warmup):
         resid.copy_(x0)
         seq.run()
     torch.cuda.synchronize()
-    # Each step starts from the same residual (a device copy, outside the timed launches).
-    times = []
-    for _ in range(steps):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in ev:
         resid.copy_(x0)
-        ev.start()
+        a.record()
         seq.run()
-        times.append(ev.stop_ms())
+        b.record()
+    torch.cuda.synchronize()
+    times = [a.elapsed_time(b) for a, b in ev]
     seq.check()
     nbytes = sum(op_bytes(o) for o in ops)
     flops = sum(op_flops(o) for o in ops)
@@ -294,6 +314,21 @@ def bench_dit(torch, mt, dev, reps=3):
     return dict(us_10_steps=best * 1e3, tflops=flops / (best * 1e-3) / 1e12, launches=len(ops))
 
 
+def bench_copy(torch, dev, mib=1024, reps=5):
+    """A plain device-to-device copy of a known size: the calibration run for the HBM byte
+    counters (FETCH_SIZE / WRITE_SIZE per dispatch against exactly mib MiB each way)."""
+    a = torch.empty(mib << 18, device=dev, dtype=torch.float32).fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    ev.start()
+    for _ in range(reps):
+        b.copy_(a)
+    ms = ev.stop_ms()
+    return dict(copy_mib=mib, reps=reps, us_per_copy=round(ms * 1e3 / reps, 2),
+                gbs_read_plus_write=round(2 * (mib << 20) * reps / (ms * 1e-3) / 1e9, 1))
+
+
 def cpu_baseline(torch, ws, target_s=10.0, M=2):
     """The oracle's vectorised restatement of the reference CPU loop (KernelTests.swift:86-101,
     K sum split 16 ways, OpenMP over output rows) on the host cores, over the first layers of
@@ -331,7 +366,7 @@ def cpu_baseline(torch, ws, target_s=10.0, M=2):
         step()
         n += 1
         dt = time.perf_counter() - t0
-        if dt >= target_s or n >= 10000:
+        if dt >= target_s or n >= 200000:
             break
     per_layer = (shape_bytes(M, QKV, H, 1) + shape_bytes(M, H, H, 2) + shape_bytes(M, INTER, H, 8)
                  + shape_bytes(M, H, INTER, 2))
@@ -348,11 +383,15 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "all"], default="all")
+    ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
+                    help="launch of the persistent decode kernel: cooperative (default) or ordinary "
+                         "(for profilers that cannot follow a cooperative launch)")
+    ap.add_argument("--only", choices=["decode", "all", "copy"], default="all",
+                    help="copy: only the 1 GiB device copy that calibrates the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the linear hot path "
-              "would shard by output features, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (the linear hot path would "
+              "shard by output features across GPUs); run with --gpus 1", file=sys.stderr)
         return 2
     ensure_built()
     import torch
@@ -360,11 +399,16 @@ def main() -> int:
     mt.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.only == "copy":
+        print(json.dumps(bench_copy(torch, dev)), flush=True)
+        return 0
     log("generating 24 layers of fp16 weights")
     ws = make_layers(torch, dev)
     torch.cuda.synchronize()
 
-    log(f"decode step (persistent sequence): {args.warmup} warmup + {args.steps} timed")
+    if args.seq_launch == "plain":
+        mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 1)
+    log(f"decode step (persistent sequence, {args.seq_launch} launch): {args.warmup} warmup + {args.steps} timed")
     d = bench_decode_seq(torch, mt, dev, ws, args.steps, args.warmup)
     t = sorted(d["times_ms"])
     mean_ms = sum(t) / len(t)
@@ -397,9 +441,11 @@ def main() -> int:
         "hbm_pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "algorithmic_bytes_per_step": d["bytes"],
         "seq_workgroups": d["groups"],
+        "seq_launch": args.seq_launch,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "seq_kernel<2, f16, f32> (one launch per decode step)"},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/seq_kernel_decode_24L_M2.md",
+                     "kernel": "mt::seq_kernel<1> (fp16 weights; one launch per decode step)"},
     }
     if args.only == "all":
         log("decode step as 96 separate launches")

@@ -43,6 +43,7 @@ typedef struct ihipStream_t *mt_stream_t;
 #define MT_EHIP (-5)       /* a HIP runtime error; the text is in mt_last_error() */
 #define MT_ENOMEM (-12)
 #define MT_EINVAL (-22)    /* a shape, alignment, dtype or pointer the kernels cannot take */
+#define MT_ERANGE (-34)     /* mt_seq_check: a run met an activation outside the fp16 range */
 #define MT_ENOTSUP (-95)
 
 /* GemvParams, Shaders.swift:39.  y[m, n] = sum_k x[m, k] w[n, k] (+ epilogue).
@@ -107,7 +108,9 @@ enum {
     MT_TUNE_GEMV_ROWS_MAX = 1,   /* M up to this goes to the GEMV family (default 8) */
     MT_TUNE_GEMV_LANES = 2,      /* lanes per output feature in the GEMV, 8..64 (0 = auto) */
     MT_TUNE_GEMM_SPLITK = 3,     /* K splits of the MFMA GEMM (0 = auto) */
-    MT_TUNE_SEQ_GROUPS = 4       /* workgroups of the persistent sequence kernel (0 = auto) */
+    MT_TUNE_SEQ_GROUPS = 4,      /* workgroups of the persistent sequence kernel (0 = auto) */
+    MT_TUNE_SEQ_LAUNCH = 5       /* 0: cooperative launch (default); 1: ordinary launch, co-residency
+                                    then rests on an otherwise idle device (profilers) */
 };
 int mt_set_tuning(int key, int value);
 
@@ -117,9 +120,14 @@ int mt_set_tuning(int key, int value);
  * (Qwen.swift:72-97).  mt_seq_create validates every op, compiles the list into a
  * dataflow plan and uploads it once; mt_seq_run runs the whole sequence as ONE
  * persistent cooperative kernel launch in which ops hand activations to each other
- * through plan-owned tagged buffers (no device-wide barriers).
- * Requirements, beyond mt_linear's for every op: 1 <= M <= 8; M * K <= 12288; K <= 6144;
- * one weight type for all ops; an op that reads (as x, or as the old y of MT_ACCUM) a
+ * through plan-owned tagged buffers (no device-wide barriers).  Dot products run on
+ * 16x16x32 MFMA with every fp32 activation split into a hi + lo pair of the weights'
+ * 16-bit type; with fp16 weights an activation (times its RMSNorm gain) must stay within
+ * the fp16 range, |x| <= 65504, or mt_seq_check reports MT_ERANGE for that run.
+ * Requirements, beyond mt_linear's for every op: 1 <= M <= 8; one weight type for all
+ * ops; a workgroup's share of an op (ceil(N / workgroups) features, twice with the gate
+ * partner) at most 64 features and at most 12 MFMA tiles of 16 x 32 weights per wave
+ * (every linear of a Qwen2-0.5B decode layer fits at one workgroup per CU on 256 CUs); an op that reads (as x, or as the old y of MT_ACCUM) a
  * region an earlier op wrote must view it with that op's row stride and within its
  * columns; a later write must cover an earlier write of the same region whole; an op
  * may overwrite a region an earlier op read from its buffer only if every workgroup
@@ -149,9 +157,10 @@ int mt_seq_run(mt_seq *seq, mt_stream_t stream);
 int mt_seq_destroy(mt_seq *seq);
 /* Workgroups the plan's kernel runs with (after mt_seq_create). */
 int mt_seq_groups(const mt_seq *seq);
-/* Synchronous health check of a plan after its runs completed: MT_EHIP if any device-wide
- * barrier of a run gave up after its spin bound (co-residency was lost), else MT_OK.
- * No counterpart in the reference (Metal has no in-kernel grid barrier). */
+/* Synchronous health check of a plan after its runs completed: MT_EHIP if a dataflow wait
+ * of a run gave up after its spin bound (co-residency was lost), MT_ERANGE if an fp16-weight
+ * run met an activation beyond the fp16 range, else MT_OK.  Both flags stay set for the
+ * plan's life.  No counterpart in the reference (Metal has no in-kernel grid waits). */
 int mt_seq_check(mt_seq *seq);
 
 /*

@@ -118,8 +118,11 @@ int mt_set_tuning(int key, int value) {
         case MT_TUNE_GEMV_LANES: slot = &g_tuning.gemv_lanes; def = 0; break;
         case MT_TUNE_GEMM_SPLITK: slot = &g_tuning.gemm_splitk; def = 0; break;
         case MT_TUNE_SEQ_GROUPS: slot = &g_tuning.seq_groups; def = 0; break;
+        case MT_TUNE_SEQ_LAUNCH: slot = &g_tuning.seq_launch; def = 0; break;
         default: return set_error(MT_EINVAL, "mt_set_tuning: unknown key %d", key);
     }
+    if (key == MT_TUNE_SEQ_LAUNCH && value > 1)
+        return set_error(MT_EINVAL, "mt_set_tuning: the sequence launch mode is 0 or 1, got %d", value);
     if (key == MT_TUNE_GEMV_ROWS_MAX && value > 8)
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMV takes at most 8 rows per block, got %d", value);
     const int old = *slot;
@@ -167,20 +170,20 @@ int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
     // Plan once with the expected workgroup count before touching the device, so a sequence
     // the dataflow form cannot take is rejected without a GPU; re-plan if the device differs.
     std::vector<SeqOp> dev;
-    int mr = 1, wt = DT_F16;
+    int wt = DT_F16;
     const int guess = g_tuning.seq_groups > 0 ? g_tuning.seq_groups : 256;
-    int rc = seq_plan(ops, n_ops, guess, dev, mr, wt);
+    int rc = seq_plan(ops, n_ops, guess, dev, wt);
     if (rc) return rc;
     if (n_ops == 0) return set_error(MT_EINVAL, "mt_seq_create: empty sequence");
     int groups = 0;
     rc = seq_limits(&groups);
     if (rc) return rc;
     if (groups != guess) {
-        rc = seq_plan(ops, n_ops, groups, dev, mr, wt);
+        rc = seq_plan(ops, n_ops, groups, dev, wt);
         if (rc) return rc;
     }
     SeqPlan *plan = nullptr;
-    rc = seq_create(dev.data(), n_ops, mr, wt, groups, &plan);
+    rc = seq_create(dev.data(), n_ops, wt, groups, &plan);
     if (rc) return rc;
     *out = reinterpret_cast<mt_seq *>(plan);
     return MT_OK;

@@ -22,6 +22,7 @@ struct Tuning {
     int gemv_lanes = 0;
     int gemm_splitk = 0;
     int seq_groups = 0;
+    int seq_launch = 0;
 };
 Tuning &tuning();
 
@@ -46,21 +47,26 @@ struct SeqOp {
     uint32_t ycol;
     int32_t xt;             // element type of an external x
     int32_t final_out;      // nonzero: this op's output is the last write of its region
+    uint32_t xoff, xld;     // tagged x: word offset of x[0][0] in the plan's tag buffer, row stride
+    uint32_t yoff, yld;     // tagged old y: the same
     int32_t pad;
 };
 struct SeqPlan;
-// Limits of the persistent sequence kernel: threads per workgroup, 16-byte weight chunks a
-// lane holds across a wait, fp32 activations a workgroup stages in LDS.
+// Limits of the persistent sequence kernel: threads per workgroup, MFMA tiles per wave per
+// op (each lane holds one 16-byte weight chunk and one 8-activation chunk per tile across
+// the op's wait), output features per workgroup per op, LDS partial sums per wave per op.
 constexpr int SEQ_THREADS_N = 512;
-constexpr int SEQ_CHMAX = 12;      // 16-byte weight chunks per thread per op (held in registers)
-constexpr int SEQ_XLDS = 12288;    // staged activations per LDS buffer (two alternate): M * K
-constexpr int SEQ_PART = 9216;     // partial dot products per op per workgroup: M * chunks
-constexpr int SEQ_RMAX = 64;       // output features per workgroup per op
+constexpr int SEQ_TMAX = 12;
+constexpr int SEQ_RMAX = 64;
+constexpr int SEQ_PARTW = 512;     // partial sums per wave per op: virtual rows * M * segments
+constexpr int SEQ_XCH = 8;         // 16-byte activation chunks per lane per op
+constexpr int SEQ_XW = 64;         // tiles x padded B columns staged per wave per op
+constexpr int SEQ_GMAX = 8192;     // K of an op with an RMSNorm gain (staged in LDS)
 // Workgroup count of the persistent kernel on the current device.
 int seq_limits(int *groups);
 // Dataflow plan of a serial op list for `groups` workgroups (host only; no HIP calls).
-int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &mr, int &wt);
-int seq_create(SeqOp *ops, uint32_t n_ops, int mr, int wt, int groups, SeqPlan **out);
+int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt);
+int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out);
 int seq_run(SeqPlan *p, hipStream_t stream);
 int seq_check(SeqPlan *p);
 void seq_destroy(SeqPlan *p);

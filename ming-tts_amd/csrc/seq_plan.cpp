@@ -24,6 +24,7 @@
 
 #include "mingtts_hip.h"
 #include "mt_internal.hpp"
+#include "seq_tiles.hpp"
 
 namespace mt {
 
@@ -70,11 +71,10 @@ bool covered(const View &in, const View &out, uint32_t &col) {
 
 }  // namespace
 
-int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &mr, int &wt) {
+int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt) {
     out.assign(n, SeqOp{});
     std::vector<View> xv(n), yv(n);
     std::vector<int> done_before(n, -1);
-    uint32_t max_m = 1;
     wt = -1;
     for (uint32_t i = 0; i < n; i++) {
         const mt_linear_op &o = ops[i];
@@ -85,21 +85,24 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
         yv[i] = View{reinterpret_cast<const char *>(o.y), static_cast<uint64_t>(p.ldy) * 4, static_cast<uint64_t>(p.N) * 4, p.M};
         if (wt < 0) wt = o.wt;
         if (o.wt != wt) return set_error(MT_EINVAL, "mt_seq_create: op %u: every op of a sequence must share the weight type", i);
-        if (p.M > max_m) max_m = p.M;
-        if (static_cast<uint64_t>(p.M) * p.K > static_cast<uint64_t>(SEQ_XLDS))
-            return set_error(MT_EINVAL, "mt_seq_create: op %u: M*K = %u exceeds the %d activations a workgroup stages",
-                             i, p.M * p.K, SEQ_XLDS);
-        // One workgroup's share of the op: ceil(N / G) features, each K / 8 chunks (twice
-        // with the gate partner); every chunk is one thread's, held in registers.
-        const uint64_t rows = (static_cast<uint64_t>(p.N) + groups - 1) / groups;
-        const uint64_t chunks = rows * (p.K / 8) * ((p.flags & MT_SILU_GATE) ? 2 : 1);
-        if (rows > static_cast<uint64_t>(SEQ_RMAX) || chunks > static_cast<uint64_t>(SEQ_CHMAX) * SEQ_THREADS_N ||
-            chunks * p.M > static_cast<uint64_t>(SEQ_PART))
-            return set_error(MT_ENOTSUP,
-                             "mt_seq_create: op %u: a workgroup's share (%llu features, %llu weight chunks at M = %u) "
-                             "exceeds the sequence kernel's limits (%d, %d, %d partials)",
-                             i, static_cast<unsigned long long>(rows), static_cast<unsigned long long>(chunks), p.M,
-                             SEQ_RMAX, SEQ_CHMAX * SEQ_THREADS_N, SEQ_PART);
+        if (o.norm && p.K > static_cast<uint32_t>(SEQ_GMAX))
+            return set_error(MT_ENOTSUP, "mt_seq_create: op %u: an RMSNorm op takes K <= %d, got %u", i, SEQ_GMAX, p.K);
+        // Every workgroup's share of the op, tiled as the kernel tiles it: at most RMAX
+        // features, at most TMAX tiles per wave (each held in registers across the wait).
+        const int nw = SEQ_THREADS_N / 64;
+        for (int g = 0; g < groups; g++) {
+            const SeqTiles t = seq_tiles(p.N, p.K, p.M, (p.flags & MT_SILU_GATE) != 0, g, groups);
+            const uint32_t per_wave = (t.T + nw - 1) / nw;
+            uint32_t smp = 1;
+            while (smp < t.S * p.M) smp <<= 1;
+            if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || per_wave > static_cast<uint32_t>(SEQ_TMAX) ||
+                t.V * p.M * t.S > static_cast<uint32_t>(SEQ_PARTW) || per_wave * smp > static_cast<uint32_t>(SEQ_XW))
+                return set_error(MT_ENOTSUP,
+                                 "mt_seq_create: op %u: a workgroup's share (%u features, %u MFMA tiles per wave of "
+                                 "%u activation columns at M = %u) exceeds the sequence kernel's limits (%d features, "
+                                 "%d tiles, %d tile columns, %d partial sums)",
+                                 i, t.nr, per_wave, smp, p.M, SEQ_RMAX, SEQ_TMAX, SEQ_XW, SEQ_PARTW);
+        }
 
         // x: latest earlier writer.
         d.xsrc = -1;
@@ -173,7 +176,6 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
                                  i, e, e);
         }
     }
-    mr = max_m <= 1 ? 1 : max_m <= 2 ? 2 : max_m <= 4 ? 4 : 8;
     return MT_OK;
 }
 

@@ -20,9 +20,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "csrc", "libmingtts_hip.so"))
 
 F32, F16, BF16 = 0, 1, 2
-OK, EHIP, ENOMEM, EINVAL, ENOTSUP = 0, -5, -12, -22, -95
+OK, EHIP, ENOMEM, EINVAL, ERANGE, ENOTSUP = 0, -5, -12, -22, -34, -95
 KERNEL_GEMV, KERNEL_GEMM = 1, 2
-TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS = 1, 2, 3, 4
+TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS, TUNE_SEQ_LAUNCH = 1, 2, 3, 4, 5
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
