@@ -5,9 +5,7 @@
 // Reference counterpart: QwenForward.dispatches encoded on one serial compute encoder
 // (Qwen.swift:72-97); every dispatch sees the writes of the ones before it.
 //
-// Why dataflow: on MI355X a device-wide barrier among 256 resident workgroups costs
-// 2.5-4 us (a counter) and agent-scope fences (L2 write-back + invalidate on every XCD)
-// cost more still, against 0.2-2.9 us of weight streaming per decode linear.  So:
+// Dataflow between workgroups:
 //   - every op writes its outputs to a plan-owned tagged buffer: one fp32 word per
 //     element whose lowest mantissa bit is replaced by the run's parity (epoch & 1),
 //     stored device-coherently.  A consumer that reads a word with the current parity has
@@ -19,27 +17,29 @@
 //   - user buffers: an op reads a user buffer only where nothing earlier in the sequence
 //     wrote it, and writes a user buffer only if it is the last op writing that region
 //     (the host plan compiler resolves both), so every user element is written once per run.
-// Work of one op in a workgroup (the tiling is in seq_tiles.hpp): its share of the weight
-// rows is cut into v_mfma_f32_16x16x32 tiles, each wave owning a contiguous range of
-// tiles.  Per op a wave
-//   1. has the op's weight chunks (the MFMA A operands) in registers already, requested
-//      during the previous op;
-//   2. requests the activations its tiles need (the B operands: SM = S * M columns of 32 k
-//      per tile) straight from the producer's tagged buffer, spread over all 64 lanes in
-//      16-byte chunks, and re-polls only the chunks whose tags are stale;
-//   3. per chunk: clears the tag bits, adds x^2 to the RMSNorm sum, multiplies by the
-//      gain (staged in LDS one op ahead), splits each fp32 value into a hi + lo pair of the
-//      weights' 16-bit type (fp32-grade inputs on the 16-bit MFMA) and writes both to the
-//      wave's LDS staging area in the B-fragment layout;
-//   4. runs two MFMAs per tile (hi and lo), writing a finished row tile's partial sums to
-//      LDS, requests the next op's weight chunks, and meets the other waves at one LDS-only
-//      barrier (global loads stay in flight across it);
-// then one lane per output sums the waves' partials in a fixed order, applies the norm
-// scale and the epilogue and stores the tagged word (and the user output when final).
-// Partials alternate between two LDS buffers by op parity, so one barrier per op suffices.
-// Every wait is bounded: past SPIN_LIMIT polls a lane gives up, sets the plan's timeout
-// flag (read by mt_seq_check) and stops waiting for the rest of the run.  An fp16 weight
-// sequence also flags activations beyond the fp16 range (the hi part would overflow).
+// Inside a workgroup (512 threads, one per CU) the waves split by role, because a wave's
+// vector loads retire in order: a wave that waits for activations must not have weight
+// loads queued in front of them.
+//   - LW loader waves walk the ops ahead of the computation and stream the workgroup's
+//     weight tiles (the MFMA A operands: 16 rows x 32 k, one 16-byte chunk per lane, as
+//     seq_tiles.hpp cuts them) straight into an LDS ring with global_load_lds_dwordx4.
+//     An empty slot holds all-ones bytes (fp16 / bf16 NaN pairs, never a weight chunk): a
+//     compute wave knows its tile has landed when its lane's 16 bytes are no longer all
+//     ones, and refills the slot with all ones once it has read it.  A slot is reused once
+//     every compute wave has moved past the tile in it (per-wave LDS watermarks).
+//   - CW compute waves each own a contiguous range of an op's tiles.  Per op a compute
+//     wave polls the activation chunks its tiles need (16-byte device-coherent loads of
+//     tagged words, re-requesting only stale ones), converts each element once (tag
+//     clear, x^2 for the RMSNorm sum, gain, fp32 -> hi + lo pair of the weights' 16-bit
+//     type) into its LDS B staging, then runs two MFMAs per tile with A from the ring,
+//     writing finished row tiles' partial sums to LDS.  The compute waves meet at an LDS
+//     counter; one lane per output sums the partials in a fixed order, applies the norm
+//     scale and the epilogue and stores the tagged word (and the user output when final).
+// LDS partial sums, sums of squares and gains alternate between two buffers by op parity,
+// so one compute-wave meeting per op suffices.  Every wait is bounded: past SPIN_LIMIT
+// polls a lane gives up, sets the plan's timeout flag (read by mt_seq_check) and stops
+// waiting for the rest of the run.  An fp16 weight sequence also flags activations beyond
+// the fp16 range (the hi part would overflow).
 #include <stdlib.h>
 #include <string.h>
 
@@ -53,11 +53,8 @@ namespace mt {
 enum : int { SYNC_EPOCH = 0, SYNC_EXIT = 32, SYNC_TIMEOUT = 64, SYNC_RANGE = 80, SYNC_WORDS = 96 };
 constexpr int SEQ_THREADS = SEQ_THREADS_N;
 constexpr int NW = SEQ_THREADS / 64;
-constexpr int TMAX = SEQ_TMAX;
 constexpr int PARTW = SEQ_PARTW;
-constexpr int XCH = SEQ_XCH;
-constexpr int XW = SEQ_XW;
-constexpr int GCH = SEQ_GMAX / 8 / SEQ_THREADS;
+constexpr int XCH = (SEQ_XLDS / 4 + SEQ_CW * 64 - 1) / (SEQ_CW * 64);  // 16-byte x chunks per compute lane
 constexpr uint32_t SPIN_LIMIT = 1u << 20;
 constexpr uint32_t BUF_DWORD3 = 0x00020000u;  // raw 32-bit buffer resource word 3 for gfx9
 constexpr int SC1 = 16;                         // buffer cache policy: device-coherent
@@ -70,6 +67,17 @@ typedef __attribute__((address_space(1))) const uint32_t *g32_cp;
 typedef __attribute__((address_space(1))) uint32_t *g32_p;
 typedef __attribute__((address_space(1))) const u32x4 *gw_cp;
 
+// Plain loads through global-address-space pointers (global_load, counted on vmcnt alone;
+// a generic pointer would make a flat load that also occupies lgkmcnt).
+template <class T>
+__device__ __forceinline__ T gld(const T *p) {
+    return *reinterpret_cast<const __attribute__((address_space(1))) T *>(reinterpret_cast<uintptr_t>(p));
+}
+// One tagged word at byte offset off of the plan's tag buffer, device-coherently (a plain
+// load: no ordering against the loads in flight before it).
+__device__ __forceinline__ uint32_t ldtag1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, SC1);
+}
 __device__ __forceinline__ uint32_t ld32(const uint32_t *p) {
     return __hip_atomic_load((g32_cp)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -107,107 +115,212 @@ __device__ __forceinline__ uint32_t round16(float x) {
     if constexpr (T == DT_BF16) return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
     else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
-// x = hi + lo in type T, packed in pairs.
+
+constexpr int CW = SEQ_CW;             // compute waves
+constexpr int LW = NW - CW;            // loader waves
+constexpr int RING = SEQ_RING;         // weight tile slots of 1 KB
+constexpr int CTHREADS = CW * 64;
+constexpr int TA = SEQ_TA;              // weight tiles a compute wave holds per op
+constexpr int CGCH = SEQ_GMAX / 8 / CTHREADS + ((SEQ_GMAX / 8) % CTHREADS ? 1 : 0);
+constexpr int OUTR = (SEQ_RMAX * 8 + CTHREADS - 1) / CTHREADS;  // outputs per compute thread
+enum : int { CTL_CONSUMED = 0, CTL_CBAR = 8, CTL_WORDS = 16 };
+static_assert(LW >= 1 && LW <= 4 && CW <= 8, "wave roles");
+
+typedef __attribute__((address_space(3))) void *lds_vp;
+
+// x = hi + lo in type T, packed in pairs; both parts rounded toward zero (fp16) or to
+// nearest (bf16) with one packed conversion per pair.
 template <int T>
-__device__ __forceinline__ void split4(const float (&x)[4], u32x2 &hi, u32x2 &lo) {
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        h[e] = round16<T>(x[e]);
-        l[e] = round16<T>(x[e] - dec1<T>(static_cast<uint16_t>(h[e])));
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (T == DT_BF16) {
+        typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, bf2));
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
     }
-    hi = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    lo = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+}
+template <int T>
+__device__ __forceinline__ void split4p(const float (&x)[4], u32x2 &hi, u32x2 &lo) {
+    const uint32_t h0 = pack2<T>(x[0], x[1]), h1 = pack2<T>(x[2], x[3]);
+    hi = u32x2{h0, h1};
+    lo = u32x2{pack2<T>(x[0] - dec_lo<T>(h0), x[1] - dec_hi<T>(h0)), pack2<T>(x[2] - dec_lo<T>(h1), x[3] - dec_hi<T>(h1))};
 }
 
-// The tiles of op o owned by wave w of workgroup g.
+// A compute wave's tiles of op o.
 struct WaveTiles {
     SeqTiles s;
     uint32_t t0, n;    // first tile, tile count
     uint32_t rt0, j0;  // row tile and block step of t0
 };
-__device__ __forceinline__ WaveTiles wave_tiles(const SeqOp &o, uint32_t g, uint32_t G, uint32_t w) {
+__device__ __forceinline__ WaveTiles wave_tiles(const SeqTiles &st, uint32_t w) {
     WaveTiles wt;
-    wt.s = seq_tiles(o.N, o.K, o.M, (o.flags & F_SILU_GATE) != 0, g, G);
-    wt.t0 = seq_tile_begin(wt.s.T, w, NW);
-    wt.n = seq_tile_begin(wt.s.T, w + 1, NW) - wt.t0;
+    wt.s = st;
+    wt.t0 = seq_tile_begin(wt.s.T, w, CW);
+    wt.n = seq_tile_begin(wt.s.T, w + 1, CW) - wt.t0;
     wt.rt0 = wt.s.KBs ? wt.t0 / wt.s.KBs : 0;
     wt.j0 = wt.t0 - wt.rt0 * wt.s.KBs;
     return wt;
 }
 
-// This lane's A chunk of every tile of the wave into wr[u] (zero outside the share):
-// A row a = lane % 16 (virtual row, or segment x virtual row when packed), k group
-// q = lane / 16 (8 k at 32-k block offset 8 q).
-__device__ __forceinline__ void load_w(const SeqOp &o, const WaveTiles &wt, u32x4 (&wr)[TMAX]) {
-    const SeqTiles &s = wt.s;
-    // Both row bases up front (uniform): the per-lane choice is then a register select.
-    const uint16_t *const w1 = o.w, *const w2 = o.w2;
+// A ring slot read that the compiler neither caches nor moves.
+__device__ __forceinline__ u32x4 ring_ld(const u32x4 *p) {
+    typedef __attribute__((address_space(3))) const volatile u32x4 *lds_cvp;
+    return *reinterpret_cast<lds_cvp>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_vp)(p))));
+}
+// 1 when a lane's chunk is still the empty-slot pattern.
+__device__ __forceinline__ uint32_t unsent(const u32x4 a) { return (a.x & a.y & a.z & a.w) == ~0u ? 1u : 0u; }
+
+// LDS word access that the compiler neither reorders nor caches.
+__device__ __forceinline__ uint32_t lds_ld(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_st(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// One weight tile into LDS at byte address slot: lane l's 16 bytes from gaddr land at
+// slot + 16 l (nontemporal: the stream does not displace L2 lines).  Issued as inline
+// assembly so that the compiler's wait-count analysis does not see an LDS write in flight
+// (it would drain the loads before every LDS access); readiness is the slot's content.
+__device__ __forceinline__ void dma_tile(uint32_t slot, const void *gaddr) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(slot), "v"(gaddr) : "memory", "m0");
+}
+
+// Loader wave l: every tile of every op whose sequence number is l mod LW, in order.
+__device__ void loader(const SeqOp *desc, const SeqTiles *tiles, uint32_t n_ops, uint32_t l, uint32_t ring_base,
+                       uint32_t *ctl, uint32_t *sync) {
     const uint32_t lane = threadIdx.x & 63, a = lane & 15, q = lane >> 4;
-    const uint32_t sa = s.S > 1 ? a / s.V : 0;
-    const uint32_t va = s.S > 1 ? a - sa * s.V : a;
-    uint32_t rt = wt.rt0, j = wt.j0;
+    uint32_t seq_base = 0;   // sequence number of the op's tile 0
+    uint32_t freed = 0;      // every compute wave is past tile freed - 1 (last read)
+    bool stop = false;
+    for (uint32_t i = 0; i < n_ops && !stop; i++) {
+        const SeqOp o = desc[i];  // by value: read once, kept in registers
+        const SeqTiles s = tiles[i];
+        const uint16_t *const w1 = o.w, *const w2 = o.w2;
+        const uint32_t K = o.K;
+        // Per lane: segment and virtual row of the lane's A row (interleaved when packed).
+        const uint32_t sa = a & (s.S - 1);
+        const uint32_t va = a >> s.ls;
+        const uint32_t kbase = sa * s.KBs * 32 + q * 8;  // k of the lane's chunk at block step 0
+        uint32_t t = (l + LW - seq_base % LW) % LW;  // first tile of this op that is ours
+        uint32_t rt = s.KBs ? t / s.KBs : 0, j = t - rt * s.KBs;
+        uint32_t row_rt = ~0u;
+        const uint16_t *row = w1;
+        bool row_ok = false;
+        for (; t < s.T; t += LW) {
+            const uint32_t seq = seq_base + t;
+            // The slot is free once every compute wave has moved past the tile RING back.
+            if (seq >= static_cast<uint32_t>(RING) && freed <= seq - RING) {
+                uint32_t spins = 0;
+                for (;;) {
+                    uint32_t mn = lds_ld(ctl + CTL_CONSUMED);
 #pragma unroll
-    for (int u = 0; u < TMAX; u++) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (static_cast<uint32_t>(u) < wt.n) {
-            const uint32_t vrow = s.S > 1 ? va : rt * 16 + a;
-            const uint32_t kb = sa * s.KBs + j, k0 = kb * 32 + q * 8;
-            if (sa < s.S && vrow < s.V && kb < s.KB && k0 < o.K) {
-                const bool up = vrow >= s.nr;
-                const uint16_t *row = (up ? w2 : w1) + static_cast<size_t>(s.r0 + (up ? vrow - s.nr : vrow)) * o.K;
-                v = __builtin_nontemporal_load((gw_cp)(row + k0));
+                    for (int w = 1; w < CW; w++) mn = min(mn, lds_ld(ctl + CTL_CONSUMED + w));
+                    freed = mn;
+                    if (mn > seq - RING) break;
+                    if (++spins > SPIN_LIMIT) {
+                        raise_flag(sync, SYNC_TIMEOUT);
+                        stop = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                if (stop) break;
             }
-            if (++j == s.KBs) {
-                j = 0;
+            if (rt != row_rt) {  // the lane's weight row for this row tile
+                row_rt = rt;
+                const uint32_t vrow = s.S > 1 ? va : rt * 16 + a;
+                const bool up = vrow >= s.nr;
+                row_ok = vrow < s.V;
+                row = row_ok ? (up ? w2 : w1) + static_cast<size_t>(s.r0 + (up ? vrow - s.nr : vrow)) * K : w1;
+            }
+            // Lanes outside the share (padding rows, K tail) fetch the first chunk of w
+            // instead; their rows and k are never used.
+            const uint32_t k0 = kbase + j * 32;
+            const bool ok = row_ok && sa * s.KBs + j < s.KB && k0 < K;
+            dma_tile(ring_base + (seq % RING) * 1024u, ok ? row + k0 : w1);
+            j += LW;
+            while (j >= s.KBs) {
+                j -= s.KBs;
                 rt++;
             }
         }
-        wr[u] = v;
+        seq_base += s.T;
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Sum over aligned lane pairs / quads of a wave (fixed order).
+__device__ __forceinline__ float dpp_pair(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_quad(float v) {
+    v = dpp_pair(v);  // quad_perm [1,0,3,2]
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
 }
 
 // Partial sums of a finished row tile from the MFMA accumulator into this wave's LDS
-// slice: pw[(v * M + m) * S + s] for virtual row v, x row m, segment s.
+// slice, pw[v * M + m] for virtual row v and x row m.  Packed tiles first add their
+// segments: lane (row group qd, column c) holds D[4 qd + i][c], and the diagonal entry of
+// (virtual row, x row) over segment s sits in lane c = m S + s, register i with
+// (4 qd + i) % S == s, so S neighbouring lanes hold the S segments.
 __device__ __forceinline__ void flush(const f32x4 acc, const SeqTiles &s, uint32_t M, uint32_t rt, float *pw) {
     const uint32_t lane = threadIdx.x & 63, c = lane & 15, qd = lane >> 4;
-    const uint32_t sc = c / M, m = c - sc * M;
+    if (s.S == 1) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t a = qd * 4 + i;
-        if (s.S > 1) {
-            const uint32_t sa = a / s.V, v = a - sa * s.V;
-            if (sa < s.S && sa == sc) pw[(v * M + m) * s.S + sa] = acc[i];
-        } else {
-            const uint32_t v = rt * 16 + a;
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = rt * 16 + qd * 4 + i;
             if (v < s.V && c < M) pw[v * M + c] = acc[i];
         }
+    } else if (s.S == 2) {  // rows 4 qd + i: virtual row 2 qd + i / 2, segment i % 2
+        const uint32_t sc = c & 1, m = c >> 1;
+        const float e0 = dpp_pair(sc ? acc[1] : acc[0]);
+        const float e1 = dpp_pair(sc ? acc[3] : acc[2]);
+        if (sc == 0 && m < M) {
+            if (2 * qd < s.V) pw[(2 * qd) * M + m] = e0;
+            if (2 * qd + 1 < s.V) pw[(2 * qd + 1) * M + m] = e1;
+        }
+    } else {  // S == 4: rows 4 qd + i: virtual row qd, segment i
+        const uint32_t sc = c & 3, m = c >> 2;
+        const float e = dpp_quad(sc == 0 ? acc[0] : sc == 1 ? acc[1] : sc == 2 ? acc[2] : acc[3]);
+        if (sc == 0 && m < M && qd < s.V) pw[qd * M + m] = e;
     }
 }
 
-// The RMSNorm gain of op o into LDS gb (16-bit, K elements): requested before a wait,
-// stored after it.
-__device__ __forceinline__ void gain_request(const SeqOp &o, u32x4 (&gr)[GCH]) {
+// The RMSNorm gain of op o into LDS gb (16-bit, K elements) by the compute threads:
+// requested before a wait, stored after it.
+__device__ __forceinline__ void gain_request(const SeqOp &o, u32x4 (&gr)[CGCH]) {
     if (!o.norm) return;
 #pragma unroll
-    for (int r = 0; r < GCH; r++) {
-        const uint32_t ch = threadIdx.x + r * SEQ_THREADS;
-        if (ch * 8 < o.K) gr[r] = *reinterpret_cast<const u32x4 *>(o.norm + ch * 8);
+    for (int r = 0; r < CGCH; r++) {  // no lane-divergent branch around the loads
+        const uint32_t ch = threadIdx.x + r * CTHREADS;
+        gr[r] = gld(reinterpret_cast<const u32x4 *>(o.norm + (ch * 8 < o.K ? ch * 8 : 0u)));
     }
 }
-__device__ __forceinline__ void gain_store(const SeqOp &o, const u32x4 (&gr)[GCH], uint16_t *gb) {
+__device__ __forceinline__ void gain_store(const SeqOp &o, const u32x4 (&gr)[CGCH], uint16_t *gb) {
     if (!o.norm) return;
 #pragma unroll
-    for (int r = 0; r < GCH; r++) {
-        const uint32_t ch = threadIdx.x + r * SEQ_THREADS;
+    for (int r = 0; r < CGCH; r++) {
+        const uint32_t ch = threadIdx.x + r * CTHREADS;
         if (ch * 8 < o.K) *reinterpret_cast<u32x4 *>(gb + ch * 8) = gr[r];
     }
 }
 
-// LDS-only workgroup barrier: global loads in flight stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
+// The compute waves' meeting after op i: an LDS counter every compute wave bumps once per
+// op (bounded wait).
+__device__ __forceinline__ void compute_meet(uint32_t *ctl, uint32_t target, uint32_t *sync, bool &gave_up) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctl + CTL_CBAR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    uint32_t spins = 0;
+    while (lds_ld(ctl + CTL_CBAR) < target && !gave_up) {
+        if (++spins > SPIN_LIMIT) {
+            gave_up = true;
+            raise_flag(sync, SYNC_TIMEOUT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(0);
+    }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
@@ -217,106 +330,176 @@ __device__ __forceinline__ void lds_barrier() {
 template <int WT>
 __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
                                                          uint32_t *sync, const uint32_t *tags, uint32_t tag_bytes) {
-    __shared__ __attribute__((aligned(16))) float part[2][NW * PARTW];
+    __shared__ __attribute__((aligned(1024))) u32x4 ring[RING][64];
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][SEQ_XLDS];  // the op's x as [hi, lo][M][K]
+    __shared__ __attribute__((aligned(16))) float part[2][CW * PARTW];
     __shared__ __attribute__((aligned(16))) uint16_t gbuf[2][SEQ_GMAX];
-    __shared__ __attribute__((aligned(16))) uint16_t xst[NW][2][XW * 32];  // [wave][hi, lo][(u SMP + c) 32 + k]
-    __shared__ float ssw[2][NW * 16];
+    __shared__ float ssw[2][CW * 8];
+    __shared__ uint32_t ctl[CTL_WORDS];
+    __shared__ __attribute__((aligned(16))) SeqOp sdesc[SEQ_OPS_MAX];
+    __shared__ SeqTiles stile[SEQ_OPS_MAX];
     const uint32_t G = gridDim.x, g = blockIdx.x;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // The op descriptors and this workgroup's tiling of every op, staged in LDS once (no
+    // op then waits for a descriptor load); an empty ring; each compute wave's next tile is
+    // its first of op 0.
+    for (uint32_t e = tid; e < n_ops * (sizeof(SeqOp) / 16); e += SEQ_THREADS)
+        reinterpret_cast<u32x4 *>(sdesc)[e] = gld(reinterpret_cast<const u32x4 *>(ops) + e);
+    for (uint32_t e = tid; e < RING * 64u; e += SEQ_THREADS) (&ring[0][0])[e] = u32x4{~0u, ~0u, ~0u, ~0u};
+    __syncthreads();
+    for (uint32_t t = tid; t < n_ops; t += SEQ_THREADS) {
+        const SeqOp &o = sdesc[t];
+        stile[t] = seq_tiles(o.N, o.K, o.M, (o.flags & F_SILU_GATE) != 0, g, G);
+    }
+    __syncthreads();
+    if (tid < CTL_WORDS) {
+        uint32_t v = 0;
+        if (tid >= CTL_CONSUMED && tid < CTL_CONSUMED + CW && n_ops > 0) v = wave_tiles(stile[0], tid - CTL_CONSUMED).t0;
+        ctl[tid] = v;
+    }
+    __syncthreads();
+    if (w >= static_cast<uint32_t>(CW)) {
+        const uint32_t ring_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_vp)(&ring[0][0])));
+        loader(sdesc, stile, n_ops, w - CW, ring_base, ctl, sync);
+        return;
+    }
+
     const uint32_t epoch = __hip_atomic_load(sync + SYNC_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t parity = epoch & 1u;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(tags), 0, static_cast<int>(tag_bytes), BUF_DWORD3);
     bool gave_up = false;
-    u32x4 wr[TMAX];
-    u32x4 gr[GCH];
+    u32x4 gr[CGCH];
+    uint32_t seq_base = 0;
 
     if (n_ops > 0) {
-        const SeqOp o0 = ops[0];
-        load_w(o0, wave_tiles(o0, g, G, w), wr);
-        gain_request(o0, gr);
-        gain_store(o0, gr, gbuf[0]);
-        lds_barrier();
+        gain_request(sdesc[0], gr);
+        gain_store(sdesc[0], gr, gbuf[0]);
+        compute_meet(ctl, CW, sync, gave_up);
     }
     for (uint32_t i = 0; i < n_ops; i++) {
-        const SeqOp o = ops[i];
         const int b = i & 1;
-        const WaveTiles wt = wave_tiles(o, g, G, w);
+        const SeqOp o = sdesc[i];  // by value: read once, kept in registers
+        const WaveTiles wt = wave_tiles(stile[i], w);
         const SeqTiles &s = wt.s;
         const uint32_t M = o.M;
         const bool norm = o.norm != nullptr;
 
-        // Output lanes: bias and old y of output (feature r0 + v, row m), requested first.
-        const uint32_t nout = s.nr * M;
-        const uint32_t ov = tid / M, om = tid - ov * M;
-        float bias = 0.0f, yold = 0.0f;
-        uint32_t yw = 0;
-        const uint32_t *yp = nullptr;
-        if (tid < nout) {
-            if (o.flags & F_BIAS) bias = dec1<WT>(o.bias[s.r0 + ov]);
-            if (o.flags & F_ACCUM) {
-                if (o.ysrc >= 0) {
-                    yp = tags + o.yoff + static_cast<size_t>(om) * o.yld + s.r0 + ov;
-                    yw = ld32(yp);
-                } else {
-                    yold = o.y[static_cast<size_t>(om) * o.ldy + s.r0 + ov];
-                }
-            }
-        }
-        // The next op's RMSNorm gain, stored to LDS after this op's wait.
-        const bool next = i + 1 < n_ops;
-        const SeqOp on = ops[next ? i + 1 : i];
-        if (next) gain_request(on, gr);
-
-        // Activation chunks of the wave's tiles: chunk e = lane + 64 r is tile u, B column
-        // c (x row m of segment sc), 4 k at 4 h into the tile's 32-k block.  Columns are
-        // padded to SMP, a power of two.
-        const uint32_t SM = s.S * M;
-        const uint32_t lsm = SM <= 1 ? 0u : SM <= 2 ? 1u : SM <= 4 ? 2u : SM <= 8 ? 3u : 4u;
-        const uint32_t SMP = 1u << lsm, nch = wt.n << (lsm + 3);
-        const uint32_t magic = (256u + M - 1) / M;  // c * magic >> 8 == c / M for c < 16
+        // The op's activations x [M][K] are staged once per workgroup: chunk e = tid + 384 r
+        // is 4 k of one row of the row-major x; every compute lane polls its chunks, then
+        // converts them into LDS as hi + lo halves (xs[0], xs[1], row-major [M][K]).
+        const uint32_t K = o.K, K4 = K >> 2, nchunk = M * K4;
+        const uint32_t rows_used = (nchunk + CTHREADS - 1) / CTHREADS;  // chunk rounds (uniform)
+        const uint32_t k4magic = 0xFFFFFFFFu / K4 + 1u;                 // e / K4 = umulhi(e, k4magic)
         const bool ext = o.xsrc < 0;
+        // Loads are issued without branches around them (lanes past the op read past the end
+        // of the tag buffer, which returns zeros): a load under a lane-divergent branch makes
+        // the compiler wait for every load in flight where the branch rejoins.
         u32x4 xv[XCH];
-        uint32_t live = 0;  // chunks this lane holds
-        auto chunk = [&](int r, uint32_t &u, uint32_t &c, uint32_t &m, uint32_t &k, uint32_t &rt) {
-            const uint32_t e = lane + 64u * r;
-            u = e >> (lsm + 3);
-            c = (e >> 3) & (SMP - 1);
-            const uint32_t sc = (c * magic) >> 8;
-            m = c - sc * M;
-            uint32_t j = wt.j0 + u;
-            rt = wt.rt0;
-            if (j >= s.KBs) {
-                j -= s.KBs;
-                rt++;
-            }
-            const uint32_t kb = sc * s.KBs + j;
-            k = kb * 32 + (e & 7) * 4;
-            return e < nch && c < SM && kb < s.KB && k < o.K;
-        };
 #pragma unroll
         for (int r = 0; r < XCH; r++) {
-            uint32_t u, c, m, k, rt;
             xv[r] = u32x4{0u, 0u, 0u, 0u};
-            if (chunk(r, u, c, m, k, rt)) {
-                live |= 1u << r;
+            if (static_cast<uint32_t>(r) < rows_used) {
+                const uint32_t e = tid + CTHREADS * r;
+                const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
+                const bool ok = e < nchunk;
                 if (!ext) {
-                    xv[r] = ldtag4(rsrc, (o.xoff + m * o.xld + k) * 4u);
-                } else if (o.xt == DT_F32) {
-                    const float *p = static_cast<const float *>(o.x) + static_cast<size_t>(m) * o.ldx + k;
-                    xv[r] = u32x4{__float_as_uint(p[0]), __float_as_uint(p[1]), __float_as_uint(p[2]),
-                                  __float_as_uint(p[3])};
-                } else {
-                    const uint16_t *p = static_cast<const uint16_t *>(o.x) + static_cast<size_t>(m) * o.ldx + k;
-                    float f[4];
+                    xv[r] = ldtag4(rsrc, ok ? (o.xoff + m * o.xld + k) * 4u : 0xFFFFFFF0u);
+                } else if (ok) {
+                    if (o.xt == DT_F32) {
+                        const float *p = static_cast<const float *>(o.x) + static_cast<size_t>(m) * o.ldx + k;
+                        xv[r] = u32x4{__float_as_uint(gld(p)), __float_as_uint(gld(p + 1)), __float_as_uint(gld(p + 2)),
+                                      __float_as_uint(gld(p + 3))};
+                    } else {
+                        const uint16_t *p = static_cast<const uint16_t *>(o.x) + static_cast<size_t>(m) * o.ldx + k;
+                        float f[4];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) f[e] = o.xt == DT_BF16 ? dec1<DT_BF16>(p[e]) : dec1<DT_F16>(p[e]);
-                    xv[r] = u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
-                                  __float_as_uint(f[3])};
+                        for (int ee = 0; ee < 4; ee++)
+                            f[ee] = o.xt == DT_BF16 ? dec1<DT_BF16>(gld(p + ee)) : dec1<DT_F16>(gld(p + ee));
+                        xv[r] = u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                                      __float_as_uint(f[3])};
+                    }
                 }
             }
         }
+        // Output lanes: bias and old y of outputs (feature r0 + v, row m), requested after
+        // the activations (which the wave waits for first).
+        const uint32_t nout = s.nr * M;
+        uint32_t yw[OUTR], braw[OUTR];  // old y (tagged word or user fp32 bits), raw 16-bit bias
+#pragma unroll
+        for (int r = 0; r < OUTR; r++) {
+            const uint32_t idx = tid + r * CTHREADS;
+            const uint32_t ov = idx / M, om = idx - ov * M;
+            const bool live_out = idx < nout;
+            braw[r] = 0;
+            yw[r] = 0;
+            // Uniform branches only; lanes past the outputs read element 0.
+            if (o.flags & F_BIAS) braw[r] = gld(o.bias + (live_out ? s.r0 + ov : 0u));
+            if (o.flags & F_ACCUM) {
+                if (o.ysrc >= 0)
+                    yw[r] = ldtag1(rsrc, live_out ? (o.yoff + om * o.yld + s.r0 + ov) * 4u : 0xFFFFFFF0u);
+                else
+                    yw[r] = gld(reinterpret_cast<const uint32_t *>(o.y) +
+                                (live_out ? static_cast<size_t>(om) * o.ldy + s.r0 + ov : 0u));
+            }
+        }
+        // The next op's RMSNorm gain, stored to LDS after this op's MFMAs.
+        const bool next = i + 1 < n_ops;
+        const SeqOp on = sdesc[next ? i + 1 : i];
+        const WaveTiles wtn = wave_tiles(stile[next ? i + 1 : i], w);
+        if (next) gain_request(on, gr);
+
+        // The wave's weight tiles (MFMA A operands) from the ring into registers while the
+        // activations are in flight; their slots are freed right away.
+        const uint32_t seq0 = seq_base + wt.t0;
+        const uint32_t sa = (lane & 15) & (s.S - 1), qa = lane >> 4;
+        // K tails (K % 32, or a last segment shorter than KBs): chunks past K are zeros (the
+        // ring holds filler there).
+        const bool tails = (K & 31u) != 0 || s.S * s.KBs != s.KB;
+        u32x4 A[TA];
+#pragma unroll
+        for (int k = 0; k < TA; k++) {
+            A[k] = u32x4{0u, 0u, 0u, 0u};
+            if (static_cast<uint32_t>(k) < wt.n) A[k] = ring[(seq0 + k) % RING][lane];
+        }
+        {
+            uint32_t spins = 0;
+            for (;;) {  // every lane's chunk of every tile landed?
+                uint32_t miss = 0;
+#pragma unroll
+                for (int k = 0; k < TA; k++)
+                    if (static_cast<uint32_t>(k) < wt.n) miss |= unsent(A[k]);
+                if (!__ballot(miss) || gave_up) break;
+                if (++spins > SPIN_LIMIT) {
+                    gave_up = true;
+                    raise_flag(sync, SYNC_TIMEOUT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(0);
+#pragma unroll
+                for (int k = 0; k < TA; k++)
+                    if (static_cast<uint32_t>(k) < wt.n && __ballot(unsent(A[k])))
+                        A[k] = ring_ld(&ring[(seq0 + k) % RING][lane]);
+            }
+        }
+        {
+            uint32_t j = wt.j0;
+#pragma unroll
+            for (int k = 0; k < TA; k++) {
+                if (static_cast<uint32_t>(k) < wt.n) {
+                    ring[(seq0 + k) % RING][lane] = u32x4{~0u, ~0u, ~0u, ~0u};  // the slot is empty again
+                    if (tails && (sa * s.KBs + j) * 32 + qa * 8 >= K) A[k] = u32x4{0u, 0u, 0u, 0u};
+                    if (++j == s.KBs) j = 0;
+                }
+            }
+        }
+        // Nothing more of this op's tiles: the wave's next tile is its first of op i + 1.
+        const uint32_t next_first = seq_base + s.T + (next ? wtn.t0 : 0u);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if (lane == 0) lds_st(ctl + CTL_CONSUMED + w, next_first);
+
         // Wait for the tagged chunks: every round re-requests all stale ones at once.
         if (!ext) {
             uint32_t spins = 0;
@@ -324,7 +507,8 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                 uint32_t stale = 0;
 #pragma unroll
                 for (int r = 0; r < XCH; r++)
-                    if (((live >> r) & 1u) && !tagged4(xv[r], parity)) stale |= 1u << r;
+                    if (static_cast<uint32_t>(r) < rows_used && tid + CTHREADS * r < nchunk && !tagged4(xv[r], parity))
+                        stale |= 1u << r;
                 if (!stale) break;
                 if (++spins > SPIN_LIMIT) {
                     gave_up = true;
@@ -334,77 +518,90 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                 __builtin_amdgcn_s_sleep(1);
 #pragma unroll
                 for (int r = 0; r < XCH; r++) {
-                    if ((stale >> r) & 1u) {
-                        uint32_t u, c, m, k, rt;
-                        chunk(r, u, c, m, k, rt);
+                    if (static_cast<uint32_t>(r) < rows_used && ((stale >> r) & 1u)) {
+                        const uint32_t e = tid + CTHREADS * r;
+                        const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
                         xv[r] = ldtag4(rsrc, (o.xoff + m * o.xld + k) * 4u);
                     }
                 }
             }
         }
-        // Convert the chunks into the wave's B staging area (zeros past K).
-        uint16_t *xh = xst[w][0], *xl = xst[w][1];
+        // Convert: hi = x rounded toward zero to the weights' 16-bit type (to nearest for
+        // bf16), lo = the rest, rounded the same way; x^2 summed per row for the RMSNorm.
         const uint16_t *gb = gbuf[b];
-        float ss0 = 0.0f, ss1 = 0.0f;
+        float ssr[8];
+#pragma unroll
+        for (int mm = 0; mm < 8; mm++) ssr[mm] = 0.0f;
         bool range_ok = true;
+        const uint32_t clear = ext ? ~0u : ~1u;  // tagged words: drop the tag bit
 #pragma unroll
         for (int r = 0; r < XCH; r++) {
-            uint32_t u, c, m, k, rt;
-            const bool ok = chunk(r, u, c, m, k, rt);
-            const uint32_t e = lane + 64u * r;
-            if (e < nch && c < SM) {
-                float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (ok) {
-                    const uint32_t clear = ext ? ~0u : ~1u;  // tagged words: drop the tag bit
-                    x[0] = __uint_as_float(xv[r].x & clear);
-                    x[1] = __uint_as_float(xv[r].y & clear);
-                    x[2] = __uint_as_float(xv[r].z & clear);
-                    x[3] = __uint_as_float(xv[r].w & clear);
-                    if (norm) {
-                        if (rt == 0) {  // each x element once per workgroup
-                            float t = x[0] * x[0];
-                            t = fmaf(x[1], x[1], t);
-                            t = fmaf(x[2], x[2], t);
-                            t = fmaf(x[3], x[3], t);
-                            if (r & 1) ss1 += t; else ss0 += t;
-                        }
-                        const u32x2 gg = *reinterpret_cast<const u32x2 *>(gb + k);
-                        x[0] *= dec_lo<WT>(gg.x);
-                        x[1] *= dec_hi<WT>(gg.x);
-                        x[2] *= dec_lo<WT>(gg.y);
-                        x[3] *= dec_hi<WT>(gg.y);
-                    }
-                    if constexpr (WT == DT_F16)
-                        range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
+            const uint32_t e = tid + CTHREADS * r;
+            if (static_cast<uint32_t>(r) < rows_used && e < nchunk) {
+                const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
+                float x[4];
+                x[0] = __uint_as_float(xv[r].x & clear);
+                x[1] = __uint_as_float(xv[r].y & clear);
+                x[2] = __uint_as_float(xv[r].z & clear);
+                x[3] = __uint_as_float(xv[r].w & clear);
+                if (norm) {
+                    float t = x[0] * x[0];
+                    t = fmaf(x[1], x[1], t);
+                    t = fmaf(x[2], x[2], t);
+                    t = fmaf(x[3], x[3], t);
+#pragma unroll
+                    for (int mm = 0; mm < 8; mm++)
+                        if (static_cast<uint32_t>(mm) < M) ssr[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
+                    const u32x2 gg = *reinterpret_cast<const u32x2 *>(gb + k);
+                    x[0] *= dec_lo<WT>(gg.x);
+                    x[1] *= dec_hi<WT>(gg.x);
+                    x[2] *= dec_lo<WT>(gg.y);
+                    x[3] *= dec_hi<WT>(gg.y);
                 }
+                if constexpr (WT == DT_F16)
+                    range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
                 u32x2 hi, lo;
-                split4<WT>(x, hi, lo);
-                const uint32_t at = ((u << lsm) + c) * 32 + (e & 7) * 4;
-                *reinterpret_cast<u32x2 *>(xh + at) = hi;
-                *reinterpret_cast<u32x2 *>(xl + at) = lo;
+                split4p<WT>(x, hi, lo);
+                *reinterpret_cast<u32x2 *>(&xs[0][m * K + k]) = hi;
+                *reinterpret_cast<u32x2 *>(&xs[1][m * K + k]) = lo;
             }
         }
         if (!range_ok) raise_flag(sync, SYNC_RANGE);
+        if (norm) {  // the wave's sum of x^2 per row
+#pragma unroll
+            for (int mm = 0; mm < 8; mm++) {
+                if (static_cast<uint32_t>(mm) < M) {
+                    float t = ssr[mm];
+                    for (int bit = 1; bit < 64; bit <<= 1) t += __shfl_xor(t, bit, 64);
+                    if (lane == 0) ssw[b][w * 8 + mm] = t;
+                }
+            }
+        }
+        compute_meet(ctl, CW * (2 * i + 2), sync, gave_up);
 
-        // MFMAs over the wave's tiles (hi and lo in two accumulators); a finished row tile
-        // goes to LDS.  Lane (c, q) reads its B fragment, 8 k of column c, from the staging.
+        // MFMAs over the wave's tiles (hi and lo in two accumulators), A in registers, B from
+        // the staging (lane (bc, q) reads column bc: x row bc / S over segment bc % S, 8 k);
+        // a finished row tile goes to LDS.
         float *pw = part[b] + w * PARTW;
         {
-            const uint32_t c = lane & 15, q = lane >> 4;
+            const uint32_t bc = lane & 15, q = lane >> 4;
+            const uint32_t SM = s.S * M;
+            const uint32_t bkb = (bc & (s.S - 1)) * s.KBs;              // segment's first block
+            const uint32_t boff = (bc >> s.ls) * K + bkb * 32 + q * 8;  // + 32 j: the tile's 8 k
+            const bool bcol = bc < SM;
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;
             uint32_t rt = wt.rt0, j = wt.j0;
 #pragma unroll
-            for (int u = 0; u < TMAX; u++) {
-                if (static_cast<uint32_t>(u) < wt.n) {
+            for (int k = 0; k < TA; k++) {
+                if (static_cast<uint32_t>(k) < wt.n) {
                     u32x4 bh = {0u, 0u, 0u, 0u}, bl = bh;
-                    if (c < SM) {
-                        const uint32_t at = ((static_cast<uint32_t>(u) << lsm) + c) * 32 + q * 8;
-                        bh = *reinterpret_cast<const u32x4 *>(xh + at);
-                        bl = *reinterpret_cast<const u32x4 *>(xl + at);
+                    if (bcol && (!tails || (bkb + j < s.KB && (bkb + j) * 32 + q * 8 < K))) {
+                        bh = *reinterpret_cast<const u32x4 *>(&xs[0][boff + j * 32]);
+                        bl = *reinterpret_cast<const u32x4 *>(&xs[1][boff + j * 32]);
                     }
-                    acc = mfma16<WT>(wr[u], bh, acc);
-                    acc2 = mfma16<WT>(wr[u], bl, acc2);
-                    if (++j == s.KBs || static_cast<uint32_t>(u) + 1 == wt.n) {
+                    acc = mfma16<WT>(A[k], bh, acc);
+                    acc2 = mfma16<WT>(A[k], bl, acc2);
+                    if (++j == s.KBs || static_cast<uint32_t>(k) + 1 == wt.n) {
                         flush(acc + acc2, s, M, rt, pw);
                         acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                         acc2 = acc;
@@ -416,83 +613,70 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                 }
             }
         }
-        if (norm) {  // the wave's sum of x^2 per B column
-            float t0 = ss0 + (SMP < 16 ? ss1 : 0.0f), t1 = SMP < 16 ? 0.0f : ss1;
-            t0 += __shfl_xor(t0, 1, 64);
-            t0 += __shfl_xor(t0, 2, 64);
-            t0 += __shfl_xor(t0, 4, 64);
-            t1 += __shfl_xor(t1, 1, 64);
-            t1 += __shfl_xor(t1, 2, 64);
-            t1 += __shfl_xor(t1, 4, 64);
-            for (uint32_t bit = 8u * SMP; bit < 64u; bit <<= 1) t0 += __shfl_xor(t0, static_cast<int>(bit), 64);
-            if ((lane & 7) == 0) {
-                const uint32_t c0 = lane >> 3;
-                if (c0 < SMP) ssw[b][w * 16 + c0] = t0;
-                if (SMP == 16) ssw[b][w * 16 + c0 + 8] = t1;
-            }
-        }
-        if (next) {
-            load_w(on, wave_tiles(on, g, G, w), wr);
-            gain_store(on, gr, gbuf[b ^ 1]);
-        }
-        lds_barrier();
+        if (next) gain_store(on, gr, gbuf[b ^ 1]);
+        compute_meet(ctl, CW * (2 * i + 3), sync, gave_up);
 
-        if (tid < nout) {
-            if (yp) {
-                uint32_t spins = 0;
-                while ((yw & 1u) != parity && !gave_up) {
+        // Outputs: sums of the waves' partials in wave order.
+#pragma unroll
+        for (int r = 0; r < OUTR; r++) {
+            const uint32_t idx = tid + r * CTHREADS;
+            if (idx >= nout) continue;
+            const uint32_t ov = idx / M, om = idx - ov * M;
+            float yold = 0.0f;
+            if (o.flags & F_ACCUM && o.ysrc < 0) yold = __uint_as_float(yw[r]);
+            if (o.flags & F_ACCUM && o.ysrc >= 0) {
+                const uint32_t yoff = (o.yoff + om * o.yld + s.r0 + ov) * 4u;
+                uint32_t v = yw[r], spins = 0;
+                while ((v & 1u) != parity && !gave_up) {
                     if (++spins > SPIN_LIMIT) {
                         gave_up = true;
                         raise_flag(sync, SYNC_TIMEOUT);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
-                    yw = ld32(yp);
+                    v = ldtag1(rsrc, yoff);
                 }
-                yold = untag(yw);
+                yold = untag(v);
             }
-            // Sum of the waves' partials for virtual row vr: the waves whose tile range
-            // meets vr's row tile, by segment, then by wave (fixed order).
             auto total = [&](uint32_t vr) {
                 const uint32_t rt = s.S > 1 ? 0 : vr / 16;
                 const uint32_t lo_t = rt * s.KBs, hi_t = lo_t + s.KBs;
-                bool take[NW];
+                const float *p = part[b] + vr * M + om;
+                float v[CW];
 #pragma unroll
-                for (int ww = 0; ww < NW; ww++) {
-                    const uint32_t b0 = seq_tile_begin(s.T, ww, NW), b1 = seq_tile_begin(s.T, ww + 1, NW);
-                    take[ww] = b0 < b1 && b0 < hi_t && b1 > lo_t;
-                }
-                const float *p = part[b] + (vr * M + om) * s.S;
+                for (int ww = 0; ww < CW; ww++) v[ww] = p[ww * PARTW];
                 float a = 0.0f;
-                for (uint32_t sg = 0; sg < s.S; sg++) {
-                    float v[NW];
 #pragma unroll
-                    for (int ww = 0; ww < NW; ww++) v[ww] = p[ww * PARTW + sg];
-#pragma unroll
-                    for (int ww = 0; ww < NW; ww++) a += take[ww] ? v[ww] : 0.0f;
+                for (int ww = 0; ww < CW; ww++) {
+                    const uint32_t b0 = seq_tile_begin(s.T, ww, CW), b1 = seq_tile_begin(s.T, ww + 1, CW);
+                    a += (b0 < b1 && b0 < hi_t && b1 > lo_t) ? v[ww] : 0.0f;
                 }
                 return a;
             };
             float scale = 1.0f;
             if (norm) {
+                float v[CW];
+#pragma unroll
+                for (int ww = 0; ww < CW; ww++) v[ww] = ssw[b][ww * 8 + om];
                 float t = 0.0f;
-                for (uint32_t sg = 0; sg < s.S; sg++) {
-                    float v[NW];
 #pragma unroll
-                    for (int ww = 0; ww < NW; ww++) v[ww] = ssw[b][ww * 16 + sg * M + om];
-#pragma unroll
-                    for (int ww = 0; ww < NW; ww++) t += v[ww];
-                }
+                for (int ww = 0; ww < CW; ww++) t += v[ww];
                 scale = 1.0f / sqrtf(t / static_cast<float>(o.K) + o.eps);
             }
             const float a1 = total(ov);
             const float a2 = (o.flags & F_SILU_GATE) ? total(ov + s.nr) : 0.0f;
+            // (the empty asm keeps the decode here, after the wait, rather than next to the load)
+            asm volatile("" : "+v"(braw[r]));
+            const float bias = (o.flags & F_BIAS) ? dec1<WT>(static_cast<uint16_t>(braw[r])) : 0.0f;
             float v = epilogue(a1 * scale, a2 * scale, bias, o.flags);
             if (o.flags & F_ACCUM) v += yold;
             const uint32_t n = s.r0 + ov;
             st_tag(o.tag + static_cast<size_t>(om) * o.N + n, v, parity);
-            if (o.final_out) o.y[static_cast<size_t>(om) * o.ldy + n] = v;
+            if (o.final_out)
+                *reinterpret_cast<__attribute__((address_space(1))) float *>(
+                    reinterpret_cast<uintptr_t>(o.y + static_cast<size_t>(om) * o.ldy + n)) = v;
         }
+        seq_base += s.T;
     }
     // The last workgroup out advances the epoch for the next run.
     if (threadIdx.x == 0) {

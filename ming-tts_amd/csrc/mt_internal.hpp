@@ -51,17 +51,19 @@ struct SeqOp {
     uint32_t yoff, yld;     // tagged old y: the same
     int32_t pad;
 };
+static_assert(sizeof(SeqOp) % 16 == 0, "SeqOp is staged into LDS in 16-byte pieces");
 struct SeqPlan;
-// Limits of the persistent sequence kernel: threads per workgroup, MFMA tiles per wave per
-// op (each lane holds one 16-byte weight chunk and one 8-activation chunk per tile across
-// the op's wait), output features per workgroup per op, LDS partial sums per wave per op.
+// Limits of the persistent sequence kernel: threads per workgroup, output features per
+// workgroup per op, and the LDS areas of its compute waves.
 constexpr int SEQ_THREADS_N = 512;
-constexpr int SEQ_TMAX = 12;
 constexpr int SEQ_RMAX = 64;
-constexpr int SEQ_PARTW = 512;     // partial sums per wave per op: virtual rows * M * segments
-constexpr int SEQ_XCH = 8;         // 16-byte activation chunks per lane per op
-constexpr int SEQ_XW = 64;         // tiles x padded B columns staged per wave per op
-constexpr int SEQ_GMAX = 8192;     // K of an op with an RMSNorm gain (staged in LDS)
+constexpr int SEQ_PARTW = 128;     // partial sums per compute wave per op: virtual rows * M
+constexpr int SEQ_XLDS = 10240;    // M * K of an op: its activations staged in LDS (hi + lo)
+constexpr int SEQ_OPS_MAX = 96;    // ops of a sequence (their descriptors are staged in LDS)
+constexpr int SEQ_CW = 6;          // compute waves per workgroup (the other waves load weights)
+constexpr int SEQ_TA = 16;         // MFMA tiles of one op a compute wave holds in registers
+constexpr int SEQ_RING = 88;       // LDS ring of 1 KB weight tiles
+constexpr int SEQ_GMAX = 2048;     // K of an op with an RMSNorm gain (staged in LDS)
 // Workgroup count of the persistent kernel on the current device.
 int seq_limits(int *groups);
 // Dataflow plan of a serial op list for `groups` workgroups (host only; no HIP calls).

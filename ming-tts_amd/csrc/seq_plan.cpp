@@ -72,6 +72,8 @@ bool covered(const View &in, const View &out, uint32_t &col) {
 }  // namespace
 
 int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt) {
+    if (n > static_cast<uint32_t>(SEQ_OPS_MAX))
+        return set_error(MT_ENOTSUP, "mt_seq_create: a sequence takes at most %d ops, got %u", SEQ_OPS_MAX, n);
     out.assign(n, SeqOp{});
     std::vector<View> xv(n), yv(n);
     std::vector<int> done_before(n, -1);
@@ -87,21 +89,22 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
         if (o.wt != wt) return set_error(MT_EINVAL, "mt_seq_create: op %u: every op of a sequence must share the weight type", i);
         if (o.norm && p.K > static_cast<uint32_t>(SEQ_GMAX))
             return set_error(MT_ENOTSUP, "mt_seq_create: op %u: an RMSNorm op takes K <= %d, got %u", i, SEQ_GMAX, p.K);
-        // Every workgroup's share of the op, tiled as the kernel tiles it: at most RMAX
-        // features, at most TMAX tiles per wave (each held in registers across the wait).
-        const int nw = SEQ_THREADS_N / 64;
+        // The op's activations are staged whole in the workgroup's LDS (M * K <= XLDS);
+        // every workgroup's share of the op at most RMAX features and its partial sums
+        // (virtual rows x M per compute wave) within the LDS slice.
+        if (static_cast<uint64_t>(p.M) * p.K > static_cast<uint64_t>(SEQ_XLDS))
+            return set_error(MT_ENOTSUP, "mt_seq_create: op %u: M * K = %u exceeds the %d activations a workgroup stages",
+                             i, p.M * p.K, SEQ_XLDS);
         for (int g = 0; g < groups; g++) {
             const SeqTiles t = seq_tiles(p.N, p.K, p.M, (p.flags & MT_SILU_GATE) != 0, g, groups);
-            const uint32_t per_wave = (t.T + nw - 1) / nw;
-            uint32_t smp = 1;
-            while (smp < t.S * p.M) smp <<= 1;
-            if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || per_wave > static_cast<uint32_t>(SEQ_TMAX) ||
-                t.V * p.M * t.S > static_cast<uint32_t>(SEQ_PARTW) || per_wave * smp > static_cast<uint32_t>(SEQ_XW))
+            const uint32_t per_wave = (t.T + SEQ_CW - 1) / SEQ_CW;
+            if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || t.V * p.M > static_cast<uint32_t>(SEQ_PARTW) ||
+                per_wave > static_cast<uint32_t>(SEQ_TA))
                 return set_error(MT_ENOTSUP,
-                                 "mt_seq_create: op %u: a workgroup's share (%u features, %u MFMA tiles per wave of "
-                                 "%u activation columns at M = %u) exceeds the sequence kernel's limits (%d features, "
-                                 "%d tiles, %d tile columns, %d partial sums)",
-                                 i, t.nr, per_wave, smp, p.M, SEQ_RMAX, SEQ_TMAX, SEQ_XW, SEQ_PARTW);
+                                 "mt_seq_create: op %u: a workgroup's share (%u features, %u partial sums at M = %u, %u "
+                                 "MFMA tiles per compute wave) exceeds the sequence kernel's limits (%d features, %d "
+                                 "partial sums, %d tiles)",
+                                 i, t.nr, t.V * p.M, p.M, per_wave, SEQ_RMAX, SEQ_PARTW, SEQ_TA);
         }
 
         // x: latest earlier writer.

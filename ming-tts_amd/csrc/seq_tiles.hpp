@@ -5,14 +5,17 @@
 // "virtual rows" are those features' weight rows, followed (SiLU-gate) by the partner W2's
 // rows: V = nr or 2 nr.  The share is computed with v_mfma_f32_16x16x32 tiles: A = 16
 // virtual rows x 32 k of weights (one 16-byte chunk per lane), B = 32 k x 16 columns of
-// activations (x rows), D = 16 x 16 fp32 partial sums.
-//   - V > 16: RT = ceil(V / 16) row tiles, S = 1 segment; column c of B is x row c.
-//   - V <= 16: one row tile holds S = min(16 / V, 16 / M, KB) K-segments of the share side
-//     by side: A row s V + v is feature v over segment s, B column s M + m is x row m over
-//     segment s, and only the diagonal blocks (segment s against segment s) of D are kept.
+// activations, D = 16 x 16 fp32 partial sums.
+//   - V > 16: RT = ceil(V / 16) row tiles, S = 1 segment; A row a of row tile rt is
+//     virtual row 16 rt + a and B column c is x row c.
+//   - V <= 16: one row tile holds S in {1, 2, 4} K-segments of the share side by side
+//     (the largest with V S <= 16, M S <= 8, S <= KB), interleaved: A row a is virtual row
+//     a / S over segment a % S, B column c is x row c / S over segment c % S, and only the
+//     diagonal entries (segment s against segment s) of D are kept.  For a given (virtual
+//     row, x row) they sit in S neighbouring lanes, so a lane-group sum adds the segments.
 // Segment s covers 32-k blocks s KBs .. s KBs + KBs - 1 (KBs = ceil(KB / S)); a tile is
-// (row tile rt, block step j), numbered t = rt KBs + j, T = RT KBs in all, and wave w of
-// the workgroup's NW waves takes the contiguous tile range [w T / NW, (w + 1) T / NW).
+// (row tile rt, block step j), numbered t = rt KBs + j, T = RT KBs in all, and compute
+// wave w of the workgroup's NW takes the contiguous tile range [w T / NW, (w + 1) T / NW).
 #pragma once
 
 #include <stdint.h>
@@ -22,7 +25,8 @@ namespace mt {
 struct SeqTiles {
     uint32_t r0, nr;  // features of the share
     uint32_t V;       // virtual rows
-    uint32_t S;       // K segments per row tile
+    uint32_t S;       // K segments per row tile (1, 2 or 4)
+    uint32_t ls;      // log2 S
     uint32_t RT;      // row tiles
     uint32_t KB;      // 32-k blocks of K
     uint32_t KBs;     // blocks per segment
@@ -36,17 +40,17 @@ __host__ __device__ inline SeqTiles seq_tiles(uint32_t N, uint32_t K, uint32_t M
     t.nr = static_cast<uint32_t>(static_cast<uint64_t>(g + 1) * N / G) - t.r0;
     t.V = t.nr * (gated ? 2u : 1u);
     t.KB = (K + 31) / 32;
+    t.S = 1;
+    t.ls = 0;
     if (t.V == 0) {
-        t.S = 1;
         t.RT = 0;
     } else if (t.V <= 16) {
-        uint32_t s = 16 / t.V;
-        if (16 / M < s) s = 16 / M;
-        if (t.KB < s) s = t.KB;
-        t.S = s < 1 ? 1 : s;
+        while (t.S < 4 && 2 * t.S * t.V <= 16 && 2 * t.S * M <= 8 && 2 * t.S <= t.KB) {
+            t.S *= 2;
+            t.ls++;
+        }
         t.RT = 1;
     } else {
-        t.S = 1;
         t.RT = (t.V + 15) / 16;
     }
     t.KBs = (t.KB + t.S - 1) / t.S;
