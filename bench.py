@@ -386,8 +386,9 @@ def main() -> int:
     ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
-    ap.add_argument("--only", choices=["decode", "all", "copy"], default="all",
-                    help="copy: only the 1 GiB device copy that calibrates the HBM byte counters")
+    ap.add_argument("--only", choices=["decode", "all", "copy", "gemm"], default="all",
+                    help="copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
+                         "gemm: only the prefill and DiT GEMM stacks")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: there is no multi-GPU path (the linear hot path would "
@@ -405,6 +406,16 @@ def main() -> int:
     log("generating 24 layers of fp16 weights")
     ws = make_layers(torch, dev)
     torch.cuda.synchronize()
+    if args.only == "gemm":
+        out = {"prefill": [], "dit_head": None}
+        for M in (64, 256, 512):
+            log(f"prefill stack M={M}")
+            out["prefill"].append({k: (round(v, 3) if isinstance(v, float) else v)
+                                   for k, v in bench_prefill(torch, mt, dev, ws, M).items()})
+        log("DiT head")
+        out["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
+        print(json.dumps(out), flush=True)
+        return 0
 
     if args.seq_launch == "plain":
         mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 1)

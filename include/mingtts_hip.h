@@ -107,10 +107,14 @@ int mt_linear_kernel(uint32_t M, uint32_t N, uint32_t K, mt_dtype xt, mt_dtype w
 enum {
     MT_TUNE_GEMV_ROWS_MAX = 1,   /* M up to this goes to the GEMV family (default 8) */
     MT_TUNE_GEMV_LANES = 2,      /* lanes per output feature in the GEMV, 8..64 (0 = auto) */
-    MT_TUNE_GEMM_SPLITK = 3,     /* K splits of the MFMA GEMM (0 = auto) */
+    MT_TUNE_GEMM_SPLITK = 3,     /* K splits of the pipelined MFMA GEMM (0 = auto) */
     MT_TUNE_SEQ_GROUPS = 4,      /* workgroups of the persistent sequence kernel (0 = auto) */
-    MT_TUNE_SEQ_LAUNCH = 5       /* 0: cooperative launch (default); 1: ordinary launch, co-residency
+    MT_TUNE_SEQ_LAUNCH = 5,      /* 0: cooperative launch (default); 1: ordinary launch, co-residency
                                     then rests on an otherwise idle device (profilers) */
+    MT_TUNE_GEMM_TILE = 6,       /* MFMA GEMM tile (x rows x weight rows) for activations of the
+                                    weights' type: 0 = auto, 1 = 128 x 128, 2 = 64 x 128, 3 = 64 x 64,
+                                    4 = the register-staged kernel that other activation types use */
+    MT_TUNE_GEMM_STAGES = 7      /* LDS pipeline depth of that GEMM, 2..4 stages of 64 k (0 = auto) */
 };
 int mt_set_tuning(int key, int value);
 
@@ -125,9 +129,12 @@ int mt_set_tuning(int key, int value);
  * 16-bit type; with fp16 weights an activation (times its RMSNorm gain) must stay within
  * the fp16 range, |x| <= 65504, or mt_seq_check reports MT_ERANGE for that run.
  * Requirements, beyond mt_linear's for every op: 1 <= M <= 8; one weight type for all
- * ops; a workgroup's share of an op (ceil(N / workgroups) features, twice with the gate
- * partner) at most 64 features and at most 12 MFMA tiles of 16 x 32 weights per wave
- * (every linear of a Qwen2-0.5B decode layer fits at one workgroup per CU on 256 CUs); an op that reads (as x, or as the old y of MT_ACCUM) a
+ * ops; at most 96 ops; M * K <= 10240 per op (its activations are staged in LDS); K <= 2048
+ * for an op with an RMSNorm gain; a workgroup's share of an op (ceil(N / workgroups)
+ * features) at most 64 features, with (features, twice with the gate partner) x M <= 128,
+ * and at most 16 MFMA tiles of 16 x 32 weights per compute wave (six per workgroup) --
+ * every linear of a Qwen2-0.5B decode layer fits at one workgroup per CU on 256 CUs; an
+ * op that reads (as x, or as the old y of MT_ACCUM) a
  * region an earlier op wrote must view it with that op's row stride and within its
  * columns; a later write must cover an earlier write of the same region whole; an op
  * may overwrite a region an earlier op read from its buffer only if every workgroup

@@ -119,10 +119,16 @@ int mt_set_tuning(int key, int value) {
         case MT_TUNE_GEMM_SPLITK: slot = &g_tuning.gemm_splitk; def = 0; break;
         case MT_TUNE_SEQ_GROUPS: slot = &g_tuning.seq_groups; def = 0; break;
         case MT_TUNE_SEQ_LAUNCH: slot = &g_tuning.seq_launch; def = 0; break;
+        case MT_TUNE_GEMM_TILE: slot = &g_tuning.gemm_tile; def = 0; break;
+        case MT_TUNE_GEMM_STAGES: slot = &g_tuning.gemm_stages; def = 0; break;
         default: return set_error(MT_EINVAL, "mt_set_tuning: unknown key %d", key);
     }
     if (key == MT_TUNE_SEQ_LAUNCH && value > 1)
         return set_error(MT_EINVAL, "mt_set_tuning: the sequence launch mode is 0 or 1, got %d", value);
+    if (key == MT_TUNE_GEMM_STAGES && (value == 1 || value > 4))
+        return set_error(MT_EINVAL, "mt_set_tuning: the GEMM pipeline depth is 2..4 stages, got %d", value);
+    if (key == MT_TUNE_GEMM_TILE && value > 4)
+        return set_error(MT_EINVAL, "mt_set_tuning: the GEMM tile choice is 0..4, got %d", value);
     if (key == MT_TUNE_GEMV_ROWS_MAX && value > 8)
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMV takes at most 8 rows per block, got %d", value);
     const int old = *slot;

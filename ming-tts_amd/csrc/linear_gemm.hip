@@ -1,4 +1,7 @@
-// MFMA GEMM of mt_linear for prefill and DiT shapes (M above the GEMV row limit).
+// Register-staged MFMA GEMM of mt_linear for prefill and DiT shapes (M above the GEMV row
+// limit) whose activations need converting: fp32 x, 16-bit x of the other type, or a fused
+// RMSNorm.  Activations of the weights' own type go to the pipelined kernel of
+// linear_gemm_lds.hip instead.
 //
 // Reference kernel replaced: gemm_kernel<32,64,32,4> (Shaders.swift:297-410), which stages
 // X (fp32) and W (bf16 -> fp32) through threadgroup memory and multiplies 8x8 fp32 tiles.
@@ -267,6 +270,7 @@ gemm_fn pick_x(int xt, bool gated, bool norm) {
 }  // namespace
 
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int /*splitk_override*/) {
+    if (xt == wt && a.norm == nullptr && tuning().gemm_tile != 4) return launch_gemm_tiled(a, wt, stream);
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
     gemm_fn fn = wt == DT_BF16 ? pick_x<DT_BF16>(xt, gated, norm) : pick_x<DT_F16>(xt, gated, norm);

@@ -21,6 +21,8 @@ struct Tuning {
     int gemv_rows_max = 8;
     int gemv_lanes = 0;
     int gemm_splitk = 0;
+    int gemm_tile = 0;
+    int gemm_stages = 0;
     int seq_groups = 0;
     int seq_launch = 0;
 };
@@ -85,5 +87,22 @@ int launch_attention(const float *q, uint32_t ldq, uint32_t rows, uint32_t hq, u
 int gemv_lanes_log2(uint32_t K, int override_lanes);
 int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes);
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int splitk_override);
+
+// Compute units of the current device (cached per device), or <= 0 when it cannot be queried.
+int device_cus();
+// Split-K workspace of `stream` on the current device: at least `part_bytes` of partial sums
+// and `counters` zeroed arrival counters (the kernels leave them zero again).  Grows by
+// synchronising the stream, so it is not for use under graph capture once it must grow.
+int stream_workspace(hipStream_t stream, size_t part_bytes, uint32_t counters, void **part, uint32_t **cnt);
+
+// Pipelined MFMA GEMM for activations of the weights' type.
+struct TiledPlan {
+    int shape;                // index of the (bm, bn) tile shape
+    uint32_t bm, bn;          // x rows and weight rows per tile
+    uint32_t tiles_m, tiles_n, splits, kps;
+    int stages;               // LDS pipeline depth (64-k stages)
+};
+TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, int shape_override, int splitk_override);
+int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream);
 
 }  // namespace mt

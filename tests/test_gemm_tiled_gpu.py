@@ -1,0 +1,119 @@
+"""The pipelined MFMA GEMM (activations of the weights' type) under every tile shape and
+forced split-K count, on ragged shapes, against the oracle's fp32 reference loop and fp64
+recomputation; split-K runs are re-run to show the arrival counters re-arm and the
+partial sums are added in a fixed order (bit-identical results)."""
+import numpy as np
+import pytest
+import torch
+
+import mingtts as mt
+import oracle as O
+from _gpu_util import assert_linear_parity, expected, run_linear, say
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [  # (M, N, K, flags, bias)
+    (77, 100, 200, O.GELU, True),         # ragged everywhere; K tail inside a 64-k stage
+    (130, 260, 136, O.ACCUM, False),      # two x-row tiles of 128 plus 2 rows
+    (64, 70, 896, O.SILU_GATE, True),     # gated, features past N inside the tile
+    (9, 896, 4864, O.ACCUM, False),       # long K, 9 rows
+    (512, 1152, 896, O.BIAS, True),
+    (33, 4864, 896, O.SILU_GATE | O.ACCUM, False),
+    (200, 64, 8, O.SILU, True),           # K = 8: one chunk of one stage
+]
+
+
+def _case(seed, M, N, K, flags, bias, wt):
+    rng = np.random.default_rng(seed)
+    gated = bool(flags & O.SILU_GATE)
+    wb, _ = O.round16(rng.standard_normal((N, K)).astype(np.float32) * np.float32(0.05), wt)
+    w2b = O.round16(rng.standard_normal((N, K)).astype(np.float32) * np.float32(0.05), wt)[0] if gated else wb
+    bb = O.round16(rng.standard_normal(N).astype(np.float32) * np.float32(0.05), wt)[0] if bias else None
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    return dict(m=M, n=N, k=K, flags=flags | (O.BIAS if bias else 0), x=x, w=wb, w2=w2b, bias=bb, y0=y0, wt=wt)
+
+
+def _with_tuning(tile, splits, fn):
+    old_t = mt.set_tuning(mt.TUNE_GEMM_TILE, tile)
+    old_s = mt.set_tuning(mt.TUNE_GEMM_SPLITK, splits)
+    old_r = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, 0)
+    try:
+        return fn()
+    finally:
+        mt.set_tuning(mt.TUNE_GEMM_TILE, old_t)
+        mt.set_tuning(mt.TUNE_GEMM_SPLITK, old_s)
+        mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old_r)
+
+
+def _ids(s):
+    return f"M{s[0]}_N{s[1]}_K{s[2]}_f{s[3]}"
+
+
+@pytest.mark.parametrize("splits", [0, 1, 3, 8])
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_tiles_and_splits(gpu, shape, tile, splits):
+    M, N, K, flags, bias = shape
+    if flags & O.SILU_GATE and tile == 3:
+        pytest.skip("a gated tile always has 128 weight rows")
+    say(f"tiled tile={tile} splits={splits} {_ids(shape)}")
+    c = _case(M * 7 + N + K, M, N, K, flags, bias, O.F16)
+    got, xu = _with_tuning(tile, splits, lambda: run_linear(c, O.F16, gpu))
+    assert_linear_parity(got, *expected(c, xu), K, f"tile {tile} splits {splits} {_ids(shape)}")
+    if splits != 1:
+        again, _ = _with_tuning(tile, splits, lambda: run_linear(c, O.F16, gpu))
+        np.testing.assert_array_equal(again, got)
+
+
+@pytest.mark.parametrize("shape", SHAPES[:4], ids=_ids)
+def test_bf16(gpu, shape):
+    M, N, K, flags, bias = shape
+    say(f"tiled bf16 {_ids(shape)}")
+    c = _case(M + 3 * N + K, M, N, K, flags, bias, O.BF16)
+    got, xu = _with_tuning(0, 0, lambda: run_linear(c, O.BF16, gpu))
+    assert_linear_parity(got, *expected(c, xu), K, f"bf16 {_ids(shape)}")
+
+
+def test_workspace_grows_and_streams_are_independent(gpu):
+    """A small split launch, a much larger one (the workspace grows), then both again on a
+    second stream: every result matches the first run of the same case bit for bit."""
+    small = _case(5, 64, 256, 4864, O.ACCUM, False, O.F16)
+    large = _case(6, 256, 4864, 896, O.SILU_GATE, False, O.F16)
+    say("tiled workspace growth")
+    r_small, xs = _with_tuning(3, 16, lambda: run_linear(small, O.F16, gpu))
+    r_large, xl = _with_tuning(1, 4, lambda: run_linear(large, O.F16, gpu))
+    assert_linear_parity(r_small, *expected(small, xs), 4864, "small split")
+    assert_linear_parity(r_large, *expected(large, xl), 896, "large split")
+    s = torch.cuda.Stream(device=gpu)
+    with torch.cuda.stream(s):
+        again_small, _ = _with_tuning(3, 16, lambda: run_linear(small, O.F16, gpu, stream=s.cuda_stream))
+        again_large, _ = _with_tuning(1, 4, lambda: run_linear(large, O.F16, gpu, stream=s.cuda_stream))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(again_small, r_small)
+    np.testing.assert_array_equal(again_large, r_large)
+
+
+def test_nan_rows_past_m_are_not_read(gpu):
+    """x rows past M hold NaN in memory: the tile's zero-filled rows keep them out."""
+    M, N, K = 70, 96, 192
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((M + 64, K)).astype(np.float32)
+    x[M:] = np.nan
+    wb, _ = O.round16(rng.standard_normal((N, K)).astype(np.float32) * np.float32(0.05), O.F16)
+    xb, xr = O.round16(x, O.F16)
+    from _gpu_util import dev16
+    x_d = dev16(xb, O.F16, gpu)
+    y_d = torch.zeros(M, N, device=gpu)
+    say("tiled NaN rows past M")
+
+    def go():
+        rc = mt.linear_raw(x_d, O.F16, dev16(wb, O.F16, gpu), None, O.F16, None, y_d, M, N, K, K, N, 0, None)
+        assert rc == 0, mt.last_error()
+        torch.cuda.synchronize()
+        return y_d.cpu().numpy()
+
+    got = _with_tuning(1, 2, go)
+    want64 = O.linear_f64(xr[:M], wb, None, O.F16, None, None, M, N, K, 0)
+    assert np.all(np.isfinite(got))
+    assert O.normwise_rel_err(got, want64) <= 1e-5
