@@ -17,29 +17,24 @@
 //   - user buffers: an op reads a user buffer only where nothing earlier in the sequence
 //     wrote it, and writes a user buffer only if it is the last op writing that region
 //     (the host plan compiler resolves both), so every user element is written once per run.
-// Inside a workgroup (512 threads, one per CU) the waves split by role, because a wave's
-// vector loads retire in order: a wave that waits for activations must not have weight
-// loads queued in front of them.
-//   - LW loader waves walk the ops ahead of the computation and stream the workgroup's
-//     weight tiles (the MFMA A operands: 16 rows x 32 k, one 16-byte chunk per lane, as
-//     seq_tiles.hpp cuts them) straight into an LDS ring with global_load_lds_dwordx4.
-//     An empty slot holds all-ones bytes (fp16 / bf16 NaN pairs, never a weight chunk): a
-//     compute wave knows its tile has landed when its lane's 16 bytes are no longer all
-//     ones, and refills the slot with all ones once it has read it.  A slot is reused once
-//     every compute wave has moved past the tile in it (per-wave LDS watermarks).
-//   - CW compute waves each own a contiguous range of an op's tiles.  Per op a compute
-//     wave polls the activation chunks its tiles need (16-byte device-coherent loads of
-//     tagged words, re-requesting only stale ones), converts each element once (tag
+// Inside a workgroup (512 threads, one per CU) every wave computes.  A wave owns a
+// contiguous range of each op's MFMA tiles (16 weight rows x 32 k, one 16-byte chunk per
+// lane, as seq_tiles.hpp cuts them) and keeps them in registers, loaded one op ahead:
+//   - a wave's vector loads retire in order, so per op it issues its activation loads
+//     first and the next op's weight tiles after them; waiting for the activations then
+//     never waits for the weight stream, which lands while the op computes;
+//   - per op a wave polls the activation chunks it stages (16-byte device-coherent loads
+//     of tagged words, re-requesting only stale ones) and converts each element once (tag
 //     clear, x^2 for the RMSNorm sum, gain, fp32 -> hi + lo pair of the weights' 16-bit
-//     type) into its LDS B staging, then runs two MFMAs per tile with A from the ring,
-//     writing finished row tiles' partial sums to LDS.  The compute waves meet at an LDS
-//     counter; one lane per output sums the partials in a fixed order, applies the norm
-//     scale and the epilogue and stores the tagged word (and the user output when final).
-// LDS partial sums, sums of squares and gains alternate between two buffers by op parity,
-// so one compute-wave meeting per op suffices.  Every wait is bounded: past SPIN_LIMIT
-// polls a lane gives up, sets the plan's timeout flag (read by mt_seq_check) and stops
-// waiting for the rest of the run.  An fp16 weight sequence also flags activations beyond
-// the fp16 range (the hi part would overflow).
+//     type) into the workgroup's LDS B staging; after a workgroup barrier it runs two
+//     MFMAs per tile (hi and lo) and writes finished row tiles' partial sums to LDS; after
+//     a second barrier one lane per output sums the partials in a fixed order, applies the
+//     norm scale and the epilogue and stores the tagged word (and the user output when
+//     final).
+// LDS partial sums, sums of squares and gains alternate between two buffers by op parity.
+// Every wait is bounded: past SPIN_LIMIT polls a lane gives up, sets the plan's timeout
+// flag (read by mt_seq_check) and stops waiting for the rest of the run.  An fp16 weight
+// sequence also flags activations beyond the fp16 range (the hi part would overflow).
 #include <stdlib.h>
 #include <string.h>
 
@@ -116,15 +111,16 @@ __device__ __forceinline__ uint32_t round16(float x) {
     else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 
-constexpr int CW = SEQ_CW;             // compute waves
-constexpr int LW = NW - CW;            // loader waves
-constexpr int RING = SEQ_RING;         // weight tile slots of 1 KB
+constexpr int CW = SEQ_CW;             // waves (all compute)
 constexpr int CTHREADS = CW * 64;
-constexpr int TA = SEQ_TA;              // weight tiles a compute wave holds per op
+constexpr int TA = SEQ_TA;              // weight tiles a wave holds per op
 constexpr int CGCH = SEQ_GMAX / 8 / CTHREADS + ((SEQ_GMAX / 8) % CTHREADS ? 1 : 0);
-constexpr int OUTR = (SEQ_RMAX * 8 + CTHREADS - 1) / CTHREADS;  // outputs per compute thread
-enum : int { CTL_CONSUMED = 0, CTL_CBAR = 8, CTL_WORDS = 16 };
-static_assert(LW >= 1 && LW <= 4 && CW <= 8, "wave roles");
+constexpr int OUTR = (SEQ_RMAX * 8 + CTHREADS - 1) / CTHREADS;  // outputs per thread
+static_assert(CW == NW, "every wave computes");
+constexpr int XPAD = 256;  // LDS staging padding past M K: the largest B over-read is 32 S + 8 elements
+
+// Loaded in place of a weight chunk outside the op's share (padding rows, K tails).
+__device__ __attribute__((aligned(16))) uint32_t g_zero_chunk[4];
 
 typedef __attribute__((address_space(3))) void *lds_vp;
 
@@ -147,108 +143,61 @@ __device__ __forceinline__ void split4p(const float (&x)[4], u32x2 &hi, u32x2 &l
     lo = u32x2{pack2<T>(x[0] - dec_lo<T>(h0), x[1] - dec_hi<T>(h0)), pack2<T>(x[2] - dec_lo<T>(h1), x[3] - dec_hi<T>(h1))};
 }
 
-// A compute wave's tiles of op o.
+// A wave's tiles of an op: the contiguous range [t0, t0 + n) of the workgroup's tiles,
+// starting at row tile rt0, block step j0 (staged in LDS for every op at kernel start).
 struct WaveTiles {
-    SeqTiles s;
-    uint32_t t0, n;    // first tile, tile count
-    uint32_t rt0, j0;  // row tile and block step of t0
+    uint16_t t0, n, rt0, j0;
 };
 __device__ __forceinline__ WaveTiles wave_tiles(const SeqTiles &st, uint32_t w) {
     WaveTiles wt;
-    wt.s = st;
-    wt.t0 = seq_tile_begin(wt.s.T, w, CW);
-    wt.n = seq_tile_begin(wt.s.T, w + 1, CW) - wt.t0;
-    wt.rt0 = wt.s.KBs ? wt.t0 / wt.s.KBs : 0;
-    wt.j0 = wt.t0 - wt.rt0 * wt.s.KBs;
+    const uint32_t t0 = seq_tile_begin(st.T, w, CW);
+    wt.t0 = static_cast<uint16_t>(t0);
+    wt.n = static_cast<uint16_t>(seq_tile_begin(st.T, w + 1, CW) - t0);
+    const uint32_t rt0 = st.KBs ? t0 / st.KBs : 0;
+    wt.rt0 = static_cast<uint16_t>(rt0);
+    wt.j0 = static_cast<uint16_t>(t0 - rt0 * st.KBs);
     return wt;
 }
-
-// A ring slot read that the compiler neither caches nor moves.
-__device__ __forceinline__ u32x4 ring_ld(const u32x4 *p) {
-    typedef __attribute__((address_space(3))) const volatile u32x4 *lds_cvp;
-    return *reinterpret_cast<lds_cvp>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_vp)(p))));
-}
-// 1 when a lane's chunk is still the empty-slot pattern.
-__device__ __forceinline__ uint32_t unsent(const u32x4 a) { return (a.x & a.y & a.z & a.w) == ~0u ? 1u : 0u; }
 
 // LDS word access that the compiler neither reorders nor caches.
 __device__ __forceinline__ uint32_t lds_ld(const uint32_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ void lds_st(uint32_t *p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
 
-// One weight tile into LDS at byte address slot: lane l's 16 bytes from gaddr land at
-// slot + 16 l (nontemporal: the stream does not displace L2 lines).  Issued as inline
-// assembly so that the compiler's wait-count analysis does not see an LDS write in flight
-// (it would drain the loads before every LDS access); readiness is the slot's content.
-__device__ __forceinline__ void dma_tile(uint32_t slot, const void *gaddr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(slot), "v"(gaddr) : "memory", "m0");
-}
-
-// Loader wave l: every tile of every op whose sequence number is l mod LW, in order.
-__device__ void loader(const SeqOp *desc, const SeqTiles *tiles, uint32_t n_ops, uint32_t l, uint32_t ring_base,
-                       uint32_t *ctl, uint32_t *sync) {
+// A wave's weight tiles of op o into registers (nontemporal 16-byte loads: the stream does
+// not displace L2 lines).  All TA loads are issued whatever the wave's tile count (unused
+// ones read the zero chunk), so the number of loads behind the activations is fixed and
+// the activation wait never drains them.
+__device__ __forceinline__ void tile_loads(const SeqOp &o, const SeqTiles &s, const WaveTiles &wt, u32x4 (&A)[TA]) {
     const uint32_t lane = threadIdx.x & 63, a = lane & 15, q = lane >> 4;
-    uint32_t seq_base = 0;   // sequence number of the op's tile 0
-    uint32_t freed = 0;      // every compute wave is past tile freed - 1 (last read)
-    bool stop = false;
-    for (uint32_t i = 0; i < n_ops && !stop; i++) {
-        const SeqOp o = desc[i];  // by value: read once, kept in registers
-        const SeqTiles s = tiles[i];
-        const uint16_t *const w1 = o.w, *const w2 = o.w2;
-        const uint32_t K = o.K;
-        // Per lane: segment and virtual row of the lane's A row (interleaved when packed).
-        const uint32_t sa = a & (s.S - 1);
-        const uint32_t va = a >> s.ls;
-        const uint32_t kbase = sa * s.KBs * 32 + q * 8;  // k of the lane's chunk at block step 0
-        uint32_t t = (l + LW - seq_base % LW) % LW;  // first tile of this op that is ours
-        uint32_t rt = s.KBs ? t / s.KBs : 0, j = t - rt * s.KBs;
-        uint32_t row_rt = ~0u;
-        const uint16_t *row = w1;
-        bool row_ok = false;
-        for (; t < s.T; t += LW) {
-            const uint32_t seq = seq_base + t;
-            // The slot is free once every compute wave has moved past the tile RING back.
-            if (seq >= static_cast<uint32_t>(RING) && freed <= seq - RING) {
-                uint32_t spins = 0;
-                for (;;) {
-                    uint32_t mn = lds_ld(ctl + CTL_CONSUMED);
+    const uint32_t sa = a & (s.S - 1), va = a >> s.ls;
+    const uint32_t kbase = sa * s.KBs * 32 + q * 8;  // k of the lane's chunk at block step 0
+    // The lane's chunks are real for block steps j < jlim (its segment's blocks, k < K).
+    const uint32_t jseg = s.KB > sa * s.KBs ? s.KB - sa * s.KBs : 0u;
+    const uint32_t jk = o.K > kbase ? (o.K - kbase + 31) / 32 : 0u;
+    const uint32_t jlim = jseg < jk ? jseg : jk;
+    // The lane's weight row in row tile rt (a wave's tiles span at most two row tiles).
+    auto row_of = [&](uint32_t rt, bool &ok) {
+        const uint32_t vrow = s.S > 1 ? va : rt * 16 + a;
+        const bool up = vrow >= s.nr;
+        ok = vrow < s.V;
+        return (up ? o.w2 : o.w) + static_cast<size_t>(s.r0 + (up ? vrow - s.nr : vrow)) * o.K + kbase;
+    };
+    bool rok;
+    const uint16_t *p = row_of(wt.rt0, rok) + wt.j0 * 32u;
+    uint32_t j = wt.j0;
+    const u32x4 *zero = reinterpret_cast<const u32x4 *>(g_zero_chunk);
 #pragma unroll
-                    for (int w = 1; w < CW; w++) mn = min(mn, lds_ld(ctl + CTL_CONSUMED + w));
-                    freed = mn;
-                    if (mn > seq - RING) break;
-                    if (++spins > SPIN_LIMIT) {
-                        raise_flag(sync, SYNC_TIMEOUT);
-                        stop = true;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                if (stop) break;
-            }
-            if (rt != row_rt) {  // the lane's weight row for this row tile
-                row_rt = rt;
-                const uint32_t vrow = s.S > 1 ? va : rt * 16 + a;
-                const bool up = vrow >= s.nr;
-                row_ok = vrow < s.V;
-                row = row_ok ? (up ? w2 : w1) + static_cast<size_t>(s.r0 + (up ? vrow - s.nr : vrow)) * K : w1;
-            }
-            // Lanes outside the share (padding rows, K tail) fetch the first chunk of w
-            // instead; their rows and k are never used.
-            const uint32_t k0 = kbase + j * 32;
-            const bool ok = row_ok && sa * s.KBs + j < s.KB && k0 < K;
-            dma_tile(ring_base + (seq % RING) * 1024u, ok ? row + k0 : w1);
-            j += LW;
-            while (j >= s.KBs) {
-                j -= s.KBs;
-                rt++;
-            }
+    for (int k = 0; k < TA; k++) {
+        const bool ok = static_cast<uint32_t>(k) < wt.n && rok && j < jlim;
+        const u32x4 *src = ok ? reinterpret_cast<const u32x4 *>(p) : zero;
+        A[k] = __builtin_nontemporal_load(reinterpret_cast<gw_cp>(reinterpret_cast<uintptr_t>(src)));
+        p += 32;
+        if (++j == s.KBs) {
+            j = 0;
+            p = row_of(wt.rt0 + 1u, rok);
         }
-        seq_base += s.T;
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Sum over aligned lane pairs / quads of a wave (fixed order).
@@ -290,12 +239,15 @@ __device__ __forceinline__ void flush(const f32x4 acc, const SeqTiles &s, uint32
 
 // The RMSNorm gain of op o into LDS gb (16-bit, K elements) by the compute threads:
 // requested before a wait, stored after it.
-__device__ __forceinline__ void gain_request(const SeqOp &o, u32x4 (&gr)[CGCH]) {
-    if (!o.norm) return;
+__device__ __forceinline__ void gain_request(const SeqOp &o, bool live, u32x4 (&gr)[CGCH]) {
+    // Issued whether or not the op has a gain (then it reads the first chunks of w), so the
+    // number of loads in flight behind the activations does not depend on the op.
+    const bool use = live && o.norm != nullptr;
+    const uint16_t *src = use ? o.norm : o.w;
 #pragma unroll
     for (int r = 0; r < CGCH; r++) {  // no lane-divergent branch around the loads
         const uint32_t ch = threadIdx.x + r * CTHREADS;
-        gr[r] = gld(reinterpret_cast<const u32x4 *>(o.norm + (ch * 8 < o.K ? ch * 8 : 0u)));
+        gr[r] = gld(reinterpret_cast<const u32x4 *>(src + (use && ch * 8 < o.K ? ch * 8 : 0u)));
     }
 }
 __device__ __forceinline__ void gain_store(const SeqOp &o, const u32x4 (&gr)[CGCH], uint16_t *gb) {
@@ -307,21 +259,18 @@ __device__ __forceinline__ void gain_store(const SeqOp &o, const u32x4 (&gr)[CGC
     }
 }
 
-// The compute waves' meeting after op i: an LDS counter every compute wave bumps once per
-// op (bounded wait).
-__device__ __forceinline__ void compute_meet(uint32_t *ctl, uint32_t target, uint32_t *sync, bool &gave_up) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctl + CTL_CBAR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    uint32_t spins = 0;
-    while (lds_ld(ctl + CTL_CBAR) < target && !gave_up) {
-        if (++spins > SPIN_LIMIT) {
-            gave_up = true;
-            raise_flag(sync, SYNC_TIMEOUT);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(0);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+// Sum over the 64 lanes of a wave in a fixed order: DPP within rows of 16 (quad swaps,
+// then half-row and row mirrors), then the four rows' sums.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    const int iv = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
 }
 
 // One 512-thread workgroup per CU runs every op of the sequence in order (see the top of
@@ -330,41 +279,33 @@ __device__ __forceinline__ void compute_meet(uint32_t *ctl, uint32_t target, uin
 template <int WT>
 __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
                                                          uint32_t *sync, const uint32_t *tags, uint32_t tag_bytes) {
-    __shared__ __attribute__((aligned(1024))) u32x4 ring[RING][64];
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][SEQ_XLDS];  // the op's x as [hi, lo][M][K]
+    // The op's x as [hi, lo][M][K]; MFMA B reads past M K (K tails) land in the padding,
+    // which holds zeros or earlier ops' finite values.
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][SEQ_XLDS + XPAD];
     __shared__ __attribute__((aligned(16))) float part[2][CW * PARTW];
     __shared__ __attribute__((aligned(16))) uint16_t gbuf[2][SEQ_GMAX];
     __shared__ float ssw[2][CW * 8];
-    __shared__ uint32_t ctl[CTL_WORDS];
     __shared__ __attribute__((aligned(16))) SeqOp sdesc[SEQ_OPS_MAX];
     __shared__ SeqTiles stile[SEQ_OPS_MAX];
+    __shared__ WaveTiles swt[SEQ_OPS_MAX][CW];
     const uint32_t G = gridDim.x, g = blockIdx.x;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     // The op descriptors and this workgroup's tiling of every op, staged in LDS once (no
-    // op then waits for a descriptor load); an empty ring; each compute wave's next tile is
-    // its first of op 0.
+    // op then waits for a descriptor load).
     for (uint32_t e = tid; e < n_ops * (sizeof(SeqOp) / 16); e += SEQ_THREADS)
         reinterpret_cast<u32x4 *>(sdesc)[e] = gld(reinterpret_cast<const u32x4 *>(ops) + e);
-    for (uint32_t e = tid; e < RING * 64u; e += SEQ_THREADS) (&ring[0][0])[e] = u32x4{~0u, ~0u, ~0u, ~0u};
+    for (uint32_t e = tid; e < 2 * (SEQ_XLDS + XPAD) / 8; e += SEQ_THREADS)
+        reinterpret_cast<u32x4 *>(&xs[0][0])[e] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
     for (uint32_t t = tid; t < n_ops; t += SEQ_THREADS) {
         const SeqOp &o = sdesc[t];
         stile[t] = seq_tiles(o.N, o.K, o.M, (o.flags & F_SILU_GATE) != 0, g, G);
     }
     __syncthreads();
-    if (tid < CTL_WORDS) {
-        uint32_t v = 0;
-        if (tid >= CTL_CONSUMED && tid < CTL_CONSUMED + CW && n_ops > 0) v = wave_tiles(stile[0], tid - CTL_CONSUMED).t0;
-        ctl[tid] = v;
-    }
+    for (uint32_t e = tid; e < n_ops * CW; e += SEQ_THREADS) swt[e / CW][e % CW] = wave_tiles(stile[e / CW], e % CW);
     __syncthreads();
-    if (w >= static_cast<uint32_t>(CW)) {
-        const uint32_t ring_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_vp)(&ring[0][0])));
-        loader(sdesc, stile, n_ops, w - CW, ring_base, ctl, sync);
-        return;
-    }
 
     const uint32_t epoch = __hip_atomic_load(sync + SYNC_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t parity = epoch & 1u;
@@ -372,18 +313,19 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(tags), 0, static_cast<int>(tag_bytes), BUF_DWORD3);
     bool gave_up = false;
     u32x4 gr[CGCH];
-    uint32_t seq_base = 0;
+    u32x4 A[TA];  // this op's weight tiles
 
     if (n_ops > 0) {
-        gain_request(sdesc[0], gr);
+        gain_request(sdesc[0], true, gr);
+        tile_loads(sdesc[0], stile[0], swt[0][w], A);
         gain_store(sdesc[0], gr, gbuf[0]);
-        compute_meet(ctl, CW, sync, gave_up);
+        __syncthreads();
     }
     for (uint32_t i = 0; i < n_ops; i++) {
         const int b = i & 1;
         const SeqOp o = sdesc[i];  // by value: read once, kept in registers
-        const WaveTiles wt = wave_tiles(stile[i], w);
-        const SeqTiles &s = wt.s;
+        const SeqTiles s = stile[i];
+        const WaveTiles wt = swt[i][w];
         const uint32_t M = o.M;
         const bool norm = o.norm != nullptr;
 
@@ -398,16 +340,24 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
         // of the tag buffer, which returns zeros): a load under a lane-divergent branch makes
         // the compiler wait for every load in flight where the branch rejoins.
         u32x4 xv[XCH];
+        if (!ext) {
+            // Tagged chunks: all XCH loads issued (chunks past the op read past the end of
+            // the tag buffer, which returns zeros), so the count of loads behind them is
+            // fixed.
 #pragma unroll
-        for (int r = 0; r < XCH; r++) {
-            xv[r] = u32x4{0u, 0u, 0u, 0u};
-            if (static_cast<uint32_t>(r) < rows_used) {
+            for (int r = 0; r < XCH; r++) {
                 const uint32_t e = tid + CTHREADS * r;
                 const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
                 const bool ok = e < nchunk;
-                if (!ext) {
-                    xv[r] = ldtag4(rsrc, ok ? (o.xoff + m * o.xld + k) * 4u : 0xFFFFFFF0u);
-                } else if (ok) {
+                xv[r] = ldtag4(rsrc, ok ? (o.xoff + m * o.xld + k) * 4u : 0xFFFFFFF0u);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < XCH; r++) {
+                xv[r] = u32x4{0u, 0u, 0u, 0u};
+                const uint32_t e = tid + CTHREADS * r;
+                if (static_cast<uint32_t>(r) < rows_used && e < nchunk) {
+                    const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
                     if (o.xt == DT_F32) {
                         const float *p = static_cast<const float *>(o.x) + static_cast<size_t>(m) * o.ldx + k;
                         xv[r] = u32x4{__float_as_uint(gld(p)), __float_as_uint(gld(p + 1)), __float_as_uint(gld(p + 2)),
@@ -445,71 +395,30 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                                 (live_out ? static_cast<size_t>(om) * o.ldy + s.r0 + ov : 0u));
             }
         }
-        // The next op's RMSNorm gain, stored to LDS after this op's MFMAs.
+        // The next op's RMSNorm gain (stored to LDS after this op's MFMAs) and weight tiles,
+        // requested behind the activations.
         const bool next = i + 1 < n_ops;
         const SeqOp on = sdesc[next ? i + 1 : i];
-        const WaveTiles wtn = wave_tiles(stile[next ? i + 1 : i], w);
-        if (next) gain_request(on, gr);
+        const SeqTiles sn = stile[next ? i + 1 : i];
+        const WaveTiles wtn = swt[next ? i + 1 : i][w];
+        gain_request(on, next, gr);
+        u32x4 An[TA];
+        tile_loads(on, sn, wtn, An);
 
-        // The wave's weight tiles (MFMA A operands) from the ring into registers while the
-        // activations are in flight; their slots are freed right away.
-        const uint32_t seq0 = seq_base + wt.t0;
-        const uint32_t sa = (lane & 15) & (s.S - 1), qa = lane >> 4;
-        // K tails (K % 32, or a last segment shorter than KBs): chunks past K are zeros (the
-        // ring holds filler there).
-        const bool tails = (K & 31u) != 0 || s.S * s.KBs != s.KB;
-        u32x4 A[TA];
-#pragma unroll
-        for (int k = 0; k < TA; k++) {
-            A[k] = u32x4{0u, 0u, 0u, 0u};
-            if (static_cast<uint32_t>(k) < wt.n) A[k] = ring[(seq0 + k) % RING][lane];
-        }
-        {
-            uint32_t spins = 0;
-            for (;;) {  // every lane's chunk of every tile landed?
-                uint32_t miss = 0;
-#pragma unroll
-                for (int k = 0; k < TA; k++)
-                    if (static_cast<uint32_t>(k) < wt.n) miss |= unsent(A[k]);
-                if (!__ballot(miss) || gave_up) break;
-                if (++spins > SPIN_LIMIT) {
-                    gave_up = true;
-                    raise_flag(sync, SYNC_TIMEOUT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(0);
-#pragma unroll
-                for (int k = 0; k < TA; k++)
-                    if (static_cast<uint32_t>(k) < wt.n && __ballot(unsent(A[k])))
-                        A[k] = ring_ld(&ring[(seq0 + k) % RING][lane]);
-            }
-        }
-        {
-            uint32_t j = wt.j0;
-#pragma unroll
-            for (int k = 0; k < TA; k++) {
-                if (static_cast<uint32_t>(k) < wt.n) {
-                    ring[(seq0 + k) % RING][lane] = u32x4{~0u, ~0u, ~0u, ~0u};  // the slot is empty again
-                    if (tails && (sa * s.KBs + j) * 32 + qa * 8 >= K) A[k] = u32x4{0u, 0u, 0u, 0u};
-                    if (++j == s.KBs) j = 0;
-                }
-            }
-        }
-        // Nothing more of this op's tiles: the wave's next tile is its first of op i + 1.
-        const uint32_t next_first = seq_base + s.T + (next ? wtn.t0 : 0u);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        if (lane == 0) lds_st(ctl + CTL_CONSUMED + w, next_first);
-
-        // Wait for the tagged chunks: every round re-requests all stale ones at once.
+        // Wait for the tagged chunks: every round re-requests all stale ones at once.  The
+        // first check stands outside the loop, so its wait covers the activations alone and
+        // not the weight tiles requested behind them.
         if (!ext) {
-            uint32_t spins = 0;
-            while (!gave_up) {
+            auto stale_mask = [&]() {
                 uint32_t stale = 0;
 #pragma unroll
                 for (int r = 0; r < XCH; r++)
-                    if (static_cast<uint32_t>(r) < rows_used && tid + CTHREADS * r < nchunk && !tagged4(xv[r], parity))
-                        stale |= 1u << r;
-                if (!stale) break;
+                    if (tid + CTHREADS * r < nchunk && !tagged4(xv[r], parity)) stale |= 1u << r;
+                return stale;
+            };
+            uint32_t stale = stale_mask();
+            uint32_t spins = 0;
+            while (stale && !gave_up) {
                 if (++spins > SPIN_LIMIT) {
                     gave_up = true;
                     raise_flag(sync, SYNC_TIMEOUT);
@@ -518,12 +427,13 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                 __builtin_amdgcn_s_sleep(1);
 #pragma unroll
                 for (int r = 0; r < XCH; r++) {
-                    if (static_cast<uint32_t>(r) < rows_used && ((stale >> r) & 1u)) {
+                    if ((stale >> r) & 1u) {
                         const uint32_t e = tid + CTHREADS * r;
                         const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
                         xv[r] = ldtag4(rsrc, (o.xoff + m * o.xld + k) * 4u);
                     }
                 }
+                stale = stale_mask();
             }
         }
         // Convert: hi = x rounded toward zero to the weights' 16-bit type (to nearest for
@@ -571,50 +481,52 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
 #pragma unroll
             for (int mm = 0; mm < 8; mm++) {
                 if (static_cast<uint32_t>(mm) < M) {
-                    float t = ssr[mm];
-                    for (int bit = 1; bit < 64; bit <<= 1) t += __shfl_xor(t, bit, 64);
+                    const float t = wave_sum(ssr[mm]);
                     if (lane == 0) ssw[b][w * 8 + mm] = t;
                 }
             }
         }
-        compute_meet(ctl, CW * (2 * i + 2), sync, gave_up);
+        __syncthreads();  // the op's x is staged
 
         // MFMAs over the wave's tiles (hi and lo in two accumulators), A in registers, B from
-        // the staging (lane (bc, q) reads column bc: x row bc / S over segment bc % S, 8 k);
-        // a finished row tile goes to LDS.
+        // the staging (lane (bc, q) reads column bc: x row bc / S over segment bc % S, 8 k).
+        // The wave's tiles span at most two row tiles (the plan checks it): tiles [0, ks) are
+        // in row tile rt0 and the rest in rt0 + 1, each with its own accumulators, flushed to
+        // LDS at the end.  B chunks past K meet zero A chunks (and hold finite values).
         float *pw = part[b] + w * PARTW;
         {
             const uint32_t bc = lane & 15, q = lane >> 4;
-            const uint32_t SM = s.S * M;
             const uint32_t bkb = (bc & (s.S - 1)) * s.KBs;              // segment's first block
             const uint32_t boff = (bc >> s.ls) * K + bkb * 32 + q * 8;  // + 32 j: the tile's 8 k
-            const bool bcol = bc < SM;
-            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;
-            uint32_t rt = wt.rt0, j = wt.j0;
+            const bool bcol = bc < s.S * M;
+            const uint32_t n = wt.n;
+            const uint32_t ks = min(n, s.KBs - wt.j0);
+            f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a0l = a0, a1 = a0, a1l = a0;
+            uint32_t bo = boff + wt.j0 * 32u;
 #pragma unroll
             for (int k = 0; k < TA; k++) {
-                if (static_cast<uint32_t>(k) < wt.n) {
+                if (static_cast<uint32_t>(k) < n) {
+                    if (static_cast<uint32_t>(k) == ks) bo = boff;
                     u32x4 bh = {0u, 0u, 0u, 0u}, bl = bh;
-                    if (bcol && (!tails || (bkb + j < s.KB && (bkb + j) * 32 + q * 8 < K))) {
-                        bh = *reinterpret_cast<const u32x4 *>(&xs[0][boff + j * 32]);
-                        bl = *reinterpret_cast<const u32x4 *>(&xs[1][boff + j * 32]);
+                    if (bcol) {
+                        bh = *reinterpret_cast<const u32x4 *>(&xs[0][bo]);
+                        bl = *reinterpret_cast<const u32x4 *>(&xs[1][bo]);
                     }
-                    acc = mfma16<WT>(A[k], bh, acc);
-                    acc2 = mfma16<WT>(A[k], bl, acc2);
-                    if (++j == s.KBs || static_cast<uint32_t>(k) + 1 == wt.n) {
-                        flush(acc + acc2, s, M, rt, pw);
-                        acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                        acc2 = acc;
+                    if (static_cast<uint32_t>(k) < ks) {
+                        a0 = mfma16<WT>(A[k], bh, a0);
+                        a0l = mfma16<WT>(A[k], bl, a0l);
+                    } else {
+                        a1 = mfma16<WT>(A[k], bh, a1);
+                        a1l = mfma16<WT>(A[k], bl, a1l);
                     }
-                    if (j == s.KBs) {
-                        j = 0;
-                        rt++;
-                    }
+                    bo += 32;
                 }
             }
+            if (n > 0) flush(a0 + a0l, s, M, wt.rt0, pw);
+            if (n > ks) flush(a1 + a1l, s, M, wt.rt0 + 1u, pw);
         }
         if (next) gain_store(on, gr, gbuf[b ^ 1]);
-        compute_meet(ctl, CW * (2 * i + 3), sync, gave_up);
+        __syncthreads();  // every wave's partial sums are in LDS
 
         // Outputs: sums of the waves' partials in wave order.
 #pragma unroll
@@ -676,7 +588,8 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                 *reinterpret_cast<__attribute__((address_space(1))) float *>(
                     reinterpret_cast<uintptr_t>(o.y + static_cast<size_t>(om) * o.ldy + n)) = v;
         }
-        seq_base += s.T;
+#pragma unroll
+        for (int k = 0; k < TA; k++) A[k] = An[k];
     }
     // The last workgroup out advances the epoch for the next run.
     if (threadIdx.x == 0) {

@@ -56,15 +56,14 @@ struct SeqOp {
 static_assert(sizeof(SeqOp) % 16 == 0, "SeqOp is staged into LDS in 16-byte pieces");
 struct SeqPlan;
 // Limits of the persistent sequence kernel: threads per workgroup, output features per
-// workgroup per op, and the LDS areas of its compute waves.
+// workgroup per op, and the LDS areas of its waves.
 constexpr int SEQ_THREADS_N = 512;
 constexpr int SEQ_RMAX = 64;
 constexpr int SEQ_PARTW = 128;     // partial sums per compute wave per op: virtual rows * M
 constexpr int SEQ_XLDS = 10240;    // M * K of an op: its activations staged in LDS (hi + lo)
 constexpr int SEQ_OPS_MAX = 96;    // ops of a sequence (their descriptors are staged in LDS)
-constexpr int SEQ_CW = 6;          // compute waves per workgroup (the other waves load weights)
-constexpr int SEQ_TA = 16;         // MFMA tiles of one op a compute wave holds in registers
-constexpr int SEQ_RING = 88;       // LDS ring of 1 KB weight tiles
+constexpr int SEQ_CW = 8;          // waves per workgroup, each computing a share of every op
+constexpr int SEQ_TA = 12;         // MFMA tiles of one op a wave holds in registers
 constexpr int SEQ_GMAX = 2048;     // K of an op with an RMSNorm gain (staged in LDS)
 // Workgroup count of the persistent kernel on the current device.
 int seq_limits(int *groups);

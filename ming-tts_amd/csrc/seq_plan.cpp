@@ -98,6 +98,17 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
         for (int g = 0; g < groups; g++) {
             const SeqTiles t = seq_tiles(p.N, p.K, p.M, (p.flags & MT_SILU_GATE) != 0, g, groups);
             const uint32_t per_wave = (t.T + SEQ_CW - 1) / SEQ_CW;
+            // A wave's contiguous tile range may span at most two row tiles.
+            uint32_t span = 1;
+            for (int w = 0; w < SEQ_CW; w++) {
+                const uint32_t t0 = seq_tile_begin(t.T, w, SEQ_CW), t1 = seq_tile_begin(t.T, w + 1, SEQ_CW);
+                if (t1 > t0 && t.KBs) span = std::max(span, (t1 - 1) / t.KBs - t0 / t.KBs + 1);
+            }
+            if (span > 2)
+                return set_error(MT_ENOTSUP,
+                                 "mt_seq_create: op %u: a wave's share of the tiles spans %u row tiles of 16 weight "
+                                 "rows (K = %u is too short for the sequence kernel's limit of 2)",
+                                 i, span, p.K);
             if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || t.V * p.M > static_cast<uint32_t>(SEQ_PARTW) ||
                 per_wave > static_cast<uint32_t>(SEQ_TA))
                 return set_error(MT_ENOTSUP,
