@@ -21,8 +21,8 @@
 // contiguous range of each op's MFMA tiles (16 weight rows x 32 k, one 16-byte chunk per
 // lane, as seq_tiles.hpp cuts them) and keeps them in registers, loaded one op ahead:
 //   - a wave's vector loads retire in order, so per op it issues its activation loads
-//     first and the next op's weight tiles after them; waiting for the activations then
-//     never waits for the weight stream, which lands while the op computes;
+//     first and the next op's weight tiles right after them; waiting for the activations
+//     then never waits for the weight stream, which lands while the op computes;
 //   - per op a wave polls the activation chunks it stages (16-byte device-coherent loads
 //     of tagged words, re-requesting only stale ones) and converts each element once (tag
 //     clear, x^2 for the RMSNorm sum, gain, fp32 -> hi + lo pair of the weights' 16-bit
@@ -165,9 +165,11 @@ __device__ __forceinline__ uint32_t lds_ld(const uint32_t *p) {
 }
 
 // A wave's weight tiles of op o into registers (nontemporal 16-byte loads: the stream does
-// not displace L2 lines).  All TA loads are issued whatever the wave's tile count (unused
-// ones read the zero chunk), so the number of loads behind the activations is fixed and
-// the activation wait never drains them.
+// not displace L2 lines), exactly NL loads whatever the wave's tile count, so that the
+// number of loads in flight behind the activations is known where they are awaited;
+// chunks outside the share (padding rows, K tails, tiles past the wave's count) read the
+// zero chunk.
+template <int NL>
 __device__ __forceinline__ void tile_loads(const SeqOp &o, const SeqTiles &s, const WaveTiles &wt, u32x4 (&A)[TA]) {
     const uint32_t lane = threadIdx.x & 63, a = lane & 15, q = lane >> 4;
     const uint32_t sa = a & (s.S - 1), va = a >> s.ls;
@@ -188,7 +190,7 @@ __device__ __forceinline__ void tile_loads(const SeqOp &o, const SeqTiles &s, co
     uint32_t j = wt.j0;
     const u32x4 *zero = reinterpret_cast<const u32x4 *>(g_zero_chunk);
 #pragma unroll
-    for (int k = 0; k < TA; k++) {
+    for (int k = 0; k < NL; k++) {  // exactly NL loads: tiles past the wave's n read the zero chunk
         const bool ok = static_cast<uint32_t>(k) < wt.n && rok && j < jlim;
         const u32x4 *src = ok ? reinterpret_cast<const u32x4 *>(p) : zero;
         A[k] = __builtin_nontemporal_load(reinterpret_cast<gw_cp>(reinterpret_cast<uintptr_t>(src)));
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
 
     if (n_ops > 0) {
         gain_request(sdesc[0], true, gr);
-        tile_loads(sdesc[0], stile[0], swt[0][w], A);
+        tile_loads<TA>(sdesc[0], stile[0], swt[0][w], A);
         gain_store(sdesc[0], gr, gbuf[0]);
         __syncthreads();
     }
@@ -341,15 +343,17 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
         // the compiler wait for every load in flight where the branch rejoins.
         u32x4 xv[XCH];
         if (!ext) {
-            // Tagged chunks: all XCH loads issued (chunks past the op read past the end of
-            // the tag buffer, which returns zeros), so the count of loads behind them is
-            // fixed.
+            // Tagged chunks (lanes past the op read past the end of the tag buffer, which
+            // returns zeros).
 #pragma unroll
             for (int r = 0; r < XCH; r++) {
-                const uint32_t e = tid + CTHREADS * r;
-                const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
-                const bool ok = e < nchunk;
-                xv[r] = ldtag4(rsrc, ok ? (o.xoff + m * o.xld + k) * 4u : 0xFFFFFFF0u);
+                xv[r] = u32x4{0u, 0u, 0u, 0u};
+                if (static_cast<uint32_t>(r) < rows_used) {  // uniform; the tiles requested after these are not
+                    const uint32_t e = tid + CTHREADS * r;
+                    const uint32_t m = __umulhi(e, k4magic), k = (e - m * K4) * 4;
+                    const bool ok = e < nchunk;
+                    xv[r] = ldtag4(rsrc, ok ? (o.xoff + m * o.xld + k) * 4u : 0xFFFFFFF0u);
+                }
             }
         } else {
 #pragma unroll
@@ -402,21 +406,36 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
         const SeqTiles sn = stile[next ? i + 1 : i];
         const WaveTiles wtn = swt[next ? i + 1 : i][w];
         gain_request(on, next, gr);
-        u32x4 An[TA];
-        tile_loads(on, sn, wtn, An);
 
-        // Wait for the tagged chunks: every round re-requests all stale ones at once.  The
-        // first check stands outside the loop, so its wait covers the activations alone and
-        // not the weight tiles requested behind them.
-        if (!ext) {
-            auto stale_mask = [&]() {
-                uint32_t stale = 0;
+        // The next op's weight tiles, requested right behind the activations: a wave's loads
+        // return in order, so they land after the activations, while this op computes.  The
+        // count issued is 2, 6 or TA (the wave's tiles of the next op rounded up), each with
+        // its own first check of the activations, so that check waits for the activations
+        // alone and not for the tiles behind them.
+        auto stale_mask = [&]() {
+            uint32_t st = 0;
+            if (!ext) {
 #pragma unroll
                 for (int r = 0; r < XCH; r++)
-                    if (tid + CTHREADS * r < nchunk && !tagged4(xv[r], parity)) stale |= 1u << r;
-                return stale;
-            };
-            uint32_t stale = stale_mask();
+                    if (static_cast<uint32_t>(r) < rows_used && tid + CTHREADS * r < nchunk && !tagged4(xv[r], parity))
+                        st |= 1u << r;
+            }
+            return st;
+        };
+        u32x4 An[TA];
+        uint32_t stale;
+        if (wtn.n <= 2) {
+            tile_loads<2>(on, sn, wtn, An);
+            stale = stale_mask();
+        } else if (wtn.n <= 6) {
+            tile_loads<6>(on, sn, wtn, An);
+            stale = stale_mask();
+        } else {
+            tile_loads<TA>(on, sn, wtn, An);
+            stale = stale_mask();
+        }
+        // Stale chunks: every round re-requests all of them at once.
+        {
             uint32_t spins = 0;
             while (stale && !gave_up) {
                 if (++spins > SPIN_LIMIT) {
