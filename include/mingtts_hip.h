@@ -132,7 +132,8 @@ int mt_set_tuning(int key, int value);
  * ops; at most 96 ops; M * K <= 10240 per op (its activations are staged in LDS); K <= 2048
  * for an op with an RMSNorm gain; a workgroup's share of an op (ceil(N / workgroups)
  * features) at most 64 features, with (features, twice with the gate partner) x M <= 128,
- * and at most 16 MFMA tiles of 16 x 32 weights per compute wave (six per workgroup) --
+ * and at most 12 MFMA tiles of 16 x 32 weights per wave (eight per workgroup), spanning at
+ * most two row tiles of 16 weight rows --
  * every linear of a Qwen2-0.5B decode layer fits at one workgroup per CU on 256 CUs; an
  * op that reads (as x, or as the old y of MT_ACCUM) a
  * region an earlier op wrote must view it with that op's row stride and within its
