@@ -277,8 +277,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // One 512-thread workgroup per CU runs every op of the sequence in order (see the top of
 // the file).  tags / tag_bytes: the plan's tagged activation buffer, read through a buffer
-// resource with device-coherent loads.
-template <int WT>
+// resource with device-coherent loads.  MS: the rows M of every op when the plan has one
+// common M the kernel is specialised for (1 or 2), else 0 (M read per op).
+template <int WT, int MS>
 __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
                                                          uint32_t *sync, const uint32_t *tags, uint32_t tag_bytes) {
     // The op's x as [hi, lo][M][K]; MFMA B reads past M K (K tails) land in the padding,
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
         const SeqOp o = sdesc[i];  // by value: read once, kept in registers
         const SeqTiles s = stile[i];
         const WaveTiles wt = swt[i][w];
-        const uint32_t M = o.M;
+        const uint32_t M = MS ? static_cast<uint32_t>(MS) : o.M;
         const bool norm = o.norm != nullptr;
 
         // The op's activations x [M][K] are staged once per workgroup: chunk e = tid + 384 r
@@ -638,7 +639,7 @@ int seq_limits(int *groups_out) {
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e == hipSuccess)
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(seq_kernel<DT_F16>),
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(seq_kernel<DT_F16, 0>),
                                                          SEQ_THREADS, 0);
     if (e != hipSuccess || cus <= 0 || per_cu <= 0)
         return set_error(MT_EHIP, "mt_seq_create: occupancy query failed (%s, cus %d, per_cu %d)", hipGetErrorString(e),
@@ -661,7 +662,15 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out) {
     SeqPlan *p = new SeqPlan();
     p->n_ops = n_ops;
     p->device = dev;
-    p->fn = wt == DT_BF16 ? seq_kernel<DT_BF16> : seq_kernel<DT_F16>;
+    // One common M of 1 or 2 (the decode step's single row or CFG pair) selects a kernel
+    // specialised for it.
+    uint32_t m_all = n_ops ? ops[0].M : 0;
+    for (uint32_t i = 1; i < n_ops; i++)
+        if (ops[i].M != m_all) m_all = 0;
+    if (wt == DT_BF16)
+        p->fn = m_all == 1 ? seq_kernel<DT_BF16, 1> : m_all == 2 ? seq_kernel<DT_BF16, 2> : seq_kernel<DT_BF16, 0>;
+    else
+        p->fn = m_all == 1 ? seq_kernel<DT_F16, 1> : m_all == 2 ? seq_kernel<DT_F16, 2> : seq_kernel<DT_F16, 0>;
     p->groups = groups;
     p->tag_bytes = static_cast<uint32_t>((tag_words ? tag_words : 1) * 4);
     e = hipMalloc(&p->d_ops, sizeof(SeqOp) * (n_ops ? n_ops : 1));
