@@ -211,31 +211,40 @@ __device__ __forceinline__ float dpp_quad(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
 }
 
+// Sum over aligned lane octets (quads, then the half-row mirror): fixed order.
+__device__ __forceinline__ float dpp_oct(float v) {
+    v = dpp_quad(v);
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+}
+
 // Partial sums of a finished row tile from the MFMA accumulator into this wave's LDS
-// slice, pw[v * M + m] for virtual row v and x row m.  Packed tiles first add their
-// segments: lane (row group qd, column c) holds D[4 qd + i][c], and the diagonal entry of
-// (virtual row, x row) over segment s sits in lane c = m S + s, register i with
-// (4 qd + i) % S == s, so S neighbouring lanes hold the S segments.
+// slice, pw[v * M + m] for virtual row v and x row m.  B column c carries x row m over
+// segment s, half h (hi or lo): c = 2 (m S + s) + h.  Lane (row group qd, column c) holds
+// D[4 qd + i][c]; the entry of (virtual row, x row) over segment s sits in the columns
+// with that segment and the rows (4 qd + i) with (4 qd + i) % S == s, so the 2 S
+// neighbouring lanes of x row m add the segments and both halves.
 __device__ __forceinline__ void flush(const f32x4 acc, const SeqTiles &s, uint32_t M, uint32_t rt, float *pw) {
     const uint32_t lane = threadIdx.x & 63, c = lane & 15, qd = lane >> 4;
-    if (s.S == 1) {
+    if (s.S == 1) {  // rows 4 qd + i: virtual row rt 16 + 4 qd + i; columns 2 m + h
+        const uint32_t m = c >> 1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            const float e = dpp_pair(acc[i]);
             const uint32_t v = rt * 16 + qd * 4 + i;
-            if (v < s.V && c < M) pw[v * M + c] = acc[i];
+            if ((c & 1) == 0 && v < s.V && m < M) pw[v * M + m] = e;
         }
     } else if (s.S == 2) {  // rows 4 qd + i: virtual row 2 qd + i / 2, segment i % 2
-        const uint32_t sc = c & 1, m = c >> 1;
-        const float e0 = dpp_pair(sc ? acc[1] : acc[0]);
-        const float e1 = dpp_pair(sc ? acc[3] : acc[2]);
-        if (sc == 0 && m < M) {
+        const uint32_t sc = (c >> 1) & 1, m = c >> 2;
+        const float e0 = dpp_quad(sc ? acc[1] : acc[0]);
+        const float e1 = dpp_quad(sc ? acc[3] : acc[2]);
+        if ((c & 3) == 0 && m < M) {
             if (2 * qd < s.V) pw[(2 * qd) * M + m] = e0;
             if (2 * qd + 1 < s.V) pw[(2 * qd + 1) * M + m] = e1;
         }
     } else {  // S == 4: rows 4 qd + i: virtual row qd, segment i
-        const uint32_t sc = c & 3, m = c >> 2;
-        const float e = dpp_quad(sc == 0 ? acc[0] : sc == 1 ? acc[1] : sc == 2 ? acc[2] : acc[3]);
-        if (sc == 0 && m < M && qd < s.V) pw[qd * M + m] = e;
+        const uint32_t sc = (c >> 1) & 3, m = c >> 3;
+        const float e = dpp_oct(sc == 0 ? acc[0] : sc == 1 ? acc[1] : sc == 2 ? acc[2] : acc[3]);
+        if ((c & 7) == 0 && m < M && qd < s.V) pw[qd * M + m] = e;
     }
 }
 
@@ -508,42 +517,37 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
         }
         __syncthreads();  // the op's x is staged
 
-        // MFMAs over the wave's tiles (hi and lo in two accumulators), A in registers, B from
-        // the staging (lane (bc, q) reads column bc: x row bc / S over segment bc % S, 8 k).
-        // The wave's tiles span at most two row tiles (the plan checks it): tiles [0, ks) are
-        // in row tile rt0 and the rest in rt0 + 1, each with its own accumulators, flushed to
-        // LDS at the end.  B chunks past K meet zero A chunks (and hold finite values).
+        // MFMAs over the wave's tiles, A in registers, B from the staging: lane (bc, q) reads
+        // column bc = 2 (m S + s) + h, 8 k of x row m over segment s from half h (hi or lo),
+        // so one MFMA covers both halves (2 S M <= 16 columns).  The wave's tiles span at
+        // most two row tiles (the plan checks it): tiles [0, ks) are in row tile rt0 and the
+        // rest in rt0 + 1, each with its own accumulator, flushed to LDS at the end.  B
+        // chunks past K meet zero A chunks (and hold finite values).
         float *pw = part[b] + w * PARTW;
         {
             const uint32_t bc = lane & 15, q = lane >> 4;
-            const uint32_t bkb = (bc & (s.S - 1)) * s.KBs;              // segment's first block
-            const uint32_t boff = (bc >> s.ls) * K + bkb * 32 + q * 8;  // + 32 j: the tile's 8 k
-            const bool bcol = bc < s.S * M;
+            const uint32_t col = bc >> 1, h = bc & 1;
+            const uint32_t bkb = (col & (s.S - 1)) * s.KBs;  // segment's first block
+            const uint32_t boff = h * (SEQ_XLDS + XPAD) + (col >> s.ls) * K + bkb * 32 + q * 8;
+            const bool bcol = col < s.S * M;
+            const uint16_t *xsb = &xs[0][0];
             const uint32_t n = wt.n;
             const uint32_t ks = min(n, s.KBs - wt.j0);
-            f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a0l = a0, a1 = a0, a1l = a0;
+            f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
             uint32_t bo = boff + wt.j0 * 32u;
 #pragma unroll
             for (int k = 0; k < TA; k++) {
                 if (static_cast<uint32_t>(k) < n) {
                     if (static_cast<uint32_t>(k) == ks) bo = boff;
-                    u32x4 bh = {0u, 0u, 0u, 0u}, bl = bh;
-                    if (bcol) {
-                        bh = *reinterpret_cast<const u32x4 *>(&xs[0][bo]);
-                        bl = *reinterpret_cast<const u32x4 *>(&xs[1][bo]);
-                    }
-                    if (static_cast<uint32_t>(k) < ks) {
-                        a0 = mfma16<WT>(A[k], bh, a0);
-                        a0l = mfma16<WT>(A[k], bl, a0l);
-                    } else {
-                        a1 = mfma16<WT>(A[k], bh, a1);
-                        a1l = mfma16<WT>(A[k], bl, a1l);
-                    }
+                    u32x4 bv = {0u, 0u, 0u, 0u};
+                    if (bcol) bv = *reinterpret_cast<const u32x4 *>(xsb + bo);
+                    if (static_cast<uint32_t>(k) < ks) a0 = mfma16<WT>(A[k], bv, a0);
+                    else a1 = mfma16<WT>(A[k], bv, a1);
                     bo += 32;
                 }
             }
-            if (n > 0) flush(a0 + a0l, s, M, wt.rt0, pw);
-            if (n > ks) flush(a1 + a1l, s, M, wt.rt0 + 1u, pw);
+            if (n > 0) flush(a0, s, M, wt.rt0, pw);
+            if (n > ks) flush(a1, s, M, wt.rt0 + 1u, pw);
         }
         if (next) gain_store(on, gr, gbuf[b ^ 1]);
         __syncthreads();  // every wave's partial sums are in LDS

@@ -5,14 +5,16 @@
 // "virtual rows" are those features' weight rows, followed (SiLU-gate) by the partner W2's
 // rows: V = nr or 2 nr.  The share is computed with v_mfma_f32_16x16x32 tiles: A = 16
 // virtual rows x 32 k of weights (one 16-byte chunk per lane), B = 32 k x 16 columns of
-// activations, D = 16 x 16 fp32 partial sums.
+// activations, D = 16 x 16 fp32 partial sums.  Every activation is split into hi + lo
+// halves of the weights' type, and the two halves are separate B columns.
 //   - V > 16: RT = ceil(V / 16) row tiles, S = 1 segment; A row a of row tile rt is
-//     virtual row 16 rt + a and B column c is x row c.
+//     virtual row 16 rt + a and B column c is x row c / 2, half c % 2.
 //   - V <= 16: one row tile holds S in {1, 2, 4} K-segments of the share side by side
 //     (the largest with V S <= 16, M S <= 8, S <= KB), interleaved: A row a is virtual row
-//     a / S over segment a % S, B column c is x row c / S over segment c % S, and only the
-//     diagonal entries (segment s against segment s) of D are kept.  For a given (virtual
-//     row, x row) they sit in S neighbouring lanes, so a lane-group sum adds the segments.
+//     a / S over segment a % S, B column c is x row (c / 2) / S over segment (c / 2) % S,
+//     half c % 2, and only the entries of D whose row and column have the same segment
+//     are kept.  For a given (virtual row, x row) they sit in 2 S neighbouring lanes, so a
+//     lane-group sum adds the segments and both halves.
 // Segment s covers 32-k blocks s KBs .. s KBs + KBs - 1 (KBs = ceil(KB / S)); a tile is
 // (row tile rt, block step j), numbered t = rt KBs + j, T = RT KBs in all, and compute
 // wave w of the workgroup's NW takes the contiguous tile range [w T / NW, (w + 1) T / NW).
