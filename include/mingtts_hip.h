@@ -114,7 +114,8 @@ enum {
     MT_TUNE_GEMM_TILE = 6,       /* MFMA GEMM tile (x rows x weight rows) for activations of the
                                     weights' type: 0 = auto, 1 = 128 x 128, 2 = 64 x 128, 3 = 64 x 64,
                                     4 = the register-staged kernel that other activation types use */
-    MT_TUNE_GEMM_STAGES = 7      /* LDS pipeline depth of that GEMM, 2..4 stages of 64 k (0 = auto) */
+    MT_TUNE_GEMM_STAGES = 7      /* loads of that GEMM: 2..4 = direct-to-LDS stages of 64 k, 1 = two
+                                    register-staged stages into two LDS buffers (0 = auto) */
 };
 int mt_set_tuning(int key, int value);
 

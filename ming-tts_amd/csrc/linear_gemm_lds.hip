@@ -111,9 +111,10 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     constexpr int NT = TS::NT, NW = TS::NW, WMT = TS::WMT, WNT = TS::WNT, KKW = TS::KKW, NACC = TS::NACC;
     constexpr int SB = TS::SB, LPW = TS::LPW, FN = TS::FN, CLD = TS::CLD, NE = TS::NE;
     constexpr int CBYTES = TS::NCT * BM * CLD * 4;
-    constexpr int LBYTES = P * SB > CBYTES ? P * SB : CBYTES;
+    constexpr int NBUF = P == 1 ? 2 : P;  // LDS stages (P == 1: register-staged loads, two LDS buffers)
+    constexpr int LBYTES = NBUF * SB > CBYTES ? NBUF * SB : CBYTES;
     static_assert(!GATED || BN == 128, "a gated tile is 64 features of W and W2");
-    static_assert(LPW * 8 * NW == BM + BN && P >= 2 && P <= 4 && LBYTES <= 160 * 1024, "tile shape");
+    static_assert(LPW * 8 * NW == BM + BN && P >= 1 && P <= 4 && LBYTES <= 160 * 1024, "tile shape");
     static_assert(NE % (4 * NT) == 0, "partial tiles move as float4 per thread");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LBYTES];
     __shared__ uint32_t last_flag;
@@ -220,7 +221,55 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
                     acc[q % NACC][i][j] = mfma32x<WT>(f.a[q][i], f.b[q][j], acc[q % NACC][i][j]);
     };
 
-    if constexpr (P == 2) {
+    if constexpr (P == 1) {
+        // Register staging: stages s + 1 and s + 2 travel global -> registers while stage s is
+        // multiplied; stage s + 1 is then written to the other LDS buffer (same swizzled
+        // layout as the direct loads).  Loads past the K range read the zero chunk, so every
+        // step issues the same loads and the waits stay exact.
+        u32x4t rg0[LPW], rg1[LPW];
+        auto gload = [&](u32x4t (&rg)[LPW], uint32_t kstep) {
+            const uint32_t k = kstep * TBK;
+            const bool kok = kstep < KT && k + 8 * c < K;
+#pragma unroll
+            for (int i = 0; i < LPW; i++) {
+                const char *g = (rowok[i] && kok) ? src[i] + 2 * static_cast<size_t>(k) : zero;
+                rg[i] = __builtin_nontemporal_load(
+                    reinterpret_cast<const __attribute__((address_space(1))) u32x4t *>(reinterpret_cast<uintptr_t>(g)));
+            }
+        };
+        auto commit = [&](const u32x4t (&rg)[LPW], uint32_t buf) {
+#pragma unroll
+            for (int i = 0; i < LPW; i++)
+                *reinterpret_cast<u32x4t *>(lds + buf * SB + (wave + NW * i) * 1024 + lane * 16) = rg[i];
+        };
+        gload(rg0, ks0);
+        gload(rg1, ks0 + 1);
+        commit(rg0, 0);
+        gload(rg0, ks0 + 2);
+        __syncthreads();
+        for (uint32_t s = 0; s < nsteps; s += 2) {
+            {  // stage s in buffer 0; rg1 holds s + 1, rg0 is bound for s + 2
+                Frags f;
+                load(f, 0);
+                mma(f);
+                if (s + 1 < nsteps) {
+                    commit(rg1, 1);
+                    gload(rg1, ks0 + s + 3);
+                }
+                __syncthreads();
+            }
+            if (s + 1 < nsteps) {  // stage s + 1 in buffer 1; rg0 holds s + 2
+                Frags f;
+                load(f, 1);
+                mma(f);
+                if (s + 2 < nsteps) {
+                    commit(rg0, 0);
+                    gload(rg0, ks0 + s + 4);
+                }
+                __syncthreads();
+            }
+        }
+    } else if constexpr (P == 2) {
         // Double buffer: stage s + 1 is in flight while stage s is read from LDS and multiplied.
         issue(0, ks0);
         uint32_t buf = 0;
@@ -393,6 +442,7 @@ tiled_fn pick_tiled_p(int shape) {
 template <int WT, bool GATED>
 tiled_fn pick_tiled(int shape, int stages) {
     switch (stages) {
+        case 1: return pick_tiled_p<WT, GATED, 1>(shape);
         case 2: return pick_tiled_p<WT, GATED, 2>(shape);
         case 3: return pick_tiled_p<WT, GATED, 3>(shape);
         default: return pick_tiled_p<WT, GATED, 4>(shape);
@@ -452,7 +502,7 @@ int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream) {
     if (cus <= 0) return set_error(MT_EHIP, "gemm: cannot query the device");
     const Tuning &tu = tuning();
     TiledPlan p = tiled_plan(a.M, a.N, a.K, gated, cus, tu.gemm_tile, tu.gemm_splitk);
-    if (tu.gemm_stages >= 2) p.stages = tu.gemm_stages;
+    if (tu.gemm_stages >= 1) p.stages = tu.gemm_stages;
     if (p.bm == 0) return set_error(MT_EINVAL, "gemm: tile shape %d does not apply to this linear", tu.gemm_tile);
     TiledArgs t;
     t.x = static_cast<const uint16_t *>(a.x);

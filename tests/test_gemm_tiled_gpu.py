@@ -34,15 +34,17 @@ def _case(seed, M, N, K, flags, bias, wt):
     return dict(m=M, n=N, k=K, flags=flags | (O.BIAS if bias else 0), x=x, w=wb, w2=w2b, bias=bb, y0=y0, wt=wt)
 
 
-def _with_tuning(tile, splits, fn):
+def _with_tuning(tile, splits, fn, stages=0):
     old_t = mt.set_tuning(mt.TUNE_GEMM_TILE, tile)
     old_s = mt.set_tuning(mt.TUNE_GEMM_SPLITK, splits)
+    old_p = mt.set_tuning(mt.TUNE_GEMM_STAGES, stages)
     old_r = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, 0)
     try:
         return fn()
     finally:
         mt.set_tuning(mt.TUNE_GEMM_TILE, old_t)
         mt.set_tuning(mt.TUNE_GEMM_SPLITK, old_s)
+        mt.set_tuning(mt.TUNE_GEMM_STAGES, old_p)
         mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old_r)
 
 
@@ -64,6 +66,21 @@ def test_tiles_and_splits(gpu, shape, tile, splits):
     if splits != 1:
         again, _ = _with_tuning(tile, splits, lambda: run_linear(c, O.F16, gpu))
         np.testing.assert_array_equal(again, got)
+
+
+@pytest.mark.parametrize("stages", [1, 2, 3, 4])
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_pipeline_depths(gpu, shape, tile, stages):
+    """Every load pipeline (register-staged, 2-4 direct-to-LDS stages) on every tile, with a
+    split of 2 where K allows it."""
+    M, N, K, flags, bias = shape
+    if flags & O.SILU_GATE and tile == 3:
+        pytest.skip("a gated tile always has 128 weight rows")
+    say(f"tiled stages={stages} tile={tile} {_ids(shape)}")
+    c = _case(M * 11 + N + K, M, N, K, flags, bias, O.F16)
+    got, xu = _with_tuning(tile, 2, lambda: run_linear(c, O.F16, gpu), stages=stages)
+    assert_linear_parity(got, *expected(c, xu), K, f"stages {stages} tile {tile} {_ids(shape)}")
 
 
 @pytest.mark.parametrize("shape", SHAPES[:4], ids=_ids)
