@@ -9,8 +9,11 @@
 //   - Operands travel global -> LDS with global_load_lds_dwordx4 (no register staging) into a
 //     ring of P stages of 64 k each; stage s + 1 .. s + P - 1 are in flight while stage s is
 //     multiplied.  A stage holds the tile's BM x rows then its BN weight rows, 128 bytes each.
-//     Within a row, 16-byte chunk c sits in slot c ^ (row & 7), so the MFMA operand reads
-//     (32 rows of one chunk per half-wave) hit 8 different slots of every 8 rows.
+//     Within a row, 16-byte chunk c sits in slot c ^ g(row), g(r) = (r & 7) ^ ((r >> 3) & 1):
+//     the MFMA operand reads (32 rows of one chunk per half-wave) then hit 8 different slots
+//     in every 8 consecutive rows, and 16 different (row parity, slot) bank groups in every
+//     16, so they are conflict-free whether LDS serves 8 lanes over 32 banks or 16 lanes
+//     over 64 banks per cycle.
 //   - Waves 0-3 and 4-7 form two 2 x 2 grids over the tile, each wave (BM / 2) x (BN / 2);
 //     the first grid multiplies k 0-31 of every stage, the second k 32-63.  Two waves per
 //     SIMD hide each other's LDS reads, and each stage is read from LDS only twice.  The two
@@ -100,7 +103,7 @@ struct TileShape {
     static constexpr int SB = (BM + BN) * 128;        // bytes per stage
     static constexpr int LPW = (BM + BN) / (8 * NW);  // 1 KB direct loads per wave per stage
     static constexpr int FN = GATED ? 64 : BN;        // output features per tile
-    static constexpr int CLD = FN + 4;                // row stride of the fp32 tile in LDS
+    static constexpr int CLD = FN + 8;                // row stride of the fp32 tile in LDS
     static constexpr int NCT = GATED ? 2 : 1;         // fp32 tile planes (gated: W and W2 sums)
     static constexpr int NE = NCT * BM * FN;          // partial-tile elements
 };
@@ -136,8 +139,9 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     const uint32_t nsteps = min(ks0 + a.kps, KT) - ks0;
 
     // Direct-load sources of this lane: row block b = wave + NW i holds rows 8 b .. 8 b + 7 of
-    // the stage; the lane fetches chunk c = (lane & 7) ^ (row & 7) of row 8 b + lane / 8.
-    const uint32_t c = (lane & 7) ^ ((lane >> 3) & 7);
+    // the stage; the lane fills slot lane & 7 of row 8 b + lane / 8, so it fetches chunk
+    // c_i = (lane & 7) ^ g(row) = (lane & 7) ^ (lane >> 3) ^ (b & 1).
+    uint32_t ci[LPW];
     const char *src[LPW];
     bool rowok[LPW];
     const uint32_t lds0 =
@@ -146,6 +150,7 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     for (int i = 0; i < LPW; i++) {
         const int b = wave + NW * i;
         const int r = 8 * b + (lane >> 3);
+        ci[i] = (lane & 7) ^ (lane >> 3) ^ (b & 1);
         const uint16_t *base;
         uint32_t row, lim;
         size_t ld;
@@ -158,16 +163,15 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
             base = j < 64 ? a.w : a.w2; row = n0 + (j & 63); lim = N; ld = K;
         }
         rowok[i] = row < lim;
-        src[i] = reinterpret_cast<const char *>(base + static_cast<size_t>(rowok[i] ? row : 0) * ld + 8 * c);
+        src[i] = reinterpret_cast<const char *>(base + static_cast<size_t>(rowok[i] ? row : 0) * ld + 8 * ci[i]);
     }
     const char *zero = reinterpret_cast<const char *>(g_zero_chunk);
 
     auto issue = [&](uint32_t buf, uint32_t kstep) {
         const uint32_t k = kstep * TBK;
-        const bool kok = k + 8 * c < K;
 #pragma unroll
         for (int i = 0; i < LPW; i++) {
-            const char *g = (rowok[i] && kok) ? src[i] + 2 * static_cast<size_t>(k) : zero;
+            const char *g = (rowok[i] && k + 8 * ci[i] < K) ? src[i] + 2 * static_cast<size_t>(k) : zero;
             dma16(__builtin_amdgcn_readfirstlane(lds0 + buf * SB + (wave + NW * i) * 1024), g);
         }
     };
@@ -178,11 +182,12 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
         else wait_vm<0>();
     };
 
-    // MFMA operand reads: row (l & 31) of each 32-row tile, chunk 2 kk + l / 32 of the stage,
-    // kk = KKW kh .. KKW kh + KKW - 1 for this wave's part of the stage.
+    // MFMA operand reads: row (l & 31) of each 32-row tile (g(row) = g(l & 31), the tiles
+    // start at multiples of 16 rows), chunk 2 kk + l / 32 of the stage, kk = KKW kh .. KKW kh
+    // + KKW - 1 for this wave's part of the stage.
     uint32_t swz[KKW];
 #pragma unroll
-    for (int q = 0; q < KKW; q++) swz[q] = (((2 * (KKW * kh + q) + (lane >> 5)) ^ (lane & 7)) << 4);
+    for (int q = 0; q < KKW; q++) swz[q] = (((2 * (KKW * kh + q) + (lane >> 5)) ^ (lane & 7) ^ ((lane >> 3) & 1)) << 4);
     const uint32_t arow = (32 * wm * WMT + (lane & 31)) * 128;
     uint32_t brow[WNT];
 #pragma unroll
@@ -229,10 +234,9 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
         u32x4t rg0[LPW], rg1[LPW];
         auto gload = [&](u32x4t (&rg)[LPW], uint32_t kstep) {
             const uint32_t k = kstep * TBK;
-            const bool kok = kstep < KT && k + 8 * c < K;
 #pragma unroll
             for (int i = 0; i < LPW; i++) {
-                const char *g = (rowok[i] && kok) ? src[i] + 2 * static_cast<size_t>(k) : zero;
+                const char *g = (rowok[i] && kstep < KT && k + 8 * ci[i] < K) ? src[i] + 2 * static_cast<size_t>(k) : zero;
                 rg[i] = __builtin_nontemporal_load(
                     reinterpret_cast<const __attribute__((address_space(1))) u32x4t *>(reinterpret_cast<uintptr_t>(g)));
             }
