@@ -314,6 +314,60 @@ def bench_dit(torch, mt, dev, reps=3):
     return dict(us_10_steps=best * 1e3, tflops=flops / (best * 1e-3) / 1e12, launches=len(ops))
 
 
+def bench_gemm_ops(torch, mt, dev, ws, reps=5):
+    """Each prefill linear alone, 24 launches over the 24 layers' distinct weights, captured in
+    a HIP graph and replayed (so host launch cost is excluded): this library's mt_linear next to
+    hipBLASLt (torch.matmul, fp16 out, gate and up concatenated into one 9728-row weight) on the
+    same shapes.  Returns µs per launch."""
+    L = mt.load()
+    gu = [torch.cat([p["gate"], p["up"]], 0).contiguous() for p in ws]
+    rows = []
+    for M in (64, 256, 512):
+        x = torch.randn(M, H, device=dev).half()
+        xi = torch.randn(M, INTER, device=dev).half()
+        kinds = [("qkv", x, [p["qkv"] for p in ws], None, QKV, 0, [p["qkv"] for p in ws]),
+                 ("o", x, [p["o"] for p in ws], None, H, mt.GemvFlags.accumulate, [p["o"] for p in ws]),
+                 ("gate|up", x, [p["gate"] for p in ws], [p["up"] for p in ws], INTER, mt.GemvFlags.siluGate, gu),
+                 ("down", xi, [p["down"] for p in ws], None, H, mt.GemvFlags.accumulate, [p["down"] for p in ws])]
+        for name, xx, wl, w2l, N, fl, blas_w in kinds:
+            y = torch.zeros(M, N, device=dev)
+            ops = [mt.op(xx, wl[i], y, M, flags=fl, w2=(w2l[i] if w2l else None)) for i in range(len(ws))]
+            cs = torch.cuda.Stream(device=dev)
+
+            def ours():
+                for o in ops:
+                    rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, cs.cuda_stream)
+                    if rc:
+                        raise RuntimeError(mt.last_error())
+
+            def blas():
+                for w in blas_w:
+                    torch.matmul(xx, w.t())
+
+            row = dict(M=M, op=name)
+            for tag, fn in (("mt_linear_us", ours), ("hipblaslt_us", blas)):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.stream(cs):
+                    fn()  # eager run first: split-K workspace growth is refused under capture
+                    torch.cuda.synchronize()
+                    with torch.cuda.graph(g, stream=cs):
+                        fn()
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                ev = Events(torch)
+                best = None
+                for _ in range(reps):
+                    ev.start()
+                    g.replay()
+                    ms = ev.stop_ms()
+                    best = ms if best is None else min(best, ms)
+                row[tag] = round(best * 1e3 / len(ops), 2)
+                del g
+            rows.append(row)
+    return rows
+
+
 def bench_copy(torch, dev, mib=1024, reps=5):
     """A plain device-to-device copy of a known size: the calibration run for the HBM byte
     counters (FETCH_SIZE / WRITE_SIZE per dispatch against exactly mib MiB each way)."""
@@ -389,6 +443,9 @@ def main() -> int:
     ap.add_argument("--only", choices=["decode", "all", "copy", "gemm"], default="all",
                     help="copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
                          "gemm: only the prefill and DiT GEMM stacks")
+    ap.add_argument("--vs-blas", action="store_true",
+                    help="with --only gemm: also time each prefill linear alone (graph replay) "
+                         "next to hipBLASLt on the same shapes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: there is no multi-GPU path (the linear hot path would "
@@ -414,6 +471,9 @@ def main() -> int:
                                    for k, v in bench_prefill(torch, mt, dev, ws, M).items()})
         log("DiT head")
         out["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
+        if args.vs_blas:
+            log("per-op graph replay: mt_linear vs hipBLASLt")
+            out["per_op_graph_replay"] = bench_gemm_ops(torch, mt, dev, ws)
         print(json.dumps(out), flush=True)
         return 0
 
