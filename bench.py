@@ -152,6 +152,54 @@ def bench_decode_seq(torch, mt, dev, ws, steps, warmup, M=2):
     return res
 
 
+def bench_decode_layers(torch, mt, dev, ws, steps, warmup, M=2, cap=512):
+    """The whole decode layer (Qwen.swift:84-91) in one persistent launch: per layer the four
+    linears plus a decode attention item (RoPE, K/V append at the row's position, GQA over
+    the row's fp16 cache of 512 slots, 14 q / 2 kv heads), 120 items per step.  Positions are
+    the batch-2 attention workload's (lengths ~ U[32, 512], seed 0).  Timed as the linear
+    step is (HIP events around each launch)."""
+    import numpy as np
+    HQ, HKV = 14, 2
+    lens = np.random.default_rng(0).integers(32, 513, M).astype(np.int32)
+    pos = torch.from_numpy(lens - 1).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    caches = [(torch.randn(M, HKV, cap, 64, generator=g, device=dev).half(),
+               torch.randn(M, HKV, cap, 64, generator=g, device=dev).half()) for _ in ws]
+    i = torch.arange(32, device=dev, dtype=torch.float32)
+    inv_freq = (1.0 / torch.pow(torch.tensor(1e6, device=dev), 2.0 * i / 64.0)).float()
+    resid = torch.randn(M, H, device=dev)
+    qkv = torch.zeros(M, QKV, device=dev)
+    att = torch.zeros(M, HQ * 64, device=dev)
+    mlp = torch.zeros(M, INTER, device=dev)
+    x0 = resid.clone()
+    items = []
+    for p, (kc, vc) in zip(ws, caches):
+        items.append(mt.op(resid, p["qkv"], qkv, M, bias=p["qkv_b"], norm=p["norm1"]))
+        items.append(mt.attn_op(qkv, M, HQ, HKV, pos, kc, vc, cap, HKV * cap * 64, inv_freq, att))
+        items.append(mt.op(att, p["o"], resid, M, flags=mt.GemvFlags.accumulate))
+        items.append(mt.op(resid, p["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=p["up"], norm=p["norm2"]))
+        items.append(mt.op(mlp, p["down"], resid, M, flags=mt.GemvFlags.accumulate))
+    seq = mt.Seq(items)
+    for _ in range(warmup):
+        resid.copy_(x0)
+        seq.run()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in ev:
+        resid.copy_(x0)
+        a.record()
+        seq.run()
+        b.record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in ev)
+    seq.check()
+    seq.close()
+    kv_bytes = len(ws) * sum(2 * HKV * int(n) * 64 * 2 for n in lens)
+    return dict(us=1e3 * sum(t) / len(t), us_median=1e3 * t[len(t) // 2], items=len(items),
+                positions=[int(n) - 1 for n in lens], kv_cache_bytes_read=kv_bytes)
+
+
 def bench_decode_per_op(torch, mt, dev, ws, steps, M=2):
     resid = torch.randn(M, H, device=dev)
     qkv = torch.zeros(M, QKV, device=dev)
@@ -440,8 +488,9 @@ def main() -> int:
     ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
-    ap.add_argument("--only", choices=["decode", "all", "copy", "gemm"], default="all",
-                    help="copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
+    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm"], default="all",
+                    help="decode: only the linear decode step; layer: it and the decode step with attention; "
+                         "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
                          "gemm: only the prefill and DiT GEMM stacks")
     ap.add_argument("--vs-blas", action="store_true",
                     help="with --only gemm: also time each prefill linear alone (graph replay) "
@@ -516,8 +565,12 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/seq_kernel_decode_24L_M2.md",
-                     "kernel": "mt::seq_kernel<1> (fp16 weights; one launch per decode step)"},
+                     "kernel": "mt::seq_kernel<1, 2, false> (fp16 weights, M = 2, linears only; one launch per decode step)"},
     }
+    if args.only in ("all", "layer"):
+        log("decode layers with attention (persistent sequence, 120 items)")
+        line["decode_layer_step"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                     for k, v in bench_decode_layers(torch, mt, dev, ws, args.steps, args.warmup).items()}
     if args.only == "all":
         log("decode step as 96 separate launches")
         p = bench_decode_per_op(torch, mt, dev, ws, max(5, args.steps // 5))

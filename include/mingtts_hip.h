@@ -19,6 +19,10 @@
  *   mt_seq_*             QwenForward.dispatches    Sources/MingTTS/Engine/Qwen.swift:72-97
  *                        encoded on one serial       (each dispatch sees the writes of the
  *                        compute encoder             ones before it)
+ *   mt_attn_op           Encoder.ropeCache +       Sources/MingTTS/Engine/Kernels.swift:180-206,
+ *   (mt_seq_create_items) Encoder.attention of one Sources/MingTTS/Engine/Qwen.swift:86-87
+ *                        decode layer, inside the
+ *                        sequence
  *   mt_rope_cache        Encoder.ropeCache         Sources/MingTTS/Engine/Kernels.swift:180-191
  *   mt_attention         Encoder.attention         Sources/MingTTS/Engine/Kernels.swift:193-206
  *   mt_attention_decode  Encoder.attention over B  Sources/MingTTS/Engine/Kernels.swift:193-206
@@ -130,9 +134,10 @@ int mt_set_tuning(int key, int value);
  * 16-bit type; with fp16 weights an activation (times its RMSNorm gain) must stay within
  * the fp16 range, |x| <= 65504, or mt_seq_check reports MT_ERANGE for that run.
  * Requirements, beyond mt_linear's for every op: 1 <= M <= 8; one weight type for all
- * ops; at most 96 ops; M * K <= 10240 per op (its activations are staged in LDS); K <= 2048
- * for an op with an RMSNorm gain; a workgroup's share of an op (ceil(N / workgroups)
- * features) at most 64 features, with (features, twice with the gate partner) x M <= 128,
+ * ops; at most 128 ops (linears and attention items); M * K <= 10240 per op (its
+ * activations are staged in LDS); K <= 2048 for an op with an RMSNorm gain; a
+ * workgroup's share of an op (ceil(N / workgroups) features) at most 64 features, with
+ * (features, twice with the gate partner) x M <= 128,
  * and at most 12 MFMA tiles of 16 x 32 weights per wave (eight per workgroup), spanning at
  * most two row tiles of 16 weight rows --
  * every linear of a Qwen2-0.5B decode layer fits at one workgroup per CU on 256 CUs; an
@@ -162,6 +167,48 @@ typedef struct mt_linear_op {
 
 typedef struct mt_seq mt_seq;
 int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out);
+
+/*
+ * The decode attention of one layer as an item of a sequence: mt_rope_cache_decode then
+ * mt_attention_decode (Encoder.ropeCache + Encoder.attention, Kernels.swift:180-206;
+ * Qwen.swift:86-87) for B independent rows, one query each.  Row b sits at position
+ * pos[b] (a device array of B uint32, read at run time): its k head(s) rotated by NeoX
+ * RoPE and its raw v heads are appended to sequence b's caches (k_cache / v_cache + b *
+ * cache_stride elements, layout [hkv, cache_len, 64]) at pos[b], and its hq query heads,
+ * rotated, attend over keys [max(0, len_b - window), len_b), len_b = min(pos[b] + 1,
+ * cache_len) (window 0 = unlimited; a pos[b] >= cache_len appends nothing), with scores
+ * scaled by `scale`; out row b (stride ldo) gets the hq heads of 64.  qkv rows are
+ * [q (hq*64) | k (hkv*64) | v (hkv*64)] at stride ldq; they are read, not modified (the
+ * rotated q stays inside the kernel).  Requirements: as mt_rope_cache_decode and
+ * mt_attention_decode; B <= 8; the caches of the sequence's attention items must not
+ * overlap each other or any linear's x or y.
+ */
+typedef struct mt_attn_op {
+    const float *qkv;
+    uint32_t ldq, B, hq, hkv;
+    const uint32_t *pos;
+    void *k_cache;
+    void *v_cache;
+    int32_t cache_t;      /* mt_dtype: MT_F32 or MT_F16 */
+    uint32_t cache_len;   /* <= 4096 */
+    uint64_t cache_stride;
+    const float *inv_freq;  /* 32 floats: 1 / theta^(2i / 64) */
+    float *out;
+    uint32_t ldo;
+    uint32_t window;
+    float scale;
+} mt_attn_op;
+
+enum { MT_SEQ_LINEAR = 0, MT_SEQ_ATTENTION = 1 };
+typedef struct mt_seq_item {
+    int32_t kind;          /* MT_SEQ_LINEAR: `linear` is the op; MT_SEQ_ATTENTION: `attn` */
+    mt_linear_op linear;
+    mt_attn_op attn;
+} mt_seq_item;
+/* mt_seq_create over a list of linears and attention items: the whole decode layer
+ * (QwenForward.dispatches, Qwen.swift:84-91) as one persistent launch.  An attention
+ * item's output is an activation like a linear's (a later linear reads it as x). */
+int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out);
 int mt_seq_run(mt_seq *seq, mt_stream_t stream);
 int mt_seq_destroy(mt_seq *seq);
 /* Workgroups the plan's kernel runs with (after mt_seq_create). */

@@ -159,40 +159,80 @@ int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *
     return launch_gemm(a, xt, wt, s, g_tuning.gemm_splitk);
 }
 
-int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
+// Shared checks of the rope / attention entry points.
+static int validate_heads(const char *who, uint32_t hq, uint32_t hkv, int ct, uint32_t cache_len) {
+    if (hq == 0 || hkv == 0 || hq % hkv) return set_error(MT_EINVAL, "%s: hq %u must be a positive multiple of hkv %u", who, hq, hkv);
+    if (ct != DT_F32 && ct != DT_F16) return set_error(MT_EINVAL, "%s: cache dtype must be f32 or f16", who);
+    if (cache_len == 0 || cache_len > 4096) return set_error(MT_EINVAL, "%s: cache_len %u outside 1..4096", who, cache_len);
+    return MT_OK;
+}
+
+int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out) {
     if (!out) return set_error(MT_EINVAL, "mt_seq_create: null out");
     *out = nullptr;
-    if (n_ops && !ops) return set_error(MT_EINVAL, "mt_seq_create: null ops");
-    for (uint32_t i = 0; i < n_ops; i++) {
-        const mt_linear_op &o = ops[i];
+    if (n_items && !items) return set_error(MT_EINVAL, "mt_seq_create: null ops");
+    for (uint32_t i = 0; i < n_items; i++) {
         char who[48];
         snprintf(who, sizeof(who), "mt_seq_create: op %u", i);
-        LinearArgs a;
-        int rc = validate_linear(who, o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.norm, o.y, o.p, a);
-        if (rc) return rc;
-        if (o.p.M == 0 || o.p.N == 0) return set_error(MT_EINVAL, "%s: empty op", who);
-        if (o.p.M > 8) return set_error(MT_EINVAL, "%s: a sequence takes M <= 8, got %u", who, o.p.M);
+        if (items[i].kind == MT_SEQ_ATTENTION) {
+            const mt_attn_op &a = items[i].attn;
+            int rc = validate_heads(who, a.hq, a.hkv, a.cache_t, a.cache_len);
+            if (rc) return rc;
+            if (a.B == 0 || a.B > 8) return set_error(MT_EINVAL, "%s: an attention item takes 1 <= B <= 8, got %u", who, a.B);
+            if (!a.qkv || !a.pos || !a.k_cache || !a.v_cache || !a.inv_freq || !a.out)
+                return set_error(MT_EINVAL, "%s: null pointer", who);
+            if (a.ldq < (a.hq + 2 * a.hkv) * 64 || a.ldo < a.hq * 64)
+                return set_error(MT_EINVAL, "%s: ldq < (hq + 2 hkv) * 64 or ldo < hq * 64", who);
+            if (!aligned(a.qkv, 16) || a.ldq % 4 || !aligned(a.out, 16) || a.ldo % 4 || !aligned(a.k_cache, 16) ||
+                !aligned(a.v_cache, 16) || a.cache_stride % 8)
+                return set_error(MT_EINVAL, "%s: qkv, out and the caches must be 16-byte aligned with 16-byte row strides",
+                                 who);
+            if (a.B > 1 && a.cache_stride < static_cast<uint64_t>(a.hkv) * a.cache_len * 64)
+                return set_error(MT_EINVAL, "%s: cache_stride smaller than one cache", who);
+        } else if (items[i].kind == MT_SEQ_LINEAR) {
+            const mt_linear_op &o = items[i].linear;
+            LinearArgs a;
+            int rc = validate_linear(who, o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.norm, o.y, o.p, a);
+            if (rc) return rc;
+            if (o.p.M == 0 || o.p.N == 0) return set_error(MT_EINVAL, "%s: empty op", who);
+            if (o.p.M > 8) return set_error(MT_EINVAL, "%s: a sequence takes M <= 8, got %u", who, o.p.M);
+        } else {
+            return set_error(MT_EINVAL, "%s: unknown kind %d", who, items[i].kind);
+        }
     }
     // Plan once with the expected workgroup count before touching the device, so a sequence
     // the dataflow form cannot take is rejected without a GPU; re-plan if the device differs.
     std::vector<SeqOp> dev;
     int wt = DT_F16;
     const int guess = g_tuning.seq_groups > 0 ? g_tuning.seq_groups : 256;
-    int rc = seq_plan(ops, n_ops, guess, dev, wt);
+    int rc = seq_plan(items, n_items, guess, dev, wt);
     if (rc) return rc;
-    if (n_ops == 0) return set_error(MT_EINVAL, "mt_seq_create: empty sequence");
+    if (n_items == 0) return set_error(MT_EINVAL, "mt_seq_create: empty sequence");
     int groups = 0;
     rc = seq_limits(&groups);
     if (rc) return rc;
     if (groups != guess) {
-        rc = seq_plan(ops, n_ops, groups, dev, wt);
+        rc = seq_plan(items, n_items, groups, dev, wt);
         if (rc) return rc;
     }
     SeqPlan *plan = nullptr;
-    rc = seq_create(dev.data(), n_ops, wt, groups, &plan);
+    rc = seq_create(dev.data(), n_items, wt, groups, &plan);
     if (rc) return rc;
     *out = reinterpret_cast<mt_seq *>(plan);
     return MT_OK;
+}
+
+int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out) {
+    if (!out) return set_error(MT_EINVAL, "mt_seq_create: null out");
+    *out = nullptr;
+    if (n_ops && !ops) return set_error(MT_EINVAL, "mt_seq_create: null ops");
+    std::vector<mt_seq_item> items(n_ops);
+    for (uint32_t i = 0; i < n_ops; i++) {
+        items[i] = mt_seq_item{};
+        items[i].kind = MT_SEQ_LINEAR;
+        items[i].linear = ops[i];
+    }
+    return mt_seq_create_items(items.data(), n_ops, out);
 }
 
 int mt_seq_run(mt_seq *seq, mt_stream_t stream) {
@@ -213,14 +253,6 @@ int mt_seq_destroy(mt_seq *seq) {
 int mt_seq_groups(const mt_seq *seq) {
     if (!seq) return set_error(MT_EINVAL, "mt_seq_groups: null plan");
     return seq_groups(reinterpret_cast<const SeqPlan *>(seq));
-}
-
-// Shared checks of the rope / attention entry points.
-static int validate_heads(const char *who, uint32_t hq, uint32_t hkv, int ct, uint32_t cache_len) {
-    if (hq == 0 || hkv == 0 || hq % hkv) return set_error(MT_EINVAL, "%s: hq %u must be a positive multiple of hkv %u", who, hq, hkv);
-    if (ct != DT_F32 && ct != DT_F16) return set_error(MT_EINVAL, "%s: cache dtype must be f32 or f16", who);
-    if (cache_len == 0 || cache_len > 4096) return set_error(MT_EINVAL, "%s: cache_len %u outside 1..4096", who, cache_len);
-    return MT_OK;
 }
 
 int mt_rope_cache(float *qkv, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv, uint32_t pos0, void *k_cache,

@@ -51,9 +51,20 @@ struct SeqOp {
     int32_t final_out;      // nonzero: this op's output is the last write of its region
     uint32_t xoff, xld;     // tagged x: word offset of x[0][0] in the plan's tag buffer, row stride
     uint32_t yoff, yld;     // tagged old y: the same
+    int32_t kind;           // SEQ_LINEAR, or SEQ_ATTN (below)
+    // A decode attention item (kind SEQ_ATTN): x is the qkv rows (M = B rows, K = (hq + 2 hkv)
+    // 64 words read), y the output (N = hq 64), w / w2 the k / v caches, eps the score scale;
+    // no weights, bias, norm or flags.
+    uint32_t heads;         // hq | hkv << 16
+    uint32_t cache_len, window;
+    const uint32_t *pos;    // [M] positions
+    const float *inv_freq;  // 32 RoPE frequencies
+    uint64_t cache_stride;  // elements between row b's caches and row b + 1's
+    int32_t cache_t;        // cache element type
     int32_t pad;
 };
 static_assert(sizeof(SeqOp) % 16 == 0, "SeqOp is staged into LDS in 16-byte pieces");
+enum : int32_t { SEQ_LINEAR = 0, SEQ_ATTN = 1 };
 struct SeqPlan;
 // Limits of the persistent sequence kernel: threads per workgroup, output features per
 // workgroup per op, and the LDS areas of its waves.
@@ -61,14 +72,15 @@ constexpr int SEQ_THREADS_N = 512;
 constexpr int SEQ_RMAX = 64;
 constexpr int SEQ_PARTW = 128;     // partial sums per compute wave per op: virtual rows * M
 constexpr int SEQ_XLDS = 10240;    // M * K of an op: its activations staged in LDS (hi + lo)
-constexpr int SEQ_OPS_MAX = 96;    // ops of a sequence (their descriptors are staged in LDS)
+constexpr int SEQ_OPS_MAX = 128;   // ops of a sequence (their descriptors are staged in LDS)
 constexpr int SEQ_CW = 8;          // waves per workgroup, each computing a share of every op
 constexpr int SEQ_TA = 12;         // MFMA tiles of one op a wave holds in registers
 constexpr int SEQ_GMAX = 2048;     // K of an op with an RMSNorm gain (staged in LDS)
 // Workgroup count of the persistent kernel on the current device.
 int seq_limits(int *groups);
-// Dataflow plan of a serial op list for `groups` workgroups (host only; no HIP calls).
-int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt);
+// Dataflow plan of a serial list of linears and attention items for `groups` workgroups
+// (host only; no HIP calls).
+int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt);
 int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out);
 int seq_run(SeqPlan *p, hipStream_t stream);
 int seq_check(SeqPlan *p);

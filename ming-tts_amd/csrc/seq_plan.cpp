@@ -1,6 +1,6 @@
-// Plan compiler of mt_seq_create: turns a list of linears (serial-encoder semantics, as
-// QwenForward.dispatches issues them, Qwen.swift:72-97) into the dataflow form the
-// persistent kernel runs.
+// Plan compiler of mt_seq_create: turns a list of linears and decode attention items
+// (serial-encoder semantics, as QwenForward.dispatches issues them, Qwen.swift:72-97) into
+// the dataflow form the persistent kernel runs.
 //
 // For every op it resolves
 //   - where x comes from: the tagged output of the latest earlier op that wrote x's region
@@ -71,51 +71,102 @@ bool covered(const View &in, const View &out, uint32_t &col) {
 
 }  // namespace
 
-int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt) {
+int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt) {
     if (n > static_cast<uint32_t>(SEQ_OPS_MAX))
         return set_error(MT_ENOTSUP, "mt_seq_create: a sequence takes at most %d ops, got %u", SEQ_OPS_MAX, n);
     out.assign(n, SeqOp{});
     std::vector<View> xv(n), yv(n);
+    std::vector<View> caches;  // byte ranges of the attention items' k and v caches
     std::vector<int> done_before(n, -1);
     wt = -1;
     for (uint32_t i = 0; i < n; i++) {
-        const mt_linear_op &o = ops[i];
-        const mt_gemv_params &p = o.p;
         SeqOp &d = out[i];
-        const size_t xs = o.xt == MT_F32 ? 4 : 2;
-        xv[i] = View{static_cast<const char *>(o.x), static_cast<uint64_t>(p.ldx) * xs, static_cast<uint64_t>(p.K) * xs, p.M};
-        yv[i] = View{reinterpret_cast<const char *>(o.y), static_cast<uint64_t>(p.ldy) * 4, static_cast<uint64_t>(p.N) * 4, p.M};
-        if (wt < 0) wt = o.wt;
-        if (o.wt != wt) return set_error(MT_EINVAL, "mt_seq_create: op %u: every op of a sequence must share the weight type", i);
-        if (o.norm && p.K > static_cast<uint32_t>(SEQ_GMAX))
-            return set_error(MT_ENOTSUP, "mt_seq_create: op %u: an RMSNorm op takes K <= %d, got %u", i, SEQ_GMAX, p.K);
-        // The op's activations are staged whole in the workgroup's LDS (M * K <= XLDS);
-        // every workgroup's share of the op at most RMAX features and its partial sums
-        // (virtual rows x M per compute wave) within the LDS slice.
-        if (static_cast<uint64_t>(p.M) * p.K > static_cast<uint64_t>(SEQ_XLDS))
-            return set_error(MT_ENOTSUP, "mt_seq_create: op %u: M * K = %u exceeds the %d activations a workgroup stages",
-                             i, p.M * p.K, SEQ_XLDS);
-        for (int g = 0; g < groups; g++) {
-            const SeqTiles t = seq_tiles(p.N, p.K, p.M, (p.flags & MT_SILU_GATE) != 0, g, groups);
-            const uint32_t per_wave = (t.T + SEQ_CW - 1) / SEQ_CW;
-            // A wave's contiguous tile range may span at most two row tiles.
-            uint32_t span = 1;
-            for (int w = 0; w < SEQ_CW; w++) {
-                const uint32_t t0 = seq_tile_begin(t.T, w, SEQ_CW), t1 = seq_tile_begin(t.T, w + 1, SEQ_CW);
-                if (t1 > t0 && t.KBs) span = std::max(span, (t1 - 1) / t.KBs - t0 / t.KBs + 1);
+        if (items[i].kind == MT_SEQ_ATTENTION) {
+            const mt_attn_op &a = items[i].attn;
+            const uint32_t K = (a.hq + 2 * a.hkv) * 64, N = a.hq * 64;
+            xv[i] = View{reinterpret_cast<const char *>(a.qkv), static_cast<uint64_t>(a.ldq) * 4, uint64_t(K) * 4, a.B};
+            yv[i] = View{reinterpret_cast<const char *>(a.out), static_cast<uint64_t>(a.ldo) * 4, uint64_t(N) * 4, a.B};
+            const uint64_t es = a.cache_t == MT_F32 ? 4 : 2;
+            const uint64_t span = ((a.B - 1) * a.cache_stride + static_cast<uint64_t>(a.hkv) * a.cache_len * 64) * es;
+            for (const void *c : {static_cast<const void *>(a.k_cache), static_cast<const void *>(a.v_cache)}) {
+                const View cv{static_cast<const char *>(c), span, span, 1};
+                for (const View &o : caches)
+                    if (overlap(cv, o))
+                        return set_error(MT_ENOTSUP, "mt_seq_create: op %u: attention caches overlap", i);
+                caches.push_back(cv);
             }
-            if (span > 2)
-                return set_error(MT_ENOTSUP,
-                                 "mt_seq_create: op %u: a wave's share of the tiles spans %u row tiles of 16 weight "
-                                 "rows (K = %u is too short for the sequence kernel's limit of 2)",
-                                 i, span, p.K);
-            if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || t.V * p.M > static_cast<uint32_t>(SEQ_PARTW) ||
-                per_wave > static_cast<uint32_t>(SEQ_TA))
-                return set_error(MT_ENOTSUP,
-                                 "mt_seq_create: op %u: a workgroup's share (%u features, %u partial sums at M = %u, %u "
-                                 "MFMA tiles per compute wave) exceeds the sequence kernel's limits (%d features, %d "
-                                 "partial sums, %d tiles)",
-                                 i, t.nr, t.V * p.M, p.M, per_wave, SEQ_RMAX, SEQ_PARTW, SEQ_TA);
+            d.kind = SEQ_ATTN;
+            d.x = a.qkv;
+            d.xt = MT_F32;
+            d.ldx = a.ldq;
+            d.w = static_cast<const uint16_t *>(a.k_cache);
+            d.w2 = static_cast<const uint16_t *>(a.v_cache);
+            d.y = a.out;
+            d.ldy = a.ldo;
+            d.M = a.B;
+            d.N = N;
+            d.K = K;
+            d.eps = a.scale;
+            d.heads = a.hq | (a.hkv << 16);
+            d.cache_len = a.cache_len;
+            d.window = a.window;
+            d.pos = a.pos;
+            d.inv_freq = a.inv_freq;
+            d.cache_stride = a.cache_stride;
+            d.cache_t = a.cache_t;
+        } else {
+            const mt_linear_op &o = items[i].linear;
+            const mt_gemv_params &p = o.p;
+            const size_t xs = o.xt == MT_F32 ? 4 : 2;
+            xv[i] = View{static_cast<const char *>(o.x), static_cast<uint64_t>(p.ldx) * xs, static_cast<uint64_t>(p.K) * xs, p.M};
+            yv[i] = View{reinterpret_cast<const char *>(o.y), static_cast<uint64_t>(p.ldy) * 4, static_cast<uint64_t>(p.N) * 4, p.M};
+            if (wt < 0) wt = o.wt;
+            if (o.wt != wt) return set_error(MT_EINVAL, "mt_seq_create: op %u: every op of a sequence must share the weight type", i);
+            if (o.norm && p.K > static_cast<uint32_t>(SEQ_GMAX))
+                return set_error(MT_ENOTSUP, "mt_seq_create: op %u: an RMSNorm op takes K <= %d, got %u", i, SEQ_GMAX, p.K);
+            // The op's activations are staged whole in the workgroup's LDS (M * K <= XLDS);
+            // every workgroup's share of the op at most RMAX features and its partial sums
+            // (virtual rows x M per compute wave) within the LDS slice.
+            if (static_cast<uint64_t>(p.M) * p.K > static_cast<uint64_t>(SEQ_XLDS))
+                return set_error(MT_ENOTSUP, "mt_seq_create: op %u: M * K = %u exceeds the %d activations a workgroup stages",
+                                 i, p.M * p.K, SEQ_XLDS);
+            for (int g = 0; g < groups; g++) {
+                const SeqTiles t = seq_tiles(p.N, p.K, p.M, (p.flags & MT_SILU_GATE) != 0, g, groups);
+                const uint32_t per_wave = (t.T + SEQ_CW - 1) / SEQ_CW;
+                // A wave's contiguous tile range may span at most two row tiles.
+                uint32_t span = 1;
+                for (int w = 0; w < SEQ_CW; w++) {
+                    const uint32_t t0 = seq_tile_begin(t.T, w, SEQ_CW), t1 = seq_tile_begin(t.T, w + 1, SEQ_CW);
+                    if (t1 > t0 && t.KBs) span = std::max(span, (t1 - 1) / t.KBs - t0 / t.KBs + 1);
+                }
+                if (span > 2)
+                    return set_error(MT_ENOTSUP,
+                                     "mt_seq_create: op %u: a wave's share of the tiles spans %u row tiles of 16 weight "
+                                     "rows (K = %u is too short for the sequence kernel's limit of 2)",
+                                     i, span, p.K);
+                if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || t.V * p.M > static_cast<uint32_t>(SEQ_PARTW) ||
+                    per_wave > static_cast<uint32_t>(SEQ_TA))
+                    return set_error(MT_ENOTSUP,
+                                     "mt_seq_create: op %u: a workgroup's share (%u features, %u partial sums at M = %u, %u "
+                                     "MFMA tiles per compute wave) exceeds the sequence kernel's limits (%d features, %d "
+                                     "partial sums, %d tiles)",
+                                     i, t.nr, t.V * p.M, p.M, per_wave, SEQ_RMAX, SEQ_PARTW, SEQ_TA);
+            }
+            d.kind = SEQ_LINEAR;
+            d.x = o.x;
+            d.xt = o.xt;
+            d.ldx = p.ldx;
+            d.w = static_cast<const uint16_t *>(o.w);
+            d.w2 = static_cast<const uint16_t *>((p.flags & MT_SILU_GATE) ? o.w2 : o.w);
+            d.bias = static_cast<const uint16_t *>(o.bias);
+            d.norm = static_cast<const uint16_t *>(o.norm);
+            d.y = o.y;
+            d.ldy = p.ldy;
+            d.M = p.M;
+            d.N = p.N;
+            d.K = p.K;
+            d.flags = p.flags | (o.bias ? MT_BIAS : 0);
+            d.eps = p.eps;
         }
 
         // x: latest earlier writer.
@@ -123,7 +174,7 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
         for (int j = static_cast<int>(i) - 1; j >= 0; j--) {
             if (!overlap(xv[i], yv[j])) continue;
             uint32_t col = 0;
-            if (o.xt != MT_F32 || !covered(xv[i], yv[j], col))
+            if (d.xt != MT_F32 || !covered(xv[i], yv[j], col))
                 return set_error(MT_ENOTSUP, "mt_seq_create: op %u reads x from op %d's output at another layout", i, j);
             d.xsrc = j;
             d.xcol = col;
@@ -131,7 +182,7 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
         }
         // old y of an accumulate: latest earlier writer.
         d.ysrc = -1;
-        if (p.flags & MT_ACCUM) {
+        if (d.flags & MT_ACCUM) {
             for (int j = static_cast<int>(i) - 1; j >= 0; j--) {
                 if (!overlap(yv[i], yv[j])) continue;
                 uint32_t col = 0;
@@ -146,28 +197,31 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
         int db = -1;
         if (d.xsrc >= 0) {
             db = std::max(db, done_before[d.xsrc]);
-            const mt_linear_op &src = ops[d.xsrc];
-            // x spans all of the producer's features and each workgroup owns at least one
-            if (d.xcol == 0 && p.K == src.p.N && src.p.N >= static_cast<uint32_t>(groups)) db = std::max(db, d.xsrc);
+            const SeqOp &src = out[d.xsrc];
+            // A linear reads all of x.  When x spans all of a linear producer's features and
+            // each workgroup owns at least one, every workgroup has finished the producer.
+            // When x spans all heads of an attention item whose own x spans all of a linear
+            // producer's features (q, k and v heads), those heads consumed every feature of
+            // that producer: every workgroup has finished it.  (The attention item itself
+            // runs on a few workgroups; its own x reads prove nothing.)
+            if (d.kind == SEQ_LINEAR && d.xcol == 0 && d.K == src.N) {
+                if (src.kind == SEQ_LINEAR && src.N >= static_cast<uint32_t>(groups)) db = std::max(db, d.xsrc);
+                if (src.kind == SEQ_ATTN && src.xsrc >= 0) {
+                    const SeqOp &pp = out[src.xsrc];
+                    if (pp.kind == SEQ_LINEAR && src.xcol == 0 && src.K == pp.N && pp.N >= static_cast<uint32_t>(groups))
+                        db = std::max(db, src.xsrc);
+                }
+            }
         }
         if (d.ysrc >= 0) db = std::max(db, done_before[d.ysrc]);
         done_before[i] = db;
-
-        d.x = o.x;
-        d.xt = o.xt;
-        d.ldx = p.ldx;
-        d.w = static_cast<const uint16_t *>(o.w);
-        d.w2 = static_cast<const uint16_t *>((p.flags & MT_SILU_GATE) ? o.w2 : o.w);
-        d.bias = static_cast<const uint16_t *>(o.bias);
-        d.norm = static_cast<const uint16_t *>(o.norm);
-        d.y = o.y;
-        d.ldy = p.ldy;
-        d.M = p.M;
-        d.N = p.N;
-        d.K = p.K;
-        d.flags = p.flags | (o.bias ? MT_BIAS : 0);
-        d.eps = p.eps;
     }
+    if (wt < 0) wt = MT_F16;
+    // The caches are touched by their attention items alone.
+    for (const View &c : caches)
+        for (uint32_t i = 0; i < n; i++)
+            if (overlap(c, xv[i]) || overlap(c, yv[i]))
+                return set_error(MT_ENOTSUP, "mt_seq_create: op %u's x or y overlaps an attention cache", i);
     // final writers and write-after-read
     for (uint32_t i = 0; i < n; i++) {
         out[i].final_out = 1;
@@ -182,7 +236,7 @@ int seq_plan(const mt_linear_op *ops, uint32_t n, int groups, std::vector<SeqOp>
         if (!out[i].final_out) continue;
         for (uint32_t e = 0; e < i; e++) {
             const bool reads_x = out[e].xsrc < 0 && overlap(xv[e], yv[i]);
-            const bool reads_y = (ops[e].p.flags & MT_ACCUM) && out[e].ysrc < 0 && e != i && overlap(yv[e], yv[i]);
+            const bool reads_y = (out[e].flags & MT_ACCUM) && out[e].ysrc < 0 && e != i && overlap(yv[e], yv[i]);
             if ((reads_x || reads_y) && static_cast<int>(e) > done_before[i])
                 return set_error(MT_ENOTSUP,
                                  "mt_seq_create: op %u writes a region op %u read from the user buffer, and not every "

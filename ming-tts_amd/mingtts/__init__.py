@@ -27,7 +27,8 @@ KERNEL_GEMV, KERNEL_GEMM = 1, 2
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
-    "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create", "mt_seq_run",
+    "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
+    "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_last_error", "mt_version",
 )
@@ -64,6 +65,24 @@ class LinearOp(ctypes.Structure):
                 ("p", GemvParams), ("xt", ctypes.c_int32), ("wt", ctypes.c_int32)]
 
 
+class AttnOp(ctypes.Structure):
+    """mt_attn_op: the decode attention of one layer as an item of a sequence."""
+    _fields_ = [("qkv", ctypes.c_void_p), ("ldq", ctypes.c_uint32), ("B", ctypes.c_uint32),
+                ("hq", ctypes.c_uint32), ("hkv", ctypes.c_uint32), ("pos", ctypes.c_void_p),
+                ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p), ("cache_t", ctypes.c_int32),
+                ("cache_len", ctypes.c_uint32), ("cache_stride", ctypes.c_uint64), ("inv_freq", ctypes.c_void_p),
+                ("out", ctypes.c_void_p), ("ldo", ctypes.c_uint32), ("window", ctypes.c_uint32),
+                ("scale", ctypes.c_float)]
+
+
+SEQ_LINEAR, SEQ_ATTENTION = 0, 1
+
+
+class SeqItem(ctypes.Structure):
+    """mt_seq_item: a linear or an attention item of a sequence."""
+    _fields_ = [("kind", ctypes.c_int32), ("linear", LinearOp), ("attn", AttnOp)]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -86,6 +105,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_set_tuning.restype = i32
     L.mt_seq_create.argtypes = [ctypes.POINTER(LinearOp), u32, ctypes.POINTER(vp)]
     L.mt_seq_create.restype = i32
+    L.mt_seq_create_items.argtypes = [ctypes.POINTER(SeqItem), u32, ctypes.POINTER(vp)]
+    L.mt_seq_create_items.restype = i32
     L.mt_seq_run.argtypes = [vp, vp]
     L.mt_seq_run.restype = i32
     L.mt_seq_destroy.argtypes = [vp]
@@ -181,12 +202,24 @@ def set_tuning(key: int, value: int) -> int:
 
 
 class Seq:
-    """A persistent linear sequence plan (mt_seq_*)."""
+    """A persistent sequence plan (mt_seq_*) of linears (``LinearOp``) and, optionally,
+    decode attention items (``AttnOp``)."""
 
-    def __init__(self, ops: Sequence[LinearOp]):
-        arr = (LinearOp * len(ops))(*ops)
+    def __init__(self, ops: Sequence):
         h = ctypes.c_void_p()
-        check(load().mt_seq_create(arr, len(ops), ctypes.byref(h)))
+        if all(isinstance(o, LinearOp) for o in ops):
+            arr = (LinearOp * len(ops))(*ops)
+            check(load().mt_seq_create(arr, len(ops), ctypes.byref(h)))
+        else:
+            items = (SeqItem * len(ops))()
+            for i, o in enumerate(ops):
+                if isinstance(o, AttnOp):
+                    items[i].kind = SEQ_ATTENTION
+                    items[i].attn = o
+                else:
+                    items[i].kind = SEQ_LINEAR
+                    items[i].linear = o
+            check(load().mt_seq_create_items(items, len(ops), ctypes.byref(h)))
         self.handle = h
         self.n_ops = len(ops)
 
@@ -222,6 +255,16 @@ def op(x, w, y, M, flags=0, w2=None, bias=None, ldx=None, ldy=None, xt=None, wt=
                     GemvParams(M, N, K, x.stride(0) if ldx is None else ldx, y.stride(0) if ldy is None else ldy,
                                flags, eps if norm is not None else 0.0),
                     dtype_code(x) if xt is None else xt, dtype_code(w) if wt is None else wt)
+
+
+def attn_op(qkv, B, hq, hkv, pos, kc, vc, cache_len, cache_stride, inv_freq, out, ldq=None, ldo=None,
+            window=0, scale=0.125) -> AttnOp:
+    """An mt_attn_op over torch tensors: rows b < B of qkv ([B, (hq + 2 hkv) 64] at stride
+    ldq), positions pos (device uint32/int32 [B]), caches kc / vc ([B, hkv, cache_len, 64]
+    at cache_stride elements per row), out [B, hq 64]."""
+    return AttnOp(_ptr(qkv), qkv.stride(0) if ldq is None else ldq, B, hq, hkv, _ptr(pos), _ptr(kc), _ptr(vc),
+                  dtype_code(kc), cache_len, cache_stride, _ptr(inv_freq), _ptr(out),
+                  out.stride(0) if ldo is None else ldo, window, scale)
 
 
 def rope_cache(qkv, ldq, M, hq, hkv, pos0, kc, vc, cache_len, inv_freq, stream=None) -> None:

@@ -164,3 +164,73 @@ def test_rope_and_attention_reject_bad_arguments():
     assert L.mt_rope_cache(A, 1152, 2, 14, 2, 511, A, A, mt.F32, 512, A, None) == mt.EINVAL
     assert L.mt_rope_cache_decode(A, 1152, 2, 14, 2, None, A, A, mt.F16, 512, 65536, A, None) == mt.EINVAL
     assert L.mt_attention(A, 1152, 0, 14, 2, 0, 0, A, A, mt.F32, 512, A, 896, 0.125, None) == mt.OK  # empty
+
+
+def test_seq_item_layout_matches_the_header(tmp_path):
+    """The ctypes mirrors of mt_attn_op and mt_seq_item have the C compiler's sizes and
+    offsets."""
+    import ctypes
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "mingtts_hip.h"\n'
+                   'int main(void) { printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(mt_attn_op), '
+                   'offsetof(mt_attn_op, cache_stride), offsetof(mt_attn_op, scale), sizeof(mt_seq_item), '
+                   'offsetof(mt_seq_item, linear), offsetof(mt_seq_item, attn), sizeof(mt_linear_op)); return 0; }\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(mt.AttnOp), mt.AttnOp.cache_stride.offset, mt.AttnOp.scale.offset,
+            ctypes.sizeof(mt.SeqItem), mt.SeqItem.linear.offset, mt.SeqItem.attn.offset, ctypes.sizeof(mt.LinearOp)]
+    assert got == want
+
+
+def _items(ops):
+    import ctypes
+    items = (mt.SeqItem * len(ops))()
+    for i, o in enumerate(ops):
+        if isinstance(o, mt.AttnOp):
+            items[i].kind, items[i].attn = mt.SEQ_ATTENTION, o
+        else:
+            items[i].kind, items[i].linear = mt.SEQ_LINEAR, o
+    return items
+
+
+def test_seq_attention_items_are_checked_before_the_device():
+    """Attention items: argument errors are MT_EINVAL, cache aliasing is MT_ENOTSUP, both
+    before any device call (a valid list gets as far as the device query)."""
+    import ctypes
+    L = mt.load()
+    h = ctypes.c_void_p()
+    QKV, OUT, KC, VC, RES, POS, INV = (k << 20 for k in (1, 2, 4, 6, 8, 10, 11))
+    W = 16 << 20
+    stride = 2 * 512 * 64
+
+    def attn(**kw):
+        a = dict(qkv=QKV, ldq=1152, B=2, hq=14, hkv=2, pos=POS, k_cache=KC, v_cache=VC, cache_t=mt.F16,
+                 cache_len=512, cache_stride=stride, inv_freq=INV, out=OUT, ldo=896, window=0, scale=0.125)
+        a.update(kw)
+        return mt.AttnOp(*(a[f[0]] for f in mt.AttnOp._fields_))
+
+    def lin(x, y, N=1152, K=896, ldx=None, ldy=None, flags=0):
+        return mt.LinearOp(x, W, None, None, None, y,
+                           mt.GemvParams(2, N, K, K if ldx is None else ldx, N if ldy is None else ldy, flags, 0.0),
+                           mt.F32, mt.F16)
+
+    layer = [lin(RES, QKV), attn(), lin(OUT, RES, N=896, flags=mt.GemvFlags.accumulate)]
+    rc = L.mt_seq_create_items(_items(layer), len(layer), ctypes.byref(h))
+    assert rc not in (mt.EINVAL, mt.ENOTSUP), mt.last_error()   # planned; the device query fails here
+    for bad, needle in ((attn(B=9), "1 <= B <= 8"), (attn(hkv=3), "multiple of hkv"),
+                        (attn(cache_t=mt.BF16), "cache dtype"), (attn(cache_len=5000), "cache_len"),
+                        (attn(ldq=1024), "ldq"), (attn(k_cache=KC + 8), "16-byte aligned"),
+                        (attn(pos=None), "null pointer"), (attn(cache_stride=1000), "cache_stride")):
+        ops = [lin(RES, QKV), bad]
+        assert L.mt_seq_create_items(_items(ops), 2, ctypes.byref(h)) == mt.EINVAL, needle
+        assert needle in mt.last_error(), mt.last_error()
+    for ops, needle in (([lin(RES, QKV), attn(v_cache=KC)], "attention caches overlap"),
+                        ([lin(RES, KC), attn()], "overlaps an attention cache"),
+                        ([attn(), attn(out=RES)], "attention caches overlap")):
+        assert L.mt_seq_create_items(_items(ops), len(ops), ctypes.byref(h)) == mt.ENOTSUP, needle
+        assert needle in mt.last_error(), mt.last_error()
+    items = _items([lin(RES, QKV)])
+    items[0].kind = 7
+    assert L.mt_seq_create_items(items, 1, ctypes.byref(h)) == mt.EINVAL
+    assert "unknown kind" in mt.last_error()
