@@ -416,6 +416,74 @@ def bench_gemm_ops(torch, mt, dev, ws, reps=5):
     return rows
 
 
+def bench_flow_step(torch, mt, dev, reps=5):
+    """The flow stage of one generation step at the reference's flow-head shape
+    (MingEngine.encodeStep, Engine.swift:395-402; DiTForward.encode, DiT.swift:35-52): 10 ODE
+    steps of flow_assemble, 8 DiT blocks (hidden 1024, 16 heads, batch 2 x seq 3 = 6 rows:
+    rmsnorm+qkv 3072x1024, dit_attention, out 1024x1024 +=, rmsnorm+ff1 4096x1024 GELU,
+    ff2 1024x4096 +=), the final rmsnorm + 64x1024 linear and flow_euler: 430 launches, bf16
+    weights ~ N(0, 0.02^2), captured in a HIP graph and replayed."""
+    HID, HEADS, LAT, BLOCKS, STEPS = 1024, 16, 64, 8, 10
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+
+    def w(*shape, scale=0.02):
+        return (torch.randn(*shape, generator=g, device=dev) * scale).bfloat16()
+
+    def gain(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=dev)).bfloat16()
+
+    blocks = [dict(n1=gain(HID), qkv=w(3 * HID, HID), qkv_b=w(3 * HID), out=w(HID, HID), out_b=w(HID), n2=gain(HID),
+                   ff1=w(4 * HID, HID), ff1_b=w(4 * HID), ff2=w(HID, 4 * HID), ff2_b=w(HID)) for _ in range(BLOCKS)]
+    fin_n, fin_w, fin_b = gain(HID), w(LAT, HID), w(LAT)
+    xw, xb, cb = w(HID, LAT, scale=0.05), w(HID, scale=0.05), w(HID, scale=1.0)
+    i = torch.arange(32, device=dev, dtype=torch.float32)
+    invf = (1.0 / torch.pow(torch.tensor(1e4, device=dev), 2.0 * i / 64.0)).float()
+    y = torch.randn(LAT, device=dev)
+    hist, cemb = torch.randn(LAT, device=dev), torch.randn(HID, device=dev)
+    temb = torch.randn(STEPS, HID, device=dev)
+    x = torch.zeros(6, HID, device=dev)
+    qkv = torch.zeros(6, 3 * HID, device=dev)
+    att = torch.zeros(6, HID, device=dev)
+    ff = torch.zeros(6, 4 * HID, device=dev)
+    pred = torch.zeros(6, LAT, device=dev)
+    cs = torch.cuda.Stream(device=dev)
+    sched = [k / STEPS for k in range(STEPS + 1)]
+
+    def step():
+        for k in range(STEPS):
+            mt.flow_assemble(y, hist, cemb, cb, temb[k], xw, xb, x, stream=cs.cuda_stream)
+            for p in blocks:
+                mt.linear(x, p["qkv"], qkv, 6, bias=p["qkv_b"], norm=p["n1"], stream=cs.cuda_stream)
+                mt.dit_attention(qkv, 2, 3, HEADS, invf, att, stream=cs.cuda_stream)
+                mt.linear(att, p["out"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["out_b"], stream=cs.cuda_stream)
+                mt.linear(x, p["ff1"], ff, 6, flags=mt.GemvFlags.gelu, bias=p["ff1_b"], norm=p["n2"],
+                          stream=cs.cuda_stream)
+                mt.linear(ff, p["ff2"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=cs.cuda_stream)
+            mt.linear(x, fin_w, pred, 6, bias=fin_b, norm=fin_n, stream=cs.cuda_stream)
+            mt.flow_euler(y, pred, 2, 5, 2.0, sched[k + 1] - sched[k], stream=cs.cuda_stream)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cs):
+            step()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    best = None
+    for _ in range(reps):
+        ev.start()
+        graph.replay()
+        ms = ev.stop_ms()
+        best = ms if best is None else min(best, ms)
+    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
+    return dict(us_per_generation_step=best * 1e3, us_per_ode_step=best * 1e3 / STEPS, launches=STEPS * (3 + 5 * BLOCKS),
+                weight_mb_per_ode_step=wbytes / 1e6)
+
+
 def bench_copy(torch, dev, mib=1024, reps=5):
     """A plain device-to-device copy of a known size: the calibration run for the HBM byte
     counters (FETCH_SIZE / WRITE_SIZE per dispatch against exactly mib MiB each way)."""
@@ -520,6 +588,8 @@ def main() -> int:
                                    for k, v in bench_prefill(torch, mt, dev, ws, M).items()})
         log("DiT head")
         out["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
+        log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
+        out["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
         if args.vs_blas:
             log("per-op graph replay: mt_linear vs hipBLASLt")
             out["per_op_graph_replay"] = bench_gemm_ops(torch, mt, dev, ws)
@@ -590,6 +660,8 @@ def main() -> int:
                                     for k, v in bench_attention(torch, mt, dev).items()}
         log("DiT head")
         line["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
+        log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
+        line["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
     if not args.no_cpu:
         log("CPU baseline (oracle, host cores)")
         cb = cpu_baseline(torch, ws)

@@ -28,6 +28,9 @@
  *   mt_attention_decode  Encoder.attention over B  Sources/MingTTS/Engine/Kernels.swift:193-206
  *                        independent caches at
  *                        M = 1 each
+ *   mt_dit_attention     Encoder.ditAttention      Sources/MingTTS/Engine/Kernels.swift:208-220
+ *   mt_flow_assemble     Encoder.flowAssemble      Sources/MingTTS/Engine/Kernels.swift:222-235
+ *   mt_flow_euler        Encoder.flowEuler         Sources/MingTTS/Engine/Kernels.swift:237-246
  *   mt_last_error        MingTTSError text         Sources/MingTTS/Engine/MetalContext.swift:6-26
  */
 #ifndef MINGTTS_HIP_H
@@ -118,8 +121,10 @@ enum {
     MT_TUNE_GEMM_TILE = 6,       /* MFMA GEMM tile (x rows x weight rows) for activations of the
                                     weights' type: 0 = auto, 1 = 128 x 128, 2 = 64 x 128, 3 = 64 x 64,
                                     4 = the register-staged kernel that other activation types use */
-    MT_TUNE_GEMM_STAGES = 7      /* loads of that GEMM: 2..4 = direct-to-LDS stages of 64 k, 1 = two
+    MT_TUNE_GEMM_STAGES = 7,     /* loads of that GEMM: 2..4 = direct-to-LDS stages of 64 k, 1 = two
                                     register-staged stages into two LDS buffers (0 = auto) */
+    MT_TUNE_GEMV_MFMA = 8        /* 3..8 rows of the GEMV family: 0 = MFMA with x staged once per
+                                    workgroup (default), 1 = lane-group GEMV */
 };
 int mt_set_tuning(int key, int value);
 
@@ -266,6 +271,40 @@ int mt_attention_decode(const float *q, uint32_t ldq, uint32_t B, uint32_t hq, u
                         const void *v_cache, mt_dtype cache_t, uint32_t cache_len,
                         uint64_t cache_stride, float *out, uint32_t ldo, float scale,
                         mt_stream_t stream);
+
+/*
+ * The DiT flow step around its linears (MingEngine.encodeStep's flow loop,
+ * Engine.swift:395-402; DiTForward.encode, DiT.swift:35-52).
+ *
+ * mt_dit_attention -- Encoder.ditAttention (Kernels.swift:208-220, Shaders.swift:598-648):
+ * full attention inside each of B sequences of S <= 8 rows.  qkv rows (stride ld floats) are
+ * [q (H*64) | k (H*64) | v (H*64)]; q and k of row i (position i in its sequence) are rotated
+ * by interleaved RoPE (pairs 2p, 2p + 1, angle = i * inv_freq[p], 32 frequencies); scores
+ * q.k * scale, max-subtracted softmax over the sequence's S keys, out = sum p v (row stride
+ * ldo).  qkv / out 8-byte aligned with even strides.
+ */
+int mt_dit_attention(const float *qkv, uint32_t ld, uint32_t B, uint32_t S, uint32_t H, const float *inv_freq,
+                     float *out, uint32_t ldo, float scale, mt_stream_t stream);
+
+/*
+ * mt_flow_assemble -- Encoder.flowAssemble (Kernels.swift:222-235, Shaders.swift:650-676):
+ * the six flow-input rows x (stride ldx floats, hidden wide): row r, slot r % 3 = 0: temb +
+ * cemb (r < 3) or temb + cond_bias (r >= 3); 1: x_b + x_w history; 2: x_b + x_w y.  x_w is
+ * the x-embedder [hidden, latent_dim] and x_b / cond_bias [hidden], all of type wt (MT_BF16
+ * as the reference, or MT_F16); y, history [latent_dim], cemb, temb [hidden] fp32.
+ * latent_dim a multiple of 8 and x_w 16-byte aligned.
+ */
+int mt_flow_assemble(const float *y, const float *history, const float *cemb, const void *cond_bias,
+                     const float *temb, const void *x_w, const void *x_b, mt_dtype wt, float *x, uint32_t ldx,
+                     uint32_t hidden, uint32_t latent_dim, mt_stream_t stream);
+
+/*
+ * mt_flow_euler -- Encoder.flowEuler (Kernels.swift:237-246, Shaders.swift:678-693): with c
+ * = pred[pred_row], u = pred[null_row] (row stride ldp), y += (c + (c - u) cfg) dt; capture
+ * (2 * latent_dim floats, or NULL) receives c then u.
+ */
+int mt_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row, float *capture,
+                  uint32_t latent_dim, float cfg, float dt, mt_stream_t stream);
 
 /* Text of the last error on this thread ("" if none). */
 const char *mt_last_error(void);

@@ -121,10 +121,13 @@ int mt_set_tuning(int key, int value) {
         case MT_TUNE_SEQ_LAUNCH: slot = &g_tuning.seq_launch; def = 0; break;
         case MT_TUNE_GEMM_TILE: slot = &g_tuning.gemm_tile; def = 0; break;
         case MT_TUNE_GEMM_STAGES: slot = &g_tuning.gemm_stages; def = 0; break;
+        case MT_TUNE_GEMV_MFMA: slot = &g_tuning.gemv_mfma; def = 0; break;
         default: return set_error(MT_EINVAL, "mt_set_tuning: unknown key %d", key);
     }
     if (key == MT_TUNE_SEQ_LAUNCH && value > 1)
         return set_error(MT_EINVAL, "mt_set_tuning: the sequence launch mode is 0 or 1, got %d", value);
+    if (key == MT_TUNE_GEMV_MFMA && value > 1)
+        return set_error(MT_EINVAL, "mt_set_tuning: the small-M kernel choice is 0 or 1, got %d", value);
     if (key == MT_TUNE_GEMM_STAGES && value > 4)
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMM pipeline depth is 1..4, got %d", value);
     if (key == MT_TUNE_GEMM_TILE && value > 4)
@@ -313,6 +316,42 @@ int mt_attention_decode(const float *q, uint32_t ldq, uint32_t B, uint32_t hq, u
         return set_error(MT_EINVAL, "mt_attention_decode: cache_stride smaller than one cache");
     return launch_attention(q, ldq, B, hq, hkv, 0, lens, window, k_cache, v_cache, cache_t, cache_len, cache_stride,
                             out, ldo, scale, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mt_dit_attention(const float *qkv, uint32_t ld, uint32_t B, uint32_t S, uint32_t H, const float *inv_freq,
+                     float *out, uint32_t ldo, float scale, mt_stream_t stream) {
+    if (B == 0 || S == 0 || H == 0) return MT_OK;
+    if (S > 8) return set_error(MT_EINVAL, "mt_dit_attention: at most 8 rows per sequence, got %u", S);
+    if (!qkv || !inv_freq || !out) return set_error(MT_EINVAL, "mt_dit_attention: null pointer");
+    if (static_cast<uint64_t>(ld) < 3ull * H * 64 || static_cast<uint64_t>(ldo) < static_cast<uint64_t>(H) * 64)
+        return set_error(MT_EINVAL, "mt_dit_attention: ld < 3 H 64 or ldo < H 64");
+    if (!aligned(qkv, 8) || ld % 2 || !aligned(out, 8) || ldo % 2)
+        return set_error(MT_EINVAL, "mt_dit_attention: qkv / out must be 8-byte aligned with even strides");
+    if (static_cast<uint64_t>(B) * S * H > 0x7FFFFFFFull) return set_error(MT_EINVAL, "mt_dit_attention: too many items");
+    return launch_dit_attention(qkv, ld, B, S, H, inv_freq, out, ldo, scale, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mt_flow_assemble(const float *y, const float *history, const float *cemb, const void *cond_bias,
+                     const float *temb, const void *x_w, const void *x_b, mt_dtype wt, float *x, uint32_t ldx,
+                     uint32_t hidden, uint32_t latent_dim, mt_stream_t stream) {
+    if (hidden == 0) return MT_OK;
+    if (wt != MT_BF16 && wt != MT_F16) return set_error(MT_EINVAL, "mt_flow_assemble: weights must be f16 or bf16");
+    if (!y || !history || !cemb || !cond_bias || !temb || !x_w || !x_b || !x)
+        return set_error(MT_EINVAL, "mt_flow_assemble: null pointer");
+    if (latent_dim == 0 || latent_dim % 8 || !aligned(x_w, 16))
+        return set_error(MT_EINVAL, "mt_flow_assemble: latent_dim must be a positive multiple of 8 and x_w 16-byte aligned");
+    if (ldx < hidden) return set_error(MT_EINVAL, "mt_flow_assemble: ldx %u < hidden %u", ldx, hidden);
+    return launch_flow_assemble(y, history, cemb, cond_bias, temb, x_w, x_b, wt, x, ldx, hidden, latent_dim,
+                                reinterpret_cast<hipStream_t>(stream));
+}
+
+int mt_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row, float *capture,
+                  uint32_t latent_dim, float cfg, float dt, mt_stream_t stream) {
+    if (latent_dim == 0) return MT_OK;
+    if (!y || !pred) return set_error(MT_EINVAL, "mt_flow_euler: null pointer");
+    if (ldp < latent_dim) return set_error(MT_EINVAL, "mt_flow_euler: ldp %u < latent_dim %u", ldp, latent_dim);
+    return launch_flow_euler(y, pred, ldp, pred_row, null_row, capture, latent_dim, cfg, dt,
+                             reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -1,4 +1,5 @@
-// Standalone decode GEMV launches of mt_linear (M up to 8 rows per row block).
+// Standalone decode GEMV launches of mt_linear (M up to 8 rows per row block; 3..8 rows go
+// to the MFMA kernel of linear_gemv_mfma.hip unless tuned otherwise).
 //
 // Reference kernel replaced: gemv_kernel<MR> (Shaders.swift:47-108) and, for 3..8 rows,
 // gemm8_kernel (Shaders.swift:188-283).  One wave64 holds 64 / L output features; the
@@ -71,6 +72,7 @@ int gemv_lanes_log2(uint32_t K, int override_lanes) {
 }
 
 int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes) {
+    if (a.M >= 3 && a.M <= 8 && tuning().gemv_mfma != 1) return launch_gemv_mfma(a, xt, wt, stream);
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
     const int mr = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : 8;

@@ -23,6 +23,7 @@ struct Tuning {
     int gemm_splitk = 0;
     int gemm_tile = 0;
     int gemm_stages = 0;
+    int gemv_mfma = 0;
     int seq_groups = 0;
     int seq_launch = 0;
 };
@@ -95,8 +96,18 @@ int launch_attention(const float *q, uint32_t ldq, uint32_t rows, uint32_t hq, u
                      uint32_t cache_len, uint64_t cache_stride, float *out, uint32_t ldo, float scale,
                      hipStream_t stream);
 
+int launch_dit_attention(const float *qkv, uint32_t ld, uint32_t B, uint32_t S, uint32_t H, const float *inv_freq,
+                         float *out, uint32_t ldo, float scale, hipStream_t stream);
+int launch_flow_assemble(const float *y, const float *history, const float *cemb, const void *cbias, const float *temb,
+                         const void *xw, const void *xb, int wt, float *x, uint32_t ldx, uint32_t hidden,
+                         uint32_t latent, hipStream_t stream);
+int launch_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row, float *capture,
+                      uint32_t latent, float cfg, float dt, hipStream_t stream);
+
 int gemv_lanes_log2(uint32_t K, int override_lanes);
 int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes);
+// 3 <= M <= 8 on MFMA, x staged once per workgroup of 16 output features.
+int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream);
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int splitk_override);
 
 // Compute units of the current device (cached per device), or <= 0 when it cannot be queried.

@@ -23,14 +23,15 @@ F32, F16, BF16 = 0, 1, 2
 OK, EHIP, ENOMEM, EINVAL, ERANGE, ENOTSUP = 0, -5, -12, -22, -34, -95
 KERNEL_GEMV, KERNEL_GEMM = 1, 2
 (TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS, TUNE_SEQ_LAUNCH, TUNE_GEMM_TILE,
- TUNE_GEMM_STAGES) = 1, 2, 3, 4, 5, 6, 7
+ TUNE_GEMM_STAGES, TUNE_GEMV_MFMA) = 1, 2, 3, 4, 5, 6, 7, 8
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
     "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
-    "mt_attention", "mt_attention_decode", "mt_last_error", "mt_version",
+    "mt_attention", "mt_attention_decode", "mt_dit_attention", "mt_flow_assemble", "mt_flow_euler",
+    "mt_last_error", "mt_version",
 )
 
 
@@ -123,6 +124,12 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_attention.restype = i32
     L.mt_attention_decode.argtypes = [vp, u32, u32, u32, u32, vp, u32, vp, vp, i32, u32, u64, vp, u32, f32, vp]
     L.mt_attention_decode.restype = i32
+    L.mt_dit_attention.argtypes = [vp, u32, u32, u32, u32, vp, vp, u32, f32, vp]
+    L.mt_dit_attention.restype = i32
+    L.mt_flow_assemble.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, vp, u32, u32, u32, vp]
+    L.mt_flow_assemble.restype = i32
+    L.mt_flow_euler.argtypes = [vp, vp, u32, u32, u32, vp, u32, f32, f32, vp]
+    L.mt_flow_euler.restype = i32
     L.mt_last_error.argtypes = []
     L.mt_last_error.restype = ctypes.c_char_p
     L.mt_version.argtypes = []
@@ -287,6 +294,29 @@ def attention_decode(q, ldq, B, hq, hkv, lens, window, kc, vc, cache_len, cache_
     check(load().mt_attention_decode(_ptr(q), ldq, B, hq, hkv, _ptr(lens), window, _ptr(kc), _ptr(vc),
                                      dtype_code(kc), cache_len, cache_stride, _ptr(out), ldo, scale,
                                      _stream(stream)))
+
+
+def dit_attention(qkv, B, S, H, inv_freq, out, ld=None, ldo=None, scale=0.125, stream=None) -> None:
+    """Encoder.ditAttention: full attention with interleaved RoPE inside each of B sequences
+    of S rows (Kernels.swift:208-220)."""
+    check(load().mt_dit_attention(_ptr(qkv), qkv.stride(0) if ld is None else ld, B, S, H, _ptr(inv_freq), _ptr(out),
+                                  out.stride(0) if ldo is None else ldo, scale, _stream(stream)))
+
+
+def flow_assemble(y, history, cemb, cond_bias, temb, x_w, x_b, x, ldx=None, stream=None) -> None:
+    """Encoder.flowAssemble: the six flow-input rows (Kernels.swift:222-235); x_w [hidden,
+    latent_dim] of the weights' 16-bit type."""
+    hidden, latent = x_w.shape
+    check(load().mt_flow_assemble(_ptr(y), _ptr(history), _ptr(cemb), _ptr(cond_bias), _ptr(temb), _ptr(x_w),
+                                  _ptr(x_b), dtype_code(x_w), _ptr(x), x.stride(0) if ldx is None else ldx, hidden,
+                                  latent, _stream(stream)))
+
+
+def flow_euler(y, pred, pred_row, null_row, cfg, dt, capture=None, ldp=None, stream=None) -> None:
+    """Encoder.flowEuler: y += (c + (c - u) cfg) dt with c, u rows of pred (Kernels.swift:237-246)."""
+    latent = y.numel()
+    check(load().mt_flow_euler(_ptr(y), _ptr(pred), pred.stride(0) if ldp is None else ldp, pred_row, null_row,
+                               _ptr(capture), latent, cfg, dt, _stream(stream)))
 
 
 # ------------------------------------------- mirror of the reference types --

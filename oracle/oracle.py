@@ -17,6 +17,9 @@ Contents (reference paths relative to the reference checkout):
   restating Shaders.swift:451-596 and the CPU reference of KernelTests.swift:207-268.
 * ``gemv_case`` -- regenerates the reference's linear known-answer tests bit for bit
   (KernelTests.swift:72-103).
+* ``rope_interleaved`` / ``dit_attention_f64`` / ``flow_assemble_f64`` / ``flow_euler_f64``
+  -- the DiT flow step around its linears: Shaders.swift:598-693 and the CPU reference of
+  KernelTests.swift:282-318.
 """
 from __future__ import annotations
 
@@ -334,3 +337,61 @@ def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, qpos: int, window
         p = np.exp(s - s.max())
         out[h] = (p / p.sum()) @ vv
     return out
+
+
+# ---------------------------------------------------- DiT flow step --
+
+def rope_interleaved(v: np.ndarray, pos, invf: np.ndarray) -> np.ndarray:
+    """x_transformers interleaved rotary of 64-wide heads: pairs (2p, 2p + 1), angle pos *
+    inv_freq[p], formed in fp32 as the reference forms it (Shaders.swift:605-608, 627;
+    KernelTests.swift:291-300); cos, sin and the rotation in fp64.  v: [..., 64]."""
+    v = np.asarray(v, np.float64)
+    a = (np.asarray(pos, np.float32)[..., None] * invf.astype(np.float32)).astype(np.float64)
+    c, s = np.cos(a), np.sin(a)
+    x, y = v[..., 0::2], v[..., 1::2]
+    out = np.empty_like(v)
+    out[..., 0::2] = x * c - y * s
+    out[..., 1::2] = y * c + x * s
+    return out
+
+
+def dit_attention_f64(qkv: np.ndarray, B: int, S: int, H: int, invf: np.ndarray, scale: float = 0.125) -> np.ndarray:
+    """Full (non-causal) attention inside each of B sequences of S rows (Shaders.swift:612-648,
+    KernelTests.swift:301-316): qkv rows [q | k | v] of H heads; q and k of row i rotated at
+    position i; max-subtracted softmax of q.k * scale over the sequence's S keys; out = sum p v.
+    fp64.  Returns [B * S, H * 64]."""
+    D = H * 64
+    qkv = np.asarray(qkv, np.float64)
+    out = np.zeros((B * S, D), np.float64)
+    pos = np.arange(S)
+    for b in range(B):
+        rows = qkv[b * S:(b + 1) * S]
+        for h in range(H):
+            q = rope_interleaved(rows[:, h * 64:(h + 1) * 64], pos, invf)
+            k = rope_interleaved(rows[:, D + h * 64:D + (h + 1) * 64], pos, invf)
+            v = rows[:, 2 * D + h * 64:2 * D + (h + 1) * 64]
+            sc = q @ k.T * scale
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            out[b * S:(b + 1) * S, h * 64:(h + 1) * 64] = (p / p.sum(axis=1, keepdims=True)) @ v
+    return out
+
+
+def flow_assemble_f64(y, history, cemb, cbias_bits, temb, xw_bits, xb_bits, wt: int) -> np.ndarray:
+    """The six flow-input rows (Shaders.swift:650-676): row r, slot r % 3 = 0: temb + cemb
+    (rows 0-2) or temb + the cond embedder's bias (rows 3-5); 1: x_b + x_w history; 2: x_b +
+    x_w y.  16-bit weights decoded exactly; fp64 sums.  Returns [6, hidden]."""
+    w = decode16(xw_bits, wt).astype(np.float64)
+    b = decode16(xb_bits, wt).astype(np.float64)
+    cb = decode16(cbias_bits, wt).astype(np.float64)
+    t = np.asarray(temb, np.float64)
+    rows = [t + np.asarray(cemb, np.float64), b + w @ np.asarray(history, np.float64), b + w @ np.asarray(y, np.float64)]
+    rows += [t + cb, rows[1], rows[2]]
+    return np.stack(rows)
+
+
+def flow_euler_f64(y, pred, pred_row: int, null_row: int, cfg: float, dt: float):
+    """The CFG Euler step of the flow sampler (Shaders.swift:678-693): c = pred[pred_row], u =
+    pred[null_row]; y + (c + (c - u) cfg) dt, and the capture [c, u].  fp64."""
+    c = np.asarray(pred[pred_row], np.float64)
+    u = np.asarray(pred[null_row], np.float64)
+    return np.asarray(y, np.float64) + (c + (c - u) * cfg) * dt, np.concatenate([c, u])

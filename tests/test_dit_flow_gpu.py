@@ -1,0 +1,178 @@
+"""The DiT flow step around its linears on the GPU (Shaders.swift:598-693): dit_attention on
+the reference's own known-answer case (KernelTests.swift:282-318) and other shapes,
+flow_assemble and flow_euler against the oracle, and one whole flow step (assembly, DiT
+blocks of the reference's flow head shape -- hidden 1024, 16 heads, 2 x 3 rows -- final
+layer, Euler update; Engine.swift:395-402, DiT.swift:35-52) against an fp64 chain."""
+import numpy as np
+import pytest
+import torch
+
+import mingtts as mt
+import oracle as O
+from _gpu_util import dev16, say
+
+pytestmark = pytest.mark.gpu
+
+
+def invf_1e4():
+    """The reference test's frequencies: 1 / powf(1e4, 2n / 64) in fp32 (KernelTests.swift:286)."""
+    n = np.arange(32, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(1e4), np.float32(2.0) * n / np.float32(64))).astype(np.float32)
+
+
+def test_dit_attention_reference_kat(gpu):
+    """testDitAttention: B 2, S 3, H 16, qkv from the KAT RNG (state 11), atol 2e-5."""
+    B, S, H = 2, 3, 16
+    D = H * 64
+    ld = 3 * D
+    qkv = O.LCG(11).floats(B * S * ld)
+    invf = invf_1e4()
+    out = torch.zeros(B * S, D, device=gpu)
+    say("dit_attention KAT")
+    mt.dit_attention(torch.from_numpy(qkv.reshape(B * S, ld)).to(gpu), B, S, H, torch.from_numpy(invf).to(gpu), out)
+    torch.cuda.synchronize()
+    want = O.dit_attention_f64(qkv.reshape(B * S, ld), B, S, H, invf)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("B,S,H,pad", [(1, 1, 1, 0), (3, 8, 16, 0), (2, 5, 2, 64), (4, 2, 3, 2)])
+def test_dit_attention_shapes(gpu, B, S, H, pad):
+    D = H * 64
+    ld = 3 * D + pad
+    rng = np.random.default_rng(B * 100 + S * 10 + H)
+    qkv = rng.standard_normal((B * S, ld)).astype(np.float32)
+    invf = invf_1e4()
+    out = torch.full((B * S, D + pad), 7.0, device=gpu)
+    say(f"dit_attention B={B} S={S} H={H} pad={pad}")
+    mt.dit_attention(torch.from_numpy(qkv).to(gpu), B, S, H, torch.from_numpy(invf).to(gpu), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = O.dit_attention_f64(qkv, B, S, H, invf)
+    np.testing.assert_allclose(got[:, :D], want, rtol=0, atol=2e-5)
+    assert np.all(got[:, D:] == 7.0)   # the row padding is not written
+
+
+def test_dit_attention_rejects_long_sequences():
+    assert mt.load().mt_dit_attention(1 << 20, 3072, 1, 9, 16, 1 << 20, 2 << 20, 1024, 0.125, None) == mt.EINVAL
+    assert "at most 8 rows" in mt.last_error()
+
+
+@pytest.mark.parametrize("wt,hidden,ldx", [(O.BF16, 1024, 1024), (O.F16, 96, 100), (O.BF16, 300, 304)])
+def test_flow_assemble(gpu, wt, hidden, ldx):
+    latent = 64
+    rng = np.random.default_rng(hidden + wt)
+    w, _ = O.round16(rng.standard_normal((hidden, latent)).astype(np.float32) * np.float32(0.05), wt)
+    xb, _ = O.round16(rng.standard_normal(hidden).astype(np.float32) * np.float32(0.05), wt)
+    cb, _ = O.round16(rng.standard_normal(hidden).astype(np.float32), wt)
+    y, hist = rng.standard_normal(latent).astype(np.float32), rng.standard_normal(latent).astype(np.float32)
+    cemb, temb = rng.standard_normal(hidden).astype(np.float32), rng.standard_normal(hidden).astype(np.float32)
+    x = torch.full((6, ldx), -3.0, device=gpu)
+    say(f"flow_assemble wt={wt} hidden={hidden}")
+    t = lambda a: torch.from_numpy(a).to(gpu)
+    mt.flow_assemble(t(y), t(hist), t(cemb), dev16(cb, wt, gpu), t(temb), dev16(w, wt, gpu), dev16(xb, wt, gpu), x)
+    torch.cuda.synchronize()
+    got = x.cpu().numpy()
+    want = O.flow_assemble_f64(y, hist, cemb, cb, temb, w, xb, wt)
+    np.testing.assert_allclose(got[:, :hidden], want, rtol=1e-6, atol=1e-6)
+    assert np.all(got[:, hidden:] == -3.0)
+
+
+def test_flow_euler(gpu):
+    latent = 64
+    rng = np.random.default_rng(3)
+    pred = rng.standard_normal((6, latent)).astype(np.float32)
+    y0 = rng.standard_normal(latent).astype(np.float32)
+    for cfg, dt, capture in ((2.0, 0.0625, True), (0.0, 0.125, False)):
+        y = torch.from_numpy(y0.copy()).to(gpu)
+        cap = torch.zeros(2 * latent, device=gpu) if capture else None
+        say(f"flow_euler cfg={cfg}")
+        mt.flow_euler(y, torch.from_numpy(pred).to(gpu), 2, 5, cfg, dt, capture=cap)
+        torch.cuda.synchronize()
+        want, want_cap = O.flow_euler_f64(y0, pred, 2, 5, cfg, dt)
+        np.testing.assert_allclose(y.cpu().numpy(), want, rtol=1e-6, atol=1e-7)
+        if capture:
+            np.testing.assert_array_equal(cap.cpu().numpy(), want_cap.astype(np.float32))
+
+
+HID, HEADS, LAT = 1024, 16, 64
+
+
+def dit_weights(blocks, seed):
+    """bf16 weights ~ N(0, 0.02^2) of the flow head's DiT blocks (Weights.swift:146-172) and
+    gains ~ 1 + N(0, 0.1^2), seeded per block."""
+    out = []
+    for i in range(blocks):
+        rng = np.random.default_rng(seed * 100 + i)
+        def w(*shape):
+            return O.round16(rng.standard_normal(shape).astype(np.float32) * np.float32(0.02), O.BF16)[0]
+        def g(n):
+            return O.round16((1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32), O.BF16)[0]
+        out.append(dict(norm1=g(HID), qkv=w(3 * HID, HID), qkv_b=w(3 * HID), out=w(HID, HID), out_b=w(HID),
+                        norm2=g(HID), ff1=w(4 * HID, HID), ff1_b=w(4 * HID), ff2=w(HID, 4 * HID), ff2_b=w(HID)))
+    return out
+
+
+def oracle_flow_step(blocks, final, x0, invf, y0, cfg, dt):
+    """DiTForward.encode over the six assembled rows (batch 2 x seq 3) then the Euler update,
+    fp64 per op with fp32 activations between ops."""
+    x = x0.astype(np.float32).copy()
+    M = 6
+    for p in blocks:
+        qkv = O.linear_np64(O.rmsnorm_f64(x, p["norm1"], O.BF16), p["qkv"], None, O.BF16, p["qkv_b"], None,
+                            O.BIAS).astype(np.float32)
+        att = O.dit_attention_f64(qkv, 2, 3, HEADS, invf).astype(np.float32)
+        x = O.linear_f64(att, p["out"], None, O.BF16, p["out_b"], x, M, HID, HID, O.ACCUM).astype(np.float32)
+        ff = O.linear_np64(O.rmsnorm_f64(x, p["norm2"], O.BF16), p["ff1"], None, O.BF16, p["ff1_b"], None,
+                           O.BIAS | O.GELU).astype(np.float32)
+        x = O.linear_f64(ff, p["ff2"], None, O.BF16, p["ff2_b"], x, M, HID, 4 * HID, O.ACCUM).astype(np.float32)
+    pred = O.linear_np64(O.rmsnorm_f64(x, final["norm"], O.BF16), final["w"], None, O.BF16, final["b"], None,
+                         O.BIAS).astype(np.float32)
+    y1, _ = O.flow_euler_f64(y0, pred, 2, 5, cfg, dt)
+    return x, pred, y1
+
+
+def test_flow_step_matches_fp64_chain(gpu):
+    """One ODE step of the flow head: assemble, 2 DiT blocks, final norm + linear, Euler."""
+    rng = np.random.default_rng(21)
+    blocks = dit_weights(2, 21)
+    final = dict(norm=O.round16((1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32), O.BF16)[0],
+                 w=O.round16(rng.standard_normal((LAT, HID)).astype(np.float32) * np.float32(0.02), O.BF16)[0],
+                 b=O.round16(rng.standard_normal(LAT).astype(np.float32) * np.float32(0.02), O.BF16)[0])
+    xw = O.round16(rng.standard_normal((HID, LAT)).astype(np.float32) * np.float32(0.05), O.BF16)[0]
+    xb = O.round16(rng.standard_normal(HID).astype(np.float32) * np.float32(0.05), O.BF16)[0]
+    cb = O.round16(rng.standard_normal(HID).astype(np.float32), O.BF16)[0]
+    y0 = rng.standard_normal(LAT).astype(np.float32)
+    hist = rng.standard_normal(LAT).astype(np.float32)
+    cemb = rng.standard_normal(HID).astype(np.float32)
+    temb = rng.standard_normal(HID).astype(np.float32)
+    invf = invf_1e4()
+    cfg, dt = 2.0, 0.0625
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    b16 = lambda a: dev16(a, O.BF16, gpu)
+    dw = [{k: b16(v) for k, v in p.items()} for p in blocks]
+    x = torch.zeros(6, HID, device=gpu)
+    qkv = torch.zeros(6, 3 * HID, device=gpu)
+    att = torch.zeros(6, HID, device=gpu)
+    ff = torch.zeros(6, 4 * HID, device=gpu)
+    pred = torch.zeros(6, LAT, device=gpu)
+    y = t(y0.copy())
+    invf_d = t(invf)
+    say("flow step: assemble, 2 DiT blocks, final, euler")
+    mt.flow_assemble(y, t(hist), t(cemb), b16(cb), t(temb), b16(xw), b16(xb), x)
+    lin = lambda xx, w, out, flags=0, bias=None, norm=None: mt.linear(xx, w, out, 6, flags=flags, bias=bias, norm=norm)
+    for d in dw:
+        lin(x, d["qkv"], qkv, bias=d["qkv_b"], norm=d["norm1"])
+        mt.dit_attention(qkv, 2, 3, HEADS, invf_d, att)
+        lin(att, d["out"], x, flags=mt.GemvFlags.accumulate, bias=d["out_b"])
+        lin(x, d["ff1"], ff, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"])
+        lin(ff, d["ff2"], x, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])
+    lin(x, b16(final["w"]), pred, bias=b16(final["b"]), norm=b16(final["norm"]))
+    mt.flow_euler(y, pred, 2, 5, cfg, dt)
+    torch.cuda.synchronize()
+    x0 = O.flow_assemble_f64(y0, hist, cemb, cb, temb, xw, xb, O.BF16)
+    want_x, want_pred, want_y = oracle_flow_step(blocks, final, x0, invf, y0, cfg, dt)
+    for got, want, what in ((x, want_x, "hidden"), (pred, want_pred, "velocity"), (y, want_y, "latent")):
+        g = got.cpu().numpy()
+        assert np.all(np.isfinite(g)), what
+        rel = O.normwise_rel_err(g, want)
+        assert rel <= 1e-3, f"{what}: normwise {rel:.3g}"

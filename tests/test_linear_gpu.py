@@ -48,15 +48,18 @@ def test_reference_kats_forced_gemm(gpu, case):
 @pytest.mark.parametrize("lanes", [8, 16, 32, 64])
 @pytest.mark.parametrize("case", [c for c in O.KAT_ALL if c[0] <= 8], ids=_id)
 def test_reference_kats_gemv_lane_splits(gpu, case, lanes):
-    """The GEMV at every lane split (the analogue of the reference's kSplit/columnTiles sweep)."""
+    """The lane-group GEMV at every lane split (the analogue of the reference's kSplit /
+    columnTiles sweep), also for the 3..8 rows that go to the MFMA kernel by default."""
     m, n, k, flags, bias, xs = case
     old = mt.set_tuning(mt.TUNE_GEMV_LANES, lanes)
+    old_mfma = mt.set_tuning(mt.TUNE_GEMV_MFMA, 1)
     try:
         say(f"kat gemv lanes {lanes} {_id(case)}")
         c = O.gemv_case(m, n, k, flags, bias, xs, wt=O.F16)
         got, xu = run_linear(c, O.F32, gpu)
     finally:
         mt.set_tuning(mt.TUNE_GEMV_LANES, old)
+        mt.set_tuning(mt.TUNE_GEMV_MFMA, old_mfma)
     assert_linear_parity(got, *expected(c, xu), k, f"lanes {lanes} " + _id(case))
 
 

@@ -348,3 +348,87 @@ def test_attention_matches_torch_sdpa():
         vv = torch.from_numpy(np.repeat(v[:, start:qpos + 1], hq // hkv, axis=0))[None]
         want = F.scaled_dot_product_attention(torch.from_numpy(q)[None, :, None, :], kk, vv, scale=0.125)
         np.testing.assert_allclose(got, want[0, :, 0].numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_interleaved_rope_invariants():
+    """x_transformers rotary (Shaders.swift:605-608): identity at position 0, norm-preserving,
+    relative-position dot products, and pairs (2p, 2p + 1) rotating together."""
+    invf = (1.0 / np.power(np.float32(1e4), np.float32(2.0) * np.arange(32, dtype=np.float32) / np.float32(64))).astype(np.float32)
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((4, 64))
+    k = rng.standard_normal((4, 64))
+    np.testing.assert_allclose(O.rope_interleaved(q, 0, invf), q, atol=0)
+    for p in (1, 2, 7):
+        np.testing.assert_allclose(np.linalg.norm(O.rope_interleaved(q, p, invf), axis=-1), np.linalg.norm(q, axis=-1),
+                                   rtol=1e-12)
+    d1 = np.sum(O.rope_interleaved(q, 2, invf) * O.rope_interleaved(k, 5, invf), -1)
+    d2 = np.sum(O.rope_interleaved(q, 4, invf) * O.rope_interleaved(k, 7, invf), -1)
+    # equal up to the fp32 rounding of the angles (the reference forms them in fp32)
+    np.testing.assert_allclose(d1, d2, rtol=0, atol=1e-5)
+    e = np.zeros(64)
+    e[2] = 1.0   # dim 2 pairs with dim 3 at frequency invf[1]
+    r = O.rope_interleaved(e, 3, invf)
+    a = float(np.float32(3) * invf[1])
+    assert np.count_nonzero(np.abs(r) > 1e-15) == 2
+    assert abs(r[2] - math.cos(a)) < 1e-12 and abs(r[3] - math.sin(a)) < 1e-12
+
+
+def test_dit_attention_matches_torch_sdpa():
+    """Full attention per sequence on the rotated q / k against torch's fp64 SDPA; one row
+    per sequence returns v; NeoX pairing in place of the interleaved one is caught."""
+    B, S, H = 2, 3, 4
+    D = H * 64
+    invf = (1.0 / np.power(np.float32(1e4), np.float32(2.0) * np.arange(32, dtype=np.float32) / np.float32(64))).astype(np.float32)
+    qkv = O.LCG(11).floats(B * S * 3 * D).reshape(B * S, 3 * D).astype(np.float64)
+    got = O.dit_attention_f64(qkv, B, S, H, invf)
+    pos = np.arange(S)
+    for b in range(B):
+        rows = qkv[b * S:(b + 1) * S]
+        q = np.stack([O.rope_interleaved(rows[:, h * 64:(h + 1) * 64], pos, invf) for h in range(H)])
+        k = np.stack([O.rope_interleaved(rows[:, D + h * 64:D + (h + 1) * 64], pos, invf) for h in range(H)])
+        v = np.stack([rows[:, 2 * D + h * 64:2 * D + (h + 1) * 64] for h in range(H)])
+        want = F.scaled_dot_product_attention(torch.from_numpy(q)[None], torch.from_numpy(k)[None],
+                                              torch.from_numpy(v)[None], scale=0.125)[0].numpy()
+        np.testing.assert_allclose(got[b * S:(b + 1) * S].reshape(S, H, 64), want.transpose(1, 0, 2), rtol=1e-10,
+                                   atol=1e-12)
+    one = O.dit_attention_f64(qkv[:2], 2, 1, H, invf)   # S = 1: softmax of one key
+    np.testing.assert_array_equal(one, qkv[:2, 2 * D:])
+    # a plausible mistake: NeoX pairs (i, i + 32) in place of interleaved (2p, 2p + 1)
+    neox = np.empty_like(got)
+    for b in range(B):
+        rows = qkv[b * S:(b + 1) * S]
+        for h in range(H):
+            q = O.rope_neox(rows[:, h * 64:(h + 1) * 64], pos, invf)
+            k = O.rope_neox(rows[:, D + h * 64:D + (h + 1) * 64], pos, invf)
+            sc = q @ k.T * 0.125
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            neox[b * S:(b + 1) * S, h * 64:(h + 1) * 64] = (p / p.sum(1, keepdims=True)) @ rows[:, 2 * D + h * 64:2 * D + (h + 1) * 64]
+    assert np.max(np.abs(neox - got)) > 100 * 2e-5   # far outside the reference test's atol
+
+
+def test_flow_assemble_and_euler_closed_forms():
+    """Flow input rows against torch's fp64 linear and the slot layout; the Euler step at cfg
+    0 and 1."""
+    rng = np.random.default_rng(12)
+    hidden, latent = 96, 64
+    w, _ = O.round16(rng.standard_normal((hidden, latent)).astype(np.float32) * np.float32(0.05), O.BF16)
+    xb, _ = O.round16(rng.standard_normal(hidden).astype(np.float32) * np.float32(0.05), O.BF16)
+    cb, _ = O.round16(rng.standard_normal(hidden).astype(np.float32), O.BF16)
+    y, hist = rng.standard_normal(latent), rng.standard_normal(latent)
+    cemb, temb = rng.standard_normal(hidden), rng.standard_normal(hidden)
+    x = O.flow_assemble_f64(y, hist, cemb, cb, temb, w, xb, O.BF16)
+    wt = torch.from_numpy(O.decode16(w, O.BF16).astype(np.float64))
+    bt = torch.from_numpy(O.decode16(xb, O.BF16).astype(np.float64))
+    np.testing.assert_allclose(x[1], F.linear(torch.from_numpy(hist), wt, bt).numpy(), rtol=1e-12)
+    np.testing.assert_allclose(x[2], F.linear(torch.from_numpy(y), wt, bt).numpy(), rtol=1e-12)
+    np.testing.assert_array_equal(x[4], x[1])
+    np.testing.assert_array_equal(x[5], x[2])
+    np.testing.assert_allclose(x[0], temb + cemb, rtol=1e-15)
+    np.testing.assert_allclose(x[3], temb + O.decode16(cb, O.BF16), rtol=1e-15)
+    pred = rng.standard_normal((6, latent))
+    y0 = rng.standard_normal(latent)
+    y1, cap = O.flow_euler_f64(y0, pred, 2, 5, 0.0, 0.25)
+    np.testing.assert_allclose(y1, y0 + pred[2] * 0.25, rtol=1e-15)
+    y2, _ = O.flow_euler_f64(y0, pred, 2, 5, 1.0, 0.5)
+    np.testing.assert_allclose(y2, y0 + (2 * pred[2] - pred[5]) * 0.5, rtol=1e-14)
+    np.testing.assert_array_equal(cap, np.concatenate([pred[2], pred[5]]))
