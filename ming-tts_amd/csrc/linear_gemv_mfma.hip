@@ -19,8 +19,15 @@
 //     are zero), so one MFMA covers both halves of every row; neighbouring lanes add the
 //     halves;
 //   - the waves' partial sums meet in LDS and one lane per output adds them in wave order,
-//     applies the norm scale and the epilogue, and stores.  The order is fixed, so results
-//     are bit-identical from run to run.
+//     applies the norm scale and the epilogue, and stores;
+//   - when the 16-feature tiles alone cannot fill the chip (N <= 2032), S workgroups share a
+//     tile, each over its own range of 32-k blocks: each stores its partial sums (and
+//     its rows' x^2 sums) to the stream's workspace with device-coherent stores, waits for
+//     them and counts itself in; the last arrival adds the S records in split order and runs
+//     the epilogue.
+// Every summation order is fixed, so results are bit-identical from run to run.
+#include <algorithm>
+
 #include "mt_device.hpp"
 #include "mt_internal.hpp"
 
@@ -76,14 +83,30 @@ __device__ __forceinline__ float wave_sum64(float v) {
     return v;
 }
 
+// Split-K arguments: S workgroups per tile (tile = block % tiles, split = block / tiles), kps
+// 32-k blocks each; part / part_bytes / cnt: the stream's workspace (S > 1 only).
+struct GmSplit {
+    uint32_t tiles, splits, kps, part_bytes;
+    float *part;
+    uint32_t *cnt;
+};
+
+constexpr int SC1 = 16;  // buffer cache policy: device-coherent
+
 template <int WT, int XT, bool GATED, bool NORM>
-__global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a) {
+__global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a, GmSplit sp) {
+    constexpr int NCT = GATED ? 2 : 1;
+    constexpr int REC = NCT * 128 + 8;  // a workgroup's sums: [plane][feature][row], then x^2 per row
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][8][GM_XLD];  // [hi, lo][row][k of the chunk]
-    __shared__ float part[GM_NW][GATED ? 2 : 1][16][8];
+    __shared__ float part[GM_NW][NCT][16][8];
     __shared__ float ssw[GM_NW][8];
+    __shared__ float tot[REC];
+    __shared__ uint32_t last_flag;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t M = a.M, K = a.K;
-    const uint32_t r0 = blockIdx.x * 16;
+    const uint32_t tile = blockIdx.x % sp.tiles, split = blockIdx.x / sp.tiles;
+    const uint32_t r0 = tile * 16;
+    const uint32_t ks = split * sp.kps * 32, ke = min(K, (split + 1) * sp.kps * 32);  // this split's k range
 
     // A lane: weight row r0 + (lane & 15), 8 k from 8 (lane >> 4) of each 32-k block.
     const uint32_t arow = r0 + (lane & 15);
@@ -100,8 +123,8 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a) {
 #pragma unroll
     for (int m = 0; m < 8; m++) ss[m] = 0.0f;
 
-    for (uint32_t kc0 = 0; kc0 < K; kc0 += GM_KC) {
-        const uint32_t kn = min(static_cast<uint32_t>(GM_KC), K - kc0);
+    for (uint32_t kc0 = ks; kc0 < ke; kc0 += GM_KC) {
+        const uint32_t kn = min(static_cast<uint32_t>(GM_KC), ke - kc0);
         const uint32_t nkb = (kn + 31) / 32;
         // This wave's weight tiles of the chunk: blocks w, w + 8, ... (requested first).
         u32x4g at[GM_BPW], at2[GM_BPW];
@@ -109,7 +132,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a) {
         for (int u = 0; u < GM_BPW; u++) {
             const uint32_t jb = w + GM_NW * u;
             const uint32_t k = kc0 + jb * 32 + 8 * (lane >> 4);  // K % 8 == 0: a chunk is all in or all out
-            const bool ok = aok && jb < nkb && k < K;
+            const bool ok = aok && jb < nkb && k < ke;
             const u32x4g *src = ok ? reinterpret_cast<const u32x4g *>(wrow + kc0 + jb * 32) : zero;
             at[u] = __builtin_nontemporal_load(reinterpret_cast<gw_cp4>(reinterpret_cast<uintptr_t>(src)));
             if constexpr (GATED) {
@@ -197,20 +220,50 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a) {
         }
     }
     __syncthreads();
+    // The workgroup's sums in wave order: element e of the record.
+    float mine = 0.0f;
+    if (tid < static_cast<uint32_t>(REC)) {
+        if (tid < static_cast<uint32_t>(NCT * 128)) {
+            const uint32_t p = tid >> 7, f = (tid >> 3) & 15, m = tid & 7;
+#pragma unroll
+            for (int ww = 0; ww < GM_NW; ww++) mine += part[ww][p][f][m];
+        } else if constexpr (NORM) {
+            const uint32_t m = tid - NCT * 128;
+#pragma unroll
+            for (int ww = 0; ww < GM_NW; ww++) mine += ssw[ww][m];
+        }
+    }
+    if (sp.splits > 1) {
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(sp.part, 0, static_cast<int>(sp.part_bytes), 0x00020000);
+        const uint32_t base = tile * sp.splits * static_cast<uint32_t>(REC) * 4u;
+        if (tid < static_cast<uint32_t>(REC))
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mine), rsrc, base + (split * REC + tid) * 4u, 0, SC1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(sp.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_flag = old == sp.splits - 1;
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        if (tid == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid < static_cast<uint32_t>(REC)) {  // the records in split order
+            float t = 0.0f;
+            for (uint32_t s = 0; s < sp.splits; s++)
+                t += s == split ? mine
+                                : __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, base + (s * REC + tid) * 4u, 0, SC1));
+            mine = t;
+        }
+    }
+    if (tid < static_cast<uint32_t>(REC)) tot[tid] = mine;
+    __syncthreads();
     if (tid < 16 * M) {
         const uint32_t f = tid / M, m = tid - f * M, n = r0 + f;
         if (n < a.N) {
-            float s1 = 0.0f, s2 = 0.0f;
-#pragma unroll
-            for (int ww = 0; ww < GM_NW; ww++) {
-                s1 += part[ww][0][f][m];
-                if constexpr (GATED) s2 += part[ww][GATED ? 1 : 0][f][m];
-            }
+            float s1 = tot[f * 8 + m], s2 = GATED ? tot[128 + f * 8 + m] : 0.0f;
             if constexpr (NORM) {
-                float t = 0.0f;
-#pragma unroll
-                for (int ww = 0; ww < GM_NW; ww++) t += ssw[ww][m];
-                const float scale = 1.0f / sqrtf(t / static_cast<float>(K) + a.eps);
+                const float scale = 1.0f / sqrtf(tot[NCT * 128 + m] / static_cast<float>(K) + a.eps);
                 s1 *= scale;
                 s2 *= scale;
             }
@@ -223,7 +276,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a) {
     }
 }
 
-typedef void (*gm_fn)(LinearArgs);
+typedef void (*gm_fn)(LinearArgs, GmSplit);
 
 template <int WT, int XT>
 gm_fn gm_variant(bool gated, bool norm) {
@@ -245,8 +298,32 @@ gm_fn gm_x(int xt, bool gated, bool norm) {
 int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
+    GmSplit sp{};
+    sp.tiles = (a.N + 15) / 16;
+    const uint32_t kb = (a.K + 31) / 32;
+    // Splits: enough workgroups for 256 CUs when the tiles are few, each split at least 8
+    // blocks (one per wave); MT_TUNE_GEMM_SPLITK forces a count.
+    uint32_t s = 1;
+    const int forced = tuning().gemm_splitk;
+    if (forced > 0) s = static_cast<uint32_t>(forced);
+    else if (sp.tiles < 128) s = std::max(1u, std::min((256u + sp.tiles - 1) / sp.tiles, kb / 8));
+    s = std::min(s, std::min(kb, 64u));
+    sp.kps = (kb + s - 1) / s;
+    sp.splits = (kb + sp.kps - 1) / sp.kps;  // no empty split
+    if (sp.splits > 1) {
+        const int rec = (gated ? 2 : 1) * 128 + 8;
+        const size_t pb = static_cast<size_t>(sp.tiles) * sp.splits * rec * 4;
+        if (pb > 0x7FFFFFF0u) return set_error(MT_ENOTSUP, "gemv_mfma: split-K workspace beyond 2 GiB");
+        void *part = nullptr;
+        uint32_t *cnt = nullptr;
+        const int rc = stream_workspace(stream, pb, sp.tiles, &part, &cnt);
+        if (rc) return rc;
+        sp.part = static_cast<float *>(part);
+        sp.part_bytes = static_cast<uint32_t>(pb);
+        sp.cnt = cnt;
+    }
     gm_fn fn = wt == DT_BF16 ? gm_x<DT_BF16>(xt, gated, norm) : gm_x<DT_F16>(xt, gated, norm);
-    hipLaunchKernelGGL(fn, dim3((a.N + 15) / 16), dim3(GM_THREADS), 0, stream, a);
+    hipLaunchKernelGGL(fn, dim3(sp.tiles * sp.splits), dim3(GM_THREADS), 0, stream, a, sp);
     return check_launch("gemv_mfma");
 }
 

@@ -97,3 +97,43 @@ def test_rows_past_m_are_not_read(gpu):
     got = y_d.cpu().numpy()
     assert np.all(np.isfinite(got))
     assert O.normwise_rel_err(got, O.linear_f64(c["x"][:M], c["w"], None, O.F16, None, None, M, N, K, 0)) <= 1e-5
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7])
+@pytest.mark.parametrize("M,N,K,flags,norm", [(6, 1024, 4096, O.ACCUM, False), (4, 96, 1000, O.SILU_GATE, True),
+                                              (8, 300, 2056, O.GELU, True)])
+def test_forced_splits_bit_exact_reruns(gpu, splits, M, N, K, flags, norm):
+    """Split-K counts forced through MT_TUNE_GEMM_SPLITK (the x^2 sums of a fused norm travel
+    with the partial sums): parity, and a re-run bit for bit (the arrival counters re-arm and
+    the splits are added in split order)."""
+    gated = bool(flags & O.SILU_GATE)
+    c = O.gemv_case(M, N, K, flags, False, 1.0, wt=O.F16)
+    x = np.ascontiguousarray(c["x"][:M]) * np.float32(3.0)
+    gbits, _ = O.round16(1.0 + 0.1 * O.gaussian(5 + K, K), O.F16)
+    x_d, xu = dev_x(x, O.F32, gpu)
+    say(f"gemv_mfma splits={splits} M={M} N={N} K={K} norm={norm}")
+    old = mt.set_tuning(mt.TUNE_GEMM_SPLITK, splits)
+    try:
+        outs = []
+        for _ in range(2):
+            y_d = torch.from_numpy(c["y0"].copy()).to(gpu)
+            args = (dev16(c["w"], O.F16, gpu), dev16(c["w2"], O.F16, gpu) if gated else None, O.F16, None, y_d,
+                    M, N, K, K, N, c["flags"])
+            if norm:
+                rc = mt.linear_rmsnorm_raw(x_d, O.F32, dev16(gbits, O.F16, gpu), *args, 1e-6, None)
+            else:
+                rc = mt.linear_raw(x_d, O.F32, *args, None)
+            assert rc == 0, mt.last_error()
+            torch.cuda.synchronize()
+            outs.append(y_d.cpu().numpy())
+    finally:
+        mt.set_tuning(mt.TUNE_GEMM_SPLITK, old)
+    np.testing.assert_array_equal(outs[1], outs[0])
+    w2 = c["w2"] if gated else None
+    if norm:
+        want64 = O.linear_np64(O.rmsnorm_f64(xu, gbits, O.F16), c["w"], w2, O.F16, None, c["y0"], c["flags"])
+        want32 = O.linear_f32(O.rmsnorm_f32(xu, gbits, O.F16), c["w"], w2, O.F16, None, c["y0"], M, N, K, c["flags"])
+    else:
+        want64 = O.linear_f64(xu, c["w"], w2, O.F16, None, c["y0"], M, N, K, c["flags"])
+        want32 = O.linear_f32(xu, c["w"], w2, O.F16, None, c["y0"], M, N, K, c["flags"])
+    assert_linear_parity(outs[0], want32, want64, K, f"splits {splits} M={M} N={N} K={K}")
