@@ -123,8 +123,10 @@ enum {
                                     4 = the register-staged kernel that other activation types use */
     MT_TUNE_GEMM_STAGES = 7,     /* loads of that GEMM: 2..4 = direct-to-LDS stages of 64 k, 1 = two
                                     register-staged stages into two LDS buffers (0 = auto) */
-    MT_TUNE_GEMV_MFMA = 8        /* 3..8 rows of the GEMV family: 0 = MFMA with x staged once per
-                                    workgroup (default), 1 = lane-group GEMV */
+    MT_TUNE_GEMV_MFMA = 8        /* the MFMA kernel that stages x once per 16 output features: 0 =
+                                    for 3..16 rows (default; 3..8 with a fused norm), 1 = never
+                                    (lane-group GEMV up to 8 rows, GEMM above), 2 = up to 64 rows of
+                                    x of the weights' type (32 otherwise) */
 };
 int mt_set_tuning(int key, int value);
 

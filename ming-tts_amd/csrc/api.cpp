@@ -126,8 +126,8 @@ int mt_set_tuning(int key, int value) {
     }
     if (key == MT_TUNE_SEQ_LAUNCH && value > 1)
         return set_error(MT_EINVAL, "mt_set_tuning: the sequence launch mode is 0 or 1, got %d", value);
-    if (key == MT_TUNE_GEMV_MFMA && value > 1)
-        return set_error(MT_EINVAL, "mt_set_tuning: the small-M kernel choice is 0 or 1, got %d", value);
+    if (key == MT_TUNE_GEMV_MFMA && value > 2)
+        return set_error(MT_EINVAL, "mt_set_tuning: the small-M kernel choice is 0, 1 or 2, got %d", value);
     if (key == MT_TUNE_GEMM_STAGES && value > 4)
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMM pipeline depth is 1..4, got %d", value);
     if (key == MT_TUNE_GEMM_TILE && value > 4)

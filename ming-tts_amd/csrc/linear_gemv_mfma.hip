@@ -9,10 +9,12 @@
 // Here x is staged once per workgroup and the weights stream once:
 //   - a 512-thread workgroup owns 16 output features (one 16-row MFMA A tile; with the SiLU
 //     gate, the 16 matching rows of W2 too) over all of K;
-//   - its 8 waves split K in 32-k blocks (block j to wave j mod 8); a wave requests its A
+//   - its 8 waves split K in 32-k blocks (pairs of blocks, so that one wave reads both
+//     halves of each 128-byte weight line); a wave requests its A
 //     tiles (one 16-byte chunk of weights per lane, nontemporal) before it stages x, so the
 //     weight stream is in flight while x is converted;
-//   - x is staged in LDS in chunks of 2048 k as hi + lo halves of the weights' 16-bit type
+//   - x is staged in LDS in chunks of 1024 k (512 for 64 columns) as hi + lo halves of the
+//     weights' 16-bit type (or as it is when x has the weights' type and no norm is fused)
 //     (hi rounded toward zero for fp16, to nearest for bf16; lo the rest), the RMSNorm gain
 //     applied first and x^2 summed per row when the norm is fused;
 //   - v_mfma_f32_16x16x32: B column c = 2 m + h holds half h of x row m (columns past 2 M
@@ -37,10 +39,7 @@ namespace {
 
 constexpr int GM_THREADS = 512;
 constexpr int GM_NW = GM_THREADS / 64;
-constexpr int GM_KC = 2048;               // k per LDS chunk
-constexpr int GM_XLD = GM_KC + 32;        // LDS row stride (elements)
-constexpr int GM_BPW = GM_KC / 32 / GM_NW;  // 32-k blocks per wave per chunk
-constexpr int GM_XCH = 8 * GM_KC / 4 / GM_THREADS;  // 4-element x chunks per thread per chunk (M <= 8)
+constexpr int GM_LDS = 65536 + 2048;  // x staging: 32768 elements per chunk plus row pads (the partial sums reuse it)
 
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2g __attribute__((ext_vector_type(2)));
@@ -93,13 +92,32 @@ struct GmSplit {
 
 constexpr int SC1 = 16;  // buffer cache policy: device-coherent
 
-template <int WT, int XT, bool GATED, bool NORM>
-__global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a, GmSplit sp) {
+// Shape of one instantiation: NG groups of 16 B columns; H2: x staged as hi + lo halves (x
+// of another type than the weights, or a fused norm), so column c is half c & 1 of row c / 2,
+// else column c is row c; MM rows at most; KC k per LDS chunk.
+template <int NG, bool H2>
+struct GmShape {
+    static constexpr int HV = H2 ? 2 : 1;
+    static constexpr int MM = 16 * NG / HV;
+    static constexpr int KC = 32768 / (HV * MM) < 1024 ? 32768 / (HV * MM) : 1024;  // 1024 or 512: at most 4 blocks per wave
+    static constexpr int XLD = KC + 16;            // row pad: rows 8 banks apart
+    static constexpr int BPW = KC / 32 / GM_NW;  // 32-k blocks per wave per chunk
+    static constexpr int XCH = MM * KC / 4 / GM_THREADS;
+    static_assert(KC % (64 * GM_NW) == 0 && HV * MM * XLD * 2 <= GM_LDS, "x staging (block pairs per wave)");
+};
+
+template <int WT, int XT, bool GATED, bool NORM, int NG>
+__global__ __launch_bounds__(GM_THREADS, 4) void gemv_mfma_kernel(LinearArgs a, GmSplit sp) {
+    constexpr bool H2 = XT != WT || NORM;
+    typedef GmShape<NG, H2> S;
+    constexpr int MM = S::MM, KC = S::KC, XLD = S::XLD, BPW = S::BPW, XCH = S::XCH;
     constexpr int NCT = GATED ? 2 : 1;
-    constexpr int REC = NCT * 128 + 8;  // a workgroup's sums: [plane][feature][row], then x^2 per row
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][8][GM_XLD];  // [hi, lo][row][k of the chunk]
-    __shared__ float part[GM_NW][NCT][16][8];
-    __shared__ float ssw[GM_NW][8];
+    constexpr int REC = NCT * 16 * MM + MM;  // a workgroup's sums: [plane][feature][row], then x^2 per row
+    static_assert(GM_NW * NCT * 16 * MM * 4 <= GM_LDS, "partial sums overlay the staging");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[GM_LDS];
+    uint16_t *xs = reinterpret_cast<uint16_t *>(smem);  // [half][row][k of the chunk], row stride XLD
+    float *part = reinterpret_cast<float *>(smem);      // after the K loop: [wave][plane][feature][row]
+    __shared__ float ssw[GM_NW][MM];
     __shared__ float tot[REC];
     __shared__ uint32_t last_flag;
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -113,24 +131,27 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a, GmS
     const bool aok = arow < a.N;
     const uint16_t *wrow = a.w + static_cast<size_t>(aok ? arow : 0) * K + 8 * (lane >> 4);
     const uint16_t *w2row = (GATED ? a.w2 : a.w) + static_cast<size_t>(aok ? arow : 0) * K + 8 * (lane >> 4);
-    // B lane: column c = lane & 15 is half c & 1 of x row c >> 1.
-    const uint32_t bc = lane & 15, bm = bc >> 1, bh = bc & 1;
-    const bool bok = bm < M;
+    // B lane of group g: column 16 g + (lane & 15).
+    const uint32_t bc = lane & 15;
     const u32x4g *zero = reinterpret_cast<const u32x4g *>(g_gm_zero);
 
-    f32x4g acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;
-    float ss[8];
+    f32x4g acc[NG], acc2[NG];
 #pragma unroll
-    for (int m = 0; m < 8; m++) ss[m] = 0.0f;
+    for (int g = 0; g < NG; g++) acc[g] = acc2[g] = f32x4g{0.0f, 0.0f, 0.0f, 0.0f};
+    float ss[MM];
+#pragma unroll
+    for (int m = 0; m < MM; m++) ss[m] = 0.0f;
 
-    for (uint32_t kc0 = ks; kc0 < ke; kc0 += GM_KC) {
-        const uint32_t kn = min(static_cast<uint32_t>(GM_KC), ke - kc0);
+    for (uint32_t kc0 = ks; kc0 < ke; kc0 += KC) {
+        const uint32_t kn = min(static_cast<uint32_t>(KC), ke - kc0);
         const uint32_t nkb = (kn + 31) / 32;
-        // This wave's weight tiles of the chunk: blocks w, w + 8, ... (requested first).
-        u32x4g at[GM_BPW], at2[GM_BPW];
+        // This wave's weight tiles of the chunk (requested first): block pairs (2 w, 2 w + 1),
+        // (2 w + 16, 2 w + 17), ..., so the two 64-byte halves of each 128-byte weight line
+        // come from one wave.
+        u32x4g at[BPW], at2[BPW];
 #pragma unroll
-        for (int u = 0; u < GM_BPW; u++) {
-            const uint32_t jb = w + GM_NW * u;
+        for (int u = 0; u < BPW; u++) {
+            const uint32_t jb = 2 * GM_NW * (u >> 1) + 2 * w + (u & 1);
             const uint32_t k = kc0 + jb * 32 + 8 * (lane >> 4);  // K % 8 == 0: a chunk is all in or all out
             const bool ok = aok && jb < nkb && k < ke;
             const u32x4g *src = ok ? reinterpret_cast<const u32x4g *>(wrow + kc0 + jb * 32) : zero;
@@ -140,105 +161,127 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a, GmS
                 at2[u] = __builtin_nontemporal_load(reinterpret_cast<gw_cp4>(reinterpret_cast<uintptr_t>(src2)));
             }
         }
-        // Stage x[m][kc0 .. kc0 + kn) as hi + lo; the block tail past kn holds zeros.
+        // Stage x[m][kc0 .. kc0 + kn); the block tail past kn holds zeros.
         const uint32_t k4 = kn / 4, nch = M * k4;
 #pragma unroll
-        for (int r = 0; r < GM_XCH; r++) {
+        for (int r = 0; r < XCH; r++) {
             const uint32_t e = tid + GM_THREADS * r;
             if (e < nch) {
                 const uint32_t m = e / k4, kk = (e - m * k4) * 4;
-                float x[4];
-                if constexpr (XT == DT_F32) {
-                    const float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) +
-                                                                       static_cast<size_t>(m) * a.ldx + kc0 + kk);
-                    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+                if constexpr (!H2) {  // x of the weights' type: staged as it is
+                    *reinterpret_cast<uint2 *>(xs + m * XLD + kk) =
+                        *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(a.x) + static_cast<size_t>(m) * a.ldx +
+                                                         kc0 + kk);
                 } else {
-                    const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(a.x) +
-                                                                     static_cast<size_t>(m) * a.ldx + kc0 + kk);
-                    x[0] = dec_lo<XT>(v.x); x[1] = dec_hi<XT>(v.x); x[2] = dec_lo<XT>(v.y); x[3] = dec_hi<XT>(v.y);
-                }
-                if constexpr (NORM) {
-                    float t = x[0] * x[0];
-                    t = fmaf(x[1], x[1], t);
-                    t = fmaf(x[2], x[2], t);
-                    t = fmaf(x[3], x[3], t);
+                    float x[4];
+                    if constexpr (XT == DT_F32) {
+                        const float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) +
+                                                                           static_cast<size_t>(m) * a.ldx + kc0 + kk);
+                        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+                    } else {
+                        const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(a.x) +
+                                                                         static_cast<size_t>(m) * a.ldx + kc0 + kk);
+                        x[0] = dec_lo<XT>(v.x); x[1] = dec_hi<XT>(v.x); x[2] = dec_lo<XT>(v.y); x[3] = dec_hi<XT>(v.y);
+                    }
+                    if constexpr (NORM) {
+                        float t = x[0] * x[0];
+                        t = fmaf(x[1], x[1], t);
+                        t = fmaf(x[2], x[2], t);
+                        t = fmaf(x[3], x[3], t);
 #pragma unroll
-                    for (int mm = 0; mm < 8; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
-                    const uint2 g = *reinterpret_cast<const uint2 *>(a.norm + kc0 + kk);
-                    x[0] *= dec_lo<WT>(g.x);
-                    x[1] *= dec_hi<WT>(g.x);
-                    x[2] *= dec_lo<WT>(g.y);
-                    x[3] *= dec_hi<WT>(g.y);
+                        for (int mm = 0; mm < MM; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
+                        const uint2 g = *reinterpret_cast<const uint2 *>(a.norm + kc0 + kk);
+                        x[0] *= dec_lo<WT>(g.x);
+                        x[1] *= dec_hi<WT>(g.x);
+                        x[2] *= dec_lo<WT>(g.y);
+                        x[3] *= dec_hi<WT>(g.y);
+                    }
+                    const uint32_t h0 = pack_pair<WT>(x[0], x[1]), h1 = pack_pair<WT>(x[2], x[3]);
+                    const uint32_t l0 = pack_pair<WT>(x[0] - dec_lo<WT>(h0), x[1] - dec_hi<WT>(h0));
+                    const uint32_t l1 = pack_pair<WT>(x[2] - dec_lo<WT>(h1), x[3] - dec_hi<WT>(h1));
+                    *reinterpret_cast<u32x2g *>(xs + m * XLD + kk) = u32x2g{h0, h1};
+                    *reinterpret_cast<u32x2g *>(xs + (MM + m) * XLD + kk) = u32x2g{l0, l1};
                 }
-                const uint32_t h0 = pack_pair<WT>(x[0], x[1]), h1 = pack_pair<WT>(x[2], x[3]);
-                const uint32_t l0 = pack_pair<WT>(x[0] - dec_lo<WT>(h0), x[1] - dec_hi<WT>(h0));
-                const uint32_t l1 = pack_pair<WT>(x[2] - dec_lo<WT>(h1), x[3] - dec_hi<WT>(h1));
-                *reinterpret_cast<u32x2g *>(&xs[0][m][kk]) = u32x2g{h0, h1};
-                *reinterpret_cast<u32x2g *>(&xs[1][m][kk]) = u32x2g{l0, l1};
             }
         }
         if (kn % 32) {  // zeros for the last block's k past kn (they meet zero weights)
             const uint32_t tail = nkb * 32 - kn;  // a multiple of 8
-            for (uint32_t e = tid; e < 2 * M * tail; e += GM_THREADS) {
+            for (uint32_t e = tid; e < S::HV * M * tail; e += GM_THREADS) {
                 const uint32_t h = e / (M * tail), rest = e - h * M * tail, m = rest / tail;
-                xs[h][m][kn + rest - m * tail] = 0;
+                xs[(h * MM + m) * XLD + kn + rest - m * tail] = 0;
             }
         }
         __syncthreads();  // the chunk's x is staged
 #pragma unroll
-        for (int u = 0; u < GM_BPW; u++) {
-            const uint32_t jb = w + GM_NW * u;
+        for (int u = 0; u < BPW; u++) {
+            const uint32_t jb = 2 * GM_NW * (u >> 1) + 2 * w + (u & 1);
             if (jb < nkb) {
-                u32x4g bv = {0u, 0u, 0u, 0u};
-                if (bok) bv = *reinterpret_cast<const u32x4g *>(&xs[bh][bm][jb * 32 + 8 * (lane >> 4)]);
-                acc = mfma16x32<WT>(at[u], bv, acc);
-                if constexpr (GATED) acc2 = mfma16x32<WT>(at2[u], bv, acc2);
+#pragma unroll
+                for (int g = 0; g < NG; g++) {
+                    const uint32_t col = 16 * g + bc, m = H2 ? col >> 1 : col, h = H2 ? col & 1 : 0;
+                    u32x4g bv = {0u, 0u, 0u, 0u};
+                    if (m < M) bv = *reinterpret_cast<const u32x4g *>(xs + (h * MM + m) * XLD + jb * 32 + 8 * (lane >> 4));
+                    acc[g] = mfma16x32<WT>(at[u], bv, acc[g]);
+                    if constexpr (GATED) acc2[g] = mfma16x32<WT>(at2[u], bv, acc2[g]);
+                }
             }
         }
-        __syncthreads();  // the chunk's x is no longer read
+        __syncthreads();  // the chunk's x is no longer read (the partial sums reuse its LDS)
     }
 
-    // Partial sums: lane (column c, row group q) holds D[4 q + i][c]; features 4 q + i of x
-    // row c >> 1, half c & 1: the even lane of each pair stores hi + lo.
+    // Partial sums: lane (column c, row group q) of group g holds D[4 q + i][16 g + c]:
+    // feature 4 q + i; with halves, the even lane of each pair stores hi + lo.
     {
         const uint32_t q = lane >> 4;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float e = pair_sum(acc[i]);
-            if (bh == 0 && bm < 8) part[w][0][4 * q + i][bm] = e;
-            if constexpr (GATED) {
-                const float e2 = pair_sum(acc2[i]);
-                if (bh == 0 && bm < 8) part[w][1][4 * q + i][bm] = e2;
+        for (int g = 0; g < NG; g++) {
+            const uint32_t col = 16 * g + bc, m = H2 ? col >> 1 : col;
+            const bool store = (!H2 || (col & 1) == 0) && m < static_cast<uint32_t>(MM);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float e = H2 ? pair_sum(acc[g][i]) : acc[g][i];
+                if (store) part[((w * NCT + 0) * 16 + 4 * q + i) * MM + m] = e;
+                if constexpr (GATED) {
+                    const float e2 = H2 ? pair_sum(acc2[g][i]) : acc2[g][i];
+                    if (store) part[((w * NCT + 1) * 16 + 4 * q + i) * MM + m] = e2;
+                }
             }
         }
     }
     if constexpr (NORM) {
 #pragma unroll
-        for (int m = 0; m < 8; m++) {
+        for (int m = 0; m < MM; m++) {
             const float t = wave_sum64(ss[m]);
             if (lane == 0) ssw[w][m] = t;
         }
     }
     __syncthreads();
-    // The workgroup's sums in wave order: element e of the record.
-    float mine = 0.0f;
-    if (tid < static_cast<uint32_t>(REC)) {
-        if (tid < static_cast<uint32_t>(NCT * 128)) {
-            const uint32_t p = tid >> 7, f = (tid >> 3) & 15, m = tid & 7;
+    // The workgroup's sums in wave order, then (split-K) the splits' records in split order.
+    constexpr int RPT = (REC + GM_THREADS - 1) / GM_THREADS;  // record elements per thread
+    float mine[RPT];
 #pragma unroll
-            for (int ww = 0; ww < GM_NW; ww++) mine += part[ww][p][f][m];
-        } else if constexpr (NORM) {
-            const uint32_t m = tid - NCT * 128;
+    for (int r = 0; r < RPT; r++) {
+        const uint32_t e = tid + GM_THREADS * r;
+        float t = 0.0f;
+        if (e < static_cast<uint32_t>(NCT * 16 * MM)) {
 #pragma unroll
-            for (int ww = 0; ww < GM_NW; ww++) mine += ssw[ww][m];
+            for (int ww = 0; ww < GM_NW; ww++) t += part[ww * NCT * 16 * MM + e];
+        } else if (NORM && e < static_cast<uint32_t>(REC)) {
+#pragma unroll
+            for (int ww = 0; ww < GM_NW; ww++) t += ssw[ww][e - NCT * 16 * MM];
         }
+        mine[r] = t;
     }
     if (sp.splits > 1) {
         const __amdgpu_buffer_rsrc_t rsrc =
             __builtin_amdgcn_make_buffer_rsrc(sp.part, 0, static_cast<int>(sp.part_bytes), 0x00020000);
         const uint32_t base = tile * sp.splits * static_cast<uint32_t>(REC) * 4u;
-        if (tid < static_cast<uint32_t>(REC))
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mine), rsrc, base + (split * REC + tid) * 4u, 0, SC1);
+#pragma unroll
+        for (int r = 0; r < RPT; r++) {
+            const uint32_t e = tid + GM_THREADS * r;
+            if (e < static_cast<uint32_t>(REC))
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mine[r]), rsrc, base + (split * REC + e) * 4u, 0, SC1);
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0) {
@@ -248,22 +291,31 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a, GmS
         __syncthreads();
         if (!last_flag) return;
         if (tid == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (tid < static_cast<uint32_t>(REC)) {  // the records in split order
-            float t = 0.0f;
-            for (uint32_t s = 0; s < sp.splits; s++)
-                t += s == split ? mine
-                                : __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, base + (s * REC + tid) * 4u, 0, SC1));
-            mine = t;
+#pragma unroll
+        for (int r = 0; r < RPT; r++) {
+            const uint32_t e = tid + GM_THREADS * r;
+            if (e < static_cast<uint32_t>(REC)) {
+                float t = 0.0f;
+                for (uint32_t s = 0; s < sp.splits; s++)
+                    t += s == split ? mine[r]
+                                    : __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, base + (s * REC + e) * 4u,
+                                                                                           0, SC1));
+                mine[r] = t;
+            }
         }
     }
-    if (tid < static_cast<uint32_t>(REC)) tot[tid] = mine;
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+        const uint32_t e = tid + GM_THREADS * r;
+        if (e < static_cast<uint32_t>(REC)) tot[e] = mine[r];
+    }
     __syncthreads();
-    if (tid < 16 * M) {
-        const uint32_t f = tid / M, m = tid - f * M, n = r0 + f;
+    for (uint32_t o = tid; o < 16 * M; o += GM_THREADS) {
+        const uint32_t f = o / M, m = o - f * M, n = r0 + f;
         if (n < a.N) {
-            float s1 = tot[f * 8 + m], s2 = GATED ? tot[128 + f * 8 + m] : 0.0f;
+            float s1 = tot[f * MM + m], s2 = GATED ? tot[16 * MM + f * MM + m] : 0.0f;
             if constexpr (NORM) {
-                const float scale = 1.0f / sqrtf(tot[NCT * 128 + m] / static_cast<float>(K) + a.eps);
+                const float scale = 1.0f / sqrtf(tot[NCT * 16 * MM + m] / static_cast<float>(K) + a.eps);
                 s1 *= scale;
                 s2 *= scale;
             }
@@ -278,26 +330,47 @@ __global__ __launch_bounds__(GM_THREADS) void gemv_mfma_kernel(LinearArgs a, GmS
 
 typedef void (*gm_fn)(LinearArgs, GmSplit);
 
-template <int WT, int XT>
+template <int WT, int XT, int NG>
 gm_fn gm_variant(bool gated, bool norm) {
-    if (gated) return norm ? gemv_mfma_kernel<WT, XT, true, true> : gemv_mfma_kernel<WT, XT, true, false>;
-    return norm ? gemv_mfma_kernel<WT, XT, false, true> : gemv_mfma_kernel<WT, XT, false, false>;
+    if constexpr (NG == 1) {
+        if (gated) return norm ? gemv_mfma_kernel<WT, XT, true, true, 1> : gemv_mfma_kernel<WT, XT, true, false, 1>;
+        return norm ? gemv_mfma_kernel<WT, XT, false, true, 1> : gemv_mfma_kernel<WT, XT, false, false, 1>;
+    } else {
+        (void)norm;  // a fused norm takes at most 8 rows
+        return gated ? gemv_mfma_kernel<WT, XT, true, false, NG> : gemv_mfma_kernel<WT, XT, false, false, NG>;
+    }
 }
 
-template <int WT>
+template <int WT, int NG>
 gm_fn gm_x(int xt, bool gated, bool norm) {
     switch (xt) {
-        case DT_F32: return gm_variant<WT, DT_F32>(gated, norm);
-        case DT_F16: return gm_variant<WT, DT_F16>(gated, norm);
-        default: return gm_variant<WT, DT_BF16>(gated, norm);
+        case DT_F32: return gm_variant<WT, DT_F32, NG>(gated, norm);
+        case DT_F16: return gm_variant<WT, DT_F16, NG>(gated, norm);
+        default: return gm_variant<WT, DT_BF16, NG>(gated, norm);
     }
+}
+
+template <int NG>
+gm_fn gm_w(int wt, int xt, bool gated, bool norm) {
+    return wt == DT_BF16 ? gm_x<DT_BF16, NG>(xt, gated, norm) : gm_x<DT_F16, NG>(xt, gated, norm);
 }
 
 }  // namespace
 
+// B columns the kernel needs for M rows: M for x of the weights' type without a norm, else
+// 2 M (hi + lo halves); 0 if more than 64 (or a fused norm past 8 rows).
+int gemv_mfma_columns(uint32_t M, int xt, int wt, bool norm) {
+    const bool h2 = xt != wt || norm;
+    if (norm && M > 8) return 0;
+    const uint32_t cols = h2 ? 2 * M : M;
+    return cols <= 64 ? static_cast<int>(cols) : 0;
+}
+
 int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
+    const int cols = gemv_mfma_columns(a.M, xt, wt, norm);
+    if (cols == 0) return set_error(MT_ENOTSUP, "gemv_mfma: %u rows exceed the kernel's columns", a.M);
     GmSplit sp{};
     sp.tiles = (a.N + 15) / 16;
     const uint32_t kb = (a.K + 31) / 32;
@@ -310,8 +383,10 @@ int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
     s = std::min(s, std::min(kb, 64u));
     sp.kps = (kb + s - 1) / s;
     sp.splits = (kb + sp.kps - 1) / sp.kps;  // no empty split
+    const int ng = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
     if (sp.splits > 1) {
-        const int rec = (gated ? 2 : 1) * 128 + 8;
+        const int mm = 16 * ng / ((xt != wt || norm) ? 2 : 1);
+        const int rec = (gated ? 2 : 1) * 16 * mm + mm;
         const size_t pb = static_cast<size_t>(sp.tiles) * sp.splits * rec * 4;
         if (pb > 0x7FFFFFF0u) return set_error(MT_ENOTSUP, "gemv_mfma: split-K workspace beyond 2 GiB");
         void *part = nullptr;
@@ -322,7 +397,7 @@ int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
         sp.part_bytes = static_cast<uint32_t>(pb);
         sp.cnt = cnt;
     }
-    gm_fn fn = wt == DT_BF16 ? gm_x<DT_BF16>(xt, gated, norm) : gm_x<DT_F16>(xt, gated, norm);
+    gm_fn fn = ng == 1 ? gm_w<1>(wt, xt, gated, norm) : ng == 2 ? gm_w<2>(wt, xt, gated, norm) : gm_w<4>(wt, xt, gated, norm);
     hipLaunchKernelGGL(fn, dim3(sp.tiles * sp.splits), dim3(GM_THREADS), 0, stream, a, sp);
     return check_launch("gemv_mfma");
 }

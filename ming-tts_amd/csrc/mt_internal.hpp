@@ -106,7 +106,9 @@ int launch_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_r
 
 int gemv_lanes_log2(uint32_t K, int override_lanes);
 int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes);
-// 3 <= M <= 8 on MFMA, x staged once per workgroup of 16 output features.
+// Up to 64 B columns (M rows of x of the weights' type, or 2 M with hi + lo halves; a fused
+// norm at most 8 rows) on MFMA, x staged once per workgroup of 16 output features.
+int gemv_mfma_columns(uint32_t M, int xt, int wt, bool norm);
 int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream);
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int splitk_override);
 

@@ -35,10 +35,12 @@ def _case(seed, M, N, K, flags, bias, wt):
 
 
 def _with_tuning(tile, splits, fn, stages=0):
+    """Runs fn on the pipelined GEMM (the small-row MFMA kernel switched off, every M a GEMM)."""
     old_t = mt.set_tuning(mt.TUNE_GEMM_TILE, tile)
     old_s = mt.set_tuning(mt.TUNE_GEMM_SPLITK, splits)
     old_p = mt.set_tuning(mt.TUNE_GEMM_STAGES, stages)
     old_r = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, 0)
+    old_m = mt.set_tuning(mt.TUNE_GEMV_MFMA, 1)
     try:
         return fn()
     finally:
@@ -46,6 +48,7 @@ def _with_tuning(tile, splits, fn, stages=0):
         mt.set_tuning(mt.TUNE_GEMM_SPLITK, old_s)
         mt.set_tuning(mt.TUNE_GEMM_STAGES, old_p)
         mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old_r)
+        mt.set_tuning(mt.TUNE_GEMV_MFMA, old_m)
 
 
 def _ids(s):

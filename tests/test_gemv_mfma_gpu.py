@@ -137,3 +137,25 @@ def test_forced_splits_bit_exact_reruns(gpu, splits, M, N, K, flags, norm):
         want64 = O.linear_f64(xu, c["w"], w2, O.F16, None, c["y0"], M, N, K, c["flags"])
         want32 = O.linear_f32(xu, c["w"], w2, O.F16, None, c["y0"], M, N, K, c["flags"])
     assert_linear_parity(outs[0], want32, want64, K, f"splits {splits} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("M,xt", [(9, O.F16), (16, O.F16), (33, O.BF16), (64, O.F16), (12, O.F32), (32, O.F32)])
+@pytest.mark.parametrize("shape", [(100, 1000, O.GELU, True), (896, 4864, O.SILU_GATE, False),
+                                   (1152, 896, O.ACCUM, False)], ids=_id)
+def test_skinny_rows_forced(gpu, M, xt, shape):
+    """MT_TUNE_GEMV_MFMA = 2: M > 8 on the same kernel with 2 or 4 column groups (x of the
+    weights' type staged as it is, other x as hi + lo halves)."""
+    N, K, flags, bias = shape
+    wt = O.BF16 if xt == O.BF16 else O.F16
+    say(f"gemv_mfma skinny M={M} x{xt} {_id(shape)}")
+    c = O.gemv_case(M, N, K, flags, bias, 1.0, wt=wt)
+    old = mt.set_tuning(mt.TUNE_GEMV_MFMA, 2)
+    old_r = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, 0)
+    try:
+        got, xu = run_linear(c, xt, gpu)
+        again, _ = run_linear(c, xt, gpu)
+    finally:
+        mt.set_tuning(mt.TUNE_GEMV_MFMA, old)
+        mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old_r)
+    assert_linear_parity(got, *expected(c, xu), K, f"skinny M={M} {_id(shape)}")
+    np.testing.assert_array_equal(again, got)

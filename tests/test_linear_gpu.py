@@ -33,15 +33,18 @@ def test_reference_kats_bf16_weights_fp32_activations(gpu, case):
 
 @pytest.mark.parametrize("case", O.KAT_ALL, ids=_id)
 def test_reference_kats_forced_gemm(gpu, case):
-    """Every KAT shape through the MFMA GEMM, fp32 x split into hi + lo halves."""
+    """Every KAT shape through the register-staged MFMA GEMM, fp32 x split into hi + lo halves
+    (the small-row MFMA kernel switched off)."""
     m, n, k, flags, bias, xs = case
     old = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, 0)
+    old_m = mt.set_tuning(mt.TUNE_GEMV_MFMA, 1)
     try:
         say(f"kat forced gemm {_id(case)}")
         c = O.gemv_case(m, n, k, flags, bias, xs, wt=O.BF16)
         got, xu = run_linear(c, O.F32, gpu)
     finally:
         mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old)
+        mt.set_tuning(mt.TUNE_GEMV_MFMA, old_m)
     assert_linear_parity(got, *expected(c, xu), k, "gemm " + _id(case))
 
 
@@ -202,8 +205,8 @@ def test_strided_views_and_edges(gpu):
         np.testing.assert_array_equal(got[:, N:], y0[:, N:])   # columns past N untouched
 
 
-@pytest.mark.parametrize("rows_max", [8, 0], ids=["gemv", "gemm"])
-def test_reference_rmsnorm_kat_through_identity_weights(gpu, rows_max):
+@pytest.mark.parametrize("rows_max,mfma", [(8, 0), (8, 1), (0, 1)], ids=["mfma", "gemv", "gemm"])
+def test_reference_rmsnorm_kat_through_identity_weights(gpu, rows_max, mfma):
     """KernelTests.testRMSNorm (KernelTests.swift:187-203) through the fused prologue: with
     W = I (exact in bf16) the linear returns the normalised rows themselves."""
     rows, k = 5, 896
@@ -215,12 +218,14 @@ def test_reference_rmsnorm_kat_through_identity_weights(gpu, rows_max):
     x_d = torch.from_numpy(np.concatenate([x, np.full((8, k), np.nan, np.float32)])).to(gpu)
     y_d = torch.zeros(rows, k, device=gpu)
     old = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, rows_max)
+    old_m = mt.set_tuning(mt.TUNE_GEMV_MFMA, mfma)
     try:
-        say(f"rmsnorm kat rows_max={rows_max}")
+        say(f"rmsnorm kat rows_max={rows_max} mfma={mfma}")
         mt.linear(x_d, dev16(eye, O.BF16, gpu), y_d, M=rows, norm=dev16(gb, O.BF16, gpu), eps=1e-6)
         torch.cuda.synchronize()
     finally:
         mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old)
+        mt.set_tuning(mt.TUNE_GEMV_MFMA, old_m)
     ex, i, g, w = O.worst_violation(y_d.cpu().numpy(), want, 1e-5)   # atol 1e-5 as the reference
     assert ex <= 0, f"index {i} got {g} want {w}"
 
