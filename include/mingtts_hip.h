@@ -31,6 +31,8 @@
  *   mt_dit_attention     Encoder.ditAttention      Sources/MingTTS/Engine/Kernels.swift:208-220
  *   mt_flow_assemble     Encoder.flowAssemble      Sources/MingTTS/Engine/Kernels.swift:222-235
  *   mt_flow_euler        Encoder.flowEuler         Sources/MingTTS/Engine/Kernels.swift:237-246
+ *   mt_st_*              SafeTensors               Sources/MingTTS/Engine/SafeTensors.swift:7-87
+ *   mt_arena_*           WeightArena               Sources/MingTTS/Engine/Weights.swift:8-79
  *   mt_last_error        MingTTSError text         Sources/MingTTS/Engine/MetalContext.swift:6-26
  */
 #ifndef MINGTTS_HIP_H
@@ -307,6 +309,55 @@ int mt_flow_assemble(const float *y, const float *history, const float *cemb, co
  */
 int mt_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row, float *capture,
                   uint32_t latent_dim, float cfg, float dt, mt_stream_t stream);
+
+/*
+ * The weight path (setup time; these calls read files and allocate host memory, and
+ * mt_arena_upload allocates pinned staging and a small counter buffer for its duration).
+ *
+ * mt_st_* -- SafeTensors (SafeTensors.swift:7-87): a memory-mapped .safetensors file (an
+ * 8-byte little-endian header length, a JSON header of {name: {dtype, shape, data_offsets}},
+ * the data).  A malformed header, or a file shorter than the header needs, is refused with
+ * MT_EINVAL and the reference's message.  Entries are listed in header order; mt_st_find
+ * gives a tensor's dtype (MT_BF16 / MT_F16 / MT_F32, or -1 for another), shape (up to 8
+ * dims), byte size and its bytes in the mapping (valid until mt_st_close).
+ */
+typedef struct mt_st mt_st;
+typedef struct mt_st_entry {
+    int32_t dtype;
+    uint32_t ndim;
+    uint64_t shape[8];
+    uint64_t bytes;
+    const void *host;
+} mt_st_entry;
+int mt_st_open(const char *path, mt_st **out);
+int mt_st_close(mt_st *st);
+int mt_st_count(const mt_st *st);
+int mt_st_name(const mt_st *st, uint32_t index, const char **name);
+int mt_st_find(const mt_st *st, const char *name, mt_st_entry *out);
+
+/*
+ * mt_arena_* -- WeightArena (Weights.swift:8-79): one module's 16-bit weights in one device
+ * buffer.  Plan with mt_arena_tensor (a bf16 tensor, or several concatenated along their
+ * first axis, e.g. q, k and v rows; Weights.swift:34-50) and mt_arena_padded (a bf16 [n,
+ * stored_k] weight laid out as [n, k] with zero columns past stored_k; Weights.swift:59-71);
+ * each lands at the next 256-byte-aligned offset in call order.  Then allocate
+ * mt_arena_bytes() of device memory (256-byte aligned) and mt_arena_upload it: synchronous on
+ * `stream`; the arena reads as zeros outside the tensors.  convert_to MT_F16 converts the
+ * uploaded bf16 weights to fp16 in place (round to nearest even); mt_arena_audit then gives
+ * the count of finite values that became +-inf and of nonzero values that became zero.  The
+ * st file must stay open until the upload.  No counterpart for the conversion in the
+ * reference (its kernels read bf16 only).
+ */
+typedef struct mt_arena mt_arena;
+int mt_arena_create(const mt_st *st, mt_dtype convert_to, mt_arena **out);
+int mt_arena_tensor(mt_arena *arena, const char *const *names, uint32_t n_names, uint64_t *offset,
+                    uint64_t *count);
+int mt_arena_padded(mt_arena *arena, const char *name, uint32_t n, uint32_t k, uint32_t stored_k,
+                    uint64_t *offset);
+uint64_t mt_arena_bytes(const mt_arena *arena);
+int mt_arena_upload(mt_arena *arena, void *device_base, mt_stream_t stream);
+int mt_arena_audit(const mt_arena *arena, uint64_t *overflow, uint64_t *underflow);
+int mt_arena_destroy(mt_arena *arena);
 
 /* Text of the last error on this thread ("" if none). */
 const char *mt_last_error(void);

@@ -31,6 +31,8 @@ EXPORTS = (
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_dit_attention", "mt_flow_assemble", "mt_flow_euler",
+    "mt_st_open", "mt_st_close", "mt_st_count", "mt_st_name", "mt_st_find", "mt_arena_create", "mt_arena_tensor",
+    "mt_arena_padded", "mt_arena_bytes", "mt_arena_upload", "mt_arena_audit", "mt_arena_destroy",
     "mt_last_error", "mt_version",
 )
 
@@ -84,6 +86,12 @@ class SeqItem(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int32), ("linear", LinearOp), ("attn", AttnOp)]
 
 
+class StEntry(ctypes.Structure):
+    """mt_st_entry: one tensor of a .safetensors file."""
+    _fields_ = [("dtype", ctypes.c_int32), ("ndim", ctypes.c_uint32), ("shape", ctypes.c_uint64 * 8),
+                ("bytes", ctypes.c_uint64), ("host", ctypes.c_void_p)]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -130,6 +138,31 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_flow_assemble.restype = i32
     L.mt_flow_euler.argtypes = [vp, vp, u32, u32, u32, vp, u32, f32, f32, vp]
     L.mt_flow_euler.restype = i32
+    cp = ctypes.c_char_p
+    L.mt_st_open.argtypes = [cp, ctypes.POINTER(vp)]
+    L.mt_st_open.restype = i32
+    L.mt_st_close.argtypes = [vp]
+    L.mt_st_close.restype = i32
+    L.mt_st_count.argtypes = [vp]
+    L.mt_st_count.restype = i32
+    L.mt_st_name.argtypes = [vp, u32, ctypes.POINTER(cp)]
+    L.mt_st_name.restype = i32
+    L.mt_st_find.argtypes = [vp, cp, ctypes.POINTER(StEntry)]
+    L.mt_st_find.restype = i32
+    L.mt_arena_create.argtypes = [vp, i32, ctypes.POINTER(vp)]
+    L.mt_arena_create.restype = i32
+    L.mt_arena_tensor.argtypes = [vp, ctypes.POINTER(cp), u32, ctypes.POINTER(u64), ctypes.POINTER(u64)]
+    L.mt_arena_tensor.restype = i32
+    L.mt_arena_padded.argtypes = [vp, cp, u32, u32, u32, ctypes.POINTER(u64)]
+    L.mt_arena_padded.restype = i32
+    L.mt_arena_bytes.argtypes = [vp]
+    L.mt_arena_bytes.restype = u64
+    L.mt_arena_upload.argtypes = [vp, vp, vp]
+    L.mt_arena_upload.restype = i32
+    L.mt_arena_audit.argtypes = [vp, ctypes.POINTER(u64), ctypes.POINTER(u64)]
+    L.mt_arena_audit.restype = i32
+    L.mt_arena_destroy.argtypes = [vp]
+    L.mt_arena_destroy.restype = i32
     L.mt_last_error.argtypes = []
     L.mt_last_error.restype = ctypes.c_char_p
     L.mt_version.argtypes = []
@@ -323,12 +356,19 @@ def flow_euler(y, pred, pred_row, null_row, cfg, dt, capture=None, ldp=None, str
 
 @dataclass
 class GPUTensor:
-    """GPUTensor (Kernels.swift:7-11): a tensor at an element offset of a buffer."""
+    """GPUTensor (Kernels.swift:7-11): a tensor at an element offset of a buffer, ``count``
+    elements long; ``dtype`` names the element type when the buffer is a byte arena (a
+    WeightArena's tensors sit at byte offsets of one uint8 buffer)."""
     buffer: object
     offset: int = 0
+    count: int = 0
+    dtype: Optional[int] = None
 
     def ptr(self) -> int:
         return self.buffer.data_ptr() + self.offset * self.buffer.element_size()
+
+    def elem_type(self) -> int:
+        return self.dtype if self.dtype is not None else dtype_code(self.buffer)
 
 
 @dataclass
@@ -366,7 +406,121 @@ class Encoder:
     def linear(self, x: ActView, rows: int, linear: Linear, y: ActView, flags: int = 0,
                gate: Optional[GPUTensor] = None) -> None:
         """Encoder.linear (Kernels.swift:132-161)."""
-        wt = dtype_code(linear.w.buffer)
+        wt = linear.w.elem_type()
         check(linear_raw(x.ptr(), dtype_code(x.buffer), linear.w.ptr(), gate.ptr() if gate else None, wt,
                          linear.bias.ptr() if linear.bias else None, y.ptr(), rows, linear.n, linear.k, x.ld, y.ld,
                          flags, self.stream))
+
+
+# ----------------------------------------------------------- weight path --
+
+class SafeTensors:
+    """SafeTensors (SafeTensors.swift:7-87): a memory-mapped .safetensors file (mt_st_*).
+    ``entries`` maps names (header order) to (dtype code or -1, shape, byte count)."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(load().mt_st_open(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h
+        L = load()
+        self.entries = {}
+        for i in range(check(L.mt_st_count(h))):
+            name = ctypes.c_char_p()
+            check(L.mt_st_name(h, i, ctypes.byref(name)))
+            e = self.entry(name.value.decode())
+            self.entries[name.value.decode()] = (e.dtype, tuple(e.shape[:e.ndim]), e.bytes)
+
+    def entry(self, name: str) -> StEntry:
+        e = StEntry()
+        check(load().mt_st_find(self.handle, name.encode(), ctypes.byref(e)))
+        return e
+
+    def raw(self, name: str) -> bytes:
+        """The tensor's bytes as stored."""
+        e = self.entry(name)
+        return ctypes.string_at(e.host, e.bytes)
+
+    def close(self) -> None:
+        if self.handle:
+            load().mt_st_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class WeightArena:
+    """WeightArena (Weights.swift:8-79) over mt_arena_*: plan tensors (``tensor``, ``linear``,
+    ``padded_linear``), then ``upload`` into one 256-byte-aligned device buffer (a torch uint8
+    tensor this object owns); the planned GPUTensor / Linear objects are bound to it then.
+    ``convert_to`` F16 converts the bf16 weights to fp16 at upload (``audit`` gives the
+    overflow and flush-to-zero counts)."""
+
+    def __init__(self, st: SafeTensors, convert_to: int = BF16):
+        h = ctypes.c_void_p()
+        check(load().mt_arena_create(st.handle, convert_to, ctypes.byref(h)))
+        self.handle, self.st, self.dtype = h, st, convert_to
+        self.buffer = None
+        self._planned = []
+
+    def tensor(self, *names: str) -> "GPUTensor":
+        arr = (ctypes.c_char_p * len(names))(*[n.encode() for n in names])
+        off, cnt = ctypes.c_uint64(), ctypes.c_uint64()
+        check(load().mt_arena_tensor(self.handle, arr, len(names), ctypes.byref(off), ctypes.byref(cnt)))
+        t = GPUTensor(None, off.value, cnt.value)
+        self._planned.append(t)
+        return t
+
+    def linear(self, prefix: str, n: int, k: int, bias: bool) -> "Linear":
+        w = self.tensor(prefix + ".weight")
+        if w.count != n * k:
+            raise MingTTSError(EINVAL, f"bad checkpoint: {prefix}.weight has {w.count} elements, expected {n}x{k}")
+        return Linear(w, self.tensor(prefix + ".bias") if bias else None, n, k)
+
+    def padded_linear(self, prefix: str, n: int, k: int, stored_k: int) -> "Linear":
+        off = ctypes.c_uint64()
+        check(load().mt_arena_padded(self.handle, (prefix + ".weight").encode(), n, k, stored_k, ctypes.byref(off)))
+        t = GPUTensor(None, off.value, n * k)
+        self._planned.append(t)
+        return Linear(t, None, n, k)
+
+    @property
+    def nbytes(self) -> int:
+        return load().mt_arena_bytes(self.handle)
+
+    def upload(self, device=None, stream=None) -> None:
+        import torch
+        dev = torch.device("cuda", 0) if device is None else device
+        self.buffer = torch.empty(max(self.nbytes, 256), dtype=torch.uint8, device=dev)
+        check(load().mt_arena_upload(self.handle, self.buffer.data_ptr(), _stream(stream)))
+        for t in self._planned:
+            t.buffer, t.dtype = self.buffer, self.dtype
+
+    def audit(self) -> tuple:
+        ov, un = ctypes.c_uint64(), ctypes.c_uint64()
+        check(load().mt_arena_audit(self.handle, ctypes.byref(ov), ctypes.byref(un)))
+        return ov.value, un.value
+
+    def close(self) -> None:
+        if self.handle:
+            load().mt_arena_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def load(st: SafeTensors, build, convert_to: int = BF16, device=None):
+        """WeightArena.load (Weights.swift:15-22): plans with ``build(arena)``, allocates and
+        uploads, and returns the build's result bound to the arena (kept on ``result``'s
+        arena attribute by the caller as needed)."""
+        arena = WeightArena(st, convert_to)
+        result = build(arena)
+        arena.upload(device)
+        return result, arena
