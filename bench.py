@@ -484,6 +484,70 @@ def bench_flow_step(torch, mt, dev, reps=5):
                 weight_mb_per_ode_step=wbytes / 1e6)
 
 
+def bench_vae_latent(torch, mt, dev, ws, reps=5):
+    """One latent of the streaming VAE decoder (VAEDecoder.decodeDispatches, VAEDecoder.swift:
+    81-107) after fc1: upsample4, the 24-layer sliding-window Qwen stack at M = 4 rows (rmsnorm
+    + qkv, rope_cache, attention over the last 65 keys, o +=, rmsnorm + gate|up, down +=; the
+    backbone's synthetic fp16 weights stand in for the VAE stack's, same shapes), the 3530 x
+    896 spectrum head, istft_frames (nfft 3528) and istft_emit (4 hops): 148 launches,
+    captured in a HIP graph and replayed."""
+    HQ, HKV, CAP, NFFT, HOP, RING = 14, 2, 512, 3528, 882, 8
+    pos0 = 4 * 50
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    h = [torch.randn(H, generator=g, device=dev) for _ in range(3)]
+    frames = torch.zeros(4, H, device=dev)
+    qkv = torch.zeros(4, QKV, device=dev)
+    att = torch.zeros(4, HQ * 64, device=dev)
+    mlp = torch.zeros(4, INTER, device=dev)
+    spec = torch.zeros(4, NFFT + 2, device=dev)
+    head_w = (torch.randn(NFFT + 2, H, generator=g, device=dev) * 0.02).half()
+    head_b = (torch.randn(NFFT + 2, generator=g, device=dev) * 0.02).half()
+    caches = [(torch.randn(HKV, CAP, 64, generator=g, device=dev).half(),
+               torch.randn(HKV, CAP, 64, generator=g, device=dev).half()) for _ in ws]
+    i = torch.arange(32, device=dev, dtype=torch.float32)
+    invf = (1.0 / torch.pow(torch.tensor(1e6, device=dev), 2.0 * i / 64.0)).float()
+    t = torch.arange(NFFT, device=dev, dtype=torch.float64)
+    window = (0.5 - 0.5 * torch.cos(2 * torch.pi * t / NFFT)).float()
+    cos_table = torch.cos(2 * torch.pi * t / NFFT).float()
+    ring = torch.zeros(RING, NFFT, device=dev)
+    pcm = torch.zeros(4 * HOP, device=dev)
+    cs = torch.cuda.Stream(device=dev)
+    s = cs.cuda_stream
+
+    def step():
+        mt.upsample4(h[0], h[1], h[2], frames, stream=s)
+        for p, (kc, vc) in zip(ws, caches):
+            mt.linear(frames, p["qkv"], qkv, 4, bias=p["qkv_b"], norm=p["norm1"], stream=s)
+            mt.rope_cache(qkv, QKV, 4, HQ, HKV, pos0, kc, vc, CAP, invf, stream=s)
+            mt.attention(qkv, QKV, 4, HQ, HKV, pos0, 65, kc, vc, CAP, att, HQ * 64, stream=s)
+            mt.linear(att, p["o"], frames, 4, flags=mt.GemvFlags.accumulate, stream=s)
+            mt.linear(frames, p["gate"], mlp, 4, flags=mt.GemvFlags.siluGate, w2=p["up"], norm=p["norm2"], stream=s)
+            mt.linear(mlp, p["down"], frames, 4, flags=mt.GemvFlags.accumulate, stream=s)
+        mt.linear(frames, head_w, spec, 4, bias=head_b, stream=s)
+        mt.istft_frames(spec, 4, NFFT, cos_table, window, ring, 4 * 50, RING, stream=s)
+        mt.istft_emit(ring, window, NFFT, HOP, 4 * 50 * HOP, 4 * HOP, 4 * 50 + 3, RING, pcm, stream=s)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cs):
+            step()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    best = None
+    for _ in range(reps):
+        ev.start()
+        graph.replay()
+        ms = ev.stop_ms()
+        best = ms if best is None else min(best, ms)
+    return dict(us_per_latent=best * 1e3, launches=1 + 6 * len(ws) + 3,
+                audio_ms_per_latent=4 * HOP / 44100 * 1e3)
+
+
 def bench_copy(torch, dev, mib=1024, reps=5):
     """A plain device-to-device copy of a known size: the calibration run for the HBM byte
     counters (FETCH_SIZE / WRITE_SIZE per dispatch against exactly mib MiB each way)."""
@@ -662,6 +726,9 @@ def main() -> int:
         line["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
         line["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
+        log("VAE decode of one latent (24-layer stack at M = 4, head, ISTFT; graph replay)")
+        line["vae_latent"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                              for k, v in bench_vae_latent(torch, mt, dev, ws).items()}
     if not args.no_cpu:
         log("CPU baseline (oracle, host cores)")
         cb = cpu_baseline(torch, ws)

@@ -31,6 +31,9 @@
  *   mt_dit_attention     Encoder.ditAttention      Sources/MingTTS/Engine/Kernels.swift:208-220
  *   mt_flow_assemble     Encoder.flowAssemble      Sources/MingTTS/Engine/Kernels.swift:222-235
  *   mt_flow_euler        Encoder.flowEuler         Sources/MingTTS/Engine/Kernels.swift:237-246
+ *   mt_upsample4         Encoder.upsample4         Sources/MingTTS/Engine/Kernels.swift:247-257
+ *   mt_istft_frames      Encoder.istftFrames       Sources/MingTTS/Engine/Kernels.swift:259-270
+ *   mt_istft_emit        Encoder.istftEmit         Sources/MingTTS/Engine/Kernels.swift:272-283
  *   mt_st_*              SafeTensors               Sources/MingTTS/Engine/SafeTensors.swift:7-87
  *   mt_arena_*           WeightArena               Sources/MingTTS/Engine/Weights.swift:8-79
  *   mt_last_error        MingTTSError text         Sources/MingTTS/Engine/MetalContext.swift:6-26
@@ -309,6 +312,34 @@ int mt_flow_assemble(const float *y, const float *history, const float *cemb, co
  */
 int mt_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row, float *capture,
                   uint32_t latent_dim, float cfg, float dt, mt_stream_t stream);
+
+/*
+ * The audio VAE decoder's tail (VAEDecoder.decodeDispatches, VAEDecoder.swift:81-107).
+ *
+ * mt_upsample4 -- Encoder.upsample4 (Kernels.swift:247-257, Shaders.swift:700-718): the four
+ * frames of a latent from fc1 outputs prev / cur / next ([hidden] each; prev or next NULL when
+ * absent, then clamped to cur), torch's linear upsample (align_corners = false, scale 4):
+ * rows 0..3 = 0.625 cur + 0.375 prev, 0.875 cur + 0.125 prev, 0.875 cur + 0.125 next,
+ * 0.625 cur + 0.375 next; frames row stride ldf.
+ *
+ * mt_istft_frames -- Encoder.istftFrames (Kernels.swift:259-270, Shaders.swift:720-759):
+ * spectrum rows (stride ld_spec) hold [log-magnitude, phase] of nfft / 2 + 1 bins each; frame
+ * f = irfft(min(e^logmag, 100) e^{i phase}) / nfft * window lands in ring slot (frame0 + f) %
+ * ring of ring_frames ([ring][nfft]).  cos_table[t] = cos(2 pi t / nfft).  nfft a multiple of
+ * 4, at most 4096; count <= ring.
+ *
+ * mt_istft_emit -- Encoder.istftEmit (Kernels.swift:272-283, Shaders.swift:761-787): samples
+ * s0 .. s0 + count - 1 of the stream: for s = s0 + i + (nfft - hop) / 2, out[i] = the sum of
+ * frames f <= last_frame with 0 <= s - f hop < nfft of their sample s - f hop, over the sum of
+ * window^2 at those samples.
+ */
+int mt_upsample4(const float *prev, const float *cur, const float *next, float *frames, uint32_t ldf,
+                 uint32_t hidden, mt_stream_t stream);
+int mt_istft_frames(const float *spec, uint32_t ld_spec, uint32_t count, uint32_t nfft,
+                    const float *cos_table, const float *window, float *ring_frames, uint32_t frame0,
+                    uint32_t ring, mt_stream_t stream);
+int mt_istft_emit(const float *ring_frames, const float *window, uint32_t nfft, uint32_t hop, uint32_t s0,
+                  uint32_t count, uint32_t last_frame, uint32_t ring, float *out, mt_stream_t stream);
 
 /*
  * The weight path (setup time; these calls read files and allocate host memory, and

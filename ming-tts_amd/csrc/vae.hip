@@ -1,0 +1,145 @@
+// The audio VAE decoder's tail around its linears: the x4 linear upsample of fc1 outputs, the
+// ISTFT frame synthesis and the overlap-add emission.
+//
+// Reference kernels replaced: upsample4, istft_frames and istft_emit (Shaders.swift:697-790),
+// dispatched by Encoder.upsample4 / istftFrames / istftEmit (Kernels.swift:247-283) from
+// VAEDecoder.decodeDispatches (VAEDecoder.swift:81-107).  Same arithmetic: torch's linear
+// upsample weights (0.625 / 0.375, 0.875 / 0.125, neighbours clamped when absent); frame f
+// = irfft(min(e^logmag, 100) e^{i phase}) / N * window with the DFT summed directly from a
+// cos table; out = sum of overlapping frames / sum of their window^2.
+//
+// Layout on gfx950:
+//   - upsample4: one thread per (frame row, feature);
+//   - istft_frames: one 256-thread workgroup per (frame, 512 output samples): the frame's
+//     bins (re, im) and the cos table sit in LDS; a thread computes samples t and N - t in one
+//     pass over the bins, since cos(2 pi k (N - t) / N) = cos(2 pi k t / N) and the sine terms
+//     only change sign, which halves the table reads and multiply-adds of the reference loop;
+//   - istft_emit: one thread per output sample.
+#include "mt_device.hpp"
+#include "mt_internal.hpp"
+#include "mingtts_hip.h"
+
+namespace mt {
+
+namespace {
+
+constexpr int ISTFT_NMAX = 4096;   // nfft limit of the LDS tables
+constexpr int ISTFT_SPAN = 512;    // samples t per workgroup (t and N - t: 2 per thread)
+
+__global__ __launch_bounds__(256) void upsample4_kernel(const float *prev, const float *cur, const float *next,
+                                                        float *frames, uint32_t ldf, uint32_t hidden, uint32_t has_prev,
+                                                        uint32_t has_next) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
+    if (c >= hidden) return;
+    const float h = cur[c];
+    float v;
+    if (r == 0) v = has_prev ? 0.625f * h + 0.375f * prev[c] : h;
+    else if (r == 1) v = has_prev ? 0.875f * h + 0.125f * prev[c] : h;
+    else if (r == 2) v = has_next ? 0.875f * h + 0.125f * next[c] : h;
+    else v = has_next ? 0.625f * h + 0.375f * next[c] : h;
+    frames[static_cast<size_t>(r) * ldf + c] = v;
+}
+
+// Samples t and N - t of frame blockIdx.y for t in [blockIdx.x * 512 / 2 ..): thread j takes
+// t = blockIdx.x * 256 + j (t <= N / 2) and its mirror N - t.
+__global__ __launch_bounds__(256) void istft_frames_kernel(const float *spec, uint32_t ld_spec, const float *cos_table,
+                                                           const float *window, float *ring_frames, uint32_t nfft,
+                                                           uint32_t frame0, uint32_t ring) {
+    __shared__ float re[ISTFT_NMAX / 2 + 1];
+    __shared__ float im[ISTFT_NMAX / 2 + 1];
+    __shared__ float ctab[ISTFT_NMAX];
+    const uint32_t N = nfft, bins = N / 2 + 1, f = blockIdx.y;
+    const float *row = spec + static_cast<size_t>(f) * ld_spec;
+    for (uint32_t k = threadIdx.x; k < bins; k += 256) {
+        const float mag = fminf(expf(row[k]), 100.0f);
+        const float ph = row[bins + k];
+        re[k] = mag * cosf(ph);
+        im[k] = mag * sinf(ph);
+    }
+    for (uint32_t k = threadIdx.x; k < N; k += 256) ctab[k] = cos_table[k];
+    __syncthreads();
+    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+    if (t > N / 2) return;
+    // sum over k = 1 .. N/2 - 1 of re[k] cos(2 pi k t / N) and im[k] sin(2 pi k t / N), the
+    // sine read from the cos table a quarter turn on: sin(a) = cos(a + 3 pi / 2).
+    const uint32_t quarter3 = 3 * (N / 4);
+    uint32_t idx = 0;
+    float sc = 0.0f, ss = 0.0f;
+    for (uint32_t k = 1; k < N / 2; k++) {
+        idx += t;
+        if (idx >= N) idx -= N;
+        uint32_t sidx = idx + quarter3;
+        if (sidx >= N) sidx -= N;
+        sc = fmaf(re[k], ctab[idx], sc);
+        ss = fmaf(im[k], ctab[sidx], ss);
+    }
+    const float base = re[0] + ((t & 1) ? -re[N / 2] : re[N / 2]);  // N even: t and N - t share parity
+    const float scale = 1.0f / static_cast<float>(N);
+    float *out = ring_frames + static_cast<size_t>((frame0 + f) % ring) * N;
+    out[t] = (base + 2.0f * (sc - ss)) * scale * window[t];
+    if (t > 0 && t < N / 2) out[N - t] = (base + 2.0f * (sc + ss)) * scale * window[N - t];
+}
+
+__global__ __launch_bounds__(256) void istft_emit_kernel(const float *ring_frames, const float *window, float *out,
+                                                         uint32_t nfft, uint32_t hop, uint32_t pad, uint32_t s0,
+                                                         uint32_t count, uint32_t last_frame, uint32_t ring) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    const uint32_t s = s0 + i + pad;
+    const uint32_t fhi = min(s / hop, last_frame);
+    const uint32_t flo = s >= nfft ? (s - nfft) / hop + 1 : 0u;
+    float acc = 0.0f, env = 0.0f;
+    for (uint32_t f = flo; f <= fhi; f++) {
+        const uint32_t t = s - f * hop;
+        if (t >= nfft) continue;
+        const float w = window[t];
+        acc += ring_frames[static_cast<size_t>(f % ring) * nfft + t];
+        env = fmaf(w, w, env);
+    }
+    out[i] = acc / env;
+}
+
+}  // namespace
+
+}  // namespace mt
+
+using namespace mt;
+
+extern "C" {
+
+int mt_upsample4(const float *prev, const float *cur, const float *next, float *frames, uint32_t ldf, uint32_t hidden,
+                 mt_stream_t stream) {
+    if (hidden == 0) return MT_OK;
+    if (!cur || !frames) return set_error(MT_EINVAL, "mt_upsample4: null pointer");
+    if (ldf < hidden) return set_error(MT_EINVAL, "mt_upsample4: ldf %u < hidden %u", ldf, hidden);
+    hipLaunchKernelGGL(upsample4_kernel, dim3((hidden + 255) / 256, 4), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), prev ? prev : cur, cur, next ? next : cur, frames, ldf,
+                       hidden, prev ? 1u : 0u, next ? 1u : 0u);
+    return check_launch("upsample4");
+}
+
+int mt_istft_frames(const float *spec, uint32_t ld_spec, uint32_t count, uint32_t nfft, const float *cos_table,
+                    const float *window, float *ring_frames, uint32_t frame0, uint32_t ring, mt_stream_t stream) {
+    if (count == 0) return MT_OK;
+    if (!spec || !cos_table || !window || !ring_frames) return set_error(MT_EINVAL, "mt_istft_frames: null pointer");
+    if (nfft < 8 || nfft % 4 || nfft > static_cast<uint32_t>(ISTFT_NMAX))
+        return set_error(MT_EINVAL, "mt_istft_frames: nfft %u must be a multiple of 4 in 8..%d", nfft, ISTFT_NMAX);
+    if (ld_spec < nfft + 2) return set_error(MT_EINVAL, "mt_istft_frames: ld_spec %u < nfft + 2", ld_spec);
+    if (ring == 0 || count > ring) return set_error(MT_EINVAL, "mt_istft_frames: %u frames for a ring of %u", count, ring);
+    const dim3 grid((nfft / 2 + 1 + 255) / 256, count);
+    hipLaunchKernelGGL(istft_frames_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), spec, ld_spec,
+                       cos_table, window, ring_frames, nfft, frame0, ring);
+    return check_launch("istft_frames");
+}
+
+int mt_istft_emit(const float *ring_frames, const float *window, uint32_t nfft, uint32_t hop, uint32_t s0,
+                  uint32_t count, uint32_t last_frame, uint32_t ring, float *out, mt_stream_t stream) {
+    if (count == 0) return MT_OK;
+    if (!ring_frames || !window || !out) return set_error(MT_EINVAL, "mt_istft_emit: null pointer");
+    if (hop == 0 || hop > nfft || ring == 0) return set_error(MT_EINVAL, "mt_istft_emit: hop %u, nfft %u, ring %u", hop, nfft, ring);
+    hipLaunchKernelGGL(istft_emit_kernel, dim3((count + 255) / 256), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       ring_frames, window, out, nfft, hop, (nfft - hop) / 2, s0, count, last_frame, ring);
+    return check_launch("istft_emit");
+}
+
+}  // extern "C"

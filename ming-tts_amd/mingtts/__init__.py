@@ -31,7 +31,7 @@ EXPORTS = (
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_dit_attention", "mt_flow_assemble", "mt_flow_euler",
-    "mt_st_open", "mt_st_close", "mt_st_count", "mt_st_name", "mt_st_find", "mt_arena_create", "mt_arena_tensor",
+    "mt_upsample4", "mt_istft_frames", "mt_istft_emit", "mt_st_open", "mt_st_close", "mt_st_count", "mt_st_name", "mt_st_find", "mt_arena_create", "mt_arena_tensor",
     "mt_arena_padded", "mt_arena_bytes", "mt_arena_upload", "mt_arena_audit", "mt_arena_destroy",
     "mt_last_error", "mt_version",
 )
@@ -138,6 +138,12 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_flow_assemble.restype = i32
     L.mt_flow_euler.argtypes = [vp, vp, u32, u32, u32, vp, u32, f32, f32, vp]
     L.mt_flow_euler.restype = i32
+    L.mt_upsample4.argtypes = [vp, vp, vp, vp, u32, u32, vp]
+    L.mt_upsample4.restype = i32
+    L.mt_istft_frames.argtypes = [vp, u32, u32, u32, vp, vp, vp, u32, u32, vp]
+    L.mt_istft_frames.restype = i32
+    L.mt_istft_emit.argtypes = [vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]
+    L.mt_istft_emit.restype = i32
     cp = ctypes.c_char_p
     L.mt_st_open.argtypes = [cp, ctypes.POINTER(vp)]
     L.mt_st_open.restype = i32
@@ -350,6 +356,24 @@ def flow_euler(y, pred, pred_row, null_row, cfg, dt, capture=None, ldp=None, str
     latent = y.numel()
     check(load().mt_flow_euler(_ptr(y), _ptr(pred), pred.stride(0) if ldp is None else ldp, pred_row, null_row,
                                _ptr(capture), latent, cfg, dt, _stream(stream)))
+
+
+def upsample4(prev, cur, nxt, frames, ldf=None, stream=None) -> None:
+    """Encoder.upsample4 (Kernels.swift:247-257): prev / nxt None when absent."""
+    check(load().mt_upsample4(_ptr(prev), _ptr(cur), _ptr(nxt), _ptr(frames), frames.stride(0) if ldf is None else ldf,
+                              cur.numel(), _stream(stream)))
+
+
+def istft_frames(spec, count, nfft, cos_table, window, ring_frames, frame0, ring, ld_spec=None, stream=None) -> None:
+    """Encoder.istftFrames (Kernels.swift:259-270)."""
+    check(load().mt_istft_frames(_ptr(spec), spec.stride(0) if ld_spec is None else ld_spec, count, nfft, _ptr(cos_table),
+                                 _ptr(window), _ptr(ring_frames), frame0, ring, _stream(stream)))
+
+
+def istft_emit(ring_frames, window, nfft, hop, s0, count, last_frame, ring, out, stream=None) -> None:
+    """Encoder.istftEmit (Kernels.swift:272-283)."""
+    check(load().mt_istft_emit(_ptr(ring_frames), _ptr(window), nfft, hop, s0, count, last_frame, ring, _ptr(out),
+                               _stream(stream)))
 
 
 # ------------------------------------------- mirror of the reference types --

@@ -20,6 +20,8 @@ Contents (reference paths relative to the reference checkout):
 * ``rope_interleaved`` / ``dit_attention_f64`` / ``flow_assemble_f64`` / ``flow_euler_f64``
   -- the DiT flow step around its linears: Shaders.swift:598-693 and the CPU reference of
   KernelTests.swift:282-318.
+* ``upsample4_f64`` / ``istft_frame_f64`` / ``istft_emit_f64`` -- the VAE decoder's tail:
+  Shaders.swift:697-790 and the CPU references of KernelTests.swift:322-398.
 """
 from __future__ import annotations
 
@@ -395,3 +397,45 @@ def flow_euler_f64(y, pred, pred_row: int, null_row: int, cfg: float, dt: float)
     c = np.asarray(pred[pred_row], np.float64)
     u = np.asarray(pred[null_row], np.float64)
     return np.asarray(y, np.float64) + (c + (c - u) * cfg) * dt, np.concatenate([c, u])
+
+
+# --------------------------------------------------------- VAE tail --
+
+def upsample4_f64(prev, cur, nxt) -> np.ndarray:
+    """The four frames of a latent (Shaders.swift:700-718): torch's linear x4 upsample weights
+    with an absent neighbour (None) clamped to cur.  fp64.  Returns [4, hidden]."""
+    c = np.asarray(cur, np.float64)
+    p = c if prev is None else np.asarray(prev, np.float64)
+    n = c if nxt is None else np.asarray(nxt, np.float64)
+    return np.stack([0.625 * c + 0.375 * p, 0.875 * c + 0.125 * p, 0.875 * c + 0.125 * n, 0.625 * c + 0.375 * n])
+
+
+def istft_frame_f64(row, nfft: int, window) -> np.ndarray:
+    """One synthesis frame (Shaders.swift:720-759, KernelTests.swift:361-374): bins k <=
+    nfft / 2 of magnitude min(e^row[k], 100) and phase row[bins + k]; the real inverse DFT
+    with 1 / nfft scaling (the imaginary parts of bins 0 and nfft / 2 drop out), times the
+    window.  fp64."""
+    bins = nfft // 2 + 1
+    row = np.asarray(row, np.float64)
+    mag = np.minimum(np.exp(row[:bins]), 100.0)
+    spec = mag * np.exp(1j * row[bins:2 * bins])
+    return np.fft.irfft(spec, n=nfft) * np.asarray(window, np.float64)
+
+
+def istft_emit_f64(frames, window, nfft: int, hop: int, s0: int, count: int, last_frame: int) -> np.ndarray:
+    """Overlap-add of frames[0 .. last_frame] (KernelTests.swift:375-380, Shaders.swift:761-787):
+    out[i] for s = s0 + i + (nfft - hop) / 2 is the sum of frame f's sample s - f hop over the
+    frames covering s, divided by the sum of window^2 there.  fp64."""
+    pad = (nfft - hop) // 2
+    w2 = np.asarray(window, np.float64) ** 2
+    out = np.zeros(count, np.float64)
+    for i in range(count):
+        s = s0 + i + pad
+        acc = env = 0.0
+        for f in range(0, last_frame + 1):
+            t = s - f * hop
+            if 0 <= t < nfft:
+                acc += frames[f][t]
+                env += w2[t]
+        out[i] = acc / env
+    return out

@@ -432,3 +432,46 @@ def test_flow_assemble_and_euler_closed_forms():
     y2, _ = O.flow_euler_f64(y0, pred, 2, 5, 1.0, 0.5)
     np.testing.assert_allclose(y2, y0 + (2 * pred[2] - pred[5]) * 0.5, rtol=1e-14)
     np.testing.assert_array_equal(cap, np.concatenate([pred[2], pred[5]]))
+
+
+def test_istft_frame_matches_a_direct_dft_and_upsample_matches_torch():
+    """The frame synthesis against the reference's direct double loop (KernelTests.swift:
+    361-374) at a small N, with a planted sign mistake caught; the upsample against torch's
+    linear interpolation (align_corners = False, scale 4; KernelTests.swift:384-398)."""
+    N = 24
+    bins = N // 2 + 1
+    rng = np.random.default_rng(13)
+    row = np.concatenate([rng.uniform(-1, 1, bins), rng.uniform(0, 3, bins)])
+    win = 0.5 - 0.5 * np.cos(2 * np.pi * np.arange(N) / N)
+    got = O.istft_frame_f64(row, N, win)
+    mag = np.minimum(np.exp(row[:bins]), 100.0)
+    re, im = mag * np.cos(row[bins:]), mag * np.sin(row[bins:])
+    want = np.empty(N)
+    for t in range(N):
+        acc = re[0] + (re[N // 2] if t % 2 == 0 else -re[N // 2])
+        for k in range(1, N // 2):
+            a = 2 * np.pi * (k * t % N) / N
+            acc += 2 * (re[k] * np.cos(a) - im[k] * np.sin(a))
+        want[t] = acc / N * win[t]
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-14)
+    planted = O.istft_frame_f64(np.concatenate([row[:bins], -row[bins:]]), N, win)   # conjugate phase
+    assert np.max(np.abs(planted - want)) > 1e-3
+    h = O.LCG(9).floats(5 * 32).reshape(5, 32).astype(np.float64)
+    frames = np.concatenate([O.upsample4_f64(h[i - 1] if i else None, h[i], h[i + 1] if i < 4 else None)
+                             for i in range(5)])
+    ref = F.interpolate(torch.from_numpy(h.T[None]), scale_factor=4, mode="linear", align_corners=False)[0].T.numpy()
+    np.testing.assert_allclose(frames, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_istft_emit_reconstructs_a_stream():
+    """Frames cut from a known signal with a Hann analysis window, times the synthesis window
+    (as istft_frames applies it), overlap-added with the window^2 envelope give the signal
+    back: the identity the emit step relies on."""
+    N, hop = 32, 8
+    rng = np.random.default_rng(14)
+    sig = rng.standard_normal(12 * hop + N)
+    win = 0.5 - 0.5 * np.cos(2 * np.pi * np.arange(N) / N)
+    frames = [sig[f * hop:f * hop + N] * win * win for f in range(12)]
+    pad = (N - hop) // 2
+    out = O.istft_emit_f64(frames, win, N, hop, 0, 8 * hop, 11)
+    np.testing.assert_allclose(out, sig[pad:pad + 8 * hop], rtol=1e-12)
