@@ -426,13 +426,14 @@ def bench_gemm_ops(torch, mt, dev, ws, reps=5):
     return rows
 
 
-def bench_flow_step(torch, mt, dev, reps=5):
+def bench_flow_step(torch, mt, dev, reps=5, fused=True):
     """The flow stage of one generation step at the reference's flow-head shape
     (MingEngine.encodeStep, Engine.swift:395-402; DiTForward.encode, DiT.swift:35-52): 10 ODE
     steps of flow_assemble, 8 DiT blocks (hidden 1024, 16 heads, batch 2 x seq 3 = 6 rows:
     rmsnorm+qkv 3072x1024, dit_attention, out 1024x1024 +=, rmsnorm+ff1 4096x1024 GELU,
     ff2 1024x4096 +=), the final rmsnorm + 64x1024 linear and flow_euler: 430 launches, bf16
-    weights ~ N(0, 0.02^2), captured in a HIP graph and replayed."""
+    weights ~ N(0, 0.02^2), captured in a HIP graph and replayed.  With ``fused`` each block's
+    attention runs inside its out projection (mt_dit_attention_linear): 350 launches."""
     HID, HEADS, LAT, BLOCKS, STEPS = 1024, 16, 64, 8, 10
     g = torch.Generator(device=dev)
     g.manual_seed(5)
@@ -465,8 +466,13 @@ def bench_flow_step(torch, mt, dev, reps=5):
             mt.flow_assemble(y, hist, cemb, cb, temb[k], xw, xb, x, stream=cs.cuda_stream)
             for p in blocks:
                 mt.linear(x, p["qkv"], qkv, 6, bias=p["qkv_b"], norm=p["n1"], stream=cs.cuda_stream)
-                mt.dit_attention(qkv, 2, 3, HEADS, invf, att, stream=cs.cuda_stream)
-                mt.linear(att, p["out"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["out_b"], stream=cs.cuda_stream)
+                if fused:
+                    mt.dit_attention_linear(qkv, 2, 3, HEADS, invf, p["out"], x, flags=mt.GemvFlags.accumulate,
+                                            bias=p["out_b"], stream=cs.cuda_stream)
+                else:
+                    mt.dit_attention(qkv, 2, 3, HEADS, invf, att, stream=cs.cuda_stream)
+                    mt.linear(att, p["out"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["out_b"],
+                              stream=cs.cuda_stream)
                 mt.linear(x, p["ff1"], ff, 6, flags=mt.GemvFlags.gelu, bias=p["ff1_b"], norm=p["n2"],
                           stream=cs.cuda_stream)
                 mt.linear(ff, p["ff2"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=cs.cuda_stream)
@@ -490,8 +496,9 @@ def bench_flow_step(torch, mt, dev, reps=5):
         ms = ev.stop_ms()
         best = ms if best is None else min(best, ms)
     wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
-    return dict(us_per_generation_step=best * 1e3, us_per_ode_step=best * 1e3 / STEPS, launches=STEPS * (3 + 5 * BLOCKS),
-                weight_mb_per_ode_step=wbytes / 1e6)
+    return dict(us_per_generation_step=best * 1e3, us_per_ode_step=best * 1e3 / STEPS,
+                launches=STEPS * (3 + (4 if fused else 5) * BLOCKS), weight_mb_per_ode_step=wbytes / 1e6,
+                attention="inside the out projection" if fused else "separate launch")
 
 
 def bench_vae_latent(torch, mt, dev, ws, reps=5):
@@ -736,6 +743,8 @@ def main() -> int:
         line["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
         line["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
+        line["flow_step_separate_attention"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                                for k, v in bench_flow_step(torch, mt, dev, fused=False).items()}
         log("VAE decode of one latent (24-layer stack at M = 4, head, ISTFT; graph replay)")
         line["vae_latent"] = {k: (round(v, 3) if isinstance(v, float) else v)
                               for k, v in bench_vae_latent(torch, mt, dev, ws).items()}

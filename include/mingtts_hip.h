@@ -29,6 +29,8 @@
  *                        independent caches at
  *                        M = 1 each
  *   mt_dit_attention     Encoder.ditAttention      Sources/MingTTS/Engine/Kernels.swift:208-220
+ *   mt_dit_attention_    Encoder.ditAttention +    Sources/MingTTS/Engine/DiT.swift:44-45
+ *     linear             Encoder.linear(out, +=)
  *   mt_flow_assemble     Encoder.flowAssemble      Sources/MingTTS/Engine/Kernels.swift:222-235
  *   mt_flow_euler        Encoder.flowEuler         Sources/MingTTS/Engine/Kernels.swift:237-246
  *   mt_upsample4         Encoder.upsample4         Sources/MingTTS/Engine/Kernels.swift:247-257
@@ -292,6 +294,20 @@ int mt_attention_decode(const float *q, uint32_t ldq, uint32_t B, uint32_t hq, u
  */
 int mt_dit_attention(const float *qkv, uint32_t ld, uint32_t B, uint32_t S, uint32_t H, const float *inv_freq,
                      float *out, uint32_t ldo, float scale, mt_stream_t stream);
+
+/*
+ * mt_dit_attention_linear -- the DiT block's Encoder.ditAttention followed by the out
+ * projection Encoder.linear(attn, block.out, x, flags: .accumulate) (DiT.swift:44-45) in one
+ * launch: y (op)= att W^T with the GemvFlags epilogue, where att = mt_dit_attention(qkv, p.ldx,
+ * B, S, H, inv_freq, ..., scale) is computed inside the linear's prologue and never stored.
+ * p.M = B * S (<= 32), p.K = 64 H, p.ldx = the qkv row stride (>= 3 K); the rest of p, w, wt,
+ * bias and y as mt_linear with fp32 x (no MT_SILU_GATE).  qkv 16-byte aligned with a 16-byte
+ * row stride; y must not overlap qkv.  Gives the same bits as mt_dit_attention into a buffer
+ * followed by mt_linear of that buffer.
+ */
+int mt_dit_attention_linear(const float *qkv, uint32_t B, uint32_t S, uint32_t H, const float *inv_freq, float scale,
+                            const void *w, mt_dtype wt, const void *bias, float *y, mt_gemv_params p,
+                            mt_stream_t stream);
 
 /*
  * mt_flow_assemble -- Encoder.flowAssemble (Kernels.swift:222-235, Shaders.swift:650-676):

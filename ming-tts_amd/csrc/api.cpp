@@ -331,6 +331,31 @@ int mt_dit_attention(const float *qkv, uint32_t ld, uint32_t B, uint32_t S, uint
     return launch_dit_attention(qkv, ld, B, S, H, inv_freq, out, ldo, scale, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mt_dit_attention_linear(const float *qkv, uint32_t B, uint32_t S, uint32_t H, const float *inv_freq, float scale,
+                            const void *w, mt_dtype wt, const void *bias, float *y, mt_gemv_params p,
+                            mt_stream_t stream) {
+    const char *who = "mt_dit_attention_linear";
+    if (S > 8) return set_error(MT_EINVAL, "%s: at most 8 rows per sequence, got %u", who, S);
+    if (static_cast<uint64_t>(B) * S != p.M) return set_error(MT_EINVAL, "%s: M %u is not B %u x S %u", who, p.M, B, S);
+    if (static_cast<uint64_t>(H) * 64 != p.K) return set_error(MT_EINVAL, "%s: K %u is not 64 H (H %u)", who, p.K, H);
+    if (p.flags & MT_SILU_GATE) return set_error(MT_EINVAL, "%s: MT_SILU_GATE needs a gate partner", who);
+    LinearArgs a;
+    int rc = validate_linear(who, qkv, MT_F32, w, nullptr, wt, bias, nullptr, y, p, a);
+    if (rc) return rc;
+    if (p.M == 0 || p.N == 0) return MT_OK;
+    if (!inv_freq) return set_error(MT_EINVAL, "%s: null inv_freq", who);
+    if (static_cast<uint64_t>(p.ldx) < 3ull * p.K) return set_error(MT_EINVAL, "%s: qkv row stride %u < 3 K", who, p.ldx);
+    // y must not overlap the whole q | k | v span that the prologue reads.
+    const char *qb = reinterpret_cast<const char *>(qkv);
+    const char *qe = qb + (static_cast<size_t>(p.M - 1) * p.ldx + 3ull * p.K) * 4;
+    const char *yb = reinterpret_cast<const char *>(y);
+    const char *ye = yb + (static_cast<size_t>(p.M - 1) * p.ldy + p.N) * 4;
+    if (qb < ye && yb < qe) return set_error(MT_EINVAL, "%s: qkv overlaps y", who);
+    if (gemv_mfma_columns(p.M, MT_F32, wt, false) == 0)
+        return set_error(MT_ENOTSUP, "%s: at most 32 rows, got %u", who, p.M);
+    return launch_gemv_mfma_attn(a, wt, inv_freq, S, H, scale, reinterpret_cast<hipStream_t>(stream));
+}
+
 int mt_flow_assemble(const float *y, const float *history, const float *cemb, const void *cond_bias,
                      const float *temb, const void *x_w, const void *x_b, mt_dtype wt, float *x, uint32_t ldx,
                      uint32_t hidden, uint32_t latent_dim, mt_stream_t stream) {

@@ -13,10 +13,13 @@
 //   - dit_attention: one (sequence, query row, head) item per half wave (32 lanes), lane p
 //     owning dims 2p, 2p + 1 (one interleaved-RoPE pair, one cos/sin per position); the
 //     q.k dot is a 5-step butterfly inside the half wave, so a wave runs two items and a
-//     256-thread workgroup eight.  The S <= 8 scores stay in registers;
+//     256-thread workgroup eight.  The S <= 8 scores stay in registers.  The item's
+//     arithmetic (dit_attend.hpp) is shared with the out projection that computes its x
+//     from qkv itself (mt_dit_attention_linear);
 //   - flow_assemble: one thread per output element; an embedder row (latent_dim 16-bit
 //     weights) is read in 16-byte loads;
 //   - flow_euler: one thread per latent dim.
+#include "dit_attend.hpp"
 #include "mt_device.hpp"
 #include "mt_internal.hpp"
 #include "mingtts_hip.h"
@@ -25,21 +28,7 @@ namespace mt {
 
 namespace {
 
-constexpr int DIT_MAXS = 8;
 constexpr int DIT_ITEMS = 8;  // items per 256-thread workgroup
-
-// Sum over the 32 lanes of a half wave (xor distances below 32 stay inside it).
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// x_transformers interleaved rotary pair: (x, y) -> (x c - y s, y c + x s).
-__device__ __forceinline__ float2 rope_pair(float2 v, float angle) {
-    const float c = cosf(angle), s = sinf(angle);
-    return make_float2(v.x * c - v.y * s, v.y * c + v.x * s);
-}
 
 __global__ __launch_bounds__(256) void dit_attention_kernel(const float *qkv, uint32_t ld, uint32_t B, uint32_t S,
                                                             uint32_t H, const float *inv_freq, float *out, uint32_t ldo,
@@ -48,36 +37,12 @@ __global__ __launch_bounds__(256) void dit_attention_kernel(const float *qkv, ui
     const uint32_t p = threadIdx.x & 31;
     if (item >= B * S * H) return;  // a whole half wave leaves together
     const uint32_t h = item % H, i = (item / H) % S, b = item / (H * S);
-    const uint32_t D = H * 64;
-    const float freq = inv_freq[p];
-    const float *rows = qkv + static_cast<size_t>(b) * S * ld + h * 64 + 2 * p;
-    const float2 q = rope_pair(*reinterpret_cast<const float2 *>(rows + static_cast<size_t>(i) * ld),
-                               static_cast<float>(i) * freq);
-    float sc[DIT_MAXS];
-    float mx = -INFINITY;
-#pragma unroll
-    for (uint32_t j = 0; j < DIT_MAXS; j++) {
-        if (j < S) {
-            const float2 k = rope_pair(*reinterpret_cast<const float2 *>(rows + static_cast<size_t>(j) * ld + D),
-                                       static_cast<float>(j) * freq);
-            sc[j] = half_sum(q.x * k.x + q.y * k.y) * scale;
-            mx = fmaxf(mx, sc[j]);
-        }
-    }
-    float sum = 0.0f;
-    float2 acc = make_float2(0.0f, 0.0f);
-#pragma unroll
-    for (uint32_t j = 0; j < DIT_MAXS; j++) {
-        if (j < S) {
-            const float e = expf(sc[j] - mx);
-            const float2 v = *reinterpret_cast<const float2 *>(rows + static_cast<size_t>(j) * ld + 2 * D);
-            sum += e;
-            acc.x = fmaf(e, v.x, acc.x);
-            acc.y = fmaf(e, v.y, acc.y);
-        }
-    }
+    DitItem it;
+    dit_item_load(qkv + static_cast<size_t>(b) * S * ld + h * 64 + 2 * p, ld, H * 64, i, S, it);
+    float c[DIT_MAXS], s[DIT_MAXS];
+    dit_rope_table(inv_freq[p], S, c, s);
     *reinterpret_cast<float2 *>(out + static_cast<size_t>(b * S + i) * ldo + h * 64 + 2 * p) =
-        make_float2(acc.x / sum, acc.y / sum);
+        dit_item_attend(it, i, S, c, s, scale);
 }
 
 // Row r of the flow input (rows 0-2 the conditional batch, 3-5 the unconditional one):

@@ -30,6 +30,7 @@
 // Every summation order is fixed, so results are bit-identical from run to run.
 #include <algorithm>
 
+#include "dit_attend.hpp"
 #include "mt_device.hpp"
 #include "mt_internal.hpp"
 
@@ -90,6 +91,14 @@ struct GmSplit {
     uint32_t *cnt;
 };
 
+// The DiT attention that produces x (mt_dit_attention_linear): x row m = b S + i is query
+// row i of sequence b, attended over qkv (a.x, row stride a.ldx) with H heads of 64.
+struct GmAttn {
+    const float *inv_freq;
+    uint32_t S, H;
+    float scale;
+};
+
 constexpr int SC1 = 16;  // buffer cache policy: device-coherent
 
 // Shape of one instantiation: NG groups of 16 B columns; H2: x staged as hi + lo halves (x
@@ -106,8 +115,10 @@ struct GmShape {
     static_assert(KC % (64 * GM_NW) == 0 && HV * MM * XLD * 2 <= GM_LDS, "x staging (block pairs per wave)");
 };
 
-template <int WT, int XT, bool GATED, bool NORM, int NG>
-__global__ __launch_bounds__(GM_THREADS, 4) void gemv_mfma_kernel(LinearArgs a, GmSplit sp) {
+template <int WT, int XT, bool GATED, bool NORM, int NG, bool ATT = false>
+// (The attention-x variants take 2 waves per SIMD: their prologue needs the registers, and
+// their few workgroups fill one per CU.)
+__global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(LinearArgs a, GmSplit sp, GmAttn att) {
     constexpr bool H2 = XT != WT || NORM;
     typedef GmShape<NG, H2> S;
     constexpr int MM = S::MM, KC = S::KC, XLD = S::XLD, BPW = S::BPW, XCH = S::XCH;
@@ -145,6 +156,33 @@ __global__ __launch_bounds__(GM_THREADS, 4) void gemv_mfma_kernel(LinearArgs a, 
     for (uint32_t kc0 = ks; kc0 < ke; kc0 += KC) {
         const uint32_t kn = min(static_cast<uint32_t>(KC), ke - kc0);
         const uint32_t nkb = (kn + 31) / 32;
+        // Attention x: the chunk spans whole heads, items (row, head) go to the 16 half waves;
+        // the first two items of each half wave are requested before the weights, so the
+        // wait for them does not include the weight stream.
+        DitItem di[2];
+        float freq = 0.0f;
+        const uint32_t hw = tid >> 5, nh = kn / 64, hb = kc0 / 64, items = ATT ? M * nh : 0u;
+        auto item_rows = [&](uint32_t it, uint32_t &m, uint32_t &i) {
+            const uint32_t hh = it % nh;
+            m = it / nh;
+            const uint32_t b = m / att.S;
+            i = m - b * att.S;
+            return static_cast<const float *>(a.x) + static_cast<size_t>(b) * att.S * a.ldx + (hb + hh) * 64 +
+                   2 * (tid & 31);
+        };
+        if constexpr (ATT) {
+            static_assert(XT == DT_F32 && !NORM && !GATED, "attention x is fp32, without a norm or gate");
+            freq = att.inv_freq[tid & 31];
+#pragma unroll
+            for (uint32_t u = 0; u < 2; u++) {
+                const uint32_t it = hw + 16 * u;
+                if (it < items) {
+                    uint32_t m, i;
+                    const float *rows = item_rows(it, m, i);
+                    dit_item_load(rows, a.ldx, att.H * 64, i, att.S, di[u]);
+                }
+            }
+        }
         // This wave's weight tiles of the chunk (requested first): block pairs (2 w, 2 w + 1),
         // (2 w + 16, 2 w + 17), ..., so the two 64-byte halves of each 128-byte weight line
         // come from one wave.
@@ -162,7 +200,30 @@ __global__ __launch_bounds__(GM_THREADS, 4) void gemv_mfma_kernel(LinearArgs a, 
             }
         }
         // Stage x[m][kc0 .. kc0 + kn); the block tail past kn holds zeros.
-        const uint32_t k4 = kn / 4, nch = M * k4;
+        const uint32_t k4 = kn / 4, nch = ATT ? 0u : M * k4;
+        if constexpr (ATT) {
+            // x is the attention output, staged as hi + lo pairs like any fp32 x.
+            float c[DIT_MAXS], s[DIT_MAXS];
+            dit_rope_table(freq, att.S, c, s);
+            auto stage = [&](uint32_t it, const DitItem &d) {
+                uint32_t m, i;
+                item_rows(it, m, i);
+                const float2 o = dit_item_attend(d, i, att.S, c, s, att.scale);
+                const uint32_t hi = pack_pair<WT>(o.x, o.y), lo = pack_pair<WT>(o.x - dec_lo<WT>(hi), o.y - dec_hi<WT>(hi));
+                const uint32_t kk = (it % nh) * 64 + 2 * (tid & 31);
+                *reinterpret_cast<uint32_t *>(xs + m * XLD + kk) = hi;
+                *reinterpret_cast<uint32_t *>(xs + (MM + m) * XLD + kk) = lo;
+            };
+#pragma unroll
+            for (uint32_t u = 0; u < 2; u++)
+                if (hw + 16 * u < items) stage(hw + 16 * u, di[u]);
+            for (uint32_t it = hw + 32; it < items; it += 16) {  // items past the first two, one at a time
+                uint32_t m, i;
+                const float *rows = item_rows(it, m, i);
+                dit_item_load(rows, a.ldx, att.H * 64, i, att.S, di[0]);
+                stage(it, di[0]);
+            }
+        }
 #pragma unroll
         for (int r = 0; r < XCH; r++) {
             const uint32_t e = tid + GM_THREADS * r;
@@ -328,7 +389,7 @@ __global__ __launch_bounds__(GM_THREADS, 4) void gemv_mfma_kernel(LinearArgs a, 
     }
 }
 
-typedef void (*gm_fn)(LinearArgs, GmSplit);
+typedef void (*gm_fn)(LinearArgs, GmSplit, GmAttn);
 
 template <int WT, int XT, int NG>
 gm_fn gm_variant(bool gated, bool norm) {
@@ -366,12 +427,13 @@ int gemv_mfma_columns(uint32_t M, int xt, int wt, bool norm) {
     return cols <= 64 ? static_cast<int>(cols) : 0;
 }
 
-int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
-    const bool gated = (a.flags & F_SILU_GATE) != 0;
-    const bool norm = a.norm != nullptr;
-    const int cols = gemv_mfma_columns(a.M, xt, wt, norm);
-    if (cols == 0) return set_error(MT_ENOTSUP, "gemv_mfma: %u rows exceed the kernel's columns", a.M);
-    GmSplit sp{};
+namespace {
+
+// Tiles, splits and (for S > 1) the stream's split-K workspace.  even: splits start at
+// multiples of 64 k (whole attention heads).
+int gm_splits(const LinearArgs &a, int xt, int wt, bool gated, bool norm, int ng, bool even, hipStream_t stream,
+              GmSplit &sp) {
+    sp = GmSplit{};
     sp.tiles = (a.N + 15) / 16;
     const uint32_t kb = (a.K + 31) / 32;
     // Splits: enough workgroups for 256 CUs when the tiles are few, each split at least 8
@@ -382,8 +444,8 @@ int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
     else if (sp.tiles < 128) s = std::max(1u, std::min((256u + sp.tiles - 1) / sp.tiles, kb / 8));
     s = std::min(s, std::min(kb, 64u));
     sp.kps = (kb + s - 1) / s;
+    if (even) sp.kps += sp.kps & 1u;
     sp.splits = (kb + sp.kps - 1) / sp.kps;  // no empty split
-    const int ng = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
     if (sp.splits > 1) {
         const int mm = 16 * ng / ((xt != wt || norm) ? 2 : 1);
         const int rec = (gated ? 2 : 1) * 16 * mm + mm;
@@ -397,8 +459,45 @@ int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
         sp.part_bytes = static_cast<uint32_t>(pb);
         sp.cnt = cnt;
     }
+    return MT_OK;
+}
+
+template <int WT>
+gm_fn gm_attn(int ng) {
+    return ng == 1 ? gemv_mfma_kernel<WT, DT_F32, false, false, 1, true>
+                   : ng == 2 ? gemv_mfma_kernel<WT, DT_F32, false, false, 2, true>
+                             : gemv_mfma_kernel<WT, DT_F32, false, false, 4, true>;
+}
+
+}  // namespace
+
+int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
+    const bool gated = (a.flags & F_SILU_GATE) != 0;
+    const bool norm = a.norm != nullptr;
+    const int cols = gemv_mfma_columns(a.M, xt, wt, norm);
+    if (cols == 0) return set_error(MT_ENOTSUP, "gemv_mfma: %u rows exceed the kernel's columns", a.M);
+    const int ng = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
+    GmSplit sp;
+    const int rc = gm_splits(a, xt, wt, gated, norm, ng, false, stream, sp);
+    if (rc) return rc;
     gm_fn fn = ng == 1 ? gm_w<1>(wt, xt, gated, norm) : ng == 2 ? gm_w<2>(wt, xt, gated, norm) : gm_w<4>(wt, xt, gated, norm);
-    hipLaunchKernelGGL(fn, dim3(sp.tiles * sp.splits), dim3(GM_THREADS), 0, stream, a, sp);
+    hipLaunchKernelGGL(fn, dim3(sp.tiles * sp.splits), dim3(GM_THREADS), 0, stream, a, sp, GmAttn{});
+    return check_launch("gemv_mfma");
+}
+
+int launch_gemv_mfma_attn(const LinearArgs &a, int wt, const float *inv_freq, uint32_t S, uint32_t H, float scale,
+                          hipStream_t stream) {
+    const int cols = gemv_mfma_columns(a.M, DT_F32, wt, false);
+    if (cols == 0) return set_error(MT_ENOTSUP, "gemv_mfma: %u rows exceed the kernel's columns", a.M);
+    if (a.K != H * 64 || a.norm || (a.flags & F_SILU_GATE) || S == 0 || S > DIT_MAXS || a.M % S)
+        return set_error(MT_EINVAL, "gemv_mfma: attention x needs K = 64 H, M a multiple of S <= %d, no norm or gate",
+                         DIT_MAXS);
+    const int ng = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
+    GmSplit sp;
+    const int rc = gm_splits(a, DT_F32, wt, false, false, ng, true, stream, sp);
+    if (rc) return rc;
+    gm_fn fn = wt == DT_BF16 ? gm_attn<DT_BF16>(ng) : gm_attn<DT_F16>(ng);
+    hipLaunchKernelGGL(fn, dim3(sp.tiles * sp.splits), dim3(GM_THREADS), 0, stream, a, sp, GmAttn{inv_freq, S, H, scale});
     return check_launch("gemv_mfma");
 }
 

@@ -110,6 +110,10 @@ int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int ove
 // norm at most 8 rows) on MFMA, x staged once per workgroup of 16 output features.
 int gemv_mfma_columns(uint32_t M, int xt, int wt, bool norm);
 int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream);
+// The same kernel with x computed in its prologue as the DiT attention of qkv = a.x (row
+// stride a.ldx): mt_dit_attention_linear.
+int launch_gemv_mfma_attn(const LinearArgs &a, int wt, const float *inv_freq, uint32_t S, uint32_t H, float scale,
+                          hipStream_t stream);
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int splitk_override);
 
 // Compute units of the current device (cached per device), or <= 0 when it cannot be queried.

@@ -30,7 +30,8 @@ EXPORTS = (
     "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
-    "mt_attention", "mt_attention_decode", "mt_dit_attention", "mt_flow_assemble", "mt_flow_euler",
+    "mt_attention", "mt_attention_decode", "mt_dit_attention", "mt_dit_attention_linear", "mt_flow_assemble",
+    "mt_flow_euler",
     "mt_upsample4", "mt_istft_frames", "mt_istft_emit", "mt_st_open", "mt_st_close", "mt_st_count", "mt_st_name", "mt_st_find", "mt_arena_create", "mt_arena_tensor",
     "mt_arena_padded", "mt_arena_bytes", "mt_arena_upload", "mt_arena_audit", "mt_arena_destroy",
     "mt_last_error", "mt_version",
@@ -134,6 +135,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_attention_decode.restype = i32
     L.mt_dit_attention.argtypes = [vp, u32, u32, u32, u32, vp, vp, u32, f32, vp]
     L.mt_dit_attention.restype = i32
+    L.mt_dit_attention_linear.argtypes = [vp, u32, u32, u32, vp, f32, vp, i32, vp, vp, GemvParams, vp]
+    L.mt_dit_attention_linear.restype = i32
     L.mt_flow_assemble.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, vp, u32, u32, u32, vp]
     L.mt_flow_assemble.restype = i32
     L.mt_flow_euler.argtypes = [vp, vp, u32, u32, u32, vp, u32, f32, f32, vp]
@@ -340,6 +343,16 @@ def dit_attention(qkv, B, S, H, inv_freq, out, ld=None, ldo=None, scale=0.125, s
     of S rows (Kernels.swift:208-220)."""
     check(load().mt_dit_attention(_ptr(qkv), qkv.stride(0) if ld is None else ld, B, S, H, _ptr(inv_freq), _ptr(out),
                                   out.stride(0) if ldo is None else ldo, scale, _stream(stream)))
+
+
+def dit_attention_linear(qkv, B, S, H, inv_freq, w, y, flags=0, bias=None, scale=0.125, ldq=None, ldy=None,
+                         stream=None) -> None:
+    """Encoder.ditAttention then Encoder.linear of its output (DiT.swift:44-45) in one launch:
+    y[:B S] (op)= dit_attention(qkv) @ w.T with the epilogue in ``flags``; w: [N, 64 H]."""
+    N, K = w.shape
+    p = GemvParams(B * S, N, K, qkv.stride(0) if ldq is None else ldq, y.stride(0) if ldy is None else ldy, flags, 0.0)
+    check(load().mt_dit_attention_linear(_ptr(qkv), B, S, H, _ptr(inv_freq), scale, _ptr(w), dtype_code(w), _ptr(bias),
+                                         _ptr(y), p, _stream(stream)))
 
 
 def flow_assemble(y, history, cemb, cond_bias, temb, x_w, x_b, x, ldx=None, stream=None) -> None:

@@ -166,6 +166,26 @@ def test_rope_and_attention_reject_bad_arguments():
     assert L.mt_attention(A, 1152, 0, 14, 2, 0, 0, A, A, mt.F32, 512, A, 896, 0.125, None) == mt.OK  # empty
 
 
+def test_dit_attention_linear_rejects_bad_arguments():
+    """mt_dit_attention_linear checks its attention shape on top of mt_linear's checks."""
+    L = mt.load()
+    A = ALIGNED
+
+    def call(B=2, S=3, H=16, M=6, N=1024, K=1024, ldq=3072, flags=0, inv=A, y=Y_ADDR):
+        p = mt.GemvParams(M, N, K, ldq, N, flags, 0.0)
+        return L.mt_dit_attention_linear(A, B, S, H, inv, 0.125, W_ADDR, mt.BF16, None, y, p, None)
+
+    assert call(S=9, M=18) == mt.EINVAL and "at most 8 rows" in mt.last_error()
+    assert call(M=5) == mt.EINVAL and "is not B" in mt.last_error()
+    assert call(K=960) == mt.EINVAL and "64 H" in mt.last_error()
+    assert call(flags=mt.GemvFlags.siluGate) == mt.EINVAL and "gate partner" in mt.last_error()
+    assert call(ldq=2048) == mt.EINVAL and "< 3 K" in mt.last_error()
+    assert call(inv=None) == mt.EINVAL and "inv_freq" in mt.last_error()
+    assert call(y=A + 4096) == mt.EINVAL and "overlaps y" in mt.last_error()   # y inside qkv's k span
+    assert call(B=6, S=8, M=48) == mt.ENOTSUP and "at most 32 rows" in mt.last_error()
+    assert call(B=0, M=0) == mt.OK   # empty
+
+
 def test_seq_item_layout_matches_the_header(tmp_path):
     """The ctypes mirrors of mt_attn_op and mt_seq_item have the C compiler's sizes and
     offsets."""

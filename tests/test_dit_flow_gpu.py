@@ -9,7 +9,7 @@ import torch
 
 import mingtts as mt
 import oracle as O
-from _gpu_util import dev16, say
+from _gpu_util import assert_linear_parity, dev16, say
 
 pytestmark = pytest.mark.gpu
 
@@ -55,6 +55,49 @@ def test_dit_attention_shapes(gpu, B, S, H, pad):
 def test_dit_attention_rejects_long_sequences():
     assert mt.load().mt_dit_attention(1 << 20, 3072, 1, 9, 16, 1 << 20, 2 << 20, 1024, 0.125, None) == mt.EINVAL
     assert "at most 8 rows" in mt.last_error()
+
+
+@pytest.mark.parametrize("B,S,H,N,wt,flags,bias,pad", [
+    (2, 3, 16, 1024, O.BF16, O.ACCUM, True, 0),    # the flow head's out projection (split K)
+    (2, 3, 16, 4096, O.F16, 0, False, 64),         # 256 tiles, no split; padded qkv rows
+    (1, 1, 1, 64, O.F16, 0, True, 0),              # one row
+    (4, 2, 3, 300, O.BF16, O.GELU, True, 8),       # ragged N, K = 192
+    (2, 8, 2, 200, O.F16, O.ACCUM, False, 0),      # 16 rows: two column groups
+    (4, 8, 1, 96, O.BF16, 0, True, 4),             # 32 rows: four column groups
+])
+def test_dit_attention_linear(gpu, B, S, H, N, wt, flags, bias, pad):
+    """mt_dit_attention_linear against the fp64 chain (dit attention, then the linear) to the
+    linear precision gate, and against mt_dit_attention into a buffer followed by mt_linear:
+    the same bits wherever that linear runs the same small-row MFMA kernel and split (3..16
+    rows), else within 1e-5."""
+    M, K = B * S, 64 * H
+    ldq = 3 * K + pad
+    rng = np.random.default_rng(M * 1000 + N + H)
+    qkv = rng.standard_normal((M, ldq)).astype(np.float32)
+    w, _ = O.round16(rng.standard_normal((N, K)).astype(np.float32) * np.float32(0.02), wt)
+    b16 = O.round16(rng.standard_normal(N).astype(np.float32) * np.float32(0.02), wt)[0] if bias else None
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    invf = invf_1e4()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    qkv_d, invf_d, w_d = t(qkv), t(invf), dev16(w, wt, gpu)
+    b_d = dev16(b16, wt, gpu) if bias else None
+    y = t(y0)
+    say(f"dit_attention_linear B={B} S={S} H={H} N={N} wt={wt} flags={flags} bias={bias} pad={pad}")
+    mt.dit_attention_linear(qkv_d, B, S, H, invf_d, w_d, y, flags=flags, bias=b_d)
+    att = torch.zeros(M, K, device=gpu)
+    mt.dit_attention(qkv_d, B, S, H, invf_d, att)
+    y2 = t(y0)
+    mt.linear(att, w_d, y2, M, flags=flags, bias=b_d)
+    torch.cuda.synchronize()
+    got, sep = y.cpu().numpy(), y2.cpu().numpy()
+    x_used = O.dit_attention_f64(qkv, B, S, H, invf).astype(np.float32)
+    want32 = O.linear_f32(x_used, w, None, wt, b16, y0, M, N, K, flags)
+    want64 = O.linear_f64(x_used, w, None, wt, b16, y0, M, N, K, flags)
+    assert_linear_parity(got, want32, want64, K, "fused")
+    if 3 <= M <= 16:
+        np.testing.assert_array_equal(got, sep)
+    else:
+        np.testing.assert_allclose(got, sep, rtol=1e-5, atol=1e-5)
 
 
 @pytest.mark.parametrize("wt,hidden,ldx", [(O.BF16, 1024, 1024), (O.F16, 96, 100), (O.BF16, 300, 304)])
@@ -131,8 +174,10 @@ def oracle_flow_step(blocks, final, x0, invf, y0, cfg, dt):
     return x, pred, y1
 
 
-def test_flow_step_matches_fp64_chain(gpu):
-    """One ODE step of the flow head: assemble, 2 DiT blocks, final norm + linear, Euler."""
+@pytest.mark.parametrize("fused", [False, True])
+def test_flow_step_matches_fp64_chain(gpu, fused):
+    """One ODE step of the flow head: assemble, 2 DiT blocks, final norm + linear, Euler;
+    with ``fused`` the attention runs inside the out projection (mt_dit_attention_linear)."""
     rng = np.random.default_rng(21)
     blocks = dit_weights(2, 21)
     final = dict(norm=O.round16((1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32), O.BF16)[0],
@@ -157,13 +202,17 @@ def test_flow_step_matches_fp64_chain(gpu):
     pred = torch.zeros(6, LAT, device=gpu)
     y = t(y0.copy())
     invf_d = t(invf)
-    say("flow step: assemble, 2 DiT blocks, final, euler")
+    say(f"flow step: assemble, 2 DiT blocks, final, euler (fused attention: {fused})")
     mt.flow_assemble(y, t(hist), t(cemb), b16(cb), t(temb), b16(xw), b16(xb), x)
     lin = lambda xx, w, out, flags=0, bias=None, norm=None: mt.linear(xx, w, out, 6, flags=flags, bias=bias, norm=norm)
     for d in dw:
         lin(x, d["qkv"], qkv, bias=d["qkv_b"], norm=d["norm1"])
-        mt.dit_attention(qkv, 2, 3, HEADS, invf_d, att)
-        lin(att, d["out"], x, flags=mt.GemvFlags.accumulate, bias=d["out_b"])
+        if fused:
+            mt.dit_attention_linear(qkv, 2, 3, HEADS, invf_d, d["out"], x, flags=mt.GemvFlags.accumulate,
+                                    bias=d["out_b"])
+        else:
+            mt.dit_attention(qkv, 2, 3, HEADS, invf_d, att)
+            lin(att, d["out"], x, flags=mt.GemvFlags.accumulate, bias=d["out_b"])
         lin(x, d["ff1"], ff, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"])
         lin(ff, d["ff2"], x, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])
     lin(x, b16(final["w"]), pred, bias=b16(final["b"]), norm=b16(final["norm"]))
