@@ -78,9 +78,19 @@ __device__ __forceinline__ float pair_sum(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
 }
 
+// Sum over the 64 lanes, the same bits in every lane: quad swaps, half-row and row mirrors
+// on DPP (rows of 16), then two exchanges between rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum64(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
 }
 
 // Split-K arguments: S workgroups per tile (tile = block % tiles, split = block / tiles), kps
@@ -153,6 +163,25 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
 #pragma unroll
     for (int m = 0; m < MM; m++) ss[m] = 0.0f;
 
+    // The epilogue's bias and old y of output lane o = tid + GM_THREADS j (feature o / M, row
+    // o % M), requested now so the epilogue does not wait for them (lanes past the outputs
+    // read element 0).  Only this tile's final writer stores y, so the old value is the one
+    // from before the launch.  PRE: the early requests here and of x below; the gated
+    // multi-group variants have no registers to spare for them and request at the point of use.
+    constexpr bool PRE = !(GATED && NG > 1);
+    constexpr int OPT = (16 * MM + GM_THREADS - 1) / GM_THREADS;
+    uint32_t pbias[OPT];
+    float pyold[OPT];
+#pragma unroll
+    for (int j = 0; j < OPT; j++) {
+        const uint32_t o = tid + GM_THREADS * j, f = o / M, m = o - f * M, n = r0 + f;
+        const bool ok = o < 16 * M && n < a.N;
+        pbias[j] = 0;
+        pyold[j] = 0.0f;
+        if (PRE && (a.flags & F_BIAS)) pbias[j] = a.bias[ok ? n : 0u];
+        if (PRE && (a.flags & F_ACCUM)) pyold[j] = a.y[ok ? static_cast<size_t>(m) * a.ldy + n : 0u];
+    }
+
     for (uint32_t kc0 = ks; kc0 < ke; kc0 += KC) {
         const uint32_t kn = min(static_cast<uint32_t>(KC), ke - kc0);
         const uint32_t nkb = (kn + 31) / 32;
@@ -183,7 +212,29 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
                 }
             }
         }
-        // This wave's weight tiles of the chunk (requested first): block pairs (2 w, 2 w + 1),
+        // The chunk's x (and norm gain) of the first XPF staging rounds (PRE), requested
+        // before the weights so that the conversion waits for x alone; lanes past the chunk
+        // read element 0.  Later rounds load at the point of use.
+        const uint32_t k4 = kn / 4, nch = ATT ? 0u : M * k4;
+        const uint32_t rounds = (nch + GM_THREADS - 1) / GM_THREADS;  // uniform
+        constexpr int XPF = PRE ? (XCH < 8 ? XCH : 8) : 0;
+        u32x4g xf[XT == DT_F32 ? XCH : 1];
+        u32x2g xh[XT == DT_F32 ? 1 : XCH];
+        u32x2g gn[NORM ? XCH : 1];
+        auto fetch = [&](int r) {
+            const uint32_t e = tid + GM_THREADS * r, ec = e < nch ? e : 0u;
+            const uint32_t m = ec / k4, kk = (ec - m * k4) * 4;
+            const size_t xo = static_cast<size_t>(m) * a.ldx + kc0 + kk;
+            if constexpr (XT == DT_F32)
+                xf[r] = *reinterpret_cast<const u32x4g *>(static_cast<const float *>(a.x) + xo);
+            else
+                xh[r] = *reinterpret_cast<const u32x2g *>(static_cast<const uint16_t *>(a.x) + xo);
+            if constexpr (NORM) gn[r] = *reinterpret_cast<const u32x2g *>(a.norm + kc0 + kk);
+        };
+#pragma unroll
+        for (int r = 0; r < XPF; r++)
+            if (static_cast<uint32_t>(r) < rounds) fetch(r);
+        // This wave's weight tiles of the chunk: block pairs (2 w, 2 w + 1),
         // (2 w + 16, 2 w + 17), ..., so the two 64-byte halves of each 128-byte weight line
         // come from one wave.
         u32x4g at[BPW], at2[BPW];
@@ -200,7 +251,6 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
             }
         }
         // Stage x[m][kc0 .. kc0 + kn); the block tail past kn holds zeros.
-        const uint32_t k4 = kn / 4, nch = ATT ? 0u : M * k4;
         if constexpr (ATT) {
             // x is the attention output, staged as hi + lo pairs like any fp32 x.
             float c[DIT_MAXS], s[DIT_MAXS];
@@ -228,20 +278,17 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
         for (int r = 0; r < XCH; r++) {
             const uint32_t e = tid + GM_THREADS * r;
             if (e < nch) {
+                if (r >= XPF) fetch(r);
                 const uint32_t m = e / k4, kk = (e - m * k4) * 4;
                 if constexpr (!H2) {  // x of the weights' type: staged as it is
-                    *reinterpret_cast<uint2 *>(xs + m * XLD + kk) =
-                        *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(a.x) + static_cast<size_t>(m) * a.ldx +
-                                                         kc0 + kk);
+                    *reinterpret_cast<u32x2g *>(xs + m * XLD + kk) = xh[r];
                 } else {
                     float x[4];
                     if constexpr (XT == DT_F32) {
-                        const float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) +
-                                                                           static_cast<size_t>(m) * a.ldx + kc0 + kk);
-                        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+                        x[0] = __uint_as_float(xf[r].x); x[1] = __uint_as_float(xf[r].y);
+                        x[2] = __uint_as_float(xf[r].z); x[3] = __uint_as_float(xf[r].w);
                     } else {
-                        const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(a.x) +
-                                                                         static_cast<size_t>(m) * a.ldx + kc0 + kk);
+                        const u32x2g v = xh[r];
                         x[0] = dec_lo<XT>(v.x); x[1] = dec_hi<XT>(v.x); x[2] = dec_lo<XT>(v.y); x[3] = dec_hi<XT>(v.y);
                     }
                     if constexpr (NORM) {
@@ -251,7 +298,7 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
                         t = fmaf(x[3], x[3], t);
 #pragma unroll
                         for (int mm = 0; mm < MM; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
-                        const uint2 g = *reinterpret_cast<const uint2 *>(a.norm + kc0 + kk);
+                        const u32x2g g = gn[r];
                         x[0] *= dec_lo<WT>(g.x);
                         x[1] *= dec_hi<WT>(g.x);
                         x[2] *= dec_lo<WT>(g.y);
@@ -352,12 +399,24 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
         __syncthreads();
         if (!last_flag) return;
         if (tid == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // The splits' records, added in split order: the first SR requested together, the
+        // rest one by one.
+        constexpr uint32_t SR = 8;
 #pragma unroll
         for (int r = 0; r < RPT; r++) {
             const uint32_t e = tid + GM_THREADS * r;
             if (e < static_cast<uint32_t>(REC)) {
+                float v[SR];
+#pragma unroll
+                for (uint32_t s = 0; s < SR; s++)
+                    v[s] = s < sp.splits && s != split
+                               ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, base + (s * REC + e) * 4u, 0, SC1))
+                               : mine[r];
                 float t = 0.0f;
-                for (uint32_t s = 0; s < sp.splits; s++)
+#pragma unroll
+                for (uint32_t s = 0; s < SR; s++)
+                    if (s < sp.splits) t += v[s];
+                for (uint32_t s = SR; s < sp.splits; s++)
                     t += s == split ? mine[r]
                                     : __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, base + (s * REC + e) * 4u,
                                                                                            0, SC1));
@@ -371,19 +430,20 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
         if (e < static_cast<uint32_t>(REC)) tot[e] = mine[r];
     }
     __syncthreads();
-    for (uint32_t o = tid; o < 16 * M; o += GM_THREADS) {
-        const uint32_t f = o / M, m = o - f * M, n = r0 + f;
-        if (n < a.N) {
+#pragma unroll
+    for (int j = 0; j < OPT; j++) {
+        const uint32_t o = tid + GM_THREADS * j, f = o / M, m = o - f * M, n = r0 + f;
+        if (o < 16 * M && n < a.N) {
             float s1 = tot[f * MM + m], s2 = GATED ? tot[16 * MM + f * MM + m] : 0.0f;
             if constexpr (NORM) {
                 const float scale = 1.0f / sqrtf(tot[NCT * 16 * MM + m] / static_cast<float>(K) + a.eps);
                 s1 *= scale;
                 s2 *= scale;
             }
-            const float b = (a.flags & F_BIAS) ? dec1<WT>(a.bias[n]) : 0.0f;
-            float v = epilogue(s1, s2, b, a.flags);
             float *yp = a.y + static_cast<size_t>(m) * a.ldy + n;
-            if (a.flags & F_ACCUM) v += *yp;
+            const float b = (a.flags & F_BIAS) ? dec1<WT>(PRE ? static_cast<uint16_t>(pbias[j]) : a.bias[n]) : 0.0f;
+            float v = epilogue(s1, s2, b, a.flags);
+            if (a.flags & F_ACCUM) v += PRE ? pyold[j] : *yp;
             *yp = v;
         }
     }
