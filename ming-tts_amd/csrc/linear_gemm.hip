@@ -82,6 +82,10 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // The epilogue's bias of the lane's feature, requested now so the epilogue does not wait
+    // for it (lanes past N read element 0).
+    const uint32_t bn = n0 + 32 * wn + (lane & 31);
+    const float bv = (a.flags & F_BIAS) ? dec1<WT>(a.bias[bn < a.N ? bn : 0u]) : 0.0f;
     const uint32_t M = a.M, N = a.N, K = a.K;
 
     f32x16 acc, acc2;
@@ -231,7 +235,16 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
 
     const uint32_t n = n0 + 32 * wn + (lane & 31);
     if (n >= N) return;
-    const float bv = (a.flags & F_BIAS) ? dec1<WT>(a.bias[n]) : 0.0f;
+    // The old y of the lane's 16 rows, requested before the first is used (rows past M
+    // read y[0]).
+    float yo[16];
+    if (a.flags & F_ACCUM) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t m = m0 + 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            yo[r] = a.y[m < M ? static_cast<size_t>(m) * a.ldy + n : 0u];
+        }
+    }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int ml = 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -243,9 +256,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
                 c2 *= row_scale[ml];
             }
             float v = epilogue(c, c2, bv, a.flags);
-            float *yp = a.y + static_cast<size_t>(m) * a.ldy + n;
-            if (a.flags & F_ACCUM) v += *yp;
-            *yp = v;
+            if (a.flags & F_ACCUM) v += yo[r];
+            a.y[static_cast<size_t>(m) * a.ldy + n] = v;
         }
     }
 }

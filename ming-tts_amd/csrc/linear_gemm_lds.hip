@@ -134,6 +134,13 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     const uint32_t m0 = tm * BM;
     const uint32_t n0 = tn * FN;  // first output feature
     const uint32_t M = a.M, N = a.N, K = a.K;
+    // The epilogue's feature (a thread keeps one, see below) and its bias, requested now so
+    // the epilogue does not wait for it.
+    static_assert(NT % FN == 0, "a thread keeps one feature");
+    const int en = tid % FN;
+    const uint32_t egn = n0 + en;
+    const bool enok = egn < N;
+    const float bv = (a.flags & F_BIAS) ? dec1<WT>(a.bias[enok ? egn : 0u]) : 0.0f;
     const uint32_t KT = (K + TBK - 1) / TBK;
     const uint32_t ks0 = split * a.kps;
     const uint32_t nsteps = min(ks0 + a.kps, KT) - ks0;
@@ -408,18 +415,32 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
         __syncthreads();
     }
 
-    // Epilogue from the fp32 tile: consecutive threads take consecutive features of a row.
+    // Epilogue from the fp32 tile: consecutive threads take consecutive features of a row, so
+    // a thread keeps one feature (its bias requested at entry) over rows tid / FN + (NT / FN) i.
+    // The old y of all its rows is requested before the first is used (lanes past M or N
+    // read y[0]).
+    constexpr int EPT = BM * FN / NT, MSTEP = NT / FN;
     const uint32_t flags = a.flags;
-    for (int e = tid; e < BM * FN; e += NT) {
-        const int m = e / FN, n = e % FN;
-        const uint32_t gm = m0 + m, gn = n0 + n;
-        if (gm < M && gn < N) {
-            const float bv = (flags & F_BIAS) ? dec1<WT>(a.bias[gn]) : 0.0f;
+    const int n = en, mr = tid / FN;
+    const uint32_t gn = egn;
+    const bool nok = enok;
+    float yo[EPT];
+    if (flags & F_ACCUM) {
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            const uint32_t gm = m0 + mr + MSTEP * i;
+            yo[i] = a.y[gm < M && nok ? static_cast<size_t>(gm) * a.ldy + gn : 0u];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int m = mr + MSTEP * i;
+        const uint32_t gm = m0 + m;
+        if (gm < M && nok) {
             const float c2 = GATED ? ctile[(BM + m) * CLD + n] : 0.0f;
             float v = epilogue(ctile[m * CLD + n], c2, bv, flags);
-            float *yp = a.y + static_cast<size_t>(gm) * a.ldy + gn;
-            if (flags & F_ACCUM) v += *yp;
-            *yp = v;
+            if (flags & F_ACCUM) v += yo[i];
+            a.y[static_cast<size_t>(gm) * a.ldy + gn] = v;
         }
     }
 }
