@@ -54,15 +54,41 @@ __device__ __forceinline__ void gemv_feature(const LinearArgs &a, uint32_t n, ui
     float acc[MR], acc2[MR], ss[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) { acc[m] = 0.0f; acc2[m] = 0.0f; ss[m] = 0.0f; }
+    // The epilogue's bias and old y (lane 0 of the group uses them), requested now so the
+    // epilogue does not wait for them; rows past `rows` read row row0.
+    const float bias = (a.flags & F_BIAS) ? dec1<WT>(a.bias[n]) : 0.0f;
+    float yold[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) yold[m] = 0.0f;
+    if (a.flags & F_ACCUM) {
+#pragma unroll
+        for (int m = 0; m < MR; m++) yold[m] = a.y[static_cast<size_t>(row0 + (m < rows ? m : 0)) * a.ldy + n];
+    }
+    // With at most two rows, a lane's x chunks (and gain chunks) of an iteration are requested
+    // with its weights, before any is used; more rows load them at the point of use.
+    constexpr bool XPRE = MR <= 2;
+    constexpr int XW = XT == DT_F32 ? 2 : 1;  // 16-byte loads per 8 activations
+    typedef __attribute__((address_space(1))) const u32x4 *gx_cp;
 
     for (int c0 = j; c0 < KC; c0 += U * L) {
-        u32x4 wv[U], gv[U];
+        u32x4 wv[U], gv[U], xr[XPRE ? U : 1][MR][XW], nv[XPRE && NORM ? U : 1];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             // Chunks past the row end load the row's last chunk (in bounds) and are skipped.
             const int c = min(c0 + u * L, KC - 1);
             wv[u] = __builtin_nontemporal_load(wr + c);
             if constexpr (GATED) gv[u] = __builtin_nontemporal_load(gr + c);
+            if constexpr (XPRE) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const size_t off = (static_cast<size_t>(row0 + (m < rows ? m : 0)) * a.ldx + static_cast<size_t>(c) * 8) *
+                                       (XT == DT_F32 ? 4 : 2);
+                    const gx_cp p = reinterpret_cast<gx_cp>(reinterpret_cast<uintptr_t>(static_cast<const char *>(a.x) + off));
+#pragma unroll
+                    for (int h = 0; h < XW; h++) xr[u][m][h] = p[h];
+                }
+                if constexpr (NORM) nv[u] = *reinterpret_cast<gx_cp>(reinterpret_cast<uintptr_t>(nr + c));
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -71,12 +97,27 @@ __device__ __forceinline__ void gemv_feature(const LinearArgs &a, uint32_t n, ui
                 float wf[8], gf[8], nf[8];
                 unpack8<WT>(as_uint4(wv[u]), wf);
                 if constexpr (GATED) unpack8<WT>(as_uint4(gv[u]), gf);
-                if constexpr (NORM) unpack8<WT>(as_uint4(nr[c]), nf);
+                if constexpr (NORM) unpack8<WT>(as_uint4(XPRE ? nv[XPRE ? u : 0] : nr[c]), nf);
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
                     if (m < rows) {
                         float xf[8];
-                        load_x8<XT>(a.x, static_cast<size_t>(row0 + m) * a.ldx + static_cast<size_t>(c) * 8, xf);
+                        if constexpr (XPRE) {
+                            if constexpr (XT == DT_F32) {
+#pragma unroll
+                                for (int h = 0; h < 2; h++) {
+                                    const u32x4 v = xr[XPRE ? u : 0][m][h];
+                                    xf[4 * h] = __uint_as_float(v.x);
+                                    xf[4 * h + 1] = __uint_as_float(v.y);
+                                    xf[4 * h + 2] = __uint_as_float(v.z);
+                                    xf[4 * h + 3] = __uint_as_float(v.w);
+                                }
+                            } else {
+                                unpack8<XT>(as_uint4(xr[XPRE ? u : 0][m][0]), xf);
+                            }
+                        } else {
+                            load_x8<XT>(a.x, static_cast<size_t>(row0 + m) * a.ldx + static_cast<size_t>(c) * 8, xf);
+                        }
                         if constexpr (NORM) {
                             float q = ss[m];
 #pragma unroll
@@ -111,14 +152,12 @@ __device__ __forceinline__ void gemv_feature(const LinearArgs &a, uint32_t n, ui
         }
     }
     if (j == 0) {
-        const float b = (a.flags & F_BIAS) ? dec1<WT>(a.bias[n]) : 0.0f;
 #pragma unroll
         for (int m = 0; m < MR; m++) {
             if (m < rows) {
-                float v = epilogue(acc[m], acc2[m], b, a.flags);
-                float *yp = a.y + static_cast<size_t>(row0 + m) * a.ldy + n;
-                if (a.flags & F_ACCUM) v += *yp;
-                *yp = v;
+                float v = epilogue(acc[m], acc2[m], bias, a.flags);
+                if (a.flags & F_ACCUM) v += yold[m];
+                a.y[static_cast<size_t>(row0 + m) * a.ldy + n] = v;
             }
         }
     }

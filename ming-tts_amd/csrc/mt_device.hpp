@@ -77,8 +77,21 @@ __device__ __forceinline__ float epilogue(float acc, float acc2, float b, uint32
 
 // Sum over aligned groups of `width` lanes (a power of two <= 64) of a wave64; every
 // lane of a group ends with the group sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of `width` lanes (8, 16, 32 or 64), the same bits in every lane of
+// a group: quad swaps and the half-row mirror on DPP (8), the row mirror (16), then
+// exchanges between rows.
 __device__ __forceinline__ float group_sum(float v, int width) {
-    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    if (width >= 16) v += dpp_mov<0x140>(v);  // row_mirror
+    if (width >= 32) v += __shfl_xor(v, 16, 64);
+    if (width >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
 
