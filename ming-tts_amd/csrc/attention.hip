@@ -6,11 +6,13 @@
 //
 // Attention layout on gfx950: one 256-thread workgroup per (query row, head) item.
 //   - scores: groups of 8 lanes own one key (lane r of a group reads dims 8r..8r+7, so a
-//     wave reads 8 whole key rows per load instruction), 32 keys per pass, the 8 partial
-//     dots meet by shuffles; scores land in LDS (at most 4096 keys);
+//     wave reads 8 whole key rows per load instruction), 32 keys per pass, eight passes'
+//     keys requested before any is used, the 8 partial dots meet by shuffles; scores land
+//     in LDS (at most 4096 keys);
 //   - softmax: block max and block sum through LDS;
 //   - p.v: 16 lanes cover the 64 dims of one V row (4 dims each, one coalesced row per
-//     16 lanes), 16 key phases per workgroup, partial sums meet in LDS in a fixed order.
+//     16 lanes), 16 key phases per workgroup, eight rows per lane requested at a time,
+//     partial sums meet in LDS in a fixed order.
 // Batched decode (mt_attention_decode) is the same kernel with a per-row cache base and
 // the row's query position read from a device array.
 #include "mt_device.hpp"
@@ -23,19 +25,6 @@ namespace {
 
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_MAXKEYS = 4096;
-
-template <int CT>
-__device__ __forceinline__ void load8(const void *base, size_t off, float *o) {
-    if constexpr (CT == DT_F32) {
-        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + off);
-        const float4 a = p[0], b = p[1];
-        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-        o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-    } else {
-        const uint4 v = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + off);
-        unpack8<CT>(v, o);
-    }
-}
 
 template <int CT>
 __device__ __forceinline__ float4 load4(const void *base, size_t off) {
@@ -91,13 +80,44 @@ __global__ __launch_bounds__(64) void rope_cache_kernel(float *qkv, uint32_t ldq
     }
 }
 
+// Max / sum over the 64 lanes, the same bits in every lane: quad swaps and the half-row and
+// row mirrors on DPP (rows of 16), then two exchanges between rows.
 __device__ __forceinline__ float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+__device__ __forceinline__ float wave_sum(float v) { return group_sum(v, 64); }
+
+// The 16-byte raw loads of eight cached values (one of fp16, two of fp32) and their decode.
+template <int CT>
+struct Raw8 {
+    uint4 a, b;
+};
+template <int CT>
+__device__ __forceinline__ Raw8<CT> load8_raw(const void *base, size_t off) {
+    Raw8<CT> r;
+    if constexpr (CT == DT_F32) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const float *>(base) + off);
+        r.a = p[0];
+        r.b = p[1];
+    } else {
+        r.a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + off);
+        r.b = make_uint4(0u, 0u, 0u, 0u);
+    }
+    return r;
+}
+template <int CT>
+__device__ __forceinline__ void decode8(const Raw8<CT> &r, float *o) {
+    if constexpr (CT == DT_F32) {
+        o[0] = __uint_as_float(r.a.x); o[1] = __uint_as_float(r.a.y); o[2] = __uint_as_float(r.a.z); o[3] = __uint_as_float(r.a.w);
+        o[4] = __uint_as_float(r.b.x); o[5] = __uint_as_float(r.b.y); o[6] = __uint_as_float(r.b.z); o[7] = __uint_as_float(r.b.w);
+    } else {
+        unpack8<CT>(r.a, o);
+    }
 }
 
 template <int CT>
@@ -130,19 +150,34 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
         qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
         qf[4] = b.x; qf[5] = b.y; qf[6] = b.z; qf[7] = b.w;
     }
+    // Eight passes of 32 keys per round, all requested before any is used (keys past the
+    // end re-read the last key and are skipped).
     float mx = -INFINITY;
-    for (int t = tid >> 3; t < nk; t += ATT_THREADS / 8) {
-        float kf[8];
-        load8<CT>(kc, kvbase + static_cast<size_t>(t) * 64 + 8 * r, kf);
-        float s = 0.0f;
+    constexpr int KP = ATT_THREADS / 8, KU = 8;
+    for (int t0 = tid >> 3; t0 < nk; t0 += KU * KP) {
+        Raw8<CT> kr[KU];
 #pragma unroll
-        for (int e = 0; e < 8; e++) s = fmaf(qf[e], kf[e], s);
-        s += __shfl_xor(s, 4, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 1, 64);
-        s *= scale;
-        if (r == 0) sc[t] = s;
-        mx = fmaxf(mx, s);
+        for (int u = 0; u < KU; u++) {
+            const int t = min(t0 + u * KP, nk - 1);
+            kr[u] = load8_raw<CT>(kc, kvbase + static_cast<size_t>(t) * 64 + 8 * r);
+        }
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int t = t0 + u * KP;
+            if (t < nk) {  // the 8 lanes of a key agree
+                float kf[8];
+                decode8<CT>(kr[u], kf);
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) s = fmaf(qf[e], kf[e], s);
+                s += __shfl_xor(s, 4, 64);
+                s += __shfl_xor(s, 2, 64);
+                s += __shfl_xor(s, 1, 64);
+                s *= scale;
+                if (r == 0) sc[t] = s;
+                mx = fmaxf(mx, s);
+            }
+        }
     }
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
@@ -162,30 +197,28 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
     __syncthreads();
     sum = (red[0] + red[1]) + (red[2] + red[3]);
 
-    // p . v: 16 lanes per V row (4 dims each), 16 key phases.
+    // p . v: 16 lanes per V row (4 dims each), 16 key phases, keys t = ks, ks + 16, ... in
+    // order; eight rows per round requested before any is used (rows past the end re-read
+    // the last row and are skipped).
     const int d4 = tid & 15, ks = tid >> 4;
+    constexpr int VU = 8;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    int t = ks;
-    for (; t + 48 < nk; t += 64) {
-        float4 v[4];
+    for (int t0 = ks; t0 < nk; t0 += 16 * VU) {
+        float4 v[VU];
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = load4<CT>(vc, kvbase + static_cast<size_t>(t + 16 * u) * 64 + 4 * d4);
+        for (int u = 0; u < VU; u++)
+            v[u] = load4<CT>(vc, kvbase + static_cast<size_t>(min(t0 + 16 * u, nk - 1)) * 64 + 4 * d4);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float p = sc[t + 16 * u];
-            acc.x = fmaf(p, v[u].x, acc.x);
-            acc.y = fmaf(p, v[u].y, acc.y);
-            acc.z = fmaf(p, v[u].z, acc.z);
-            acc.w = fmaf(p, v[u].w, acc.w);
+        for (int u = 0; u < VU; u++) {
+            const int t = t0 + 16 * u;
+            if (t < nk) {
+                const float p = sc[t];
+                acc.x = fmaf(p, v[u].x, acc.x);
+                acc.y = fmaf(p, v[u].y, acc.y);
+                acc.z = fmaf(p, v[u].z, acc.z);
+                acc.w = fmaf(p, v[u].w, acc.w);
+            }
         }
-    }
-    for (; t < nk; t += 16) {
-        const float4 v = load4<CT>(vc, kvbase + static_cast<size_t>(t) * 64 + 4 * d4);
-        const float p = sc[t];
-        acc.x = fmaf(p, v.x, acc.x);
-        acc.y = fmaf(p, v.y, acc.y);
-        acc.z = fmaf(p, v.z, acc.z);
-        acc.w = fmaf(p, v.w, acc.w);
     }
     part[ks][d4] = acc;
     __syncthreads();
