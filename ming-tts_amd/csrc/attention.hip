@@ -7,7 +7,7 @@
 // Attention layout on gfx950: one 256-thread workgroup per (query row, head) item.
 //   - scores: groups of 8 lanes own one key (lane r of a group reads dims 8r..8r+7, so a
 //     wave reads 8 whole key rows per load instruction), 32 keys per pass, eight passes'
-//     keys requested before any is used, the 8 partial dots meet by shuffles; scores land
+//     keys requested before any is used, the 8 partial dots meet on DPP; scores land
 //     in LDS (at most 4096 keys);
 //   - softmax: block max and block sum through LDS;
 //   - p.v: 16 lanes cover the 64 dims of one V row (4 dims each, one coalesced row per
@@ -170,9 +170,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
                 float s = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; e++) s = fmaf(qf[e], kf[e], s);
-                s += __shfl_xor(s, 4, 64);
-                s += __shfl_xor(s, 2, 64);
-                s += __shfl_xor(s, 1, 64);
+                s = octet_sum(s);
                 s *= scale;
                 if (r == 0) sc[t] = s;
                 mx = fmaxf(mx, s);

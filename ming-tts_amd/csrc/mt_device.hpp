@@ -75,11 +75,18 @@ __device__ __forceinline__ float epilogue(float acc, float acc2, float b, uint32
     return v;
 }
 
-// Sum over aligned groups of `width` lanes (a power of two <= 64) of a wave64; every
-// lane of a group ends with the group sum.
+// One DPP lane move (quad permutes, row shifts and mirrors) of a float.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned octets of lanes, the same bits in all eight: two quad swaps, then the
+// half-row mirror (lane i and 7 - i), all on DPP.
+__device__ __forceinline__ float octet_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    return v + dpp_mov<0x141>(v);  // row_half_mirror
 }
 
 // Sum over aligned groups of `width` lanes (8, 16, 32 or 64), the same bits in every lane of
