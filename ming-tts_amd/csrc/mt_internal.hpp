@@ -78,7 +78,7 @@ constexpr int SEQ_CW = 8;          // waves per workgroup, each computing a shar
 constexpr int SEQ_TA = 12;         // MFMA tiles of one op a wave holds in registers
 constexpr int SEQ_GMAX = 2048;     // K of an op with an RMSNorm gain (staged in LDS)
 // Workgroup count of the persistent kernel on the current device.
-int seq_limits(int *groups);
+int seq_limits(int *groups, int *preferred);
 // Dataflow plan of a serial list of linears and attention items for `groups` workgroups
 // (host only; no HIP calls).
 int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt);
