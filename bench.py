@@ -501,13 +501,14 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
                 attention="inside the out projection" if fused else "separate launch")
 
 
-def bench_vae_latent(torch, mt, dev, ws, reps=5):
+def bench_vae_latent(torch, mt, dev, ws, reps=5, fused=True):
     """One latent of the streaming VAE decoder (VAEDecoder.decodeDispatches, VAEDecoder.swift:
     81-107) after fc1: upsample4, the 24-layer sliding-window Qwen stack at M = 4 rows (rmsnorm
     + qkv, rope_cache, attention over the last 65 keys, o +=, rmsnorm + gate|up, down +=; the
     backbone's synthetic fp16 weights stand in for the VAE stack's, same shapes), the 3530 x
     896 spectrum head, istft_frames (nfft 3528) and istft_emit (4 hops): 148 launches,
-    captured in a HIP graph and replayed."""
+    captured in a HIP graph and replayed.  With ``fused`` each layer's rope_cache and
+    attention run as one mt_rope_attention launch: 124 launches."""
     HQ, HKV, CAP, NFFT, HOP, RING = 14, 2, 512, 3528, 882, 8
     pos0 = 4 * 50
     g = torch.Generator(device=dev)
@@ -536,8 +537,11 @@ def bench_vae_latent(torch, mt, dev, ws, reps=5):
         mt.upsample4(h[0], h[1], h[2], frames, stream=s)
         for p, (kc, vc) in zip(ws, caches):
             mt.linear(frames, p["qkv"], qkv, 4, bias=p["qkv_b"], norm=p["norm1"], stream=s)
-            mt.rope_cache(qkv, QKV, 4, HQ, HKV, pos0, kc, vc, CAP, invf, stream=s)
-            mt.attention(qkv, QKV, 4, HQ, HKV, pos0, 65, kc, vc, CAP, att, HQ * 64, stream=s)
+            if fused:
+                mt.rope_attention(qkv, QKV, 4, HQ, HKV, pos0, 65, kc, vc, CAP, invf, att, HQ * 64, stream=s)
+            else:
+                mt.rope_cache(qkv, QKV, 4, HQ, HKV, pos0, kc, vc, CAP, invf, stream=s)
+                mt.attention(qkv, QKV, 4, HQ, HKV, pos0, 65, kc, vc, CAP, att, HQ * 64, stream=s)
             mt.linear(att, p["o"], frames, 4, flags=mt.GemvFlags.accumulate, stream=s)
             mt.linear(frames, p["gate"], mlp, 4, flags=mt.GemvFlags.siluGate, w2=p["up"], norm=p["norm2"], stream=s)
             mt.linear(mlp, p["down"], frames, 4, flags=mt.GemvFlags.accumulate, stream=s)
@@ -561,7 +565,7 @@ def bench_vae_latent(torch, mt, dev, ws, reps=5):
         graph.replay()
         ms = ev.stop_ms()
         best = ms if best is None else min(best, ms)
-    return dict(us_per_latent=best * 1e3, launches=1 + 6 * len(ws) + 3,
+    return dict(us_per_latent=best * 1e3, launches=1 + (5 if fused else 6) * len(ws) + 3,
                 audio_ms_per_latent=4 * HOP / 44100 * 1e3)
 
 

@@ -25,6 +25,8 @@
  *                        sequence
  *   mt_rope_cache        Encoder.ropeCache         Sources/MingTTS/Engine/Kernels.swift:180-191
  *   mt_attention         Encoder.attention         Sources/MingTTS/Engine/Kernels.swift:193-206
+ *   mt_rope_attention    Encoder.ropeCache +       Sources/MingTTS/Engine/Kernels.swift:180-206,
+ *                        Encoder.attention         Sources/MingTTS/Engine/VAEDecoder.swift:81-107
  *   mt_attention_decode  Encoder.attention over B  Sources/MingTTS/Engine/Kernels.swift:193-206
  *                        independent caches at
  *                        M = 1 each
@@ -267,6 +269,19 @@ int mt_attention(const float *q, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t
                  uint32_t pos0, uint32_t window, const void *k_cache, const void *v_cache,
                  mt_dtype cache_t, uint32_t cache_len, float *out, uint32_t ldo, float scale,
                  mt_stream_t stream);
+
+/*
+ * mt_rope_cache then mt_attention over the same M rows (Encoder.ropeCache then
+ * Encoder.attention, Kernels.swift:180-206, as VAEDecoder.decodeDispatches issues them for the
+ * decoder's sliding-window layers, VAEDecoder.swift:81-107) in one launch, with the same
+ * effects and the same bits: q of every row is rotated in place in qkv, row m's rotated k and
+ * raw v are appended at pos0 + m, and out row m attends over [max(0, pos0 + m + 1 - window),
+ * pos0 + m].  M <= 64; out 16-byte aligned with a 16-byte row stride and apart from qkv;
+ * otherwise as the two calls.
+ */
+int mt_rope_attention(float *qkv, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv, uint32_t pos0,
+                      uint32_t window, void *k_cache, void *v_cache, mt_dtype cache_t, uint32_t cache_len,
+                      const float *inv_freq, float *out, uint32_t ldo, float scale, mt_stream_t stream);
 
 /*
  * Batched decode attention: B independent sequences, one query row each (the CFG

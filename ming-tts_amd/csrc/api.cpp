@@ -314,6 +314,28 @@ int mt_attention(const float *q, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t
                             ldo, scale, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mt_rope_attention(float *qkv, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv, uint32_t pos0, uint32_t window,
+                      void *k_cache, void *v_cache, mt_dtype cache_t, uint32_t cache_len, const float *inv_freq,
+                      float *out, uint32_t ldo, float scale, mt_stream_t stream) {
+    const char *who = "mt_rope_attention";
+    int rc = validate_heads(who, hq, hkv, cache_t, cache_len);
+    if (rc) return rc;
+    if (M == 0) return MT_OK;
+    if (M > 64) return set_error(MT_EINVAL, "%s: at most 64 rows, got %u", who, M);
+    if (!qkv || !k_cache || !v_cache || !inv_freq || !out) return set_error(MT_EINVAL, "%s: null pointer", who);
+    if (ldq < (hq + 2 * hkv) * 64 || ldo < hq * 64)
+        return set_error(MT_EINVAL, "%s: ldq %u < (hq + 2 hkv) * 64 or ldo %u < hq * 64", who, ldq, ldo);
+    if (!aligned(out, 16) || ldo % 4) return set_error(MT_EINVAL, "%s: out must be 16-byte aligned with a 16-byte row stride", who);
+    if (static_cast<uint64_t>(pos0) + M > cache_len)
+        return set_error(MT_EINVAL, "%s: positions %u..%u past cache_len %u", who, pos0, pos0 + M - 1, cache_len);
+    // out must not overlap qkv (the kernel rewrites q in place and reads k and v).
+    const char *qb = reinterpret_cast<const char *>(qkv), *qe = qb + (static_cast<size_t>(M - 1) * ldq + (hq + 2 * hkv) * 64) * 4;
+    const char *ob = reinterpret_cast<const char *>(out), *oe = ob + (static_cast<size_t>(M - 1) * ldo + hq * 64) * 4;
+    if (qb < oe && ob < qe) return set_error(MT_EINVAL, "%s: out overlaps qkv", who);
+    return launch_rope_attention(qkv, ldq, M, hq, hkv, pos0, window, k_cache, v_cache, cache_t, cache_len, inv_freq, out,
+                                 ldo, scale, reinterpret_cast<hipStream_t>(stream));
+}
+
 int mt_attention_decode(const float *q, uint32_t ldq, uint32_t B, uint32_t hq, uint32_t hkv, const uint32_t *lens,
                         uint32_t window, const void *k_cache, const void *v_cache, mt_dtype cache_t,
                         uint32_t cache_len, uint64_t cache_stride, float *out, uint32_t ldo, float scale,

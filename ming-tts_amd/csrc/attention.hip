@@ -232,7 +232,189 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
     }
 }
 
+// rope_cache then attention over one sequence's M new rows (positions pos0 .. pos0 + M - 1),
+// in one launch: workgroup (row m, head h) rotates its q (and writes it back to qkv), appends
+// row m's rotated k and raw v of kv head h / (hq / hkv) to the caches when h is the first head
+// of its group, and attends over keys [max(0, pos0 + m + 1 - window), pos0 + m].  Keys before
+// pos0 come from the cache; the chunk's own rows (pos0 ..) are rebuilt from qkv in LDS,
+// rounded to the cache type as the cache holds them, so no workgroup reads a cache row that
+// another is writing.  Every value, and every summation order, is attention_kernel's.
+constexpr int RA_MAXROWS = 64;
+template <int CT>
+__global__ __launch_bounds__(ATT_THREADS) void rope_attention_kernel(float *qkv, uint32_t ldq, uint32_t hq, uint32_t hkv,
+                                                                     uint32_t pos0, uint32_t window, void *kc, void *vc,
+                                                                     uint32_t cache_len, const float *inv_freq, float *out,
+                                                                     uint32_t ldo, float scale) {
+    __shared__ float sc[ATT_MAXKEYS];
+    __shared__ float red[ATT_THREADS / 64];
+    __shared__ float4 part[16][16];
+    __shared__ __attribute__((aligned(16))) float qs[64];
+    __shared__ __attribute__((aligned(16))) float ck[RA_MAXROWS][64];
+    __shared__ __attribute__((aligned(16))) float cv[RA_MAXROWS][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t m = blockIdx.x / hq, h = blockIdx.x % hq;
+    const uint32_t group = hq / hkv, kvh = h / group;
+    const uint32_t jEnd = pos0 + m + 1;
+    const uint32_t jStart = (window > 0 && jEnd > window) ? jEnd - window : 0;
+    const int nk = static_cast<int>(jEnd - jStart);
+    const uint32_t c0 = jStart > pos0 ? jStart - pos0 : 0u;  // first chunk row attended
+    const int nc = jStart < pos0 ? static_cast<int>(pos0 - jStart) : 0;  // keys from the cache
+    const size_t kvbase = (static_cast<size_t>(kvh) * cache_len + jStart) * 64;
+
+    // The rotations (rope_cache_kernel's arithmetic): q of (m, h), and k, v of kv head kvh
+    // for chunk rows c0 .. m; row m's k and v also go to the caches (first head of the group).
+    if (tid < 32) {
+        const uint32_t i = tid;
+        const float angle = static_cast<float>(pos0 + m) * inv_freq[i];
+        const float c = cosf(angle), sn = sinf(angle);
+        float *row = qkv + static_cast<size_t>(m) * ldq + static_cast<size_t>(h) * 64;
+        const float x0 = row[i], x1 = row[i + 32];
+        const float r0 = x0 * c - x1 * sn;
+        const float r1 = x1 * c + x0 * sn;
+        row[i] = r0;
+        row[i + 32] = r1;
+        qs[i] = r0;
+        qs[i + 32] = r1;
+    }
+    for (uint32_t e = tid; e < (m + 1 - c0) * 32; e += ATT_THREADS) {
+        const uint32_t rr = c0 + e / 32, i = e % 32, pos = pos0 + rr;
+        const float *row = qkv + static_cast<size_t>(rr) * ldq + static_cast<size_t>(hq + kvh) * 64;
+        const float angle = static_cast<float>(pos) * inv_freq[i];
+        const float c = cosf(angle), sn = sinf(angle);
+        const float x0 = row[i], x1 = row[i + 32];
+        const float r0 = x0 * c - x1 * sn;
+        const float r1 = x1 * c + x0 * sn;
+        const float *vrow = row + static_cast<size_t>(hkv) * 64;
+        float k0 = r0, k1 = r1, v0 = vrow[i], v1 = vrow[i + 32];
+        if constexpr (CT == DT_F16) {  // as the fp16 cache holds them
+            k0 = static_cast<float>(static_cast<_Float16>(k0));
+            k1 = static_cast<float>(static_cast<_Float16>(k1));
+            v0 = static_cast<float>(static_cast<_Float16>(v0));
+            v1 = static_cast<float>(static_cast<_Float16>(v1));
+        }
+        ck[rr][i] = k0;
+        ck[rr][i + 32] = k1;
+        cv[rr][i] = v0;
+        cv[rr][i + 32] = v1;
+        if (rr == m && h % group == 0) {
+            const size_t dst = (static_cast<size_t>(kvh) * cache_len + pos) * 64;
+            store1<CT>(kc, dst + i, r0);
+            store1<CT>(kc, dst + i + 32, r1);
+            store1<CT>(vc, dst + i, vrow[i]);
+            store1<CT>(vc, dst + i + 32, vrow[i + 32]);
+        }
+    }
+    __syncthreads();
+
+    // Scores: the cache's keys in rounds of eight passes, then the chunk's keys from LDS.
+    const int r = tid & 7;
+    float qf[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) qf[e] = qs[8 * r + e];
+    float mx = -INFINITY;
+    constexpr int KP = ATT_THREADS / 8, KU = 8;
+    for (int t0 = tid >> 3; t0 < nc; t0 += KU * KP) {
+        Raw8<CT> kr[KU];
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int t = min(t0 + u * KP, nc - 1);
+            kr[u] = load8_raw<CT>(kc, kvbase + static_cast<size_t>(t) * 64 + 8 * r);
+        }
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int t = t0 + u * KP;
+            if (t < nc) {
+                float kf[8];
+                decode8<CT>(kr[u], kf);
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) s = fmaf(qf[e], kf[e], s);
+                s = octet_sum(s);
+                s *= scale;
+                if (r == 0) sc[t] = s;
+                mx = fmaxf(mx, s);
+            }
+        }
+    }
+    for (int t = nc + (((tid >> 3) - nc) % KP + KP) % KP; t < nk; t += KP) {
+        const float *kf = &ck[c0 + (t - nc)][8 * r];
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) s = fmaf(qf[e], kf[e], s);
+        s = octet_sum(s);
+        s *= scale;
+        if (r == 0) sc[t] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+
+    float sum = 0.0f;
+    for (int t = tid; t < nk; t += ATT_THREADS) {
+        const float e = expf(sc[t] - mx);
+        sc[t] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+
+    // p . v in attention_kernel's order (keys ks, ks + 16, ... of each phase).
+    const int d4 = tid & 15, ks = tid >> 4;
+    constexpr int VU = 8;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int t0 = ks; t0 < nk; t0 += 16 * VU) {
+        float4 v[VU];
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int t = t0 + 16 * u;
+            v[u] = t < nc ? load4<CT>(vc, kvbase + static_cast<size_t>(t) * 64 + 4 * d4)
+                          : *reinterpret_cast<const float4 *>(&cv[c0 + (t < nk ? t - nc : 0)][4 * d4]);
+        }
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int t = t0 + 16 * u;
+            if (t < nk) {
+                const float p = sc[t];
+                acc.x = fmaf(p, v[u].x, acc.x);
+                acc.y = fmaf(p, v[u].y, acc.y);
+                acc.z = fmaf(p, v[u].z, acc.z);
+                acc.w = fmaf(p, v[u].w, acc.w);
+            }
+        }
+    }
+    part[ks][d4] = acc;
+    __syncthreads();
+    if (tid < 16) {
+        float4 o = part[0][tid];
+        for (int k = 1; k < 16; k++) {
+            const float4 pp = part[k][tid];
+            o.x += pp.x; o.y += pp.y; o.z += pp.z; o.w += pp.w;
+        }
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        float4 res = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        *reinterpret_cast<float4 *>(out + static_cast<size_t>(m) * ldo + h * 64 + 4 * tid) = res;
+    }
+}
+
 }  // namespace
+
+int launch_rope_attention(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
+                          uint32_t window, void *kc, void *vc, int ct, uint32_t cache_len, const float *inv_freq,
+                          float *out, uint32_t ldo, float scale, hipStream_t stream) {
+    dim3 grid(rows * hq);
+    if (ct == DT_F32)
+        hipLaunchKernelGGL(rope_attention_kernel<DT_F32>, grid, dim3(ATT_THREADS), 0, stream, qkv, ldq, hq, hkv, pos0,
+                           window, kc, vc, cache_len, inv_freq, out, ldo, scale);
+    else
+        hipLaunchKernelGGL(rope_attention_kernel<DT_F16>, grid, dim3(ATT_THREADS), 0, stream, qkv, ldq, hq, hkv, pos0,
+                           window, kc, vc, cache_len, inv_freq, out, ldo, scale);
+    return check_launch("rope_attention");
+}
 
 int launch_rope_cache(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
                       const uint32_t *pos_arr, void *kc, void *vc, int ct, uint32_t cache_len,

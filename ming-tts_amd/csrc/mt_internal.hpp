@@ -91,6 +91,9 @@ int seq_groups(const SeqPlan *p);
 int launch_rope_cache(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
                       const uint32_t *pos_arr, void *kc, void *vc, int ct, uint32_t cache_len,
                       uint64_t cache_stride, const float *inv_freq, hipStream_t stream);
+int launch_rope_attention(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
+                          uint32_t window, void *kc, void *vc, int ct, uint32_t cache_len, const float *inv_freq,
+                          float *out, uint32_t ldo, float scale, hipStream_t stream);
 int launch_attention(const float *q, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
                      const uint32_t *lens, uint32_t window, const void *kc, const void *vc, int ct,
                      uint32_t cache_len, uint64_t cache_stride, float *out, uint32_t ldo, float scale,

@@ -30,7 +30,7 @@ EXPORTS = (
     "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
-    "mt_attention", "mt_attention_decode", "mt_dit_attention", "mt_dit_attention_linear", "mt_flow_assemble",
+    "mt_attention", "mt_attention_decode", "mt_rope_attention", "mt_dit_attention", "mt_dit_attention_linear", "mt_flow_assemble",
     "mt_flow_euler",
     "mt_upsample4", "mt_istft_frames", "mt_istft_emit", "mt_st_open", "mt_st_close", "mt_st_count", "mt_st_name", "mt_st_find", "mt_arena_create", "mt_arena_tensor",
     "mt_arena_padded", "mt_arena_bytes", "mt_arena_upload", "mt_arena_audit", "mt_arena_destroy",
@@ -130,6 +130,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_rope_cache_decode.argtypes = [vp, u32, u32, u32, u32, vp, vp, vp, i32, u32, u64, vp, vp]
     L.mt_rope_cache_decode.restype = i32
     L.mt_attention.argtypes = [vp, u32, u32, u32, u32, u32, u32, vp, vp, i32, u32, vp, u32, f32, vp]
+    L.mt_rope_attention.argtypes = [vp, u32, u32, u32, u32, u32, u32, vp, vp, i32, u32, vp, vp, u32, f32, vp]
+    L.mt_rope_attention.restype = i32
     L.mt_attention.restype = i32
     L.mt_attention_decode.argtypes = [vp, u32, u32, u32, u32, vp, u32, vp, vp, i32, u32, u64, vp, u32, f32, vp]
     L.mt_attention_decode.restype = i32
@@ -329,6 +331,13 @@ def rope_cache_decode(qkv, ldq, B, hq, hkv, pos, kc, vc, cache_len, cache_stride
 def attention(q, ldq, M, hq, hkv, pos0, window, kc, vc, cache_len, out, ldo, scale=0.125, stream=None) -> None:
     check(load().mt_attention(_ptr(q), ldq, M, hq, hkv, pos0, window, _ptr(kc), _ptr(vc), dtype_code(kc),
                               cache_len, _ptr(out), ldo, scale, _stream(stream)))
+
+
+def rope_attention(qkv, ldq, M, hq, hkv, pos0, window, kc, vc, cache_len, inv_freq, out, ldo, scale=0.125,
+                   stream=None) -> None:
+    """rope_cache then attention over the same M rows in one launch (mt_rope_attention)."""
+    check(load().mt_rope_attention(_ptr(qkv), ldq, M, hq, hkv, pos0, window, _ptr(kc), _ptr(vc), dtype_code(kc),
+                                   cache_len, _ptr(inv_freq), _ptr(out), ldo, scale, _stream(stream)))
 
 
 def attention_decode(q, ldq, B, hq, hkv, lens, window, kc, vc, cache_len, cache_stride, out, ldo, scale=0.125,

@@ -113,3 +113,45 @@ def test_decode_window_and_length_edges(gpu):
             want = O.attention_f64(q[b].reshape(HQ, 64), kc0[b], vc0[b], int(lens[b]) - 1, window, 0.125)
             ex, i, g, w = O.worst_violation(got[b], want, 2e-5)
             assert ex <= 0, f"window {window} b={b} index {i} got {g} want {w}"
+
+
+@pytest.mark.parametrize("ct,M,pos0,window,cap", [
+    (torch.float16, 4, 200, 65, 512),    # one VAE latent's sliding-window rows
+    (torch.float32, 4, 200, 65, 512),
+    (torch.float16, 3, 0, 0, 64),        # no cached keys yet, unlimited window
+    (torch.float32, 1, 37, 1, 64),       # a window of the row itself
+    (torch.float16, 16, 100, 0, 256),    # 16 rows, unlimited window
+    (torch.float16, 8, 504, 9, 512),     # positions up to the cache's end, window inside the chunk
+])
+def test_rope_attention_equals_rope_cache_then_attention(gpu, ct, M, pos0, window, cap):
+    """mt_rope_attention against mt_rope_cache then mt_attention on copies of the same qkv and
+    caches: the same out, the same rotated q in qkv, the same cache rows, bit for bit."""
+    rng = np.random.default_rng(M * 1000 + pos0 + window)
+    qkv = rng.standard_normal((M, LD)).astype(np.float32)
+    kc0 = rng.standard_normal((HKV, cap, 64)).astype(np.float32)
+    vc0 = rng.standard_normal((HKV, cap, 64)).astype(np.float32)
+    invf = torch.from_numpy(O.inv_freq(1e6)).to(gpu)
+    t = lambda a, dt=torch.float32: torch.from_numpy(a.copy()).to(gpu).to(dt)
+    q1, k1, v1 = t(qkv), t(kc0, ct), t(vc0, ct)
+    q2, k2, v2 = t(qkv), t(kc0, ct), t(vc0, ct)
+    o1 = torch.full((M, HQ * 64), 5.0, device=gpu)
+    o2 = torch.full((M, HQ * 64), 5.0, device=gpu)
+    say(f"rope_attention ct={ct} M={M} pos0={pos0} window={window} cap={cap}")
+    mt.rope_cache(q1, LD, M, HQ, HKV, pos0, k1, v1, cap, invf)
+    mt.attention(q1, LD, M, HQ, HKV, pos0, window, k1, v1, cap, o1, HQ * 64, 0.125)
+    mt.rope_attention(q2, LD, M, HQ, HKV, pos0, window, k2, v2, cap, invf, o2, HQ * 64, 0.125)
+    torch.cuda.synchronize()
+    for a, b, what in ((o1, o2, "out"), (q1, q2, "qkv"), (k1, k2, "k cache"), (v1, v2, "v cache")):
+        np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy(), err_msg=what)
+
+
+def test_rope_attention_rejects_bad_arguments():
+    L = mt.load()
+    A = 1 << 20
+    assert L.mt_rope_attention(A, LD, 65, HQ, HKV, 0, 0, A, A, mt.F16, 512, A, A + (1 << 24), HQ * 64, 0.125, None) \
+        == mt.EINVAL and "at most 64 rows" in mt.last_error()
+    assert L.mt_rope_attention(A, LD, 4, HQ, HKV, 510, 0, A, A, mt.F16, 512, A, A + (1 << 24), HQ * 64, 0.125, None) \
+        == mt.EINVAL and "past cache_len" in mt.last_error()
+    assert L.mt_rope_attention(A, LD, 4, HQ, HKV, 0, 0, A, A, mt.F16, 512, A, A + 64, HQ * 64, 0.125, None) \
+        == mt.EINVAL and "overlaps" in mt.last_error()
+    assert L.mt_rope_attention(A, LD, 0, HQ, HKV, 0, 0, A, A, mt.F16, 512, A, A, HQ * 64, 0.125, None) == mt.OK
