@@ -24,7 +24,6 @@ namespace mt {
 namespace {
 
 constexpr int ISTFT_NMAX = 4096;   // nfft limit of the LDS tables
-constexpr int ISTFT_SPAN = 512;    // samples t per workgroup (t and N - t: 2 per thread)
 
 __global__ __launch_bounds__(256) void upsample4_kernel(const float *prev, const float *cur, const float *next,
                                                         float *frames, uint32_t ldf, uint32_t hidden, uint32_t has_prev,
