@@ -1,5 +1,5 @@
 // Persistent execution of a linear sequence (mt_seq_*): the decode step's chain of
-// dependent GEMVs as ONE launch of one workgroup per CU, synchronised by dataflow instead
+// dependent GEMVs as ONE launch of at most one workgroup per CU, synchronised by dataflow instead
 // of barriers.
 //
 // Reference counterpart: QwenForward.dispatches encoded on one serial compute encoder
@@ -17,7 +17,7 @@
 //   - user buffers: an op reads a user buffer only where nothing earlier in the sequence
 //     wrote it, and writes a user buffer only if it is the last op writing that region
 //     (the host plan compiler resolves both), so every user element is written once per run.
-// Inside a workgroup (512 threads, one per CU) every wave computes.  A wave owns a
+// Inside a workgroup (512 threads, at most one per CU) every wave computes.  A wave owns a
 // contiguous range of each op's MFMA tiles (16 weight rows x 32 k, one 16-byte chunk per
 // lane, as seq_tiles.hpp cuts them) and keeps them in registers, loaded one op ahead:
 //   - a wave's vector loads retire in order, so per op it issues its activation loads
@@ -544,7 +544,7 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     __syncthreads();  // the scratch is free again
 }
 
-// One 512-thread workgroup per CU runs every op of the sequence in order (see the top of
+// Each 512-thread workgroup (at most one per CU) runs every op of the sequence in order (see the top of
 // the file).  tags / tag_bytes: the plan's tagged activation buffer, read through a buffer
 // resource with device-coherent loads.  MS: the rows M of every op when the plan has one
 // common M the kernel is specialised for (1 or 2), else 0 (M read per op).  ATTN: the plan
