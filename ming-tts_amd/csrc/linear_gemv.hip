@@ -57,17 +57,19 @@ gemv_fn pick(int mr, int wt, int xt, bool gated, bool norm) {
 
 }  // namespace
 
-int gemv_lanes_log2(uint32_t K, int override_lanes) {
+int gemv_lanes_log2(uint32_t K, int override_lanes, uint32_t M) {
     if (override_lanes >= 8 && override_lanes <= 64) {
         int l2 = 3;
         while ((1 << l2) < override_lanes) l2++;
         return l2;
     }
-    // About eight 16-byte chunks per lane: K = 896 -> 16 lanes (7 chunks each),
-    // K = 4864 -> 64 lanes (9.5), K = 1024 -> 16 (8), K = 4096 -> 64 (8).
-    const uint32_t kc = K / 8;
+    // About eight 16-byte chunks per lane for one row, four for two or more (each chunk then
+    // feeds every row): K = 896 -> 16 lanes at M = 1 (7 chunks each), 32 at M = 2 (3.5);
+    // K = 4864 -> 64 lanes (9.5).  Measured on 4864 x 896 at M = 2: 5.2 us with 32 lanes,
+    // 5.5-5.9 us with 16.
+    const uint32_t kc = K / 8, target = M >= 2 ? 4u : 8u;
     int l2 = 3;
-    while ((1u << l2) < 64u && (1u << l2) * 8u < kc) l2++;
+    while ((1u << l2) < 64u && (1u << l2) * target < kc) l2++;
     return l2;
 }
 
@@ -76,7 +78,7 @@ int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int ove
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
     const int mr = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : 8;
-    const int l2 = gemv_lanes_log2(a.K, override_lanes);
+    const int l2 = gemv_lanes_log2(a.K, override_lanes, a.M);
     const int L = 1 << l2;
     // 256 threads per workgroup unless that leaves fewer than 512 workgroups; never below
     // one wave (64 threads).

@@ -107,7 +107,7 @@ int launch_flow_assemble(const float *y, const float *history, const float *cemb
 int launch_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row, float *capture,
                       uint32_t latent, float cfg, float dt, hipStream_t stream);
 
-int gemv_lanes_log2(uint32_t K, int override_lanes);
+int gemv_lanes_log2(uint32_t K, int override_lanes, uint32_t M);
 int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes);
 // Up to 64 B columns (M rows of x of the weights' type, or 2 M with hi + lo halves; a fused
 // norm at most 8 rows) on MFMA, x staged once per workgroup of 16 output features.
