@@ -1,8 +1,8 @@
 // One item of the DiT's full attention with interleaved RoPE (Shaders.swift:598-648):
 // query row i of one sequence of S rows, one head, computed by a half wave.  Lane p of the
 // half wave owns dims 2p, 2p + 1 (one interleaved-RoPE pair, frequency inv_freq[p]); the q.k
-// dot is a 5-step butterfly inside the half wave; fp32 scores, scaled after the dot,
-// max-subtracted softmax, fp32 p.v.  Shared by dit_attention_kernel and the out-projection
+// dot is a 5-step reduction over the half wave's 32 lanes; fp32 scores, scaled after the
+// dot, max-subtracted softmax, fp32 p.v.  Shared by dit_attention_kernel and the out-projection
 // linear that computes its own x from qkv, so both produce the same bits.  An item is
 // requested (dit_item_load) apart from its arithmetic (dit_item_attend), so a kernel can put
 // the loads of several items in flight before it waits for any.
@@ -13,21 +13,6 @@
 namespace mt {
 
 constexpr int DIT_MAXS = 8;  // rows per DiT sequence
-
-// Sum over the 32 lanes of a half wave, the same bits in every lane: quad swaps, the
-// half-row mirror (octets), the row mirror (rows of 16) on DPP, then one exchange between
-// the half wave's two rows.
-template <int CTRL>
-__device__ __forceinline__ float dit_dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float dit_half_sum(float v) {
-    v += dit_dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-    v += dit_dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-    v += dit_dpp<0x141>(v);  // row_half_mirror
-    v += dit_dpp<0x140>(v);  // row_mirror
-    return v + __shfl_xor(v, 16, 64);
-}
 
 // cos and sin of position j's angle j * freq for the lane's pair, j < S (the rest unused).
 __device__ __forceinline__ void dit_rope_table(float freq, uint32_t S, float (&c)[DIT_MAXS], float (&s)[DIT_MAXS]) {
@@ -85,7 +70,7 @@ __device__ __forceinline__ float2 dit_item_attend(const DitItem &it, uint32_t i,
     for (uint32_t j = 0; j < DIT_MAXS; j++) {
         if (j < S) {
             const float2 k = dit_rope_pair(it.k[j], c[j], s[j]);
-            sc[j] = dit_half_sum(q.x * k.x + q.y * k.y) * scale;
+            sc[j] = group_sum(q.x * k.x + q.y * k.y, 32) * scale;
             mx = fmaxf(mx, sc[j]);
         }
     }
