@@ -132,10 +132,14 @@ enum {
                                     4 = the register-staged kernel that other activation types use */
     MT_TUNE_GEMM_STAGES = 7,     /* loads of that GEMM: 2..4 = direct-to-LDS stages of 64 k, 1 = two
                                     register-staged stages into two LDS buffers (0 = auto) */
-    MT_TUNE_GEMV_MFMA = 8        /* the MFMA kernel that stages x once per 16 output features: 0 =
+    MT_TUNE_GEMV_MFMA = 8,       /* the MFMA kernel that stages x once per 16 output features: 0 =
                                     for 3..16 rows (default; 3..8 with a fused norm), 1 = never
                                     (lane-group GEMV up to 8 rows, GEMM above), 2 = up to 64 rows of
                                     x of the weights' type (32 otherwise) */
+    MT_TUNE_SEQ_LAYER = 9        /* 0: a sequence of Qwen2-0.5B decode layers (qkv 1152 x 896, o,
+                                    gate|up 2 x 4864 x 896, down at 1, 2 or 4 rows) runs on the
+                                    kernel specialised for those shapes (default); 1: on the
+                                    general sequence kernel */
 };
 int mt_set_tuning(int key, int value);
 
@@ -229,6 +233,13 @@ int mt_seq_run(mt_seq *seq, mt_stream_t stream);
 int mt_seq_destroy(mt_seq *seq);
 /* Workgroups the plan's kernel runs with (after mt_seq_create). */
 int mt_seq_groups(const mt_seq *seq);
+/* The kernel the plan runs: MT_SEQ_DECODE_LAYER when its linears repeat the Qwen2-0.5B
+ * decode layer of QwenForward.dispatches (Qwen.swift:84-91; qkv 1152 x 896 + bias with the
+ * first RMSNorm, o 896 x 896 +=, gate|up 2 x 4864 x 896 SiLU-gate with the second RMSNorm,
+ * down 896 x 4864 +=) at 1, 2 or 4 rows, with no attention items; MT_SEQ_GENERAL otherwise
+ * (or under MT_TUNE_SEQ_LAYER = 1).  Both compute the same sequence. */
+enum { MT_SEQ_GENERAL = 0, MT_SEQ_DECODE_LAYER = 1 };
+int mt_seq_kernel(const mt_seq *seq);
 /* Synchronous health check of a plan after its runs completed: MT_EHIP if a dataflow wait
  * of a run gave up after its spin bound (co-residency was lost), MT_ERANGE if an fp16-weight
  * run met an activation beyond the fp16 range, else MT_OK.  Both flags stay set for the

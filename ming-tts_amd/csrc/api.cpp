@@ -111,7 +111,7 @@ int mt_linear_kernel(uint32_t M, uint32_t N, uint32_t K, mt_dtype xt, mt_dtype w
 }
 
 int mt_set_tuning(int key, int value) {
-    int *slot = nullptr;
+    std::atomic<int> *slot = nullptr;
     int def = 0;
     switch (key) {
         case MT_TUNE_GEMV_ROWS_MAX: slot = &g_tuning.gemv_rows_max; def = 8; break;
@@ -122,10 +122,13 @@ int mt_set_tuning(int key, int value) {
         case MT_TUNE_GEMM_TILE: slot = &g_tuning.gemm_tile; def = 0; break;
         case MT_TUNE_GEMM_STAGES: slot = &g_tuning.gemm_stages; def = 0; break;
         case MT_TUNE_GEMV_MFMA: slot = &g_tuning.gemv_mfma; def = 0; break;
+        case MT_TUNE_SEQ_LAYER: slot = &g_tuning.seq_layer; def = 0; break;
         default: return set_error(MT_EINVAL, "mt_set_tuning: unknown key %d", key);
     }
     if (key == MT_TUNE_SEQ_LAUNCH && value > 1)
         return set_error(MT_EINVAL, "mt_set_tuning: the sequence launch mode is 0 or 1, got %d", value);
+    if (key == MT_TUNE_SEQ_LAYER && value > 1)
+        return set_error(MT_EINVAL, "mt_set_tuning: the decode-layer kernel choice is 0 or 1, got %d", value);
     if (key == MT_TUNE_GEMV_MFMA && value > 2)
         return set_error(MT_EINVAL, "mt_set_tuning: the small-M kernel choice is 0, 1 or 2, got %d", value);
     if (key == MT_TUNE_GEMM_STAGES && value > 4)
@@ -134,9 +137,7 @@ int mt_set_tuning(int key, int value) {
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMM tile choice is 0..4, got %d", value);
     if (key == MT_TUNE_GEMV_ROWS_MAX && value > 8)
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMV takes at most 8 rows per block, got %d", value);
-    const int old = *slot;
-    *slot = value < 0 ? def : value;
-    return old;
+    return slot->exchange(value < 0 ? def : value, std::memory_order_relaxed);
 }
 
 int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt, const void *bias,
@@ -203,36 +204,43 @@ int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out
             return set_error(MT_EINVAL, "%s: unknown kind %d", who, items[i].kind);
         }
     }
+    // Plan at a workgroup count: the dataflow form (hazards the reordering could break),
+    // then the kernel: the decode-layer kernel when the ops repeat the Qwen2-0.5B decode
+    // layer and the count fits its tiling, else the general kernel within its limits.
+    auto plan_at = [&](int g, std::vector<SeqOp> &d, int &w, bool &layer) {
+        int r = seq_plan(items, n_items, g, d, w);
+        if (r) return r;
+        layer = g_tuning.seq_layer == 0 && layer_pattern(d.data(), n_items, g);
+        return layer ? MT_OK : seq_general_limits(items, n_items, g);
+    };
     // Plan once with the expected workgroup count before touching the device, so a sequence
-    // the dataflow form cannot take is rejected without a GPU; re-plan if the device differs.
+    // no kernel can take is rejected without a GPU; re-plan for the device's counts.
     std::vector<SeqOp> dev;
     int wt = DT_F16;
-    const int guess = g_tuning.seq_groups > 0 ? g_tuning.seq_groups : 256;
-    int rc = seq_plan(items, n_items, guess, dev, wt);
+    bool layer = false;
+    const int want = g_tuning.seq_groups;
+    const int guess = want > 0 ? want : 256;
+    int rc = plan_at(guess, dev, wt, layer);
     if (rc) return rc;
     if (n_items == 0) return set_error(MT_EINVAL, "mt_seq_create: empty sequence");
     int groups = 0, preferred = 0;
     rc = seq_limits(&groups, &preferred);
     if (rc) return rc;
-    bool planned = groups == guess;
-    if (preferred != groups) {  // the preferred count when every share fits it
-        std::vector<SeqOp> d2;
-        int wt2 = DT_F16;
-        if (seq_plan(items, n_items, preferred, d2, wt2) == MT_OK) {
-            dev.swap(d2);
-            wt = wt2;
-            groups = preferred;
-            planned = true;
-        } else {
-            planned = groups == guess;
-        }
-    }
-    if (!planned) {
-        rc = seq_plan(items, n_items, groups, dev, wt);
+    // The preferred count when the plan fits it, else every workgroup the device holds.
+    std::vector<SeqOp> d2;
+    int wt2 = DT_F16;
+    bool layer2 = false;
+    if (plan_at(preferred, d2, wt2, layer2) == MT_OK) {
+        groups = preferred;
+    } else {
+        rc = plan_at(groups, d2, wt2, layer2);
         if (rc) return rc;
     }
+    dev.swap(d2);
+    wt = wt2;
+    layer = layer2;
     SeqPlan *plan = nullptr;
-    rc = seq_create(dev.data(), n_items, wt, groups, &plan);
+    rc = seq_create(dev.data(), n_items, wt, groups, layer, &plan);
     if (rc) return rc;
     *out = reinterpret_cast<mt_seq *>(plan);
     return MT_OK;
@@ -269,6 +277,11 @@ int mt_seq_destroy(mt_seq *seq) {
 int mt_seq_groups(const mt_seq *seq) {
     if (!seq) return set_error(MT_EINVAL, "mt_seq_groups: null plan");
     return seq_groups(reinterpret_cast<const SeqPlan *>(seq));
+}
+
+int mt_seq_kernel(const mt_seq *seq) {
+    if (!seq) return set_error(MT_EINVAL, "mt_seq_kernel: null plan");
+    return seq_kernel_kind(reinterpret_cast<const SeqPlan *>(seq));
 }
 
 int mt_rope_cache(float *qkv, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv, uint32_t pos0, void *k_cache,

@@ -1,0 +1,557 @@
+// Persistent decode step of a Qwen2-0.5B-shaped layer stack: mt_seq_* plans whose linears
+// repeat the layer of QwenForward.dispatches (Qwen.swift:84-91) at the backbone's shapes
+// (Weights.swift:81-92):
+//     qkv     1152 x 896, bias, RMSNorm fused        (Qwen.swift:85)
+//     o        896 x 896, += residual                (Qwen.swift:88)
+//     gate|up 2 x 4864 x 896, SiLU-gate, RMSNorm     (Qwen.swift:90)
+//     down     896 x 4864, += residual               (Qwen.swift:91)
+// at M = 1, 2 or 4 rows.  It runs the dataflow of seq_kernel (tagged activation words, one
+// 512-thread workgroup per CU, every wave computing a share of every op, two workgroup
+// barriers per op) with every op's shape known at compile time:
+//   - each op class has a fixed tiling (below); a wave's tile range, its lanes' weight and
+//     activation addresses are computed once at kernel start, so per op a wave adds one
+//     64-bit base to a lane offset and issues its weight tiles with immediate offsets;
+//   - every wave loads exactly TA tiles of an op (a wave with fewer tiles loads its
+//     neighbours' blocks and skips their MFMAs), so the number of loads in flight behind
+//     the activations is the same on every path and the wait for the activations waits
+//     for nothing issued after them;
+//   - the epilogue flags are constants; no lane-divergent branch surrounds a load.
+// Tiling (v_mfma_f32_16x16x32: A = 16 weight rows x 32 k, one 16-byte chunk per lane; B =
+// 32 k x 16 columns of activations as hi + lo halves of the weights' 16-bit type; see
+// seq_tiles.hpp for the segment interleave):
+//   qkv     S = 2 K-segments per row tile, 8 features, the 14 block steps split over the 8 waves;
+//   o, down S = 4 (M <= 2) or 2 (M = 4), 16 / S features, block steps split over the 8 waves;
+//   gate|up S = 1, three row tiles of 8 gate rows and the same features' 8 up rows; waves
+//           0-2, 3-5 and 6-7 split the 28 block steps of row tiles 0, 1 and 2.
+// A wave's partial sums go to its own slot of the op class's LDS area; one lane per output
+// adds the 8 slots in slot order (slots no wave writes stay zero), so results are the same
+// on every run.  A workgroup owns features [g N / G, (g + 1) N / G) of every op, which the
+// tiling holds for 224 <= G <= 256 (the host checks it).
+#pragma once
+
+#include "seq_kernel.hpp"
+
+namespace mt {
+
+enum : int { LC_QKV = 0, LC_O = 1, LC_GU = 2, LC_DOWN = 3 };
+
+// Compile-time shape and tiling of op class C at M rows.
+template <int C, int M>
+struct LCls {
+    static constexpr uint32_t N = C == LC_QKV ? LAY_QKV : C == LC_GU ? LAY_I : LAY_H;
+    static constexpr uint32_t K = C == LC_DOWN ? LAY_I : LAY_H;
+    static constexpr bool GATED = C == LC_GU;
+    static constexpr bool NORM = C == LC_QKV || C == LC_GU;
+    static constexpr bool BIAS = C == LC_QKV;
+    static constexpr bool ACC = C == LC_O || C == LC_DOWN;
+    static constexpr uint32_t FLAGS = (BIAS ? F_BIAS : 0u) | (ACC ? F_ACCUM : 0u) | (GATED ? F_SILU_GATE : 0u);
+    static constexpr uint32_t S = GATED ? 1u : C == LC_QKV ? 2u : (M <= 2 ? 4u : 2u);
+    static constexpr uint32_t LS = S == 4 ? 2u : S == 2 ? 1u : 0u;
+    static constexpr uint32_t KB = K / 32, KBS = KB / S;
+    static constexpr uint32_t FPT = GATED ? 8u : 16u / S;  // features per row tile
+    static constexpr uint32_t RT = GATED ? 3u : 1u;         // row tiles
+    static constexpr uint32_t NMAX = FPT * RT;              // features a workgroup can own
+    // Tiles a compute wave loads: gate|up's RT KBS tiles split evenly over the 7 compute waves;
+    // otherwise the most block steps any wave has.
+    static constexpr uint32_t TA = GATED ? RT * KBS / 7 : (KBS + 6) / 7;
+    static constexpr uint32_t K4 = K / 4, NCH = M * K4;     // 16-byte x chunks of the op
+    static constexpr uint32_t XR = (NCH + 447) / 448;       // x chunks per compute thread
+    // LDS partial sums: [row tile][x row][virtual row][slot]
+    static constexpr uint32_t VR = GATED ? 16u : FPT;
+    static constexpr uint32_t PART = RT * M * VR * 8;
+    static_assert(KB % S == 0 && 2 * S * M <= 16 && (!GATED || RT * KBS % 7 == 0), "tiling");
+};
+
+constexpr int LAY_CW = 7;  // waves of a workgroup (the block steps of qkv and o split evenly)
+constexpr int LAY_THREADS = LAY_CW * 64;
+
+
+// The fields of one op the kernel reads, packed for one scalar load (built by the plan
+// compiler next to the op descriptors).  Tagged positions are word offsets into the plan's
+// tag buffer.
+enum : uint32_t { LAY_XEXT = 1, LAY_YEXT = 2, LAY_FINAL = 4 };
+struct LayOp {
+    const uint16_t *w;     // weights (gate|up: the gate rows)
+    const uint16_t *p2;    // gate|up: W2 (the up rows); qkv: the bias
+    const uint16_t *norm;  // RMSNorm gain [K], or null
+    float *y;              // user output (final op) and user old y (LAY_YEXT)
+    uint32_t xoff, xld;    // tagged x, unless LAY_XEXT (then the op descriptor's x)
+    uint32_t yoff, yld;    // tagged old y of an accumulate, unless LAY_YEXT
+    uint32_t ldy;
+    uint32_t tag;          // this op's tagged output [M][N]
+    float eps;
+    uint32_t flags;
+};
+static_assert(sizeof(LayOp) == 64, "one 64-byte scalar load");
+
+// Compute wave w's share of an op class.  It loads TA tiles: block steps js .. of row tile
+// rt, the first ks of them; gate|up's remaining TA - ks continue at block 0 of row tile
+// rt + 1.  It multiplies loaded tiles [kb, ke) (a wave with fewer block steps than TA loads
+// its neighbour's first ones and skips them), and its partial sums go to slot w.
+struct LRange {
+    uint32_t js, kb, ke, ks, rt;
+};
+template <int C, int M>
+__host__ __device__ constexpr LRange lay_range(uint32_t w) {
+    typedef LCls<C, M> L;
+    if (L::GATED) {  // tiles [TA w, TA (w + 1)) of the RT KBS, row tile by row tile
+        const uint32_t t0 = L::TA * w, rt = t0 / L::KBS, js = t0 - rt * L::KBS;
+        const uint32_t ks = L::KBS - js < L::TA ? L::KBS - js : L::TA;
+        return LRange{js, 0, L::TA, ks, rt};
+    }
+    const uint32_t j0 = w * L::KBS / LAY_CW, j1 = (w + 1) * L::KBS / LAY_CW;
+    const uint32_t js = j0 < L::KBS - L::TA ? j0 : L::KBS - L::TA;
+    return LRange{js, j0 - js, j1 - js, L::TA, 0};
+}
+
+// Per-lane constants of an op class: byte offsets of the lane's weight chunk at its first
+// block step (woff: row tile rt; woff2: block 0 of row tile rt + 1, gate|up) and of its
+// first B chunk in the staging.
+struct LLane {
+    uint32_t woff, woff2, boff;
+};
+template <int C, int M>
+__device__ __forceinline__ uint32_t lay_row(uint32_t nr, uint32_t lane, uint32_t rt) {
+    typedef LCls<C, M> L;
+    const uint32_t a = lane & 15;
+    // gate|up: rows 0-7 of a row tile are the gate rows of features 8 rt + a, rows 8-15 the
+    // same features' up rows; otherwise row a is feature a / S over segment a % S.
+    const uint32_t f = L::GATED ? rt * 8 + (a & 7) : a >> L::LS;
+    return f < nr ? f : nr - 1;  // padding rows repeat the last feature (their sums are not used)
+}
+template <int C, int M>
+__device__ __forceinline__ LLane lay_lane(uint32_t r0, uint32_t nr, uint32_t lane, const LRange &r, uint32_t plane) {
+    typedef LCls<C, M> L;
+    const uint32_t a = lane & 15, q = lane >> 4;
+    const uint32_t k = (L::GATED ? 0u : (a & (L::S - 1)) * L::KBS * 32) + q * 8;
+    LLane ll;
+    ll.woff = ((r0 + lay_row<C, M>(nr, lane, r.rt)) * L::K + k + r.js * 32) * 2;
+    ll.woff2 = L::GATED ? ((r0 + lay_row<C, M>(nr, lane, r.rt + 1 < L::RT ? r.rt + 1 : r.rt)) * L::K + k) * 2 : ll.woff;
+    // B column c: x row m, segment s, half h (c = 2 (m S + s) + h); columns past M S read row 0.
+    const uint32_t c = lane & 15, cc = c >> 1, h = c & 1, s = cc & (L::S - 1);
+    uint32_t m = cc >> L::LS;
+    m = m < static_cast<uint32_t>(M) ? m : 0u;
+    ll.boff = (h * plane + m * L::K + s * L::KBS * 32 + q * 8 + r.js * 32) * 2;
+    return ll;
+}
+
+// Workgroup state shared by the op steps.
+template <int WT, int M>
+struct LayCtx {
+    static constexpr uint32_t PLANE = M * LAY_I + 64;  // hi / lo planes of the x staging (elements)
+    uint16_t *xs;    // [2][PLANE] staged x of the current op
+    float *part[4];  // per class: [row tile][x row][virtual row][8 slots]
+    float *ssw[4];   // per norm class: [M][8 slots] sums of x^2
+    LLane ln[4];
+    uint32_t r0[4], nr[4];
+    uint32_t tid, lane, w, parity;
+    bool up;         // gate|up: the lane's tile rows are W2's
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t *tags;
+    uint32_t *sync;
+    bool gave_up;
+};
+
+// Weight tiles [K0, K1) of an op of class C (weights w, and w2 for gate|up's up rows) for wave
+// W into An (nontemporal loads).
+template <int WT, int M, int C, int W, uint32_t K0, uint32_t K1, int NN>
+__device__ __forceinline__ void lay_tiles_w(const LayCtx<WT, M> &cx, const uint16_t *w, const uint16_t *w2,
+                                            u32x4 (&An)[NN]) {
+    typedef LCls<C, M> L;
+    static_assert(K1 <= L::TA && L::TA <= NN, "tile registers");
+    constexpr LRange r = lay_range<C, M>(W);
+    const uint16_t *base = (L::GATED && cx.up) ? w2 : w;
+    const char *p = reinterpret_cast<const char *>(base) + cx.ln[C].woff;
+    const char *p2 = reinterpret_cast<const char *>(base) + cx.ln[C].woff2;
+#pragma unroll
+    for (uint32_t k = K0; k < K1; k++) {
+        const char *a = k < r.ks ? p + k * 64 : p2 + (k - r.ks) * 64;
+        An[k] = __builtin_nontemporal_load(reinterpret_cast<gw_cp>(reinterpret_cast<uintptr_t>(a)));
+    }
+}
+// Tiles [K0, K1) of the op with packed descriptor d, for the calling wave.
+template <int WT, int M, int C, uint32_t K0, uint32_t K1, int NN>
+__device__ __forceinline__ void lay_tiles(const LayCtx<WT, M> &cx, const LayOp &d, u32x4 (&An)[NN]) {
+    if constexpr (K0 >= K1) {
+        return;
+    } else if constexpr (!LCls<C, M>::GATED) {
+        lay_tiles_w<WT, M, C, 0, K0, K1>(cx, d.w, d.p2, An);  // one row tile: the lane offsets carry the range
+    } else {
+        switch (cx.w) {
+            case 0: lay_tiles_w<WT, M, C, 0, K0, K1>(cx, d.w, d.p2, An); break;
+            case 1: lay_tiles_w<WT, M, C, 1, K0, K1>(cx, d.w, d.p2, An); break;
+            case 2: lay_tiles_w<WT, M, C, 2, K0, K1>(cx, d.w, d.p2, An); break;
+            case 3: lay_tiles_w<WT, M, C, 3, K0, K1>(cx, d.w, d.p2, An); break;
+            case 4: lay_tiles_w<WT, M, C, 4, K0, K1>(cx, d.w, d.p2, An); break;
+            case 5: lay_tiles_w<WT, M, C, 5, K0, K1>(cx, d.w, d.p2, An); break;
+            default: lay_tiles_w<WT, M, C, 6, K0, K1>(cx, d.w, d.p2, An); break;
+        }
+    }
+}
+
+// Flush of one row tile's accumulator into slot `slot`: part[rt][m][v][slot].
+template <int M, int C>
+__device__ __forceinline__ void lay_flush(const f32x4 acc, float *part, uint32_t rt, uint32_t slot, uint32_t lane) {
+    typedef LCls<C, M> L;
+    float *pp = part + rt * (M * L::VR * 8) + slot;
+    const uint32_t c = lane & 15, qd = lane >> 4;
+    if constexpr (L::S == 1) {  // rows 4 qd + i, columns 2 m + h
+        const uint32_t m = c >> 1;
+        const float e0 = dpp_pair(acc[0]), e1 = dpp_pair(acc[1]), e2 = dpp_pair(acc[2]), e3 = dpp_pair(acc[3]);
+        if ((c & 1) == 0 && m < static_cast<uint32_t>(M)) {
+            float *q = pp + (m * L::VR + qd * 4) * 8;
+            q[0] = e0;
+            q[8] = e1;
+            q[16] = e2;
+            q[24] = e3;
+        }
+    } else if constexpr (L::S == 2) {  // rows 4 qd + i: virtual row 2 qd + i / 2, segment i % 2
+        const uint32_t sc = (c >> 1) & 1, m = c >> 2;
+        const float e0 = dpp_quad(sc ? acc[1] : acc[0]);
+        const float e1 = dpp_quad(sc ? acc[3] : acc[2]);
+        if ((c & 3) == 0 && m < static_cast<uint32_t>(M)) {
+            float *q = pp + (m * L::VR + 2 * qd) * 8;
+            q[0] = e0;
+            q[8] = e1;
+        }
+    } else {  // S == 4: rows 4 qd + i: virtual row qd, segment i
+        const uint32_t sc = (c >> 1) & 3, m = c >> 3;
+        const float e = dpp_oct(sc == 0 ? acc[0] : sc == 1 ? acc[1] : sc == 2 ? acc[2] : acc[3]);
+        if ((c & 7) == 0 && m < static_cast<uint32_t>(M)) pp[(m * L::VR + qd) * 8] = e;
+    }
+}
+
+// Compute wave W's MFMAs of an op of class C (loaded tiles [kb, ke) of A, B from the
+// staging) and the flush of its partial sums into slot W of its row tile(s).
+template <int WT, int M, int C, int W, int NA>
+__device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A)[NA]) {
+    typedef LCls<C, M> L;
+    constexpr LRange r = lay_range<C, M>(W);
+    const char *bp = reinterpret_cast<const char *>(cx.xs) + cx.ln[C].boff;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;
+#pragma unroll
+    for (uint32_t k = r.kb; k < r.ke; k++) {  // block js + k of row tile rt, or k - ks of rt + 1
+        const u32x4 bv = *reinterpret_cast<const u32x4 *>(
+            k < r.ks ? bp + k * 64 : bp + (static_cast<int>(k - r.ks) - static_cast<int>(r.js)) * 64);
+        if (k < r.ks) acc = mfma16<WT>(A[k], bv, acc);
+        else acc2 = mfma16<WT>(A[k], bv, acc2);
+    }
+    lay_flush<M, C>(acc, cx.part[C], r.rt, W, cx.lane);
+    if constexpr (r.ks < L::TA) lay_flush<M, C>(acc2, cx.part[C], r.rt + 1, W, cx.lane);
+}
+
+// One op of class C (descriptor d; ops[i] holds its full descriptor for an external x): A
+// holds its weight tiles.  `issue` requests this op's share of later ops' weight tiles, right
+// behind its activations: they land while this op computes and waits.
+template <int WT, int M, int C, int NA, class ISSUE>
+__device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restrict__ ops, uint32_t i, const LayOp &d,
+                                         const u32x4 (&A)[NA], ISSUE &&issue) {
+    typedef LCls<C, M> L;
+    const uint32_t tid = cx.tid, lane = cx.lane;
+    const uint32_t r0 = cx.r0[C], nr = cx.nr[C];
+    const bool xext = (d.flags & LAY_XEXT) != 0;
+
+    // Activations: chunk e = tid + 448 r is 4 k of x row e / K4.
+    u32x4 xv[L::XR];
+    u32x2 gv[L::XR];
+#pragma unroll
+    for (uint32_t r = 0; r < L::XR; r++) {
+        const uint32_t e = tid + 448 * r;
+        const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+        const bool ok = e < L::NCH;
+        if (!xext) {
+            xv[r] = ldtag4(cx.rsrc, ok ? (d.xoff + m * d.xld + k) * 4u : 0xFFFFFFF0u);
+        } else {  // x from the user buffer (the sequence's first op)
+            const SeqOp &o = ops[i];
+            xv[r] = u32x4{0u, 0u, 0u, 0u};
+            if (ok) {
+                const size_t off = static_cast<size_t>(m) * o.ldx + k;
+                if (o.xt == DT_F32) {
+                    xv[r] = gld(reinterpret_cast<const u32x4 *>(static_cast<const float *>(o.x) + off));
+                } else {
+                    const u32x2 h = gld(reinterpret_cast<const u32x2 *>(static_cast<const uint16_t *>(o.x) + off));
+                    const bool bf = o.xt == DT_BF16;
+                    xv[r] = u32x4{__float_as_uint(bf ? dec_lo<DT_BF16>(h.x) : dec_lo<DT_F16>(h.x)),
+                                  __float_as_uint(bf ? dec_hi<DT_BF16>(h.x) : dec_hi<DT_F16>(h.x)),
+                                  __float_as_uint(bf ? dec_lo<DT_BF16>(h.y) : dec_lo<DT_F16>(h.y)),
+                                  __float_as_uint(bf ? dec_hi<DT_BF16>(h.y) : dec_hi<DT_F16>(h.y))};
+                }
+            }
+        }
+        if constexpr (L::NORM) gv[r] = gld(reinterpret_cast<const u32x2 *>(d.norm + (ok ? k : 0u)));
+    }
+    // Output lane tid: feature r0 + of, x row om.  Bias and old y requested now.
+    const uint32_t of = tid / M, om = tid - of * M;
+    const bool live = of < nr;
+    const uint32_t n = r0 + (live ? of : 0u);
+    uint32_t braw = 0, yw = 0;
+    if constexpr (L::BIAS) braw = gld(d.p2 + n);
+    if constexpr (L::ACC) {
+        if (!(d.flags & LAY_YEXT)) yw = ldtag1(cx.rsrc, (d.yoff + om * d.yld + n) * 4u);
+        else yw = gld(reinterpret_cast<const uint32_t *>(d.y) + static_cast<size_t>(om) * d.ldy + n);
+    }
+    // Later ops' weight tiles, right behind the activations.
+    issue();
+
+    // Wait for the activations; stale chunks are requested again, all at once per round.
+    if (!xext) {
+        uint32_t stale = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < L::XR; r++)
+            if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
+        uint32_t spins = 0;
+        while (stale && !cx.gave_up) {
+            if (++spins > SPIN_LIMIT) {
+                cx.gave_up = true;
+                raise_flag(cx.sync, SYNC_TIMEOUT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (uint32_t r = 0; r < L::XR; r++) {
+                if ((stale >> r) & 1u) {
+                    const uint32_t e = tid + 448 * r;
+                    const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+                    xv[r] = ldtag4(cx.rsrc, (d.xoff + m * d.xld + k) * 4u);
+                }
+            }
+            stale = 0;
+#pragma unroll
+            for (uint32_t r = 0; r < L::XR; r++)
+                if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
+        }
+    }
+    // Convert into the staging: tag bit cleared, x^2 summed per row, gain applied, split
+    // into hi + lo halves of the weights' type.
+    const uint32_t clear = xext ? ~0u : ~1u;
+    float ss[M];
+#pragma unroll
+    for (int mm = 0; mm < M; mm++) ss[mm] = 0.0f;
+    bool range_ok = true;
+#pragma unroll
+    for (uint32_t r = 0; r < L::XR; r++) {
+        const uint32_t e = tid + 448 * r;
+        if (e < L::NCH) {
+            const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+            float x[4];
+            x[0] = __uint_as_float(xv[r].x & clear);
+            x[1] = __uint_as_float(xv[r].y & clear);
+            x[2] = __uint_as_float(xv[r].z & clear);
+            x[3] = __uint_as_float(xv[r].w & clear);
+            if constexpr (L::NORM) {
+                float t = x[0] * x[0];
+                t = fmaf(x[1], x[1], t);
+                t = fmaf(x[2], x[2], t);
+                t = fmaf(x[3], x[3], t);
+#pragma unroll
+                for (int mm = 0; mm < M; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
+                x[0] *= dec_lo<WT>(gv[r].x);
+                x[1] *= dec_hi<WT>(gv[r].x);
+                x[2] *= dec_lo<WT>(gv[r].y);
+                x[3] *= dec_hi<WT>(gv[r].y);
+            }
+            if constexpr (WT == DT_F16)
+                range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
+            u32x2 hi, lo;
+            split4p<WT>(x, hi, lo);
+            *reinterpret_cast<u32x2 *>(cx.xs + m * L::K + k) = hi;
+            *reinterpret_cast<u32x2 *>(cx.xs + LayCtx<WT, M>::PLANE + m * L::K + k) = lo;
+        }
+    }
+    if (!range_ok) raise_flag(cx.sync, SYNC_RANGE);
+    if constexpr (L::NORM) {
+#pragma unroll
+        for (int mm = 0; mm < M; mm++) {
+            const float t = wave_sum(ss[mm]);
+            if (lane == 0) cx.ssw[C][mm * 8 + cx.w] = t;
+        }
+    }
+    __syncthreads();  // x staged
+
+    switch (cx.w) {  // the wave's tile range is compile-time in each case
+        case 0: lay_mma<WT, M, C, 0>(cx, A); break;
+        case 1: lay_mma<WT, M, C, 1>(cx, A); break;
+        case 2: lay_mma<WT, M, C, 2>(cx, A); break;
+        case 3: lay_mma<WT, M, C, 3>(cx, A); break;
+        case 4: lay_mma<WT, M, C, 4>(cx, A); break;
+        case 5: lay_mma<WT, M, C, 5>(cx, A); break;
+        default: lay_mma<WT, M, C, 6>(cx, A); break;
+    }
+    __syncthreads();  // every wave's partial sums are in LDS
+
+    // Outputs: the 8 slots summed in slot order, norm scale, epilogue, tagged store.
+    if (live) {
+        auto total = [&](uint32_t rt, uint32_t v) {
+            const float *p = cx.part[C] + ((rt * M + om) * L::VR + v) * 8;
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(p);
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
+            return ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
+        };
+        float a1, a2 = 0.0f;
+        if constexpr (L::GATED) {
+            a1 = total(of >> 3, of & 7);
+            a2 = total(of >> 3, 8 + (of & 7));
+        } else {
+            a1 = total(0, of);
+        }
+        if constexpr (L::NORM) {
+            const float *sp = cx.ssw[C] + om * 8;
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(sp);
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(sp + 4);
+            const float t = ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
+            const float scale = 1.0f / sqrtf(t / static_cast<float>(L::K) + d.eps);
+            a1 *= scale;
+            a2 *= scale;
+        }
+        float bias = 0.0f;
+        if constexpr (L::BIAS) {
+            asm volatile("" : "+v"(braw));
+            bias = dec1<WT>(static_cast<uint16_t>(braw));
+        }
+        float v = epilogue(a1, a2, bias, L::FLAGS);
+        if constexpr (L::ACC) {
+            if (!(d.flags & LAY_YEXT)) {
+                const uint32_t yoff = (d.yoff + om * d.yld + n) * 4u;
+                uint32_t spins = 0;
+                while ((yw & 1u) != cx.parity && !cx.gave_up) {
+                    if (++spins > SPIN_LIMIT) {
+                        cx.gave_up = true;
+                        raise_flag(cx.sync, SYNC_TIMEOUT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    yw = ldtag1(cx.rsrc, yoff);
+                }
+                v += untag(yw);
+            } else {
+                v += __uint_as_float(yw);
+            }
+        }
+        st_tag(cx.tags + d.tag + om * L::N + n, v, cx.parity);
+        if (d.flags & LAY_FINAL)
+            *reinterpret_cast<__attribute__((address_space(1))) float *>(
+                reinterpret_cast<uintptr_t>(d.y + static_cast<size_t>(om) * d.ldy + n)) = v;
+    }
+}
+
+// The kernel: n_ops = 4 L ops in the layer pattern (the host checks shapes, flags and G);
+// their packed descriptors follow the n_ops op descriptors.
+template <int WT, int M>
+__global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
+                                                           uint32_t *sync, const uint32_t *tags, uint32_t tag_bytes) {
+    typedef LayCtx<WT, M> X;
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2 * X::PLANE];
+    __shared__ __attribute__((aligned(16))) float p_qkv[LCls<LC_QKV, M>::PART];
+    __shared__ __attribute__((aligned(16))) float p_o[LCls<LC_O, M>::PART];
+    __shared__ __attribute__((aligned(16))) float p_gu[LCls<LC_GU, M>::PART];
+    __shared__ __attribute__((aligned(16))) float p_d[LCls<LC_DOWN, M>::PART];
+    __shared__ __attribute__((aligned(16))) float s_qkv[M * 8];
+    __shared__ __attribute__((aligned(16))) float s_gu[M * 8];
+    const LayOp *__restrict__ lops = reinterpret_cast<const LayOp *>(ops + n_ops);
+
+    X cx;
+    cx.xs = xs;
+    cx.part[LC_QKV] = p_qkv;
+    cx.part[LC_O] = p_o;
+    cx.part[LC_GU] = p_gu;
+    cx.part[LC_DOWN] = p_d;
+    cx.ssw[LC_QKV] = s_qkv;
+    cx.ssw[LC_GU] = s_gu;
+    cx.ssw[LC_O] = s_qkv;
+    cx.ssw[LC_DOWN] = s_gu;
+    cx.tid = threadIdx.x;
+    cx.lane = cx.tid & 63;
+    cx.w = __builtin_amdgcn_readfirstlane(cx.tid >> 6);
+    cx.sync = sync;
+    cx.tags = const_cast<uint32_t *>(tags);
+    cx.gave_up = false;
+    const uint32_t g = blockIdx.x, G = gridDim.x;
+    const uint32_t Ns[4] = {LAY_QKV, LAY_H, LAY_I, LAY_H};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        cx.r0[c] = static_cast<uint32_t>(static_cast<uint64_t>(g) * Ns[c] / G);
+        cx.nr[c] = static_cast<uint32_t>(static_cast<uint64_t>(g + 1) * Ns[c] / G) - cx.r0[c];
+    }
+    {
+        LRange rq{}, ro{}, rg{}, rd{};
+        switch (cx.w) {
+#define LAY_RANGES(W)                      \
+    case W:                                \
+        rq = lay_range<LC_QKV, M>(W);      \
+        ro = lay_range<LC_O, M>(W);        \
+        rg = lay_range<LC_GU, M>(W);       \
+        rd = lay_range<LC_DOWN, M>(W);     \
+        break;
+            LAY_RANGES(0) LAY_RANGES(1) LAY_RANGES(2) LAY_RANGES(3) LAY_RANGES(4) LAY_RANGES(5)
+            default: LAY_RANGES(6)
+#undef LAY_RANGES
+        }
+        cx.ln[LC_QKV] = lay_lane<LC_QKV, M>(cx.r0[LC_QKV], cx.nr[LC_QKV], cx.lane, rq, X::PLANE);
+        cx.ln[LC_O] = lay_lane<LC_O, M>(cx.r0[LC_O], cx.nr[LC_O], cx.lane, ro, X::PLANE);
+        cx.ln[LC_GU] = lay_lane<LC_GU, M>(cx.r0[LC_GU], cx.nr[LC_GU], cx.lane, rg, X::PLANE);
+        cx.ln[LC_DOWN] = lay_lane<LC_DOWN, M>(cx.r0[LC_DOWN], cx.nr[LC_DOWN], cx.lane, rd, X::PLANE);
+        cx.up = (cx.lane & 15) >= 8;
+    }
+    // Slots no compute wave writes (slot 7, and gate|up's row tiles a wave does not reach) stay zero.
+    for (uint32_t e = cx.tid; e < LCls<LC_QKV, M>::PART; e += LAY_THREADS) p_qkv[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < LCls<LC_O, M>::PART; e += LAY_THREADS) p_o[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < LCls<LC_GU, M>::PART; e += LAY_THREADS) p_gu[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < LCls<LC_DOWN, M>::PART; e += LAY_THREADS) p_d[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < M * 8; e += LAY_THREADS) s_qkv[e] = s_gu[e] = 0.0f;
+    const uint32_t epoch = __hip_atomic_load(sync + SYNC_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    cx.parity = epoch & 1u;
+    cx.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(tags), 0, static_cast<int>(tag_bytes), BUF_DWORD3);
+
+    // Every class has its own tile registers.  A class's tiles for layer l + 1 are requested in
+    // batches over the three ops after its layer-l op, so each op requests about the same
+    // share of the layer's weight stream (a burst would hold up the loads and stores behind it):
+    //   op qkv(l):  gate|up(l) second third, down(l) first sixth
+    //   op o(l):    gate|up(l) last third,   down(l) second sixth
+    //   op gu(l):   down(l) rest,            qkv(l+1) first half
+    //   op down(l): gate|up(l+1) first third, qkv(l+1) second half, o(l+1)
+    typedef LCls<LC_QKV, M> LQ;
+    typedef LCls<LC_O, M> LO;
+    typedef LCls<LC_GU, M> LG;
+    typedef LCls<LC_DOWN, M> LD;
+    constexpr uint32_t G1 = LG::TA / 3, G2 = 2 * LG::TA / 3, D1 = LD::TA / 6, D2 = 2 * LD::TA / 6, Q1 = LQ::TA / 2;
+    u32x4 PQ[LQ::TA], PO[LO::TA], PG[LG::TA], PD[LD::TA];
+    const uint32_t L = n_ops / 4;
+    if (L > 0) {
+        lay_tiles<WT, M, LC_QKV, 0, LQ::TA>(cx, lops[0], PQ);
+        lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[1], PO);
+        lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[2], PG);
+    }
+    __syncthreads();
+    for (uint32_t l = 0; l < L; l++) {
+        // The last layer's requests for a next layer read layer 0's weights again (unused), so
+        // every op requests the same number of tiles.
+        const uint32_t i = 4 * l, nx = l + 1 < L ? i + 4 : 0;
+        lay_step<WT, M, LC_QKV>(cx, ops, i, lops[i], PQ, [&]() {
+            lay_tiles<WT, M, LC_GU, G1, G2>(cx, lops[i + 2], PG);
+            lay_tiles<WT, M, LC_DOWN, 0, D1>(cx, lops[i + 3], PD);
+        });
+        lay_step<WT, M, LC_O>(cx, ops, i + 1, lops[i + 1], PO, [&]() {
+            lay_tiles<WT, M, LC_GU, G2, LG::TA>(cx, lops[i + 2], PG);
+            lay_tiles<WT, M, LC_DOWN, D1, D2>(cx, lops[i + 3], PD);
+        });
+        lay_step<WT, M, LC_GU>(cx, ops, i + 2, lops[i + 2], PG, [&]() {
+            lay_tiles<WT, M, LC_DOWN, D2, LD::TA>(cx, lops[i + 3], PD);
+            lay_tiles<WT, M, LC_QKV, 0, Q1>(cx, lops[nx], PQ);
+        });
+        lay_step<WT, M, LC_DOWN>(cx, ops, i + 3, lops[i + 3], PD, [&]() {
+            lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[nx + 2], PG);
+            lay_tiles<WT, M, LC_QKV, Q1, LQ::TA>(cx, lops[nx], PQ);
+            lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[nx + 1], PO);
+        });
+    }
+    // The last workgroup out advances the epoch for the next run.
+    if (cx.tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(sync + SYNC_EXIT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == G - 1) {
+            __hip_atomic_store(sync + SYNC_EXIT, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(sync + SYNC_EPOCH, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+}  // namespace mt

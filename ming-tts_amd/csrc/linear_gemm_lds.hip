@@ -525,10 +525,10 @@ int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const int cus = device_cus();
     if (cus <= 0) return set_error(MT_EHIP, "gemm: cannot query the device");
-    const Tuning &tu = tuning();
-    TiledPlan p = tiled_plan(a.M, a.N, a.K, gated, cus, tu.gemm_tile, tu.gemm_splitk);
-    if (tu.gemm_stages >= 1) p.stages = tu.gemm_stages;
-    if (p.bm == 0) return set_error(MT_EINVAL, "gemm: tile shape %d does not apply to this linear", tu.gemm_tile);
+    const int tile = tuning().gemm_tile, splitk = tuning().gemm_splitk, stages_override = tuning().gemm_stages;
+    TiledPlan p = tiled_plan(a.M, a.N, a.K, gated, cus, tile, splitk);
+    if (stages_override >= 1) p.stages = stages_override;
+    if (p.bm == 0) return set_error(MT_EINVAL, "gemm: tile shape %d does not apply to this linear", tile);
     TiledArgs t;
     t.x = static_cast<const uint16_t *>(a.x);
     t.w = a.w;

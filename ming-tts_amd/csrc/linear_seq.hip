@@ -1,6 +1,6 @@
 // Host side of the persistent linear sequence (mt_seq_*) and its linear-only kernels; the
 // kernel itself is in seq_kernel.hpp.
-#include "seq_kernel.hpp"
+#include "layer_kernel.hpp"
 
 namespace mt {
 
@@ -13,6 +13,8 @@ struct SeqPlan {
     int groups = 0;
     int device = 0;
     seq_fn fn = nullptr;
+    bool layer = false;  // runs the decode-layer kernel (packed descriptors follow the ops)
+    int threads = SEQ_THREADS;
 };
 
 int seq_limits(int *groups_out, int *preferred_out) {
@@ -36,7 +38,7 @@ int seq_limits(int *groups_out, int *preferred_out) {
     return MT_OK;
 }
 
-int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out) {
+int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, bool layer, SeqPlan **out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(MT_EHIP, "mt_seq_create: hipGetDevice: %s", hipGetErrorString(e));
@@ -54,7 +56,11 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out) {
         if (ops[i].M != m_all) m_all = 0;
     bool attn = false;
     for (uint32_t i = 0; i < n_ops; i++) attn = attn || ops[i].kind == SEQ_ATTN;
-    if (attn) {
+    if (layer) {
+        p->fn = layer_kernel_fn(wt, m_all);
+        p->layer = true;
+        p->threads = LAY_THREADS;
+    } else if (attn) {
         p->fn = seq_attn_kernel(wt, m_all == 2);
     } else if (wt == DT_BF16) {
         p->fn = m_all == 1   ? seq_kernel<DT_BF16, 1, false>
@@ -65,7 +71,8 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out) {
     }
     p->groups = groups;
     p->tag_bytes = static_cast<uint32_t>((tag_words ? tag_words : 1) * 4);
-    e = hipMalloc(&p->d_ops, sizeof(SeqOp) * (n_ops ? n_ops : 1));
+    const size_t desc_bytes = (sizeof(SeqOp) + (p->layer ? sizeof(LayOp) : 0)) * (n_ops ? n_ops : 1);
+    e = hipMalloc(&p->d_ops, desc_bytes);
     if (e == hipSuccess) e = hipMalloc(&p->d_sync, SYNC_WORDS * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&p->d_tags, p->tag_bytes);
     if (e == hipSuccess) {
@@ -88,6 +95,27 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out) {
             }
         }
         e = hipMemcpy(p->d_ops, ops, sizeof(SeqOp) * n_ops, hipMemcpyHostToDevice);
+        if (e == hipSuccess && p->layer) {
+            // The decode-layer kernel's packed descriptors, right after the op descriptors.
+            std::vector<LayOp> lay(n_ops);
+            for (uint32_t i = 0; i < n_ops; i++) {
+                const SeqOp &o = ops[i];
+                LayOp &d = lay[i];
+                d.w = o.w;
+                d.p2 = (o.flags & F_SILU_GATE) ? o.w2 : o.bias;
+                d.norm = o.norm;
+                d.y = o.y;
+                d.xoff = o.xoff;
+                d.xld = o.xld;
+                d.yoff = o.yoff;
+                d.yld = o.yld;
+                d.ldy = o.ldy;
+                d.tag = static_cast<uint32_t>(o.tag - p->d_tags);
+                d.eps = o.eps;
+                d.flags = (o.xsrc < 0 ? LAY_XEXT : 0u) | (o.ysrc < 0 ? LAY_YEXT : 0u) | (o.final_out ? LAY_FINAL : 0u);
+            }
+            e = hipMemcpy(p->d_ops + n_ops, lay.data(), sizeof(LayOp) * n_ops, hipMemcpyHostToDevice);
+        }
     }
     // Tagged words start with parity 0 and the first run uses epoch 1 (parity 1), so no
     // stale word can pass for a current one.
@@ -114,9 +142,9 @@ int seq_run(SeqPlan *p, hipStream_t stream) {
     if (tuning().seq_launch == 1) {
         // Ordinary launch: the workgroups are co-resident only while nothing else occupies
         // the CUs; the bounded waits turn a shortfall into the timeout flag.
-        e = hipLaunchKernel(reinterpret_cast<const void *>(p->fn), dim3(p->groups), dim3(SEQ_THREADS), args, 0, stream);
+        e = hipLaunchKernel(reinterpret_cast<const void *>(p->fn), dim3(p->groups), dim3(p->threads), args, 0, stream);
     } else {
-        e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(p->fn), dim3(p->groups), dim3(SEQ_THREADS), args,
+        e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(p->fn), dim3(p->groups), dim3(p->threads), args,
                                        0, stream);
     }
     if (e != hipSuccess) return set_error(MT_EHIP, "mt_seq_run: launch: %s", hipGetErrorString(e));
@@ -135,6 +163,8 @@ int seq_check(SeqPlan *p) {
 }
 
 int seq_groups(const SeqPlan *p) { return p->groups; }
+
+int seq_kernel_kind(const SeqPlan *p) { return p->layer ? MT_SEQ_DECODE_LAYER : MT_SEQ_GENERAL; }
 
 void seq_destroy(SeqPlan *p) {
     if (!p) return;

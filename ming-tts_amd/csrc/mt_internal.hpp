@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <vector>
 
 #include "mingtts_hip.h"
@@ -16,16 +17,19 @@ int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3
 // hipGetLastError after a launch, as an ABI return code.
 int check_launch(const char *what);
 
-// Process-wide tuning (mt_set_tuning).
+// Process-wide tuning (mt_set_tuning).  Every field is read and written atomically
+// (relaxed), so host threads launching on distinct streams may call mt_set_tuning
+// concurrently; a change applies to calls that read the field after it.
 struct Tuning {
-    int gemv_rows_max = 8;
-    int gemv_lanes = 0;
-    int gemm_splitk = 0;
-    int gemm_tile = 0;
-    int gemm_stages = 0;
-    int gemv_mfma = 0;
-    int seq_groups = 0;
-    int seq_launch = 0;
+    std::atomic<int> gemv_rows_max{8};
+    std::atomic<int> gemv_lanes{0};
+    std::atomic<int> gemm_splitk{0};
+    std::atomic<int> gemm_tile{0};
+    std::atomic<int> gemm_stages{0};
+    std::atomic<int> gemv_mfma{0};
+    std::atomic<int> seq_groups{0};
+    std::atomic<int> seq_launch{0};
+    std::atomic<int> seq_layer{0};
 };
 Tuning &tuning();
 
@@ -77,16 +81,29 @@ constexpr int SEQ_OPS_MAX = 128;   // ops of a sequence (their descriptors are s
 constexpr int SEQ_CW = 8;          // waves per workgroup, each computing a share of every op
 constexpr int SEQ_TA = 12;         // MFMA tiles of one op a wave holds in registers
 constexpr int SEQ_GMAX = 2048;     // K of an op with an RMSNorm gain (staged in LDS)
+// The Qwen2-0.5B decode layer (Weights.swift:81-92) the decode-layer kernel is specialised
+// for, and the workgroup counts its tiling takes.
+constexpr uint32_t LAY_H = 896, LAY_QKV = 1152, LAY_I = 4864;
+constexpr int LAY_GMIN = 224, LAY_GMAX = 256;
 // Workgroup count of the persistent kernel on the current device.
 int seq_limits(int *groups, int *preferred);
 // Dataflow plan of a serial list of linears and attention items for `groups` workgroups
 // (host only; no HIP calls).
 int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp> &out, int &wt);
-int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, SeqPlan **out);
+// The general sequence kernel's limits on each linear's share at `groups` workgroups
+// (MT_ENOTSUP with the reason when one is exceeded).
+int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups);
+// Do the planned ops repeat the Qwen2-0.5B decode layer (qkv 1152 x 896 with bias and
+// RMSNorm, o 896 x 896 accumulating, gate|up 2 x 4864 x 896 SiLU-gate with RMSNorm, down
+// 896 x 4864 accumulating) at one M of 1, 2 or 4, with `groups` in the decode-layer
+// kernel's range?
+bool layer_pattern(const SeqOp *ops, uint32_t n, int groups);
+int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, bool layer, SeqPlan **out);
 int seq_run(SeqPlan *p, hipStream_t stream);
 int seq_check(SeqPlan *p);
 void seq_destroy(SeqPlan *p);
 int seq_groups(const SeqPlan *p);
+int seq_kernel_kind(const SeqPlan *p);
 
 int launch_rope_cache(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
                       const uint32_t *pos_arr, void *kc, void *vc, int ct, uint32_t cache_len,

@@ -206,6 +206,10 @@ __device__ __forceinline__ void tile_loads(const SeqOp &o, const SeqTiles &s, co
             p = row_of(wt.rt0 + 1u, rok);
         }
     }
+    // Every register of A is written, so A carries no value of an earlier op and keeps one
+    // register assignment across the op loop (no copy, no wait for the loads at its end).
+#pragma unroll
+    for (int k = NL; k < TA; k++) A[k] = u32x4{0u, 0u, 0u, 0u};
 }
 
 // Sum over aligned lane pairs / quads of a wave (fixed order).
@@ -586,20 +590,23 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(tags), 0, static_cast<int>(tag_bytes), BUF_DWORD3);
     bool gave_up = false;
     u32x4 gr[CGCH];
-    u32x4 A[TA];  // this op's weight tiles
+    // Weight tiles of two consecutive ops: even ops multiply P0 while P1 receives the next
+    // op's tiles, odd ops the other way round.  The loop runs two ops per iteration, so no
+    // register copy (which would wait for the next op's tiles to land) ends an op.
+    u32x4 P0[TA], P1[TA];
 
     if (n_ops > 0) {
         gain_request(sdesc[0], true, gr);
-        tile_loads<TA>(sdesc[0], stile[0], swt[0][w], A);
+        tile_loads<TA>(sdesc[0], stile[0], swt[0][w], P0);
         gain_store(sdesc[0], gr, gbuf[0]);
         __syncthreads();
     }
-    for (uint32_t i = 0; i < n_ops; i++) {
+    // One op: A holds its weight tiles; An receives the next op's.
+    auto run_op = [&](uint32_t i, const u32x4 (&A)[TA], u32x4 (&An)[TA]) __attribute__((always_inline)) {
         const int b = i & 1;
         const SeqOp o = sdesc[i];  // by value: read once, kept in registers
         const SeqTiles s = stile[i];
         const WaveTiles wt = swt[i][w];
-        u32x4 An[TA];  // the next op's weight tiles
         if (ATTN && o.kind == SEQ_ATTN) {
             // Decode attention: items (row, head) go to workgroups g, g + G, ...; then every
             // workgroup requests the next op's gain and weight tiles as a linear would.
@@ -894,8 +901,10 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                         reinterpret_cast<uintptr_t>(o.y + static_cast<size_t>(om) * o.ldy + n)) = v;
             }
         }
-#pragma unroll
-        for (int k = 0; k < TA; k++) A[k] = An[k];
+    };
+    for (uint32_t i = 0; i < n_ops; i += 2) {
+        run_op(i, P0, P1);
+        if (i + 1 < n_ops) run_op(i + 1, P1, P0);
     }
     // The last workgroup out advances the epoch for the next run.
     if (threadIdx.x == 0) {
@@ -912,5 +921,7 @@ typedef void (*seq_fn)(const SeqOp *, uint32_t, uint32_t *, const uint32_t *, ui
 // The kernel of a plan with attention items (linear_seq_attn.hip): weights wt, specialised
 // for two rows when m2.
 seq_fn seq_attn_kernel(int wt, bool m2);
+// The decode-layer kernel (linear_layer.hip) for weights wt at M rows (1, 2 or 4), or null.
+seq_fn layer_kernel_fn(int wt, uint32_t M);
 
 }  // namespace mt

@@ -122,36 +122,6 @@ int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp
             yv[i] = View{reinterpret_cast<const char *>(o.y), static_cast<uint64_t>(p.ldy) * 4, static_cast<uint64_t>(p.N) * 4, p.M};
             if (wt < 0) wt = o.wt;
             if (o.wt != wt) return set_error(MT_EINVAL, "mt_seq_create: op %u: every op of a sequence must share the weight type", i);
-            if (o.norm && p.K > static_cast<uint32_t>(SEQ_GMAX))
-                return set_error(MT_ENOTSUP, "mt_seq_create: op %u: an RMSNorm op takes K <= %d, got %u", i, SEQ_GMAX, p.K);
-            // The op's activations are staged whole in the workgroup's LDS (M * K <= XLDS);
-            // every workgroup's share of the op at most RMAX features and its partial sums
-            // (virtual rows x M per compute wave) within the LDS slice.
-            if (static_cast<uint64_t>(p.M) * p.K > static_cast<uint64_t>(SEQ_XLDS))
-                return set_error(MT_ENOTSUP, "mt_seq_create: op %u: M * K = %u exceeds the %d activations a workgroup stages",
-                                 i, p.M * p.K, SEQ_XLDS);
-            for (int g = 0; g < groups; g++) {
-                const SeqTiles t = seq_tiles(p.N, p.K, p.M, (p.flags & MT_SILU_GATE) != 0, g, groups);
-                const uint32_t per_wave = (t.T + SEQ_CW - 1) / SEQ_CW;
-                // A wave's contiguous tile range may span at most two row tiles.
-                uint32_t span = 1;
-                for (int w = 0; w < SEQ_CW; w++) {
-                    const uint32_t t0 = seq_tile_begin(t.T, w, SEQ_CW), t1 = seq_tile_begin(t.T, w + 1, SEQ_CW);
-                    if (t1 > t0 && t.KBs) span = std::max(span, (t1 - 1) / t.KBs - t0 / t.KBs + 1);
-                }
-                if (span > 2)
-                    return set_error(MT_ENOTSUP,
-                                     "mt_seq_create: op %u: a wave's share of the tiles spans %u row tiles of 16 weight "
-                                     "rows (K = %u is too short for the sequence kernel's limit of 2)",
-                                     i, span, p.K);
-                if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || t.V * p.M > static_cast<uint32_t>(SEQ_PARTW) ||
-                    per_wave > static_cast<uint32_t>(SEQ_TA))
-                    return set_error(MT_ENOTSUP,
-                                     "mt_seq_create: op %u: a workgroup's share (%u features, %u partial sums at M = %u, %u "
-                                     "MFMA tiles per compute wave) exceeds the sequence kernel's limits (%d features, %d "
-                                     "partial sums, %d tiles)",
-                                     i, t.nr, t.V * p.M, p.M, per_wave, SEQ_RMAX, SEQ_PARTW, SEQ_TA);
-            }
             d.kind = SEQ_LINEAR;
             d.x = o.x;
             d.xt = o.xt;
@@ -245,6 +215,67 @@ int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp
         }
     }
     return MT_OK;
+}
+
+int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups) {
+    for (uint32_t i = 0; i < n; i++) {
+        if (items[i].kind != MT_SEQ_LINEAR) continue;
+        const mt_linear_op &o = items[i].linear;
+        const mt_gemv_params &p = o.p;
+        if (o.norm && p.K > static_cast<uint32_t>(SEQ_GMAX))
+            return set_error(MT_ENOTSUP, "mt_seq_create: op %u: an RMSNorm op takes K <= %d, got %u", i, SEQ_GMAX, p.K);
+        // The op's activations are staged whole in the workgroup's LDS (M * K <= XLDS);
+        // every workgroup's share of the op at most RMAX features and its partial sums
+        // (virtual rows x M per compute wave) within the LDS slice.
+        if (static_cast<uint64_t>(p.M) * p.K > static_cast<uint64_t>(SEQ_XLDS))
+            return set_error(MT_ENOTSUP, "mt_seq_create: op %u: M * K = %u exceeds the %d activations a workgroup stages",
+                             i, p.M * p.K, SEQ_XLDS);
+        for (int g = 0; g < groups; g++) {
+            const SeqTiles t = seq_tiles(p.N, p.K, p.M, (p.flags & MT_SILU_GATE) != 0, g, groups);
+            const uint32_t per_wave = (t.T + SEQ_CW - 1) / SEQ_CW;
+            // A wave's contiguous tile range may span at most two row tiles.
+            uint32_t span = 1;
+            for (int w = 0; w < SEQ_CW; w++) {
+                const uint32_t t0 = seq_tile_begin(t.T, w, SEQ_CW), t1 = seq_tile_begin(t.T, w + 1, SEQ_CW);
+                if (t1 > t0 && t.KBs) span = std::max(span, (t1 - 1) / t.KBs - t0 / t.KBs + 1);
+            }
+            if (span > 2)
+                return set_error(MT_ENOTSUP,
+                                 "mt_seq_create: op %u: a wave's share of the tiles spans %u row tiles of 16 weight "
+                                 "rows (K = %u is too short for the sequence kernel's limit of 2)",
+                                 i, span, p.K);
+            if (t.nr > static_cast<uint32_t>(SEQ_RMAX) || t.V * p.M > static_cast<uint32_t>(SEQ_PARTW) ||
+                per_wave > static_cast<uint32_t>(SEQ_TA))
+                return set_error(MT_ENOTSUP,
+                                 "mt_seq_create: op %u: a workgroup's share (%u features, %u partial sums at M = %u, %u "
+                                 "MFMA tiles per compute wave) exceeds the sequence kernel's limits (%d features, %d "
+                                 "partial sums, %d tiles)",
+                                 i, t.nr, t.V * p.M, p.M, per_wave, SEQ_RMAX, SEQ_PARTW, SEQ_TA);
+        }
+    }
+    return MT_OK;
+}
+
+bool layer_pattern(const SeqOp *ops, uint32_t n, int groups) {
+    if (n == 0 || n % 4 || groups < LAY_GMIN || groups > LAY_GMAX) return false;
+    const uint32_t M = ops[0].M;
+    if (M != 1 && M != 2 && M != 4) return false;
+    struct Want {
+        uint32_t N, K, flags;
+        bool norm;
+    };
+    const Want want[4] = {{LAY_QKV, LAY_H, F_BIAS, true},
+                          {LAY_H, LAY_H, F_ACCUM, false},
+                          {LAY_I, LAY_H, F_SILU_GATE, true},
+                          {LAY_H, LAY_I, F_ACCUM, false}};
+    for (uint32_t i = 0; i < n; i++) {
+        const SeqOp &o = ops[i];
+        const Want &c = want[i % 4];
+        if (o.kind != SEQ_LINEAR || o.M != M || o.N != c.N || o.K != c.K || o.flags != c.flags ||
+            (o.norm != nullptr) != c.norm || ((o.flags & F_BIAS) != 0) != (o.bias != nullptr))
+            return false;
+    }
+    return true;
 }
 
 }  // namespace mt

@@ -23,13 +23,14 @@ F32, F16, BF16 = 0, 1, 2
 OK, EHIP, ENOMEM, EINVAL, ERANGE, ENOTSUP = 0, -5, -12, -22, -34, -95
 KERNEL_GEMV, KERNEL_GEMM = 1, 2
 (TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS, TUNE_SEQ_LAUNCH, TUNE_GEMM_TILE,
- TUNE_GEMM_STAGES, TUNE_GEMV_MFMA) = 1, 2, 3, 4, 5, 6, 7, 8
+ TUNE_GEMM_STAGES, TUNE_GEMV_MFMA, TUNE_SEQ_LAYER) = 1, 2, 3, 4, 5, 6, 7, 8, 9
+SEQ_GENERAL, SEQ_DECODE_LAYER = 0, 1
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
     "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
     "mt_seq_create_items", "mt_seq_run",
-    "mt_seq_destroy", "mt_seq_groups", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
+    "mt_seq_destroy", "mt_seq_groups", "mt_seq_kernel", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_rope_attention", "mt_dit_attention", "mt_dit_attention_linear", "mt_flow_assemble",
     "mt_flow_euler",
     "mt_upsample4", "mt_istft_frames", "mt_istft_emit", "mt_st_open", "mt_st_close", "mt_st_count", "mt_st_name", "mt_st_find", "mt_arena_create", "mt_arena_tensor",
@@ -123,6 +124,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_seq_destroy.restype = i32
     L.mt_seq_groups.argtypes = [vp]
     L.mt_seq_groups.restype = i32
+    L.mt_seq_kernel.argtypes = [vp]
+    L.mt_seq_kernel.restype = i32
     L.mt_seq_check.argtypes = [vp]
     L.mt_seq_check.restype = i32
     L.mt_rope_cache.argtypes = [vp, u32, u32, u32, u32, u32, vp, vp, i32, u32, vp, vp]
@@ -283,6 +286,12 @@ class Seq:
     @property
     def groups(self) -> int:
         return check(load().mt_seq_groups(self.handle))
+
+    @property
+    def kernel(self) -> int:
+        """SEQ_DECODE_LAYER when the plan runs the kernel specialised for Qwen2-0.5B decode
+        layers, else SEQ_GENERAL."""
+        return check(load().mt_seq_kernel(self.handle))
 
     def close(self) -> None:
         if self.handle:

@@ -92,6 +92,47 @@ def test_decode_chain_matches_fp64_oracle(gpu, layers, M):
     seq.close()
 
 
+@pytest.mark.parametrize("layers,M", [(24, 2), (4, 1), (3, 4)])
+def test_decode_layer_kernel_matches_general_kernel(gpu, layers, M):
+    """A plan that repeats the Qwen2-0.5B decode layer runs the kernel specialised for its
+    shapes; MT_TUNE_SEQ_LAYER = 1 runs the same plan on the general sequence kernel.  Each is
+    bit-exact from run to run; they split K differently, so they agree to fp32 rounding, and
+    both meet the fp64 oracle chain.  (M = 4, the VAE stack's rows, exceeds the general
+    kernel's activation staging at K = 4864: there the oracle alone is the reference.)"""
+    ws, x0 = make_stack(layers, M, 31 + M, gpu)
+    resid, qkv, mlp = buffers(M, x0, gpu)
+    ops = chain_ops(ws, M, resid, qkv, mlp)
+    outs = {}
+    for mode in ((0, 1) if M <= 2 else (0,)):
+        old = mt.set_tuning(mt.TUNE_SEQ_LAYER, mode)
+        try:
+            seq = mt.Seq(ops)
+        finally:
+            mt.set_tuning(mt.TUNE_SEQ_LAYER, old)
+        say(f"seq layers={layers} M={M} layer-kernel mode {mode} kernel {seq.kernel} groups {seq.groups}")
+        assert seq.kernel == (mt.SEQ_DECODE_LAYER if mode == 0 else mt.SEQ_GENERAL)
+        runs = []
+        for _ in range(2):
+            resid.copy_(torch.from_numpy(x0))
+            qkv.zero_()
+            mlp.zero_()
+            seq.run()
+            torch.cuda.synchronize()
+            runs.append([t.cpu().numpy().copy() for t in (resid, qkv, mlp)])
+        seq.check()
+        seq.close()
+        for a, b in zip(runs[0], runs[1]):
+            np.testing.assert_array_equal(a, b)
+        outs[mode] = runs[0]
+    want = oracle_chain(ws, x0, M)
+    for j, what in enumerate(("resid", "qkv", "mlp")):
+        g = outs[0][j]
+        assert np.all(np.isfinite(g)), what
+        assert O.normwise_rel_err(g, want[j]) <= 1e-3, what
+        if 1 in outs:
+            assert O.normwise_rel_err(g, outs[1][j].astype(np.float64)) <= 1e-5, what
+
+
 def test_seq_deterministic_and_equal_to_per_op_launches(gpu):
     """Re-runs of one plan are bit-identical; the 16 same ops as separate mt_linear launches
     (fp32 FMA dot products, another summation order) agree to fp32 rounding."""
