@@ -284,14 +284,12 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     const uint32_t of = tid / M, om = tid - of * M;
     const bool live = of < nr;
     const uint32_t n = r0 + (live ? of : 0u);
+    const bool yext = (d.flags & LAY_YEXT) != 0;
     uint32_t braw = 0, yw = 0;
     if constexpr (L::BIAS) braw = gld(d.p2 + n);
-    if constexpr (L::ACC) {
-        if (!(d.flags & LAY_YEXT)) yw = ldtag1(cx.rsrc, (d.yoff + om * d.yld + n) * 4u);
-        else yw = gld(reinterpret_cast<const uint32_t *>(d.y) + static_cast<size_t>(om) * d.ldy + n);
-    }
-    // Later ops' weight tiles, right behind the activations.
-    issue();
+    if constexpr (L::ACC)  // old y: a tagged word, or the user's y; one load either way (no branch)
+        yw = ld32(yext ? reinterpret_cast<const uint32_t *>(d.y) + static_cast<size_t>(om) * d.ldy + n
+                       : cx.tags + d.yoff + om * d.yld + n);
 
     // Wait for the activations; stale chunks are requested again, all at once per round.
     if (!xext) {
@@ -378,6 +376,11 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
         default: lay_mma<WT, M, C, 6>(cx, A); break;
     }
     __syncthreads();  // every wave's partial sums are in LDS
+    // The op's own loads (x, gain, bias, old y) have landed long before this point, and no
+    // other load is in flight: waiting for them here, where it costs nothing, spares a wait for
+    // a load whose value some lanes never use where its registers are next written (the next
+    // op's activation loads, behind this op's tile batch).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
     // Outputs: the 8 slots summed in slot order, norm scale, epilogue, tagged store.
     if (live) {
@@ -410,7 +413,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
         }
         float v = epilogue(a1, a2, bias, L::FLAGS);
         if constexpr (L::ACC) {
-            if (!(d.flags & LAY_YEXT)) {
+            if (!yext) {
                 const uint32_t yoff = (d.yoff + om * d.yld + n) * 4u;
                 uint32_t spins = 0;
                 while ((yw & 1u) != cx.parity && !cx.gave_up) {
@@ -422,16 +425,17 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
                     __builtin_amdgcn_s_sleep(1);
                     yw = ldtag1(cx.rsrc, yoff);
                 }
-                v += untag(yw);
-            } else {
-                v += __uint_as_float(yw);
             }
+            v += __uint_as_float(yext ? yw : yw & ~1u);
         }
         st_tag(cx.tags + d.tag + om * L::N + n, v, cx.parity);
         if (d.flags & LAY_FINAL)
             *reinterpret_cast<__attribute__((address_space(1))) float *>(
                 reinterpret_cast<uintptr_t>(d.y + static_cast<size_t>(om) * d.ldy + n)) = v;
     }
+    // Later ops' weight tiles, behind this op's output stores: they drain while the next op's
+    // activations are being produced by the other workgroups.
+    issue();
 }
 
 // The kernel: n_ops = 4 L ops in the layer pattern (the host checks shapes, flags and G);
@@ -522,25 +526,32 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
         lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[2], PG);
     }
     __syncthreads();
+    // Each op's packed descriptor is read one op ahead (scalar loads), so no op waits for
+    // its own.
+    LayOp dq = lops[0], dn;
     for (uint32_t l = 0; l < L; l++) {
         // The last layer's requests for a next layer read layer 0's weights again (unused), so
         // every op requests the same number of tiles.
         const uint32_t i = 4 * l, nx = l + 1 < L ? i + 4 : 0;
-        lay_step<WT, M, LC_QKV>(cx, ops, i, lops[i], PQ, [&]() {
+        dn = lops[i + 1];
+        lay_step<WT, M, LC_QKV>(cx, ops, i, dq, PQ, [&]() {
             lay_tiles<WT, M, LC_GU, G1, G2>(cx, lops[i + 2], PG);
             lay_tiles<WT, M, LC_DOWN, 0, D1>(cx, lops[i + 3], PD);
         });
-        lay_step<WT, M, LC_O>(cx, ops, i + 1, lops[i + 1], PO, [&]() {
-            lay_tiles<WT, M, LC_GU, G2, LG::TA>(cx, lops[i + 2], PG);
+        dq = lops[i + 2];
+        lay_step<WT, M, LC_O>(cx, ops, i + 1, dn, PO, [&]() {
+            lay_tiles<WT, M, LC_GU, G2, LG::TA>(cx, dq, PG);
             lay_tiles<WT, M, LC_DOWN, D1, D2>(cx, lops[i + 3], PD);
         });
-        lay_step<WT, M, LC_GU>(cx, ops, i + 2, lops[i + 2], PG, [&]() {
-            lay_tiles<WT, M, LC_DOWN, D2, LD::TA>(cx, lops[i + 3], PD);
+        dn = lops[i + 3];
+        lay_step<WT, M, LC_GU>(cx, ops, i + 2, dq, PG, [&]() {
+            lay_tiles<WT, M, LC_DOWN, D2, LD::TA>(cx, dn, PD);
             lay_tiles<WT, M, LC_QKV, 0, Q1>(cx, lops[nx], PQ);
         });
-        lay_step<WT, M, LC_DOWN>(cx, ops, i + 3, lops[i + 3], PD, [&]() {
+        dq = lops[nx];
+        lay_step<WT, M, LC_DOWN>(cx, ops, i + 3, dn, PD, [&]() {
             lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[nx + 2], PG);
-            lay_tiles<WT, M, LC_QKV, Q1, LQ::TA>(cx, lops[nx], PQ);
+            lay_tiles<WT, M, LC_QKV, Q1, LQ::TA>(cx, dq, PQ);
             lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[nx + 1], PO);
         });
     }
