@@ -53,16 +53,20 @@ uint64_t mto_lcg_fill(uint64_t state, float *out, int64_t n, float scale) {
     return state;
 }
 
-/* Engine.swift:432-453.  The stream's t-th draw (t = 1, 2, ...) hashes
- * seed + golden + t * golden, so pair j (draws 2j+1, 2j+2) is independent of
- * the others and the fill parallelises without changing a single bit. */
-static double mto_splitmix_u01(uint64_t seed, uint64_t t) {
+/* Engine.swift:432-453.  The stream's t-th draw (t = 1, 2, ...) is SplitMix64's
+ * output for the state seed + golden + t * golden (the reference starts its state
+ * at seed + golden), so pair j (draws 2j+1, 2j+2) is independent of the others and
+ * the fill parallelises without changing a single bit. */
+uint64_t mto_splitmix64(uint64_t seed, uint64_t t) {
     const uint64_t golden = 0x9E3779B97F4A7C15ULL;
     uint64_t z = seed + golden + t * golden;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
-    z ^= z >> 31;
-    return (double)(z >> 11) / 9007199254740992.0; /* 2^53 */
+    return z ^ (z >> 31);
+}
+
+static double mto_splitmix_u01(uint64_t seed, uint64_t t) {
+    return (double)(mto_splitmix64(seed, t) >> 11) / 9007199254740992.0; /* 2^53 */
 }
 
 void mto_gaussian_fill(uint64_t seed, float *out, int64_t n, float scale) {

@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.mto_lcg_fill.restype = u64
         L.mto_gaussian_fill.argtypes = [u64, vp, i64, f32]
         L.mto_gaussian_fill.restype = None
+        L.mto_splitmix64.argtypes = [u64, u64]
+        L.mto_splitmix64.restype = u64
         L.mto_bf16_bits.argtypes = [f32]
         L.mto_bf16_bits.restype = ctypes.c_uint16
         L.mto_f16_bits.argtypes = [f32]
@@ -89,6 +91,12 @@ class LCG:
         out = np.empty(n, np.float32)
         self.state = lib().mto_lcg_fill(self.state, _p(out), n, scale)
         return out
+
+
+def splitmix64(seed: int, t: int) -> int:
+    """The t-th 64-bit draw (t >= 1) of the SplitMix64 stream behind ``gaussian`` for ``seed``
+    (Engine.swift:432-441: state = seed + golden, then state += golden per draw)."""
+    return int(lib().mto_splitmix64(seed & 0xFFFFFFFFFFFFFFFF, t & 0xFFFFFFFFFFFFFFFF))
 
 
 def gaussian(seed: int, n: int, scale: float = 1.0) -> np.ndarray:

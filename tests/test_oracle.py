@@ -102,6 +102,37 @@ def test_lcg_is_the_affine_recurrence_and_uniform():
     assert 1442695040888963407 % 2 == 1 and (6364136223846793005 - 1) % 4 == 0
 
 
+PHI64 = 0x9E3779B97F4A7C15  # SplitMix64 state increment
+
+
+def test_splitmix64_matches_published_reference_outputs():
+    """SplitMix64 seeded with 1234567 (state += golden before each output) starts
+    6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431,
+    16408922859458223821 (the published reference outputs of Rosetta Code's
+    "Pseudo-random numbers/Splitmix64" task).  The reference's stream starts its state one
+    golden step later (Engine.swift:434), so its seed for that stream is 1234567 - golden."""
+    want = [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431,
+            16408922859458223821]
+    seed = (1234567 - PHI64) % 2**64
+    assert [O.splitmix64(seed, t) for t in range(1, 6)] == want
+
+
+def test_gaussian_pairs_are_box_muller_of_the_stream():
+    """Pair j of ``gaussian`` is Box-Muller of draws 2j+1 and 2j+2, each taken as its top 53
+    bits / 2^53 (Engine.swift:435-450): z0 = sqrt(-2 ln u1) cos(2 pi u2), z1 = ... sin, both
+    rounded to fp32, then scaled in fp32."""
+    seed = 11
+    z = O.gaussian(seed, 8)
+    zs = O.gaussian(seed, 8, 0.02)
+    for j in range(4):
+        u1 = max((O.splitmix64(seed, 2 * j + 1) >> 11) / 2.0**53, 1e-300)
+        u2 = (O.splitmix64(seed, 2 * j + 2) >> 11) / 2.0**53
+        r = np.sqrt(-2.0 * np.log(u1))
+        z0, z1 = np.float32(r * np.cos(2 * np.pi * u2)), np.float32(r * np.sin(2 * np.pi * u2))
+        assert z[2 * j] == z0 and z[2 * j + 1] == z1
+        assert zs[2 * j] == np.float32(z0 * np.float32(0.02)) and zs[2 * j + 1] == np.float32(z1 * np.float32(0.02))
+
+
 def test_gaussian_is_standard_normal_and_seeded():
     z = O.gaussian(0, 400000)
     assert scipy.stats.kstest(z.astype(np.float64), "norm").pvalue > 1e-3
