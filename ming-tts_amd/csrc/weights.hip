@@ -385,6 +385,17 @@ int mt_arena_create(const mt_st *st, mt_dtype convert_to, mt_arena **out) {
     return MT_OK;
 }
 
+// Does a BF16 entry's byte range hold exactly its shape's elements?  (A header whose shape
+// claims more than its data_offsets span would make the copies read past the tensor.)
+static bool bf16_bytes_match(const StFile::Entry &e) {
+    uint64_t elems = 1;
+    for (uint64_t d : e.shape) {
+        if (d != 0 && elems > UINT64_MAX / 2 / d) return false;
+        elems *= d;
+    }
+    return e.end - e.begin == elems * 2;
+}
+
 int mt_arena_tensor(mt_arena *arena, const char *const *names, uint32_t n_names, uint64_t *offset, uint64_t *count) {
     Arena *a = reinterpret_cast<Arena *>(arena);
     if (!a || !names || n_names == 0 || !offset) return set_error(MT_EINVAL, "mt_arena_tensor: null argument");
@@ -397,6 +408,9 @@ int mt_arena_tensor(mt_arena *arena, const char *const *names, uint32_t n_names,
         if (it == a->st->entries.end()) return set_error(MT_EINVAL, "missing tensor %s", names[i]);
         if (it->second.dtype != "BF16")
             return set_error(MT_EINVAL, "bad checkpoint: %s is %s, expected BF16", names[i], it->second.dtype.c_str());
+        if (!bf16_bytes_match(it->second))
+            return set_error(MT_EINVAL, "bad checkpoint: %s: data_offsets span %llu bytes, its shape needs another count",
+                             names[i], static_cast<unsigned long long>(it->second.end - it->second.begin));
         es.push_back(&it->second);
         total += it->second.end - it->second.begin;
     }
@@ -424,6 +438,10 @@ int mt_arena_padded(mt_arena *arena, const char *name, uint32_t n, uint32_t k, u
     const StFile::Entry &e = it->second;
     if (e.dtype != "BF16" || e.shape.size() != 2 || e.shape[0] != n || e.shape[1] != stored_k || stored_k > k)
         return set_error(MT_EINVAL, "bad checkpoint: %s is not BF16 [%u, %u] (or k %u < stored k)", name, n, stored_k, k);
+    if (!bf16_bytes_match(e))
+        return set_error(MT_EINVAL, "bad checkpoint: %s: data_offsets span %llu bytes, its shape [%u, %u] needs %llu",
+                         name, static_cast<unsigned long long>(e.end - e.begin), n, stored_k,
+                         static_cast<unsigned long long>(n) * stored_k * 2);
     const uint64_t off = place(*a, static_cast<uint64_t>(n) * k * 2);
     ArenaCopy c;
     c.dst = off;

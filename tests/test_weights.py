@@ -118,3 +118,22 @@ def test_arena_plan(tmp_path):
     assert "expected 16x16" in str(e.value)
     arena.close()
     st.close()
+
+
+def test_arena_refuses_a_shape_larger_than_its_byte_range(tmp_path):
+    """A header whose shape claims more bytes than its data_offsets span is refused by the
+    arena (the copies would read past the tensor, and past the mapping for the last one)."""
+    hdr = {"e.weight": {"dtype": "BF16", "shape": [4, 8], "data_offsets": [0, 32]},   # needs 64
+           "ok.weight": {"dtype": "BF16", "shape": [2, 4], "data_offsets": [32, 48]}}
+    p = _header_file(tmp_path / "lie.safetensors", json.dumps(hdr).encode(), b"\0" * 48)
+    st = mt.SafeTensors(p)
+    arena = mt.WeightArena(st)
+    with pytest.raises(mt.MingTTSError) as e:
+        arena.padded_linear("e", 4, 16, 8)
+    assert e.value.code == mt.EINVAL and "data_offsets span 32 bytes" in str(e.value)
+    with pytest.raises(mt.MingTTSError) as e:
+        arena.tensor("e.weight")
+    assert "data_offsets span 32 bytes" in str(e.value)
+    assert arena.tensor("ok.weight").count == 8      # a consistent entry still plans
+    arena.close()
+    st.close()
