@@ -2,10 +2,17 @@
  * mingtts_hip.h -- C ABI of the MI355X (gfx950) linear hot path of MingTTS.
  *
  * Every entry point takes caller-owned device pointers, enqueues work on the
- * given HIP stream and returns; the caller synchronises.  No entry point
- * allocates device memory on the call path except mt_seq_create (once, at plan
- * time).  Errors are returned, never raised: 0 on success, a negative code
- * otherwise, with a message in mt_last_error() (thread-local).
+ * given HIP stream and returns; the caller synchronises.  Device memory is
+ * allocated on the call path in two places only: mt_seq_create (the plan, once)
+ * and the split-K workspace of the linears (one per device and stream, allocated
+ * by the first linear on that stream that splits K, and grown, with a stream
+ * synchronisation, when a later one needs more).  A grown workspace replaces the
+ * old one without freeing it, so a HIP graph captured earlier on the stream keeps
+ * valid addresses; growth is refused under capture (MT_EINVAL: run the same linear
+ * once before capturing).  A captured graph uses the capture stream's workspace
+ * and arrival counters: replay it on that stream, or make sure no split-K linear
+ * runs on the capture stream while it replays elsewhere.  Errors are returned, never raised: 0 on success, a
+ * negative code otherwise, with a message in mt_last_error() (thread-local).
  *
  * Reference interfaces replaced (paths relative to the reference checkout):
  *   mt_linear            Encoder.linear            Sources/MingTTS/Engine/Kernels.swift:128-161
@@ -84,8 +91,10 @@ enum {
  * three; y is always fp32 (an fp16/bf16 output alone would break 1e-3). */
 typedef enum mt_dtype { MT_F32 = 0, MT_F16 = 1, MT_BF16 = 2 } mt_dtype;
 
-/* Kernel families, as reported by mt_linear_kernel. */
-enum { MT_KERNEL_GEMV = 1, MT_KERNEL_GEMM = 2 };
+/* Kernel families, as reported by mt_linear_kernel: the lane-group GEMV (every 16-byte
+ * weight chunk feeds all rows of x), the MFMA GEMM (tiles of x rows and weight rows), and
+ * the small-row MFMA kernel that stages x once per 16 output features. */
+enum { MT_KERNEL_GEMV = 1, MT_KERNEL_GEMM = 2, MT_KERNEL_GEMV_MFMA = 3 };
 
 /*
  * One linear, Encoder.linear (Kernels.swift:128-161).
@@ -113,8 +122,12 @@ int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtyp
 int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *w, const void *w2,
                       mt_dtype wt, const void *bias, float *y, mt_gemv_params p, mt_stream_t stream);
 
-/* The kernel family mt_linear picks for a shape (MT_KERNEL_GEMV / MT_KERNEL_GEMM),
- * the analogue of Kernels.usesGemm and scalarRowsMax. */
+/* The kernel family mt_linear runs for a shape under the current tuning, the analogue of
+ * Kernels.usesGemm and scalarRowsMax: M <= MT_TUNE_GEMV_ROWS_MAX (8) -> the GEMV, except
+ * 3..8 rows on the small-row MFMA kernel (unless MT_TUNE_GEMV_MFMA = 1); larger M -> the
+ * small-row MFMA kernel up to 16 rows (up to 64 under MT_TUNE_GEMV_MFMA = 2, while its
+ * columns fit), the GEMM above.  mt_linear_rmsnorm routes the same way, except that its
+ * fused norm takes the small-row MFMA kernel up to 8 rows only. */
 int mt_linear_kernel(uint32_t M, uint32_t N, uint32_t K, mt_dtype xt, mt_dtype wt);
 
 /* Process-wide tuning overrides, the analogue of Encoder.kSplitOverride /

@@ -93,7 +93,23 @@ static int validate_linear(const char *who, const void *x, int xt, const void *w
     return MT_OK;
 }
 
-static int kernel_for(uint32_t M) { return static_cast<int>(M) <= g_tuning.gemv_rows_max ? MT_KERNEL_GEMV : MT_KERNEL_GEMM; }
+// The kernel family mt_linear (norm false) or mt_linear_rmsnorm (norm true) runs M rows on,
+// from one read of each tuning value: mt_linear_kernel reports it, the launchers follow it.
+static int linear_family(uint32_t M, int xt, int wt, bool norm) {
+    const int rows_max = g_tuning.gemv_rows_max.load(std::memory_order_relaxed);
+    const int mode = g_tuning.gemv_mfma.load(std::memory_order_relaxed);
+    if (static_cast<int>(M) <= rows_max) return M >= 3 && M <= 8 && mode != 1 ? MT_KERNEL_GEMV_MFMA : MT_KERNEL_GEMV;
+    if ((mode == 2 || (mode == 0 && M <= 16)) && gemv_mfma_columns(M, xt, wt, norm) > 0) return MT_KERNEL_GEMV_MFMA;
+    return MT_KERNEL_GEMM;
+}
+
+static int launch_family(const LinearArgs &a, int xt, int wt, hipStream_t s, const FixedWs *fixed = nullptr) {
+    switch (linear_family(a.M, xt, wt, a.norm != nullptr)) {
+        case MT_KERNEL_GEMV: return launch_gemv(a, xt, wt, s, g_tuning.gemv_lanes);
+        case MT_KERNEL_GEMV_MFMA: return launch_gemv_mfma(a, xt, wt, s, fixed);
+        default: return launch_gemm(a, xt, wt, s, fixed);
+    }
+}
 
 }  // namespace mt
 
@@ -106,8 +122,9 @@ const char *mt_last_error(void) { return g_err; }
 const char *mt_version(void) { return "mingtts_hip 0.1.0 gfx950"; }
 
 int mt_linear_kernel(uint32_t M, uint32_t N, uint32_t K, mt_dtype xt, mt_dtype wt) {
-    (void)N; (void)K; (void)xt; (void)wt;
-    return kernel_for(M);
+    (void)N;
+    (void)K;
+    return linear_family(M, xt, wt, false);
 }
 
 int mt_set_tuning(int key, int value) {
@@ -146,9 +163,7 @@ int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtyp
     int rc = validate_linear("mt_linear", x, xt, w, w2, wt, bias, nullptr, y, p, a);
     if (rc) return rc;
     if (p.M == 0 || p.N == 0) return MT_OK;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (kernel_for(p.M) == MT_KERNEL_GEMV) return launch_gemv(a, xt, wt, s, g_tuning.gemv_lanes);
-    return launch_gemm(a, xt, wt, s, g_tuning.gemm_splitk);
+    return launch_family(a, xt, wt, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *w, const void *w2, mt_dtype wt,
@@ -158,9 +173,7 @@ int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *
     int rc = validate_linear("mt_linear_rmsnorm", x, xt, w, w2, wt, bias, norm, y, p, a);
     if (rc) return rc;
     if (p.M == 0 || p.N == 0) return MT_OK;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (kernel_for(p.M) == MT_KERNEL_GEMV) return launch_gemv(a, xt, wt, s, g_tuning.gemv_lanes);
-    return launch_gemm(a, xt, wt, s, g_tuning.gemm_splitk);
+    return launch_family(a, xt, wt, reinterpret_cast<hipStream_t>(stream));
 }
 
 // Shared checks of the rope / attention entry points.

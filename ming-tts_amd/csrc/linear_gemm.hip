@@ -281,13 +281,8 @@ gemm_fn pick_x(int xt, bool gated, bool norm) {
 
 }  // namespace
 
-int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int /*splitk_override*/) {
-    // Up to 16 rows (measured: faster than the tiled GEMM at M = 16 on every Qwen linear,
-    // even at 32, slower at 64) on the MFMA kernel that stages x once per 16 output features.
-    const int mode = tuning().gemv_mfma;
-    if ((mode == 2 || (mode == 0 && a.M <= 16)) && gemv_mfma_columns(a.M, xt, wt, a.norm != nullptr) > 0)
-        return launch_gemv_mfma(a, xt, wt, stream);
-    if (xt == wt && a.norm == nullptr && tuning().gemm_tile != 4) return launch_gemm_tiled(a, wt, stream);
+int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed) {
+    if (xt == wt && a.norm == nullptr && tuning().gemm_tile != 4) return launch_gemm_tiled(a, wt, stream, fixed);
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
     gemm_fn fn = wt == DT_BF16 ? pick_x<DT_BF16>(xt, gated, norm) : pick_x<DT_F16>(xt, gated, norm);

@@ -521,7 +521,7 @@ size_t tiled_partial_bytes(const TiledPlan &p, bool gated) {
     return static_cast<size_t>(p.tiles_m) * p.tiles_n * p.splits * ne * sizeof(float);
 }
 
-int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream) {
+int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream, const FixedWs *fixed) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const int cus = device_cus();
     if (cus <= 0) return set_error(MT_EHIP, "gemm: cannot query the device");
@@ -546,7 +546,7 @@ int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream) {
         uint32_t *cnt = nullptr;
         const size_t pb = tiled_partial_bytes(p, gated);
         if (pb > 0x7FFFFFF0u) return set_error(MT_ENOTSUP, "gemm: split-K partials of %zu bytes exceed 2 GiB", pb);
-        const int rc = stream_workspace(stream, pb, tiles, &part, &cnt);
+        const int rc = split_workspace(fixed, stream, pb, tiles, &part, &cnt, "gemm");
         if (rc) return rc;
         t.part = static_cast<float *>(part);
         t.part_bytes = static_cast<uint32_t>(pb);

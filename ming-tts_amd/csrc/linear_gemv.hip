@@ -74,7 +74,6 @@ int gemv_lanes_log2(uint32_t K, int override_lanes, uint32_t M) {
 }
 
 int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int override_lanes) {
-    if (a.M >= 3 && a.M <= 8 && tuning().gemv_mfma != 1) return launch_gemv_mfma(a, xt, wt, stream);
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
     const int mr = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : 8;

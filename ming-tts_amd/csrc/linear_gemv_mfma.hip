@@ -492,7 +492,7 @@ namespace {
 // Tiles, splits and (for S > 1) the stream's split-K workspace.  even: splits start at
 // multiples of 64 k (whole attention heads).
 int gm_splits(const LinearArgs &a, int xt, int wt, bool gated, bool norm, int ng, bool even, hipStream_t stream,
-              GmSplit &sp) {
+              GmSplit &sp, const FixedWs *fixed = nullptr) {
     sp = GmSplit{};
     sp.tiles = (a.N + 15) / 16;
     const uint32_t kb = (a.K + 31) / 32;
@@ -513,7 +513,7 @@ int gm_splits(const LinearArgs &a, int xt, int wt, bool gated, bool norm, int ng
         if (pb > 0x7FFFFFF0u) return set_error(MT_ENOTSUP, "gemv_mfma: split-K workspace beyond 2 GiB");
         void *part = nullptr;
         uint32_t *cnt = nullptr;
-        const int rc = stream_workspace(stream, pb, sp.tiles, &part, &cnt);
+        const int rc = split_workspace(fixed, stream, pb, sp.tiles, &part, &cnt, "gemv_mfma");
         if (rc) return rc;
         sp.part = static_cast<float *>(part);
         sp.part_bytes = static_cast<uint32_t>(pb);
@@ -531,14 +531,14 @@ gm_fn gm_attn(int ng) {
 
 }  // namespace
 
-int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream) {
+int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
     const int cols = gemv_mfma_columns(a.M, xt, wt, norm);
     if (cols == 0) return set_error(MT_ENOTSUP, "gemv_mfma: %u rows exceed the kernel's columns", a.M);
     const int ng = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
     GmSplit sp;
-    const int rc = gm_splits(a, xt, wt, gated, norm, ng, false, stream, sp);
+    const int rc = gm_splits(a, xt, wt, gated, norm, ng, false, stream, sp, fixed);
     if (rc) return rc;
     gm_fn fn = ng == 1 ? gm_w<1>(wt, xt, gated, norm) : ng == 2 ? gm_w<2>(wt, xt, gated, norm) : gm_w<4>(wt, xt, gated, norm);
     hipLaunchKernelGGL(fn, dim3(sp.tiles * sp.splits), dim3(GM_THREADS), 0, stream, a, sp, GmAttn{});

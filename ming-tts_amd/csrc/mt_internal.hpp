@@ -12,6 +12,8 @@
 
 namespace mt {
 
+struct FixedWs;  // a fixed split-K scratch (below)
+
 // Error reporting: the message lands in the thread-local buffer read by mt_last_error().
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 // hipGetLastError after a launch, as an ABI return code.
@@ -129,12 +131,30 @@ int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int ove
 // Up to 64 B columns (M rows of x of the weights' type, or 2 M with hi + lo halves; a fused
 // norm at most 8 rows) on MFMA, x staged once per workgroup of 16 output features.
 int gemv_mfma_columns(uint32_t M, int xt, int wt, bool norm);
-int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream);
+int launch_gemv_mfma(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed = nullptr);
 // The same kernel with x computed in its prologue as the DiT attention of qkv = a.x (row
 // stride a.ldx): mt_dit_attention_linear.
 int launch_gemv_mfma_attn(const LinearArgs &a, int wt, const float *inv_freq, uint32_t S, uint32_t H, float scale,
                           hipStream_t stream);
-int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, int splitk_override);
+// The lane-group GEMV, and the MFMA GEMM (pipelined for x of the weights' type without a
+// norm, register-staged otherwise); mt_linear's routing between them and the small-row MFMA
+// kernel is linear_family in api.cpp.  The small-row kernel runs up to 16 rows because it
+// measured faster than the pipelined GEMM at M = 16 on every Qwen linear, even at 32, and
+// slower at 64.
+int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed = nullptr);
+
+// A fixed split-K scratch: arrival counters (zero between launches) and
+// room for partial sums.  A launcher given one uses it instead of the stream's workspace and
+// refuses a linear that needs more.
+struct FixedWs {
+    uint32_t *cnt;
+    uint32_t counters;
+    void *part;
+    size_t part_bytes;
+};
+// The split-K workspace of a launch: the fixed scratch when fixed != null, else the stream's.
+int split_workspace(const FixedWs *fixed, hipStream_t stream, size_t part_bytes, uint32_t counters, void **part,
+                    uint32_t **cnt, const char *who);
 
 // Compute units of the current device (cached per device), or <= 0 when it cannot be queried.
 int device_cus();
@@ -151,6 +171,6 @@ struct TiledPlan {
     int stages;               // LDS pipeline depth (64-k stages)
 };
 TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, int shape_override, int splitk_override);
-int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream);
+int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream, const FixedWs *fixed = nullptr);
 
 }  // namespace mt

@@ -513,8 +513,12 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
         }
     }
     // Workgroup maximum; every thread's part rescaled to it.
+    // A wave without keys has m = -inf.  Its slot holds -1e30 instead: this scratch is the
+    // next linear's activation staging, and past that op's M K its stale words are over-read
+    // (against zero weights) as 16-bit halves, where -inf or -FLT_MAX would be a NaN that
+    // survives the multiply by zero.  -1e30 is below any score and finite in fp16 and bf16.
     float mx = wave_max_bfly(m);
-    if (lane == 0) red[w] = mx;
+    if (lane == 0) red[w] = fmaxf(mx, -1.0e30f);
     __syncthreads();
     mx = red[0];
 #pragma unroll

@@ -3,11 +3,15 @@
 // Launches on one stream run in order, so one workspace per stream is never used by two
 // launches at once; launches on different streams get different workspaces.  The first
 // bytes hold the arrival counters (zeroed once at allocation and left zero by every
-// launch), the partial sums follow.
+// launch), the partial sums follow.  A workspace that has to grow is replaced, never freed:
+// a HIP graph captured on the stream keeps the old buffer's addresses in its nodes, and a
+// replay must still find that memory there (the retired buffers are at most as large as the
+// live one, since each growth at least doubles it).
 #include <algorithm>
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "mt_internal.hpp"
 
@@ -25,6 +29,7 @@ struct Workspace {
 
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::vector<void *> g_retired;  // replaced workspaces, kept until the process ends
 
 int g_cus[64];
 
@@ -38,6 +43,19 @@ int device_cus() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
     if (dev < 64) g_cus[dev] = cus;
     return cus;
+}
+
+int split_workspace(const FixedWs *fixed, hipStream_t stream, size_t part_bytes, uint32_t counters, void **part,
+                    uint32_t **cnt, const char *who) {
+    if (!fixed) return stream_workspace(stream, part_bytes, counters, part, cnt);
+    if (part_bytes > fixed->part_bytes || counters > fixed->counters)
+        return set_error(MT_ENOTSUP,
+                         "%s: the split-K partials (%zu bytes, %u tiles) exceed the static scratch (%zu bytes, %u "
+                         "tiles); use mt_linear",
+                         who, part_bytes, counters, fixed->part_bytes, fixed->counters);
+    *part = fixed->part;
+    *cnt = fixed->cnt;
+    return MT_OK;
 }
 
 int stream_workspace(hipStream_t stream, size_t part_bytes, uint32_t counters, void **part, uint32_t **cnt) {
@@ -54,10 +72,7 @@ int stream_workspace(hipStream_t stream, size_t part_bytes, uint32_t counters, v
         const uint32_t nc = std::max<uint32_t>(std::max(counters, w.counters * 2), 1024);
         const size_t cb = (static_cast<size_t>(nc) * 4 + COUNTER_BYTES_ALIGN - 1) / COUNTER_BYTES_ALIGN * COUNTER_BYTES_ALIGN;
         if (w.base) {
-            // Earlier launches on this stream may still read the old buffer.
-            hipError_t e = hipStreamSynchronize(stream);
-            if (e != hipSuccess) return set_error(MT_EHIP, "workspace: growing it needs a stream sync: %s", hipGetErrorString(e));
-            (void)hipFree(w.base);
+            g_retired.push_back(w.base);  // graphs captured on this stream may still use it
             w.base = nullptr;
         }
         void *p = nullptr;

@@ -21,7 +21,7 @@ LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "csrc", "libmingtts_hip.so
 
 F32, F16, BF16 = 0, 1, 2
 OK, EHIP, ENOMEM, EINVAL, ERANGE, ENOTSUP = 0, -5, -12, -22, -34, -95
-KERNEL_GEMV, KERNEL_GEMM = 1, 2
+KERNEL_GEMV, KERNEL_GEMM, KERNEL_GEMV_MFMA = 1, 2, 3
 (TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS, TUNE_SEQ_LAUNCH, TUNE_GEMM_TILE,
  TUNE_GEMM_STAGES, TUNE_GEMV_MFMA, TUNE_SEQ_LAYER) = 1, 2, 3, 4, 5, 6, 7, 8, 9
 SEQ_GENERAL, SEQ_DECODE_LAYER = 0, 1

@@ -83,17 +83,33 @@ def test_linear_rmsnorm_rejects_bad_arguments():
 
 
 def test_kernel_choice_and_tuning_round_trip():
-    """The analogue of Kernels.usesGemm / scalarRowsMax (KernelTests.swift:155-157, 165-166)."""
+    """The analogue of Kernels.usesGemm / scalarRowsMax (KernelTests.swift:155-157, 165-166):
+    the family mt_linear actually launches, under each tuning."""
     assert mt.linear_kernel(1, 1152, 896) == mt.KERNEL_GEMV
-    assert mt.linear_kernel(8, 2, 896) == mt.KERNEL_GEMV
+    assert mt.linear_kernel(2, 4864, 896) == mt.KERNEL_GEMV
+    assert mt.linear_kernel(3, 1152, 896) == mt.KERNEL_GEMV_MFMA
+    assert mt.linear_kernel(8, 2, 896) == mt.KERNEL_GEMV_MFMA
+    assert mt.linear_kernel(16, 64, 32) == mt.KERNEL_GEMV_MFMA
+    assert mt.linear_kernel(17, 64, 32) == mt.KERNEL_GEMM
     assert mt.linear_kernel(174, 1152, 896) == mt.KERNEL_GEMM
-    assert mt.linear_kernel(16, 64, 32) == mt.KERNEL_GEMM
     old = mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, 2)
     try:
-        assert mt.linear_kernel(3, 1152, 896) == mt.KERNEL_GEMM
+        assert mt.linear_kernel(3, 1152, 896) == mt.KERNEL_GEMV_MFMA   # past the GEMV rows: <= 16 rows
+        assert mt.linear_kernel(2, 1152, 896) == mt.KERNEL_GEMV
     finally:
         mt.set_tuning(mt.TUNE_GEMV_ROWS_MAX, old)
-    assert mt.linear_kernel(3, 1152, 896) == mt.KERNEL_GEMV
+    old = mt.set_tuning(mt.TUNE_GEMV_MFMA, 1)
+    try:
+        assert mt.linear_kernel(3, 1152, 896) == mt.KERNEL_GEMV
+        assert mt.linear_kernel(16, 64, 32) == mt.KERNEL_GEMM
+    finally:
+        mt.set_tuning(mt.TUNE_GEMV_MFMA, old)
+    old = mt.set_tuning(mt.TUNE_GEMV_MFMA, 2)
+    try:
+        assert mt.linear_kernel(64, 1152, 896, xt=mt.BF16, wt=mt.BF16) == mt.KERNEL_GEMV_MFMA   # 64 columns
+        assert mt.linear_kernel(33, 1152, 896) == mt.KERNEL_GEMM       # fp32 x: 2 M = 66 columns > 64
+    finally:
+        mt.set_tuning(mt.TUNE_GEMV_MFMA, old)
     assert mt.load().mt_set_tuning(99, 0) == mt.EINVAL
     assert mt.load().mt_set_tuning(mt.TUNE_GEMV_ROWS_MAX, 9) == mt.EINVAL
     assert mt.load().mt_set_tuning(mt.TUNE_SEQ_LAUNCH, 2) == mt.EINVAL

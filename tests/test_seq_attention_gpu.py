@@ -184,3 +184,34 @@ def test_layers_equal_separate_launches_and_rerun_bit_exact(gpu):
     for l in range(layers):   # the same cache rows (the rotation of k, rounded to fp16)
         got = kcs[l].cpu().numpy().astype(np.float64)
         np.testing.assert_allclose(got, ref_k[l].astype(np.float64), rtol=2e-3, atol=2e-3)
+
+
+def test_linear_after_early_attention_item_reads_no_stale_scratch(gpu):
+    """An attention item at position 5 (six keys: half the workgroup's waves see none) uses
+    the activation staging as scratch; the next linear (M = 1, K = 776, so its staged x ends
+    before that scratch does) over-reads the staging past K against zero weights.  The result
+    must be the fp64 linear of the attention output, with no NaN from the item's leftovers."""
+    cap, B, N, K = 64, 1, 64, 776
+    say("seq attention item then M=1 K=776 linear")
+    rng = np.random.default_rng(4)
+    qkv = torch.from_numpy(rng.standard_normal((B, QKV)).astype(np.float32)).to(gpu)
+    kc = torch.from_numpy(rng.standard_normal((B, HKV, cap, 64)).astype(np.float16)).to(gpu)
+    vc = torch.from_numpy(rng.standard_normal((B, HKV, cap, 64)).astype(np.float16)).to(gpu)
+    att = torch.zeros(B, HQ * 64, device=gpu)
+    y = torch.zeros(B, N, device=gpu)
+    pos_d = torch.tensor([5], dtype=torch.int32, device=gpu)
+    invf_d = torch.from_numpy(O.inv_freq(1e6)).to(gpu)
+    wb, _ = O.round16(rng.standard_normal((N, K)).astype(np.float32) * np.float32(0.05), O.F16)
+    w = torch.from_numpy(wb.view(np.int16)).to(gpu).view(torch.float16)
+    seq = mt.Seq([mt.attn_op(qkv, B, HQ, HKV, pos_d, kc, vc, cap, HKV * cap * 64, invf_d, att),
+                  mt.op(att, w, y, B, ldx=HQ * 64)])
+    for _ in range(2):
+        seq.run()
+        torch.cuda.synchronize()
+        seq.check()
+        a = att.cpu().numpy()
+        got = y.cpu().numpy()
+        assert np.all(np.isfinite(a)) and np.all(np.isfinite(got))
+        want = O.linear_f64(np.ascontiguousarray(a[:, :K]), wb, None, O.F16, None, None, B, N, K, 0)
+        assert O.normwise_rel_err(got, want) <= 1e-5
+    seq.close()
