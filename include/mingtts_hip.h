@@ -11,7 +11,8 @@
  * valid addresses; growth is refused under capture (MT_EINVAL: run the same linear
  * once before capturing).  A captured graph uses the capture stream's workspace
  * and arrival counters: replay it on that stream, or make sure no split-K linear
- * runs on the capture stream while it replays elsewhere.  Errors are returned, never raised: 0 on success, a
+ * runs on the capture stream while it replays elsewhere.  mt_linear_static
+ * allocates nothing.  Errors are returned, never raised: 0 on success, a
  * negative code otherwise, with a message in mt_last_error() (thread-local).
  *
  * Reference interfaces replaced (paths relative to the reference checkout):
@@ -111,6 +112,20 @@ enum { MT_KERNEL_GEMV = 1, MT_KERNEL_GEMM = 2, MT_KERNEL_GEMV_MFMA = 3 };
  */
 int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt,
               const void *bias, float *y, mt_gemv_params p, mt_stream_t stream);
+
+/*
+ * mt_linear without any allocation.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory on the call path (code under HIP graph capture,
+ * serving loops or harnesses that forbid hipMalloc).  Same arguments, semantics and
+ * kernels as mt_linear, with the split-K partial sums and arrival counters in a fixed
+ * device array of the library (16 MiB of partials and 4096 tiles, held on each device
+ * the library runs on until the process ends) instead of the stream's workspace.  A
+ * linear whose split needs more is refused with MT_ENOTSUP (mt_linear runs it).  Every
+ * call on a device shares that device's array: calls that overlap on one device (on
+ * different streams) race, and must be ordered by the caller.
+ */
+int mt_linear_static(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt,
+                     const void *bias, float *y, mt_gemv_params p, mt_stream_t stream);
 
 /*
  * RMSNorm fused into a linear's prologue: the reference's Encoder.rmsnorm into a scratch

@@ -166,6 +166,19 @@ int mt_linear(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtyp
     return launch_family(a, xt, wt, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mt_linear_static(const void *x, mt_dtype xt, const void *w, const void *w2, mt_dtype wt, const void *bias,
+                     float *y, mt_gemv_params p, mt_stream_t stream) {
+    LinearArgs a;
+    int rc = validate_linear("mt_linear_static", x, xt, w, w2, wt, bias, nullptr, y, p, a);
+    if (rc) return rc;
+    if (p.M == 0 || p.N == 0) return MT_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    FixedWs ws;
+    rc = static_scratch(s, ws);
+    if (rc) return rc;
+    return launch_family(a, xt, wt, s, &ws);
+}
+
 int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *w, const void *w2, mt_dtype wt,
                       const void *bias, float *y, mt_gemv_params p, mt_stream_t stream) {
     if (!norm) return set_error(MT_EINVAL, "mt_linear_rmsnorm: null norm");

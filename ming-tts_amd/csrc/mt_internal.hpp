@@ -143,7 +143,7 @@ int launch_gemv_mfma_attn(const LinearArgs &a, int wt, const float *inv_freq, ui
 // slower at 64.
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed = nullptr);
 
-// A fixed split-K scratch: arrival counters (zero between launches) and
+// A fixed split-K scratch (mt_linear_static): arrival counters (zero between launches) and
 // room for partial sums.  A launcher given one uses it instead of the stream's workspace and
 // refuses a linear that needs more.
 struct FixedWs {
@@ -152,6 +152,8 @@ struct FixedWs {
     void *part;
     size_t part_bytes;
 };
+// The fixed scratch of the current device (set up on the first call on a device), or an error.
+int static_scratch(hipStream_t stream, FixedWs &ws);
 // The split-K workspace of a launch: the fixed scratch when fixed != null, else the stream's.
 int split_workspace(const FixedWs *fixed, hipStream_t stream, size_t part_bytes, uint32_t counters, void **part,
                     uint32_t **cnt, const char *who);

@@ -28,7 +28,7 @@ SEQ_GENERAL, SEQ_DECODE_LAYER = 0, 1
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
-    "mt_linear", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
+    "mt_linear", "mt_linear_static", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_kernel", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_rope_attention", "mt_dit_attention", "mt_dit_attention_linear", "mt_flow_assemble",
@@ -108,6 +108,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     vp, u32, u64, i32, f32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
     L.mt_linear.argtypes = [vp, i32, vp, vp, i32, vp, vp, GemvParams, vp]
     L.mt_linear.restype = i32
+    L.mt_linear_static.argtypes = [vp, i32, vp, vp, i32, vp, vp, GemvParams, vp]
+    L.mt_linear_static.restype = i32
     L.mt_linear_rmsnorm.argtypes = [vp, i32, vp, vp, vp, i32, vp, vp, GemvParams, vp]
     L.mt_linear_rmsnorm.restype = i32
     L.mt_linear_kernel.argtypes = [u32, u32, u32, i32, i32]
@@ -223,6 +225,12 @@ def linear_raw(x, xt, w, w2, wt, bias, y, M, N, K, ldx, ldy, flags, stream=None)
     """mt_linear on raw pointers / tensors; returns the raw return code."""
     p = GemvParams(M, N, K, ldx, ldy, flags, 0.0)
     return load().mt_linear(_ptr(x), xt, _ptr(w), _ptr(w2), wt, _ptr(bias), _ptr(y), p, _stream(stream))
+
+
+def linear_static_raw(x, xt, w, w2, wt, bias, y, M, N, K, ldx, ldy, flags, stream=None) -> int:
+    """mt_linear_static on raw pointers / tensors; returns the raw return code."""
+    p = GemvParams(M, N, K, ldx, ldy, flags, 0.0)
+    return load().mt_linear_static(_ptr(x), xt, _ptr(w), _ptr(w2), wt, _ptr(bias), _ptr(y), p, _stream(stream))
 
 
 def linear_rmsnorm_raw(x, xt, norm, w, w2, wt, bias, y, M, N, K, ldx, ldy, flags, eps=1e-6, stream=None) -> int:
