@@ -7,11 +7,13 @@ N(0, 0.02^2), fp32 activations ~ N(0, 1), run as ONE persistent launch of the li
 sequence (96 dependent linears).  ``value`` is the step's achieved HBM rate in GB/s
 (algorithmic bytes / step time), inputs resident in HBM.
 
-Also measured in the same run (extra keys of the JSON line): the single GEMV
-(4864 x 896, fp16, from a rotated >= 1 GiB weight pool), the same decode step as 96
-separate launches, the prefill GEMM stack at M = 64 / 256 / 512 (MFMA TFLOPS), batch-2
-decode attention over fp16 caches, the DiT head MLP, and the CPU baseline (the oracle's
-vectorised restatement of the reference CPU loop on a bounded sample of the step).
+Also measured in the same run (extra keys of the JSON line), every figure a HIP-graph
+replay timed with HIP events on its stream (host launch cost excluded): the empty-dispatch
+floor, the single GEMV (4864 x 896, fp16, from a rotated >= 1 GiB weight pool), the same
+decode step as 96 separate launches, the prefill GEMM stack at M = 64 / 256 / 512 (MFMA
+TFLOPS), batch-2 decode attention over fp16 caches, the DiT head MLP warm and cold, the flow
+stage and the VAE latent; and the CPU baseline (the oracle's vectorised restatement of the
+reference CPU loop over the whole step, on every host thread and on one).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only decode]
 """
@@ -32,7 +34,7 @@ H, QKV, INTER, LAYERS = 896, 1152, 4864, 24
 METRIC = "decode-step linear µs + achieved HBM GB/s (% of 8 TB/s); prefill MFMA TFLOPS"
 
 
-PROFILE = os.path.join(ROOT, "profiles", "seq_kernel_decode_24L_M2.md")
+PROFILE = os.path.join(ROOT, "profiles", "layer_kernel_decode_24L_M2.md")
 
 
 def measured_traffic(path: str = PROFILE):
@@ -76,6 +78,49 @@ class Events:
         self.b.record()
         self.b.synchronize()
         return self.a.elapsed_time(self.b)
+
+
+def graph_us(torch, fn, stream, rounds=5) -> float:
+    """Median time (us) of one replay of a HIP graph holding fn()'s launches, each replay
+    bracketed by HIP events on the replay stream (the stream the launches were captured on),
+    so host launch cost is outside every figure.  fn runs once eagerly first: the split-K
+    workspace may not grow under capture."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+    torch.cuda.synchronize()
+    times = []
+    with torch.cuda.stream(stream):
+        g.replay()
+        torch.cuda.synchronize()
+        for _ in range(rounds):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            g.replay()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+    del g
+    return 1e3 * sorted(times)[len(times) // 2]
+
+
+def bench_launch_floor(torch, dev, n=200):
+    """The empty-dispatch floor, as the reference's GemvBench measures it (one-element copies
+    back to back, GemvBench.swift:117-123): n one-element device kernels in one graph."""
+    a = torch.zeros(1, device=dev)
+    b = torch.zeros(1, device=dev)
+    cs = torch.cuda.Stream(device=dev)
+
+    def run():
+        for _ in range(n):
+            b.add_(a)
+
+    return dict(us_per_dispatch=graph_us(torch, run, cs) / n, dispatches=n,
+                kernel="one-element elementwise add (torch), graph replay")
 
 
 def make_layers(torch, dev, layers=LAYERS, seed=0):
@@ -147,7 +192,11 @@ def bench_decode_seq(torch, mt, dev, ws, steps, warmup, M=2):
     seq.check()
     nbytes = sum(op_bytes(o) for o in ops)
     flops = sum(op_flops(o) for o in ops)
-    res = dict(groups=seq.groups, bytes=nbytes, flops=flops, times_ms=times, ops=len(ops))
+    res = dict(groups=seq.groups, bytes=nbytes, flops=flops, times_ms=times, ops=len(ops),
+               kernel=("mt::layer_kernel<1, 2> (fp16 weights, M = 2, the Qwen2-0.5B decode-layer kernel)"
+                       if seq.kernel == mt.SEQ_DECODE_LAYER else
+                       "mt::seq_kernel<1, 2, false> (fp16 weights, M = 2, linears only)")
+               + "; one launch per decode step")
     seq.close()
     return res
 
@@ -200,13 +249,16 @@ def bench_decode_layers(torch, mt, dev, ws, steps, warmup, M=2, cap=512):
                 positions=[int(n) - 1 for n in lens], kv_cache_bytes_read=kv_bytes)
 
 
-def bench_decode_per_op(torch, mt, dev, ws, steps, M=2):
+def bench_decode_per_op(torch, mt, dev, ws, rounds=5, M=2):
+    """The same decode step as 96 separate mt_linear / mt_linear_rmsnorm launches, captured in
+    a HIP graph and replayed (the reference encodes them serially into one command buffer)."""
     resid = torch.randn(M, H, device=dev)
     qkv = torch.zeros(M, QKV, device=dev)
     mlp = torch.zeros(M, INTER, device=dev)
     ops = decode_ops(mt, ws, M, resid, qkv, mlp)
     L = mt.load()
-    s = torch.cuda.current_stream().cuda_stream
+    cs = torch.cuda.Stream(device=dev)
+    s = cs.cuda_stream
 
     def step():
         for o in ops:
@@ -217,19 +269,13 @@ def bench_decode_per_op(torch, mt, dev, ws, steps, M=2):
             if rc:
                 raise RuntimeError(mt.last_error())
 
-    step()
-    torch.cuda.synchronize()
-    ev = Events(torch)
-    times = []
-    for _ in range(steps):
-        ev.start()
-        step()
-        times.append(ev.stop_ms())
-    return dict(times_ms=times)
+    return dict(us=graph_us(torch, step, cs, rounds), launches=len(ops))
 
 
-def bench_gemv_single(torch, mt, dev, reps=200, M=1):
-    """4864 x 896 fp16 GEMV, each dispatch reading a fresh slice of a >= 1 GiB pool."""
+def bench_gemv_single(torch, mt, dev, M=1, rounds=5):
+    """4864 x 896 fp16 GEMV, x fp16: one graph of back-to-back dispatches, each reading the
+    next slice of a >= 1 GiB weight pool (so no dispatch finds its weights in the 256 MB
+    Infinity Cache), the reference's rotating-pool method (GemvBench.swift:96-98, 126-131)."""
     N, K = 4864, 896
     per = N * K
     copies = (1 << 30) // (per * 2) + 1
@@ -237,22 +283,22 @@ def bench_gemv_single(torch, mt, dev, reps=200, M=1):
     x = torch.randn(M, K, device=dev).half()
     y = torch.zeros(M, N, device=dev)
     L = mt.load()
-    s = torch.cuda.current_stream().cuda_stream
+    cs = torch.cuda.Stream(device=dev)
     p = mt.GemvParams(M, N, K, K, N, 0, 0.0)
-    for i in range(copies):
-        L.mt_linear(x.data_ptr(), mt.F16, pool[i].data_ptr(), None, mt.F16, None, y.data_ptr(), p, s)
-    torch.cuda.synchronize()
-    ev = Events(torch)
-    ev.start()
-    for i in range(reps):
-        rc = L.mt_linear(x.data_ptr(), mt.F16, pool[i % copies].data_ptr(), None, mt.F16, None, y.data_ptr(), p, s)
-        if rc:
-            raise RuntimeError(mt.last_error())
-    ms = ev.stop_ms()
+
+    def run():
+        for i in range(copies):
+            rc = L.mt_linear(x.data_ptr(), mt.F16, pool[i].data_ptr(), None, mt.F16, None, y.data_ptr(), p,
+                             cs.cuda_stream)
+            if rc:
+                raise RuntimeError(mt.last_error())
+
+    us = graph_us(torch, run, cs, rounds) / copies
     nbytes = 2 * N * K + 2 * M * K + 4 * M * N
-    us = ms * 1e3 / reps
     del pool
-    return dict(M=M, us_per_dispatch=us, gbs=nbytes / (us * 1e-6) / 1e9, bytes=nbytes, pool_copies=copies)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return dict(M=M, us_per_dispatch=us, gbs=gbs, pct_of_hbm_peak=100 * gbs / HBM_PEAK_GBS, bytes=nbytes,
+                pool_copies=copies, timing="graph replay of one dispatch per pool slice")
 
 
 def bench_prefill(torch, mt, dev, ws, M, reps=3):
@@ -305,7 +351,9 @@ def bench_prefill(torch, mt, dev, ws, M, reps=3):
 
 
 def bench_attention(torch, mt, dev, reps=200):
-    """Batch-2 decode attention, 14 q / 2 kv heads, d 64, fp16 caches of 512, lengths ~ U[32, 512]."""
+    """Batch-2 decode attention, 14 q / 2 kv heads, d 64, fp16 caches of 512, lengths ~ U[32, 512]:
+    reps dispatches in one graph (the caches stay cache-resident, as the reference's layer loop
+    finds them after the RoPE append)."""
     import numpy as np
     B, HQ, HKV, CAP = 2, 14, 2, 512
     lens = np.random.default_rng(0).integers(32, 513, B).astype(np.int32)
@@ -315,29 +363,36 @@ def bench_attention(torch, mt, dev, reps=200):
     out = torch.zeros(B, HQ * 64, device=dev)
     lens_d = torch.from_numpy(lens).to(dev)
     stride = HKV * CAP * 64
-    mt.attention_decode(q, HQ * 64, B, HQ, HKV, lens_d, 0, kc, vc, CAP, stride, out, HQ * 64)
-    torch.cuda.synchronize()
-    ev = Events(torch)
-    ev.start()
-    for _ in range(reps):
-        mt.attention_decode(q, HQ * 64, B, HQ, HKV, lens_d, 0, kc, vc, CAP, stride, out, HQ * 64)
-    us = ev.stop_ms() * 1e3 / reps
+    cs = torch.cuda.Stream(device=dev)
+
+    def run():
+        for _ in range(reps):
+            mt.attention_decode(q, HQ * 64, B, HQ, HKV, lens_d, 0, kc, vc, CAP, stride, out, HQ * 64,
+                                stream=cs.cuda_stream)
+
+    us = graph_us(torch, run, cs) / reps
     nbytes = int(sum(2 * HKV * int(l) * 64 * 2 for l in lens)) + 2 * B * HQ * 64 * 4
     return dict(us_per_dispatch=us, gbs=nbytes / (us * 1e-6) / 1e9, lens=lens.tolist(), bytes=nbytes)
 
 
-def bench_dit(torch, mt, dev, reps=3):
-    """DiT head MLP (896 -> 3584 GELU -> 896, += residual) at M = 64 and adaLN 896 -> 5376
-    at M = 2, 8 blocks x 10 ODE steps = 240 launches; the 8 blocks' weights repeat across
-    steps (Infinity-Cache resident after the first step)."""
+def bench_dit(torch, mt, dev, cold=False, rounds=5):
+    """DiT head MLP (896 -> 3584 GELU -> 896, += residual) at M = 64 and adaLN 896 -> 5376 at
+    M = 2, 8 blocks x 10 ODE steps = 240 launches in one graph.  Warm: the 8 blocks' weights
+    repeat across the steps (Infinity-Cache resident after the first).  Cold: every step has
+    its own copy of the 8 blocks (1.8 GB in all, well past the 256 MB Infinity Cache), so
+    each launch streams its weights from HBM, as the rotating pool does."""
     g = torch.Generator(device=dev)
     g.manual_seed(5)
-    blocks = [dict(ff1=(torch.randn(3584, H, generator=g, device=dev) * 0.02).half(),
-                   ff1_b=(torch.randn(3584, generator=g, device=dev) * 0.02).half(),
-                   ff2=(torch.randn(H, 3584, generator=g, device=dev) * 0.02).half(),
-                   ff2_b=(torch.randn(H, generator=g, device=dev) * 0.02).half(),
-                   ada=(torch.randn(6 * H, H, generator=g, device=dev) * 0.02).half(),
-                   ada_b=(torch.randn(6 * H, generator=g, device=dev) * 0.02).half()) for _ in range(8)]
+
+    def blockset():
+        return [dict(ff1=(torch.randn(3584, H, generator=g, device=dev) * 0.02).half(),
+                     ff1_b=(torch.randn(3584, generator=g, device=dev) * 0.02).half(),
+                     ff2=(torch.randn(H, 3584, generator=g, device=dev) * 0.02).half(),
+                     ff2_b=(torch.randn(H, generator=g, device=dev) * 0.02).half(),
+                     ada=(torch.randn(6 * H, H, generator=g, device=dev) * 0.02).half(),
+                     ada_b=(torch.randn(6 * H, generator=g, device=dev) * 0.02).half()) for _ in range(8)]
+
+    sets = [blockset() for _ in range(10 if cold else 1)]
     x = torch.randn(64, H, device=dev).half()
     hmid = torch.randn(64, 3584, device=dev).half()
     t = torch.randn(2, H, device=dev).half()
@@ -345,31 +400,28 @@ def bench_dit(torch, mt, dev, reps=3):
     y2 = torch.zeros(64, H, device=dev)
     ya = torch.zeros(2, 6 * H, device=dev)
     ops = []
-    for _ in range(10):
-        for b in blocks:
+    for k in range(10):
+        for b in sets[k % len(sets)]:
             ops.append(mt.op(t, b["ada"], ya, 2, bias=b["ada_b"]))
             ops.append(mt.op(x, b["ff1"], y1, 64, flags=mt.GemvFlags.gelu, bias=b["ff1_b"]))
             ops.append(mt.op(hmid, b["ff2"], y2, 64, flags=mt.GemvFlags.accumulate, bias=b["ff2_b"]))
     L = mt.load()
-    s = torch.cuda.current_stream().cuda_stream
+    cs = torch.cuda.Stream(device=dev)
 
     def run():
         for o in ops:
-            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
+            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, cs.cuda_stream)
             if rc:
                 raise RuntimeError(mt.last_error())
 
-    run()
-    torch.cuda.synchronize()
-    ev = Events(torch)
-    best = None
-    for _ in range(reps):
-        ev.start()
-        run()
-        ms = ev.stop_ms()
-        best = ms if best is None else min(best, ms)
+    us = graph_us(torch, run, cs, rounds)
     flops = sum(op_flops(o) for o in ops)
-    return dict(us_10_steps=best * 1e3, tflops=flops / (best * 1e-3) / 1e12, launches=len(ops))
+    nbytes = sum(op_bytes(o, xsize=2) for o in ops)
+    res = dict(us_10_steps=us, us_per_launch=us / len(ops), tflops=flops / (us * 1e-6) / 1e12,
+               gbs_algorithmic=nbytes / (us * 1e-6) / 1e9, launches=len(ops),
+               weights="cold (10 distinct block sets)" if cold else "warm (one block set, cache resident)")
+    del sets
+    return res
 
 
 def bench_gemm_ops(torch, mt, dev, ws, reps=5):
@@ -584,26 +636,36 @@ def bench_copy(torch, dev, mib=1024, reps=5):
                 gbs_read_plus_write=round(2 * (mib << 20) * reps / (ms * 1e-3) / 1e9, 1))
 
 
-def cpu_baseline(torch, ws, target_s=10.0, M=2):
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), as lscpu prints it."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(torch, ws, target_s=8.0, M=2):
     """The oracle's vectorised restatement of the reference CPU loop (KernelTests.swift:86-101,
-    K sum split 16 ways, OpenMP over output rows) on the host cores, over the first layers of
-    the same decode step (same shapes, same weights), repeated for about target_s seconds."""
+    K sum split 16 ways, OpenMP over output rows) on the host cores, over the whole decode step
+    (all 24 layers, same shapes, same weights): steps repeated for about target_s seconds on
+    every OpenMP thread, then again on one thread."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
-    layers = ws[:2]
-    host = [{k: v.cpu().numpy().view(np.uint16) for k, v in p.items()} for p in layers]
+    host = [{k: v.cpu().numpy().view(np.uint16) for k, v in p.items()} for p in ws]
     rng = np.random.default_rng(1)
     resid0 = rng.standard_normal((M, H)).astype(np.float32)
-    threads = O.max_threads()
-
     gains = [(O.decode16(p["norm1"], O.F16), O.decode16(p["norm2"], O.F16)) for p in host]
 
     def norm(x, g):
         return (x * (np.float32(1.0) / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + np.float32(1e-6))) * g
                 ).astype(np.float32)
 
-    def step():
+    def step(threads):
         resid = resid0.copy()
         for p, (g1, g2) in zip(host, gains):
             qkv = O.linear_fast(norm(resid, g1), p["qkv"], None, O.F16, p["qkv_b"], None, M, QKV, H, 0, threads)
@@ -614,22 +676,29 @@ def cpu_baseline(torch, ws, target_s=10.0, M=2):
             resid = O.linear_fast(mlp, p["down"], None, O.F16, None, resid, M, H, INTER, O.ACCUM, threads)
         return resid
 
-    step()
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        step()
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= target_s or n >= 200000:
-            break
+    def timed(threads):
+        step(threads)
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            step(threads)
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= target_s:
+                return n, dt
+
+    threads = O.max_threads()
+    n, dt = timed(threads)
+    n1, dt1 = timed(1)
     per_layer = (shape_bytes(M, QKV, H, 1) + shape_bytes(M, H, H, 2) + shape_bytes(M, INTER, H, 8)
                  + shape_bytes(M, H, INTER, 2))
     nbytes = per_layer * len(host)
     return dict(value=nbytes * n / dt / 1e9, unit="GB/s", cores=threads, kind="port",
-                sample=f"{len(host)} of the 24 decode-step layers (8 linears, M=2, fp16 W) x {n} repeats, "
-                       f"{dt:.1f} s, oracle linear_fast (K sum split 16 ways) with {threads} OpenMP threads",
-                step_ms_extrapolated=1e3 * dt / n * LAYERS / len(host))
+                sample=f"the whole decode step (24 layers, 96 linears, M=2, fp16 W) x {n} steps in {dt:.1f} s on "
+                       f"{threads} OpenMP threads, then x {n1} steps in {dt1:.1f} s on 1 thread; oracle linear_fast "
+                       f"(K sum split 16 ways)",
+                step_ms=1e3 * dt / n, value_1thread=nbytes * n1 / dt1 / 1e9, step_ms_1thread=1e3 * dt1 / n1,
+                cpu_model=cpu_model(), nproc=os.cpu_count())
 
 
 def main() -> int:
@@ -719,17 +788,19 @@ def main() -> int:
         "seq_launch": args.seq_launch,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/seq_kernel_decode_24L_M2.md",
-                     "kernel": "mt::seq_kernel<1, 2, false> (fp16 weights, M = 2, linears only; one launch per decode step)"},
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/layer_kernel_decode_24L_M2.md",
+                     "kernel": d["kernel"]},
     }
     if args.only in ("all", "layer"):
         log("decode layers with attention (persistent sequence, 120 items)")
         line["decode_layer_step"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                      for k, v in bench_decode_layers(torch, mt, dev, ws, args.steps, args.warmup).items()}
     if args.only == "all":
-        log("decode step as 96 separate launches")
-        p = bench_decode_per_op(torch, mt, dev, ws, max(5, args.steps // 5))
-        line["decode_step_us_per_op_launches"] = round(1e3 * sorted(p["times_ms"])[len(p["times_ms"]) // 2], 2)
+        log("empty-dispatch floor (graph of one-element kernels)")
+        line["launch_floor"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                for k, v in bench_launch_floor(torch, dev).items()}
+        log("decode step as 96 separate launches (graph replay)")
+        line["decode_step_us_per_op_launches"] = round(bench_decode_per_op(torch, mt, dev, ws)["us"], 2)
         log("single GEMV 4864x896 from a rotated 1 GiB pool")
         line["gemv_single"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                for k, v in bench_gemv_single(torch, mt, dev).items()}
@@ -745,6 +816,9 @@ def main() -> int:
                                     for k, v in bench_attention(torch, mt, dev).items()}
         log("DiT head")
         line["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
+        log("DiT head, cold weights")
+        line["dit_head_cold"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                 for k, v in bench_dit(torch, mt, dev, cold=True).items()}
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
         line["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
         line["flow_step_separate_attention"] = {k: (round(v, 3) if isinstance(v, float) else v)
