@@ -480,12 +480,15 @@ def bench_gemm_ops(torch, mt, dev, ws, reps=5):
 
 def bench_flow_step(torch, mt, dev, reps=5, fused=True):
     """The flow stage of one generation step at the reference's flow-head shape
-    (MingEngine.encodeStep, Engine.swift:395-402; DiTForward.encode, DiT.swift:35-52): 10 ODE
-    steps of flow_assemble, 8 DiT blocks (hidden 1024, 16 heads, batch 2 x seq 3 = 6 rows:
-    rmsnorm+qkv 3072x1024, dit_attention, out 1024x1024 +=, rmsnorm+ff1 4096x1024 GELU,
-    ff2 1024x4096 +=), the final rmsnorm + 64x1024 linear and flow_euler: 430 launches, bf16
+    (MingEngine.encodeStep, Engine.swift:387-402; DiTForward.encode, DiT.swift:35-52): the
+    cond embedder (896 -> 1024, M = 1), then 10 ODE steps of the EPSS schedule with sway
+    (FlowSchedule, DiT.swift:55-65) of flow_assemble with that step's time embedding
+    (precomputed once by the time MLP, Engine.swift:186-198, outside the timed region), 8 DiT
+    blocks (hidden 1024, 16 heads, batch 2 x seq 3 = 6 rows: rmsnorm+qkv 3072x1024,
+    dit_attention, out 1024x1024 +=, rmsnorm+ff1 4096x1024 GELU, ff2 1024x4096 +=), the final
+    rmsnorm + 64x1024 linear and flow_euler with dt = t[k+1] - t[k]: 431 launches, bf16
     weights ~ N(0, 0.02^2), captured in a HIP graph and replayed.  With ``fused`` each block's
-    attention runs inside its out projection (mt_dit_attention_linear): 350 launches."""
+    attention runs inside its out projection (mt_dit_attention_linear): 351 launches."""
     HID, HEADS, LAT, BLOCKS, STEPS = 1024, 16, 64, 8, 10
     g = torch.Generator(device=dev)
     g.manual_seed(5)
@@ -503,19 +506,24 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
     i = torch.arange(32, device=dev, dtype=torch.float32)
     invf = (1.0 / torch.pow(torch.tensor(1e4, device=dev), 2.0 * i / 64.0)).float()
     y = torch.randn(LAT, device=dev)
-    hist, cemb = torch.randn(LAT, device=dev), torch.randn(HID, device=dev)
-    temb = torch.randn(STEPS, HID, device=dev)
+    hist, cemb = torch.randn(LAT, device=dev), torch.zeros(1, HID, device=dev)
+    z = torch.randn(1, H, device=dev)
+    cond_w, cond_b = w(HID, H), w(HID)
+    sched = mt.FlowSchedule.timesteps(STEPS)
+    temb = mt.time_embeddings((w(HID, 256), w(HID)), (w(HID, HID), w(HID)), sched)
     x = torch.zeros(6, HID, device=dev)
     qkv = torch.zeros(6, 3 * HID, device=dev)
     att = torch.zeros(6, HID, device=dev)
     ff = torch.zeros(6, 4 * HID, device=dev)
     pred = torch.zeros(6, LAT, device=dev)
     cs = torch.cuda.Stream(device=dev)
-    sched = [k / STEPS for k in range(STEPS + 1)]
+    dts = [float(sched[k + 1] - sched[k]) for k in range(STEPS)]
+    torch.cuda.synchronize()
 
     def step():
+        mt.linear(z, cond_w, cemb, 1, bias=cond_b, stream=cs.cuda_stream)
         for k in range(STEPS):
-            mt.flow_assemble(y, hist, cemb, cb, temb[k], xw, xb, x, stream=cs.cuda_stream)
+            mt.flow_assemble(y, hist, cemb[0], cb, temb[k], xw, xb, x, stream=cs.cuda_stream)
             for p in blocks:
                 mt.linear(x, p["qkv"], qkv, 6, bias=p["qkv_b"], norm=p["n1"], stream=cs.cuda_stream)
                 if fused:
@@ -529,7 +537,7 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
                           stream=cs.cuda_stream)
                 mt.linear(ff, p["ff2"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=cs.cuda_stream)
             mt.linear(x, fin_w, pred, 6, bias=fin_b, norm=fin_n, stream=cs.cuda_stream)
-            mt.flow_euler(y, pred, 2, 5, 2.0, sched[k + 1] - sched[k], stream=cs.cuda_stream)
+            mt.flow_euler(y, pred, 2, 5, 2.0, dts[k], stream=cs.cuda_stream)
 
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(cs):
@@ -549,7 +557,8 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
         best = ms if best is None else min(best, ms)
     wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
     return dict(us_per_generation_step=best * 1e3, us_per_ode_step=best * 1e3 / STEPS,
-                launches=STEPS * (3 + (4 if fused else 5) * BLOCKS), weight_mb_per_ode_step=wbytes / 1e6,
+                launches=1 + STEPS * (3 + (4 if fused else 5) * BLOCKS), weight_mb_per_ode_step=wbytes / 1e6,
+                schedule="EPSS 10 steps, sway -1",
                 attention="inside the out projection" if fused else "separate launch")
 
 

@@ -587,3 +587,6 @@ class WeightArena:
         result = build(arena)
         arena.upload(device)
         return result, arena
+
+
+from .flow import FlowSchedule, time_embeddings  # noqa: E402  (host side of the flow sampler)

@@ -20,6 +20,9 @@ Contents (reference paths relative to the reference checkout):
 * ``rope_interleaved`` / ``dit_attention_f64`` / ``flow_assemble_f64`` / ``flow_euler_f64``
   -- the DiT flow step around its linears: Shaders.swift:598-693 and the CPU reference of
   KernelTests.swift:282-318.
+* ``flow_timesteps_f64`` / ``sinusoid_f64`` / ``time_mlp_f64`` -- the flow sampler's
+  schedule and timestep embedding (Sources/MingTTS/Engine/DiT.swift:55-80) and the time-MLP
+  precompute (Sources/MingTTS/Engine/Engine.swift:186-198), in fp64 closed form.
 * ``upsample4_f64`` / ``istft_frame_f64`` / ``istft_emit_f64`` -- the VAE decoder's tail:
   Shaders.swift:697-790 and the CPU references of KernelTests.swift:322-398.
 """
@@ -405,6 +408,42 @@ def flow_euler_f64(y, pred, pred_row: int, null_row: int, cfg: float, dt: float)
     c = np.asarray(pred[pred_row], np.float64)
     u = np.asarray(pred[null_row], np.float64)
     return np.asarray(y, np.float64) + (c + (c - u) * cfg) * dt, np.concatenate([c, u])
+
+
+# ------------------------------------------------ flow schedule --
+
+# EPSS base timesteps in 32nds per step count, DiT.swift:58-62.
+EPSS_32NDS = {
+    5: (0, 2, 4, 8, 16, 32), 6: (0, 2, 4, 6, 8, 16, 32), 7: (0, 2, 4, 6, 8, 16, 24, 32),
+    10: (0, 2, 4, 6, 8, 12, 16, 20, 24, 28, 32), 12: (0, 2, 4, 6, 8, 10, 12, 14, 16, 20, 24, 28, 32),
+    16: (0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 28, 32),
+}
+
+
+def flow_timesteps_f64(steps: int) -> np.ndarray:
+    """FlowSchedule.timesteps (DiT.swift:57-65) in fp64 closed form: the sway -1 map
+    t - (cos(pi/2 t) - 1 + t) equals 1 - cos(pi/2 t), applied to the EPSS grid for the
+    listed step counts and to the uniform grid k / steps otherwise."""
+    if steps in EPSS_32NDS:
+        base = np.asarray(EPSS_32NDS[steps], np.float64) / 32.0
+    else:
+        base = np.arange(steps + 1, dtype=np.float64) / steps
+    return 1.0 - np.cos(np.pi / 2 * base)
+
+
+def sinusoid_f64(t: float, width: int = 256, scale: float = 1000.0) -> np.ndarray:
+    """FlowSchedule.sinusoid (DiT.swift:67-79) in fp64: [sin(a_i), cos(a_i)] for
+    a_i = scale t exp(-i ln(1e4) / (width/2 - 1)), i < width / 2."""
+    half = width // 2
+    a = scale * float(t) * np.exp(-np.arange(half, dtype=np.float64) * math.log(10000.0) / (half - 1))
+    return np.concatenate([np.sin(a), np.cos(a)])
+
+
+def time_mlp_f64(sinus, w1, b1, w2, b2, wt: int) -> np.ndarray:
+    """The time MLP of precomputeTimeEmbeddings (Engine.swift:186-198) on given sinusoid rows:
+    SiLU(x W1^T + b1) into an fp32 buffer, then W2^T + b2; fp64 per op.  Returns float64."""
+    mid = linear_np64(np.asarray(sinus, np.float64), w1, None, wt, b1, None, BIAS | SILU).astype(np.float32)
+    return linear_np64(mid, w2, None, wt, b2, None, BIAS)
 
 
 # --------------------------------------------------------- VAE tail --

@@ -2,7 +2,8 @@
 the reference's own known-answer case (KernelTests.swift:282-318) and other shapes,
 flow_assemble and flow_euler against the oracle, and one whole flow step (assembly, DiT
 blocks of the reference's flow head shape -- hidden 1024, 16 heads, 2 x 3 rows -- final
-layer, Euler update; Engine.swift:395-402, DiT.swift:35-52) against an fp64 chain."""
+layer, Euler update; Engine.swift:395-402, DiT.swift:35-52) against an fp64 chain, the time
+MLP precompute (Engine.swift:186-198), and the whole 10-step ODE loop of the EPSS schedule."""
 import numpy as np
 import pytest
 import torch
@@ -221,6 +222,91 @@ def test_flow_step_matches_fp64_chain(gpu, fused):
     x0 = O.flow_assemble_f64(y0, hist, cemb, cb, temb, xw, xb, O.BF16)
     want_x, want_pred, want_y = oracle_flow_step(blocks, final, x0, invf, y0, cfg, dt)
     for got, want, what in ((x, want_x, "hidden"), (pred, want_pred, "velocity"), (y, want_y, "latent")):
+        g = got.cpu().numpy()
+        assert np.all(np.isfinite(g)), what
+        rel = O.normwise_rel_err(g, want)
+        assert rel <= 1e-3, f"{what}: normwise {rel:.3g}"
+
+
+def test_time_embeddings_match_fp64(gpu):
+    """MingEngine.precomputeTimeEmbeddings (Engine.swift:186-198): the 10-step schedule's
+    sinusoids through time1 (256 -> 1024, SiLU) and time2 (1024 -> 1024) at M = 10, on the
+    GPU through mt.time_embeddings, against the fp64 time MLP on the same sinusoid rows."""
+    rng = np.random.default_rng(31)
+    w1 = O.round16(rng.standard_normal((HID, 256)).astype(np.float32) * np.float32(0.02), O.BF16)[0]
+    b1 = O.round16(rng.standard_normal(HID).astype(np.float32) * np.float32(0.02), O.BF16)[0]
+    w2 = O.round16(rng.standard_normal((HID, HID)).astype(np.float32) * np.float32(0.02), O.BF16)[0]
+    b2 = O.round16(rng.standard_normal(HID).astype(np.float32) * np.float32(0.02), O.BF16)[0]
+    ts = mt.FlowSchedule.timesteps(10)
+    b16 = lambda a: dev16(a, O.BF16, gpu)
+    say("time embeddings: 10 sinusoids through the time MLP")
+    temb = mt.time_embeddings((b16(w1), b16(b1)), (b16(w2), b16(b2)), ts)
+    torch.cuda.synchronize()
+    got = temb.cpu().numpy()
+    assert got.shape == (10, HID)
+    want = O.time_mlp_f64(mt.FlowSchedule.sinusoids(ts[:10]), w1, b1, w2, b2, O.BF16)
+    assert O.normwise_rel_err(got, want) <= 1e-5
+
+
+def test_flow_ode_loop_matches_fp64_chain(gpu):
+    """The flow stage of one generation step (MingEngine.encodeStep, Engine.swift:387-402): the
+    cond embedder on the LLM row (896 -> 1024, M = 1), then the 10 ODE steps of the EPSS
+    schedule with sway -- assemble with that step's time embedding, 2 DiT blocks of the flow
+    head's shape, final norm + linear, the CFG Euler step with dt = t[k+1] - t[k] and the
+    velocity captured per step -- against the same loop as an fp64 chain (fp32 between ops)."""
+    rng = np.random.default_rng(41)
+    blocks = dit_weights(2, 41)
+    bf = lambda *shape, s=0.02: O.round16(rng.standard_normal(shape).astype(np.float32) * np.float32(s), O.BF16)[0]
+    final = dict(norm=O.round16((1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32), O.BF16)[0],
+                 w=bf(LAT, HID), b=bf(LAT))
+    xw, xb = bf(HID, LAT, s=0.05), bf(HID, s=0.05)
+    cw, cbias = bf(HID, 896), bf(HID, s=1.0)
+    w1, b1, w2, b2 = bf(HID, 256), bf(HID), bf(HID, HID), bf(HID)
+    z = rng.standard_normal((1, 896)).astype(np.float32)
+    y0 = rng.standard_normal(LAT).astype(np.float32)
+    hist = rng.standard_normal(LAT).astype(np.float32)
+    invf = invf_1e4()
+    cfg = 2.0
+    ts = mt.FlowSchedule.timesteps(10)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    b16 = lambda a: dev16(a, O.BF16, gpu)
+    dw = [{k: b16(v) for k, v in p.items()} for p in blocks]
+    x = torch.zeros(6, HID, device=gpu)
+    qkv = torch.zeros(6, 3 * HID, device=gpu)
+    ff = torch.zeros(6, 4 * HID, device=gpu)
+    pred = torch.zeros(6, LAT, device=gpu)
+    cemb = torch.zeros(1, HID, device=gpu)
+    vel = torch.zeros(10, 2 * LAT, device=gpu)
+    y = t(y0.copy())
+    invf_d = t(invf)
+    say("flow ODE loop: time MLP, cond embedder, 10 steps x (assemble, 2 DiT blocks, final, euler)")
+    temb = mt.time_embeddings((b16(w1), b16(b1)), (b16(w2), b16(b2)), ts)
+    mt.linear(t(z), b16(cw), cemb, 1, bias=b16(cbias))
+    lin = lambda xx, w, out, flags=0, bias=None, norm=None: mt.linear(xx, w, out, 6, flags=flags, bias=bias, norm=norm)
+    for k in range(10):
+        mt.flow_assemble(y, t(hist), cemb[0], b16(cbias), temb[k], b16(xw), b16(xb), x)
+        for d in dw:
+            lin(x, d["qkv"], qkv, bias=d["qkv_b"], norm=d["norm1"])
+            mt.dit_attention_linear(qkv, 2, 3, HEADS, invf_d, d["out"], x, flags=mt.GemvFlags.accumulate,
+                                    bias=d["out_b"])
+            lin(x, d["ff1"], ff, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"])
+            lin(ff, d["ff2"], x, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])
+        lin(x, b16(final["w"]), pred, bias=b16(final["b"]), norm=b16(final["norm"]))
+        mt.flow_euler(y, pred, 2, 5, cfg, float(ts[k + 1] - ts[k]), capture=vel[k])
+    torch.cuda.synchronize()
+
+    temb_o = O.time_mlp_f64(mt.FlowSchedule.sinusoids(ts[:10]), w1, b1, w2, b2, O.BF16).astype(np.float32)
+    cemb_o = O.linear_np64(z, cw, None, O.BF16, cbias, None, O.BIAS).astype(np.float32)[0]
+    yo = y0.copy()
+    vel_o = []
+    for k in range(10):
+        x0 = O.flow_assemble_f64(yo, hist, cemb_o, cbias, temb_o[k], xw, xb, O.BF16)
+        _, pred_o, _ = oracle_flow_step(blocks, final, x0, invf, yo, cfg, 0.0)
+        y1, cap = O.flow_euler_f64(yo, pred_o, 2, 5, cfg, float(ts[k + 1] - ts[k]))
+        yo = y1.astype(np.float32)
+        vel_o.append(cap)
+    for got, want, what in ((temb, temb_o, "temb"), (cemb, cemb_o[None], "cemb"), (vel, np.stack(vel_o), "velocity"),
+                            (y, yo, "latent")):
         g = got.cpu().numpy()
         assert np.all(np.isfinite(g)), what
         rel = O.normwise_rel_err(g, want)
