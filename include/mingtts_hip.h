@@ -17,6 +17,7 @@
  *
  * Reference interfaces replaced (paths relative to the reference checkout):
  *   mt_linear            Encoder.linear            Sources/MingTTS/Engine/Kernels.swift:128-161
+ *   mt_rmsnorm           Encoder.rmsnorm           Sources/MingTTS/Engine/Kernels.swift:163-171
  *   mt_gemv_params       GemvParams                Sources/MingTTS/Engine/Shaders.swift:39
  *   MT_BIAS .. MT_SILU   GemvFlags                 Sources/MingTTS/Engine/Kernels.swift:21-28
  *   mt_linear_kernel     Kernels.usesGemm + the    Sources/MingTTS/Engine/Kernels.swift:81-86,
@@ -136,6 +137,17 @@ int mt_linear_static(const void *x, mt_dtype xt, const void *w, const void *w2, 
  */
 int mt_linear_rmsnorm(const void *x, mt_dtype xt, const void *norm, const void *w, const void *w2,
                       mt_dtype wt, const void *bias, float *y, mt_gemv_params p, mt_stream_t stream);
+
+/*
+ * Encoder.rmsnorm (Kernels.swift:163-171, Shaders.swift:414-440) on its own: y = x *
+ * rsqrt(mean(x^2) + eps) * g over `rows` rows of `width` fp32 values (row strides ldx, ldy),
+ * g [width] of type wt (MT_BF16 or MT_F16).  For normalised rows that are read as data (the
+ * backbone's final norm, Qwen.swift:94); before a linear use mt_linear_rmsnorm.  width and
+ * the strides multiples of 4, x and y 16-byte aligned, g 8-byte aligned; y is x (same
+ * stride) or apart from it.
+ */
+int mt_rmsnorm(const float *x, uint32_t ldx, uint32_t rows, uint32_t width, const void *g, mt_dtype wt, float *y,
+               uint32_t ldy, float eps, mt_stream_t stream);
 
 /* The kernel family mt_linear runs for a shape under the current tuning, the analogue of
  * Kernels.usesGemm and scalarRowsMax: M <= MT_TUNE_GEMV_ROWS_MAX (8) -> the GEMV, except

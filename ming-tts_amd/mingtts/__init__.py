@@ -28,7 +28,7 @@ SEQ_GENERAL, SEQ_DECODE_LAYER = 0, 1
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
-    "mt_linear", "mt_linear_static", "mt_linear_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
+    "mt_linear", "mt_linear_static", "mt_linear_rmsnorm", "mt_rmsnorm", "mt_linear_kernel", "mt_set_tuning", "mt_seq_create",
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_kernel", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_rope_attention", "mt_dit_attention", "mt_dit_attention_linear", "mt_flow_assemble",
@@ -112,6 +112,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_linear_static.restype = i32
     L.mt_linear_rmsnorm.argtypes = [vp, i32, vp, vp, vp, i32, vp, vp, GemvParams, vp]
     L.mt_linear_rmsnorm.restype = i32
+    L.mt_rmsnorm.argtypes = [vp, u32, u32, u32, vp, i32, vp, u32, f32, vp]
+    L.mt_rmsnorm.restype = i32
     L.mt_linear_kernel.argtypes = [u32, u32, u32, i32, i32]
     L.mt_linear_kernel.restype = i32
     L.mt_set_tuning.argtypes = [i32, i32]
@@ -253,6 +255,17 @@ def linear(x, w, y, M=None, flags=0, w2=None, bias=None, ldx=None, ldy=None, nor
                                  eps, stream))
     else:
         check(linear_raw(x, dtype_code(x), w, w2, dtype_code(w), bias, y, M, N, K, ldx, ldy, flags, stream))
+
+
+def rmsnorm_raw(x, ldx, rows, width, g, wt, y, ldy, eps=1e-6, stream=None) -> int:
+    """mt_rmsnorm on raw pointers / tensors; returns the raw return code."""
+    return load().mt_rmsnorm(_ptr(x), ldx, rows, width, _ptr(g), wt, _ptr(y), ldy, eps, _stream(stream))
+
+
+def rmsnorm(x, g, y, rows=None, eps=1e-6, stream=None) -> None:
+    """y[:rows] = x[:rows] * rsqrt(mean(x^2) + eps) * g (mt_rmsnorm); torch tensors, g [width]."""
+    rows = x.shape[0] if rows is None else rows
+    check(rmsnorm_raw(x, x.stride(0), rows, g.shape[0], g, dtype_code(g), y, y.stride(0), eps, stream))
 
 
 def linear_kernel(M, N, K, xt=F32, wt=BF16) -> int:
@@ -473,6 +486,11 @@ class Encoder:
         check(linear_raw(x.ptr(), dtype_code(x.buffer), linear.w.ptr(), gate.ptr() if gate else None, wt,
                          linear.bias.ptr() if linear.bias else None, y.ptr(), rows, linear.n, linear.k, x.ld, y.ld,
                          flags, self.stream))
+
+    def rmsnorm(self, x: ActView, rows: int, width: int, weight: GPUTensor, y: ActView, eps: float = 1e-6) -> None:
+        """Encoder.rmsnorm (Kernels.swift:163-171)."""
+        check(rmsnorm_raw(x.ptr(), x.ld, rows, width, weight.ptr(), weight.elem_type(), y.ptr(), y.ld, eps,
+                          self.stream))
 
 
 # ----------------------------------------------------------- weight path --
