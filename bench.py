@@ -562,14 +562,10 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
                 attention="inside the out projection" if fused else "separate launch")
 
 
-def bench_vae_latent(torch, mt, dev, ws, reps=5, fused=True):
-    """One latent of the streaming VAE decoder (VAEDecoder.decodeDispatches, VAEDecoder.swift:
-    81-107) after fc1: upsample4, the 24-layer sliding-window Qwen stack at M = 4 rows (rmsnorm
-    + qkv, rope_cache, attention over the last 65 keys, o +=, rmsnorm + gate|up, down +=; the
-    backbone's synthetic fp16 weights stand in for the VAE stack's, same shapes), the 3530 x
-    896 spectrum head, istft_frames (nfft 3528) and istft_emit (4 hops): 148 launches,
-    captured in a HIP graph and replayed.  With ``fused`` each layer's rope_cache and
-    attention run as one mt_rope_attention launch: 124 launches."""
+def vae_latent_graph(torch, mt, dev, ws, fused=True):
+    """The VAE latent of bench_vae_latent captured in a HIP graph on its own stream; returns
+    (graph, stream, launches, the tensors the graph reads and writes, to be kept alive while
+    it is replayed)."""
     HQ, HKV, CAP, NFFT, HOP, RING = 14, 2, 512, 3528, 882, 8
     pos0 = 4 * 50
     g = torch.Generator(device=dev)
@@ -619,15 +615,89 @@ def bench_vae_latent(torch, mt, dev, ws, reps=5, fused=True):
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
-    ev = Events(torch)
-    best = None
-    for _ in range(reps):
-        ev.start()
-        graph.replay()
-        ms = ev.stop_ms()
-        best = ms if best is None else min(best, ms)
-    return dict(us_per_latent=best * 1e3, launches=1 + (5 if fused else 6) * len(ws) + 3,
-                audio_ms_per_latent=4 * HOP / 44100 * 1e3)
+    keep = (h, frames, qkv, att, mlp, spec, head_w, head_b, caches, invf, window, cos_table, ring, pcm)
+    return graph, cs, 1 + (5 if fused else 6) * len(ws) + 3, keep
+
+
+def bench_vae_latent(torch, mt, dev, ws, reps=5, fused=True):
+    """One latent of the streaming VAE decoder (VAEDecoder.decodeDispatches, VAEDecoder.swift:
+    81-107) after fc1: upsample4, the 24-layer sliding-window Qwen stack at M = 4 rows (rmsnorm
+    + qkv, rope_cache, attention over the last 65 keys, o +=, rmsnorm + gate|up, down +=; the
+    backbone's synthetic fp16 weights stand in for the VAE stack's, same shapes), the 3530 x
+    896 spectrum head, istft_frames (nfft 3528) and istft_emit (4 hops): 148 launches,
+    captured in a HIP graph and replayed.  With ``fused`` each layer's rope_cache and
+    attention run as one mt_rope_attention launch: 124 launches."""
+    graph, cs, launches, keep = vae_latent_graph(torch, mt, dev, ws, fused)
+    us = graph_us_replay(torch, graph, cs, reps)
+    del graph
+    return dict(us_per_latent=us, launches=launches, audio_ms_per_latent=4 * 882 / 44100 * 1e3)
+
+
+def graph_us_replay(torch, graph, stream, rounds=5) -> float:
+    """Median replay time (us) of an already captured graph on `stream`, HIP events on it."""
+    times = []
+    with torch.cuda.stream(stream):
+        for _ in range(rounds):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+    return 1e3 * sorted(times)[len(times) // 2]
+
+
+def bench_paired(torch, mt, dev, ws, rounds=7, M=2):
+    """The paired step of the reference (MingEngine.encodeStep, Engine.swift:377-385;
+    QwenForward.encodePaired, Qwen.swift:103-115; timed paired against serial by QwenBench,
+    QwenBench.swift:135-154): the LLM token's decode step and the VAE frames of an earlier
+    latent issued together.  Here: the decode step (one persistent launch of the 24 layers'
+    96 linears at M = 2) on one stream and the VAE latent (the graph of bench_vae_latent) on
+    a second stream that starts with it; serial: the same two back to back on one stream.
+    Medians over `rounds`, each bracketed by HIP events on the first stream."""
+    graph, _, _, keep = vae_latent_graph(torch, mt, dev, ws)
+    resid = torch.randn(M, H, device=dev)
+    qkv = torch.zeros(M, QKV, device=dev)
+    mlp = torch.zeros(M, INTER, device=dev)
+    x0 = resid.clone()
+    seq = mt.Seq(decode_ops(mt, ws, M, resid, qkv, mlp))
+    sa = torch.cuda.Stream(device=dev)
+    sb = torch.cuda.Stream(device=dev)
+
+    def timed(paired: bool) -> float:
+        with torch.cuda.stream(sa):
+            resid.copy_(x0)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            if paired:
+                sb.wait_event(a)
+            seq.run(sa)
+            if paired:
+                with torch.cuda.stream(sb):
+                    graph.replay()
+                    done = torch.cuda.Event()
+                    done.record()
+                sa.wait_event(done)
+            else:
+                graph.replay()
+            b.record()
+        b.synchronize()
+        return a.elapsed_time(b)
+
+    timed(False)
+    timed(True)
+    serial, paired = [], []
+    for _ in range(rounds):
+        serial.append(timed(False))
+        paired.append(timed(True))
+    seq.check()
+    seq.close()
+    del graph
+    med = lambda v: 1e3 * sorted(v)[len(v) // 2]
+    return dict(serial_us=med(serial), paired_us=med(paired), saved_us=med(serial) - med(paired),
+                decode="persistent decode step, 24 layers, M = 2", vae="VAE latent graph, 124 launches")
 
 
 def bench_copy(torch, dev, mib=1024, reps=5):
@@ -835,6 +905,9 @@ def main() -> int:
         log("VAE decode of one latent (24-layer stack at M = 4, head, ISTFT; graph replay)")
         line["vae_latent"] = {k: (round(v, 3) if isinstance(v, float) else v)
                               for k, v in bench_vae_latent(torch, mt, dev, ws).items()}
+        log("LLM decode step paired with a VAE latent on two streams, and serial")
+        line["llm_vae_paired"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                  for k, v in bench_paired(torch, mt, dev, ws).items()}
     if not args.no_cpu:
         log("CPU baseline (oracle, host cores)")
         cb = cpu_baseline(torch, ws)
