@@ -6,8 +6,8 @@
 //     gate|up 2 x 4864 x 896, SiLU-gate, RMSNorm     (Qwen.swift:90)
 //     down     896 x 4864, += residual               (Qwen.swift:91)
 // at M = 1, 2 or 4 rows.  It runs the dataflow of seq_kernel (tagged activation words, one
-// 512-thread workgroup per CU, every wave computing a share of every op, two workgroup
-// barriers per op) with every op's shape known at compile time:
+// workgroup per CU, every wave computing a share of every op, two workgroup barriers per op)
+// with every op's shape known at compile time, on 7 waves (448 threads):
 //   - each op class has a fixed tiling (below); a wave's tile range, its lanes' weight and
 //     activation addresses are computed once at kernel start, so per op a wave adds one
 //     64-bit base to a lane offset and issues its weight tiles with immediate offsets;
@@ -15,14 +15,17 @@
 //     neighbours' blocks and skips their MFMAs), so the number of loads in flight behind
 //     the activations is the same on every path and the wait for the activations waits
 //     for nothing issued after them;
-//   - the epilogue flags are constants; no lane-divergent branch surrounds a load.
+//   - the epilogue flags are constants; no lane-divergent branch surrounds a load;
+//   - the weight tiles of later ops are requested in batches spread over the layer's four
+//     ops (the kernel's schedule), each batch issued after the op's output stores, so no
+//     op's burst of tile loads delays another op's activations or stores.
 // Tiling (v_mfma_f32_16x16x32: A = 16 weight rows x 32 k, one 16-byte chunk per lane; B =
 // 32 k x 16 columns of activations as hi + lo halves of the weights' 16-bit type; see
 // seq_tiles.hpp for the segment interleave):
-//   qkv     S = 2 K-segments per row tile, 8 features, the 14 block steps split over the 8 waves;
-//   o, down S = 4 (M <= 2) or 2 (M = 4), 16 / S features, block steps split over the 8 waves;
-//   gate|up S = 1, three row tiles of 8 gate rows and the same features' 8 up rows; waves
-//           0-2, 3-5 and 6-7 split the 28 block steps of row tiles 0, 1 and 2.
+//   qkv     S = 2 K-segments per row tile, 8 features, its 14 block steps 2 per wave;
+//   o, down S = 4 (M <= 2) or 2 (M = 4), 16 / S features, block steps split over the 7 waves;
+//   gate|up S = 1, three row tiles of 8 gate rows and the same features' 8 up rows; the
+//           84 block steps of the three row tiles in runs of 12 per wave.
 // A wave's partial sums go to its own slot of the op class's LDS area; one lane per output
 // adds the 8 slots in slot order (slots no wave writes stay zero), so results are the same
 // on every run.  A workgroup owns features [g N / G, (g + 1) N / G) of every op, which the
