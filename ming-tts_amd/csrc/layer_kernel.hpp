@@ -17,8 +17,8 @@
 //     for nothing issued after them;
 //   - the epilogue flags are constants; no lane-divergent branch surrounds a load;
 //   - the weight tiles of later ops are requested in batches spread over the layer's four
-//     ops (the kernel's schedule), each batch issued after the op's output stores, so no
-//     op's burst of tile loads delays another op's activations or stores.
+//     ops (the kernel's schedule), each issued where it delays the fewest activation polls
+//     and output stores (see lay_step).
 // Tiling (v_mfma_f32_16x16x32: A = 16 weight rows x 32 k, one 16-byte chunk per lane; B =
 // 32 k x 16 columns of activations as hi + lo halves of the weights' 16-bit type; see
 // seq_tiles.hpp for the segment interleave):
@@ -244,12 +244,21 @@ __device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A
 }
 
 // One op of class C (descriptor d; ops[i] holds its full descriptor for an external x): A
-// holds its weight tiles.  `issue` requests this op's share of later ops' weight tiles, right
-// behind its activations: they land while this op computes and waits.
-template <int WT, int M, int C, int NA, class ISSUE>
+// holds its weight tiles.  `issue` requests this op's share of later ops' weight tiles (NB
+// loads per wave).  A CU's vector-memory requests are served in order, so a batch holds up
+// whatever is requested after it until it has drained: issued after the output stores, it
+// holds up the next op's activation polls; issued as soon as the activations are current, it
+// holds up this op's stores unless it drains during the conversion and the MFMAs.  The
+// normed ops (qkv, gate|up) at M <= 2 issue theirs early: the norm's reductions give them
+// the longest window (decode step at M = 2: 421 -> 395.5 us; M = 1: 389 -> 341 us, A/B on
+// one box).  Early batches from o or at M = 4 measured slower (o: +28 us at M = 2; M = 4:
+// +40 to +110 us), so they stay behind the stores.
+template <int WT, int M, int C, uint32_t NB, int NA, class ISSUE>
 __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restrict__ ops, uint32_t i, const LayOp &d,
                                          const u32x4 (&A)[NA], ISSUE &&issue) {
     typedef LCls<C, M> L;
+    constexpr bool EARLY = L::NORM && M <= 2;
+    static_assert(NB < 16, "a batch fits the explicit wait below");
     const uint32_t tid = cx.tid, lane = cx.lane;
     const uint32_t r0 = cx.r0[C], nr = cx.nr[C];
     const bool xext = (d.flags & LAY_XEXT) != 0;
@@ -322,6 +331,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
                 if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
         }
     }
+    if constexpr (EARLY) issue();
     // Convert into the staging: tag bit cleared, x^2 summed per row, gain applied, split
     // into hi + lo halves of the weights' type.
     const uint32_t clear = xext ? ~0u : ~1u;
@@ -379,11 +389,11 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
         default: lay_mma<WT, M, C, 6>(cx, A); break;
     }
     __syncthreads();  // every wave's partial sums are in LDS
-    // The op's own loads (x, gain, bias, old y) have landed long before this point, and no
-    // other load is in flight: waiting for them here, where it costs nothing, spares a wait for
-    // a load whose value some lanes never use where its registers are next written (the next
-    // op's activation loads, behind this op's tile batch).
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // The op's own loads (x, gain, bias, old y) have landed long before this point, and the
+    // only later requests are an early batch: waiting for the rest here, where it costs
+    // nothing, spares a wait for a load whose value some lanes never use where its registers
+    // are next written (the next op's activation loads, behind this op's tile batch).
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (EARLY ? NB : 0u));  // vmcnt(NB) or vmcnt(0)
 
     // Outputs: the 8 slots summed in slot order, norm scale, epilogue, tagged store.
     if (live) {
@@ -436,9 +446,9 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
             *reinterpret_cast<__attribute__((address_space(1))) float *>(
                 reinterpret_cast<uintptr_t>(d.y + static_cast<size_t>(om) * d.ldy + n)) = v;
     }
-    // Later ops' weight tiles, behind this op's output stores: they drain while the next op's
-    // activations are being produced by the other workgroups.
-    issue();
+    // Otherwise later ops' weight tiles go behind this op's output stores: they drain while
+    // the next op's activations are being produced by the other workgroups.
+    if constexpr (!EARLY) issue();
 }
 
 // The kernel: n_ops = 4 L ops in the layer pattern (the host checks shapes, flags and G);
@@ -521,6 +531,9 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
     typedef LCls<LC_GU, M> LG;
     typedef LCls<LC_DOWN, M> LD;
     constexpr uint32_t G1 = LG::TA / 3, G2 = 2 * LG::TA / 3, D1 = LD::TA / 6, D2 = 2 * LD::TA / 6, Q1 = LQ::TA / 2;
+    // Loads per wave of each op's batch.
+    constexpr uint32_t NBQ = (G2 - G1) + D1, NBO = (LG::TA - G2) + (D2 - D1), NBG = (LD::TA - D2) + Q1,
+                       NBD = G1 + (LQ::TA - Q1) + LO::TA;
     u32x4 PQ[LQ::TA], PO[LO::TA], PG[LG::TA], PD[LD::TA];
     const uint32_t L = n_ops / 4;
     if (L > 0) {
@@ -537,22 +550,22 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
         // every op requests the same number of tiles.
         const uint32_t i = 4 * l, nx = l + 1 < L ? i + 4 : 0;
         dn = lops[i + 1];
-        lay_step<WT, M, LC_QKV>(cx, ops, i, dq, PQ, [&]() {
+        lay_step<WT, M, LC_QKV, NBQ>(cx, ops, i, dq, PQ, [&]() {
             lay_tiles<WT, M, LC_GU, G1, G2>(cx, lops[i + 2], PG);
             lay_tiles<WT, M, LC_DOWN, 0, D1>(cx, lops[i + 3], PD);
         });
         dq = lops[i + 2];
-        lay_step<WT, M, LC_O>(cx, ops, i + 1, dn, PO, [&]() {
+        lay_step<WT, M, LC_O, NBO>(cx, ops, i + 1, dn, PO, [&]() {
             lay_tiles<WT, M, LC_GU, G2, LG::TA>(cx, dq, PG);
             lay_tiles<WT, M, LC_DOWN, D1, D2>(cx, lops[i + 3], PD);
         });
         dn = lops[i + 3];
-        lay_step<WT, M, LC_GU>(cx, ops, i + 2, dq, PG, [&]() {
+        lay_step<WT, M, LC_GU, NBG>(cx, ops, i + 2, dq, PG, [&]() {
             lay_tiles<WT, M, LC_DOWN, D2, LD::TA>(cx, dn, PD);
             lay_tiles<WT, M, LC_QKV, 0, Q1>(cx, lops[nx], PQ);
         });
         dq = lops[nx];
-        lay_step<WT, M, LC_DOWN>(cx, ops, i + 3, dn, PD, [&]() {
+        lay_step<WT, M, LC_DOWN, NBD>(cx, ops, i + 3, dn, PD, [&]() {
             lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[nx + 2], PG);
             lay_tiles<WT, M, LC_QKV, Q1, LQ::TA>(cx, dq, PQ);
             lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[nx + 1], PO);
