@@ -789,10 +789,11 @@ def main() -> int:
     ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
-    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm"], default="all",
+    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill"], default="all",
                     help="decode: only the linear decode step; layer: it and the decode step with attention; "
                          "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
-                         "gemm: only the prefill and DiT GEMM stacks")
+                         "gemm: only the prefill and DiT GEMM stacks; prefill: only the prefill stack at --rows")
+    ap.add_argument("--rows", type=int, default=512, help="with --only prefill: the prompt rows M")
     ap.add_argument("--vs-blas", action="store_true",
                     help="with --only gemm: also time each prefill linear alone (graph replay) "
                          "next to hipBLASLt on the same shapes")
@@ -813,6 +814,11 @@ def main() -> int:
     log("generating 24 layers of fp16 weights")
     ws = make_layers(torch, dev)
     torch.cuda.synchronize()
+    if args.only == "prefill":
+        log(f"prefill stack M={args.rows}")
+        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
+                          for k, v in bench_prefill(torch, mt, dev, ws, args.rows).items()}), flush=True)
+        return 0
     if args.only == "gemm":
         out = {"prefill": [], "dit_head": None}
         for M in (64, 256, 512):
