@@ -5,7 +5,8 @@
 //     o        896 x 896, += residual                (Qwen.swift:88)
 //     gate|up 2 x 4864 x 896, SiLU-gate, RMSNorm     (Qwen.swift:90)
 //     down     896 x 4864, += residual               (Qwen.swift:91)
-// at M = 1, 2 or 4 rows.  It runs the dataflow of seq_kernel (tagged activation words, one
+// at M = 1, 2 or 4 rows, optionally with the layer's decode attention (rope_cache + attention,
+// Qwen.swift:86-87) as an item between qkv and o (ATT: then 5 ops per layer).  It runs the dataflow of seq_kernel (tagged activation words, one
 // workgroup per CU, every wave computing a share of every op, two workgroup barriers per op)
 // with every op's shape known at compile time, on 7 waves (448 threads):
 //   - each op class has a fixed tiling (below); a wave's tile range, its lanes' weight and
@@ -451,13 +452,31 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     if constexpr (!EARLY) issue();
 }
 
-// The kernel: n_ops = 4 L ops in the layer pattern (the host checks shapes, flags and G);
-// their packed descriptors follow the n_ops op descriptors.
+// The decode attention item of a layer (the general kernel's attend_item on this kernel's 7
+// waves): its (row, head) pairs, M 14 of them, go to workgroups g, g + G, ...; the x staging
+// is the item's scratch.  Every other workgroup goes straight on to o, whose activations
+// are this item's output.
 template <int WT, int M>
+__device__ __forceinline__ void lay_attention(LayCtx<WT, M> &cx, const SeqOp &o, uint32_t g, uint32_t G) {
+    const uint32_t hq = o.heads & 0xFFFFu, items = M * hq;
+    float *scratch = reinterpret_cast<float *>(cx.xs);
+    for (uint32_t it = g; it < items; it += G) {
+        if (o.cache_t == DT_F32)
+            attend_item<DT_F32, LAY_CW>(o, it / hq, it % hq, cx.rsrc, cx.parity, scratch, cx.gave_up, cx.sync);
+        else
+            attend_item<DT_F16, LAY_CW>(o, it / hq, it % hq, cx.rsrc, cx.parity, scratch, cx.gave_up, cx.sync);
+    }
+}
+
+// The kernel: n_ops = 4 L ops in the layer pattern, or 5 L with attention items (ATT) (the host
+// checks shapes, flags and G); their packed descriptors follow the n_ops op descriptors.
+template <int WT, int M, bool ATT>
 __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
                                                            uint32_t *sync, const uint32_t *tags, uint32_t tag_bytes) {
     typedef LayCtx<WT, M> X;
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2 * X::PLANE];
+    // The x staging; with attention items also their scratch (5120 floats).
+    constexpr uint32_t XS = ATT && 2 * X::PLANE < 10240 ? 10240u : 2 * X::PLANE;
+    __shared__ __attribute__((aligned(16))) uint16_t xs[XS];
     __shared__ __attribute__((aligned(16))) float p_qkv[LCls<LC_QKV, M>::PART];
     __shared__ __attribute__((aligned(16))) float p_o[LCls<LC_O, M>::PART];
     __shared__ __attribute__((aligned(16))) float p_gu[LCls<LC_GU, M>::PART];
@@ -535,11 +554,12 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
     constexpr uint32_t NBQ = (G2 - G1) + D1, NBO = (LG::TA - G2) + (D2 - D1), NBG = (LD::TA - D2) + Q1,
                        NBD = G1 + (LQ::TA - Q1) + LO::TA;
     u32x4 PQ[LQ::TA], PO[LO::TA], PG[LG::TA], PD[LD::TA];
-    const uint32_t L = n_ops / 4;
+    constexpr uint32_t A = ATT ? 1u : 0u, OPL = 4 + A;  // ops per layer: qkv, [attention,] o, gate|up, down
+    const uint32_t L = n_ops / OPL;
     if (L > 0) {
         lay_tiles<WT, M, LC_QKV, 0, LQ::TA>(cx, lops[0], PQ);
-        lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[1], PO);
-        lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[2], PG);
+        lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[1 + A], PO);
+        lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[2 + A], PG);
     }
     __syncthreads();
     // Each op's packed descriptor is read one op ahead (scalar loads), so no op waits for
@@ -548,27 +568,29 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
     for (uint32_t l = 0; l < L; l++) {
         // The last layer's requests for a next layer read layer 0's weights again (unused), so
         // every op requests the same number of tiles.
-        const uint32_t i = 4 * l, nx = l + 1 < L ? i + 4 : 0;
-        dn = lops[i + 1];
+        const uint32_t i = OPL * l, nx = l + 1 < L ? i + OPL : 0;
+        const uint32_t io = i + 1 + A, ig = i + 2 + A, id = i + 3 + A;  // o, gate|up, down
+        dn = lops[io];
         lay_step<WT, M, LC_QKV, NBQ>(cx, ops, i, dq, PQ, [&]() {
-            lay_tiles<WT, M, LC_GU, G1, G2>(cx, lops[i + 2], PG);
-            lay_tiles<WT, M, LC_DOWN, 0, D1>(cx, lops[i + 3], PD);
+            lay_tiles<WT, M, LC_GU, G1, G2>(cx, lops[ig], PG);
+            lay_tiles<WT, M, LC_DOWN, 0, D1>(cx, lops[id], PD);
         });
-        dq = lops[i + 2];
-        lay_step<WT, M, LC_O, NBO>(cx, ops, i + 1, dn, PO, [&]() {
+        if constexpr (ATT) lay_attention<WT, M>(cx, ops[i + 1], g, G);
+        dq = lops[ig];
+        lay_step<WT, M, LC_O, NBO>(cx, ops, io, dn, PO, [&]() {
             lay_tiles<WT, M, LC_GU, G2, LG::TA>(cx, dq, PG);
-            lay_tiles<WT, M, LC_DOWN, D1, D2>(cx, lops[i + 3], PD);
+            lay_tiles<WT, M, LC_DOWN, D1, D2>(cx, lops[id], PD);
         });
-        dn = lops[i + 3];
-        lay_step<WT, M, LC_GU, NBG>(cx, ops, i + 2, dq, PG, [&]() {
+        dn = lops[id];
+        lay_step<WT, M, LC_GU, NBG>(cx, ops, ig, dq, PG, [&]() {
             lay_tiles<WT, M, LC_DOWN, D2, LD::TA>(cx, dn, PD);
             lay_tiles<WT, M, LC_QKV, 0, Q1>(cx, lops[nx], PQ);
         });
         dq = lops[nx];
-        lay_step<WT, M, LC_DOWN, NBD>(cx, ops, i + 3, dn, PD, [&]() {
-            lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[nx + 2], PG);
+        lay_step<WT, M, LC_DOWN, NBD>(cx, ops, id, dn, PD, [&]() {
+            lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[nx + 2 + A], PG);
             lay_tiles<WT, M, LC_QKV, Q1, LQ::TA>(cx, dq, PQ);
-            lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[nx + 1], PO);
+            lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[nx + 1 + A], PO);
         });
     }
     // The last workgroup out advances the epoch for the next run.

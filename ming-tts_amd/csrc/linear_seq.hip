@@ -57,7 +57,7 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, bool layer, SeqPl
     bool attn = false;
     for (uint32_t i = 0; i < n_ops; i++) attn = attn || ops[i].kind == SEQ_ATTN;
     if (layer) {
-        p->fn = layer_kernel_fn(wt, m_all);
+        p->fn = layer_kernel_fn(wt, m_all, attn);
         p->layer = true;
         p->threads = LAY_THREADS;
     } else if (attn) {

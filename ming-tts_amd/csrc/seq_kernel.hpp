@@ -359,17 +359,19 @@ __device__ __forceinline__ float wave_sum_bfly(float v) { return group_sum(v, 64
 //     (rescaled when the maximum grows).  At the end the workgroup maximum rescales every
 //     thread's part, and the parts meet in LDS in a fixed order.
 // The head's output row is stored as tagged words (and to the user buffer when final).
-// Uses lds (floats) as scratch: 5120 words.
-template <int CT>
+// NW: the workgroup's waves (8 key groups each).  Uses lds (floats) as scratch: 5120 words.
+template <int CT, int NW = CW>
 __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t h, __amdgpu_buffer_rsrc_t rsrc,
                                             uint32_t parity, float *lds, bool &gave_up, uint32_t *sync) {
+    static_assert(NW == 7 || NW == 8, "the final sums are written out for 7 or 8 waves");
+    constexpr int KG = 8 * NW;  // key groups of 8 lanes
     // The thread index is made opaque here, so nothing derived from it is hoisted out of
     // the sequence's op loop (where it would hold registers through every linear op).
     uint32_t tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const uint32_t lane = tid & 63, w = tid >> 6;
     constexpr int KU = CT == DT_F32 ? 4 : 8;  // keys per thread per chunk
-    constexpr int CH = 64 * KU;                // keys per chunk
+    constexpr int CH = KG * KU;                // keys per chunk
     constexpr int WV = CT == DT_F32 ? 2 : 1;   // 16-byte loads per 8 elements
     const uint32_t hq = o.heads & 0xFFFFu, hkv = o.heads >> 16;
     const uint32_t kvh = h / (hq / hkv);
@@ -394,7 +396,7 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     auto chunk_loads = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < KU; u++) {
-            const int t = min(c0 + kq + 64 * u, nk - 1);  // past the keys: a valid row, unused
+            const int t = min(c0 + kq + KG * u, nk - 1);  // past the keys: a valid row, unused
             const size_t e = kvbase + static_cast<size_t>(t) * 64 + 8 * r;
 #pragma unroll
             for (int q = 0; q < WV; q++) {
@@ -485,7 +487,7 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
         if (c0 > 0) chunk_loads(c0);
 #pragma unroll
         for (int u = 0; u < KU; u++) {
-            const int t = c0 + kq + 64 * u;
+            const int t = c0 + kq + KG * u;
             if (t < nk) {  // the 8 lanes of a key group agree
                 float kf[8], vf[8];
                 if (j0 + t == pos) {
@@ -522,7 +524,7 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     __syncthreads();
     mx = red[0];
 #pragma unroll
-    for (int ww = 1; ww < CW; ww++) mx = fmaxf(mx, red[ww]);
+    for (int ww = 1; ww < NW; ww++) mx = fmaxf(mx, red[ww]);
     const float f = expf(m - mx);  // 0 for a thread without keys (m = -inf)
     const float ls = wave_sum_bfly(r == 0 ? l * f : 0.0f);
     if (lane == 0) red[8 + w] = ls;
@@ -540,8 +542,9 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     if (tid < 64) {
         float a = part2[tid];
 #pragma unroll
-        for (int k = 1; k < 8; k++) a += part2[k * 64 + tid];
-        const float sum = ((red[8] + red[9]) + (red[10] + red[11])) + ((red[12] + red[13]) + (red[14] + red[15]));
+        for (int k = 1; k < NW; k++) a += part2[k * 64 + tid];
+        const float sum = NW == 8 ? ((red[8] + red[9]) + (red[10] + red[11])) + ((red[12] + red[13]) + (red[14] + red[15]))
+                                  : ((red[8] + red[9]) + (red[10] + red[11])) + ((red[12] + red[13]) + red[14]);
         const float v = sum > 0.0f ? a / sum : 0.0f;
         const uint32_t n = h * 64 + tid;
         st_tag(o.tag + static_cast<size_t>(b) * o.N + n, v, parity);
@@ -926,6 +929,7 @@ typedef void (*seq_fn)(const SeqOp *, uint32_t, uint32_t *, const uint32_t *, ui
 // for two rows when m2.
 seq_fn seq_attn_kernel(int wt, bool m2);
 // The decode-layer kernel (linear_layer.hip) for weights wt at M rows (1, 2 or 4), or null.
-seq_fn layer_kernel_fn(int wt, uint32_t M);
+seq_fn layer_kernel_fn(int wt, uint32_t M, bool att);
+seq_fn layer_attn_kernel_fn(int wt, uint32_t M);
 
 }  // namespace mt

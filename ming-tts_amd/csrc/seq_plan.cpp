@@ -257,9 +257,14 @@ int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups) {
 }
 
 bool layer_pattern(const SeqOp *ops, uint32_t n, int groups) {
-    if (n == 0 || n % 4 || groups < LAY_GMIN || groups > LAY_GMAX) return false;
+    if (n < 2 || groups < LAY_GMIN || groups > LAY_GMAX) return false;
     const uint32_t M = ops[0].M;
     if (M != 1 && M != 2 && M != 4) return false;
+    // With attention items every layer is qkv, attention, o, gate|up, down; the item's rows are
+    // the plan's M and its heads the backbone's 14 q / 2 kv (o's K = 14 x 64).
+    const bool att = ops[1].kind == SEQ_ATTN;
+    const uint32_t per = att ? 5 : 4;
+    if (n % per) return false;
     struct Want {
         uint32_t N, K, flags;
         bool norm;
@@ -270,7 +275,13 @@ bool layer_pattern(const SeqOp *ops, uint32_t n, int groups) {
                           {LAY_H, LAY_I, F_ACCUM, false}};
     for (uint32_t i = 0; i < n; i++) {
         const SeqOp &o = ops[i];
-        const Want &c = want[i % 4];
+        uint32_t j = i % per;
+        if (att && j == 1) {
+            if (o.kind != SEQ_ATTN || o.M != M || o.heads != (14u | (2u << 16)) || o.N != LAY_H) return false;
+            continue;
+        }
+        if (att && j > 1) j--;
+        const Want &c = want[j];
         if (o.kind != SEQ_LINEAR || o.M != M || o.N != c.N || o.K != c.K || o.flags != c.flags ||
             (o.norm != nullptr) != c.norm || ((o.flags & F_BIAS) != 0) != (o.bias != nullptr))
             return false;

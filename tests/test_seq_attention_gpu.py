@@ -128,6 +128,48 @@ def test_layers_match_fp64_oracle(gpu, layers, B, cap, cache_np, window, pos):
             np.testing.assert_array_equal(vg[b][:, keep], v0[l][b][:, keep])
 
 
+@pytest.mark.parametrize("B,cache_np", [(2, np.float16), (1, np.float32)])
+def test_decode_layer_kernel_with_attention_matches_general_kernel(gpu, B, cache_np):
+    """Whole decode layers at the backbone's shapes run the decode-layer kernel with its
+    attention items; MT_TUNE_SEQ_LAYER = 1 runs the same plan on the general kernel.  They
+    split K and sum the attention's key groups differently (7 waves against 8), so they agree
+    to fp32 rounding; the new cache rows agree to the cache type's rounding."""
+    layers, cap = 6, 512
+    pos = [441, 338][:B]
+    outs = {}
+    for mode in (0, 1):
+        ws, x0, kcs, vcs, k0, v0, resid, qkv, att, mlp, pos_d, invf, invf_d = _setup(layers, B, cap, 53, cache_np,
+                                                                                    gpu, pos)
+        old = mt.set_tuning(mt.TUNE_SEQ_LAYER, mode)
+        try:
+            seq = mt.Seq(layer_items(ws, B, resid, qkv, att, mlp, kcs, vcs, pos_d, invf_d, cap))
+        finally:
+            mt.set_tuning(mt.TUNE_SEQ_LAYER, old)
+        say(f"seq+attention B={B} mode {mode} kernel {seq.kernel} groups {seq.groups}")
+        assert seq.kernel == (mt.SEQ_DECODE_LAYER if mode == 0 else mt.SEQ_GENERAL)
+        runs = []
+        for _ in range(2):
+            for l in range(layers):
+                kcs[l].copy_(torch.from_numpy(k0[l]))
+                vcs[l].copy_(torch.from_numpy(v0[l]))
+            resid.copy_(torch.from_numpy(x0))
+            seq.run()
+            torch.cuda.synchronize()
+            runs.append([t.cpu().numpy().copy() for t in (resid, qkv, att, mlp)] +
+                        [np.stack([k.cpu().numpy() for k in kcs]).astype(np.float64)])
+        seq.check()
+        seq.close()
+        for a, b in zip(runs[0], runs[1]):
+            np.testing.assert_array_equal(a, b)
+        outs[mode] = runs[0]
+    want = oracle_layers(ws, x0, B, k0, v0, pos, invf, 0, cache_np)
+    for j, what in enumerate(("resid", "qkv", "attention", "mlp")):
+        assert O.normwise_rel_err(outs[0][j], want[j]) <= 1e-3, what
+        assert O.normwise_rel_err(outs[0][j], outs[1][j].astype(np.float64)) <= 1e-4, what
+    tol = 2e-3 if cache_np == np.float16 else 1e-5
+    np.testing.assert_allclose(outs[0][4], outs[1][4], rtol=tol, atol=tol)
+
+
 def test_layers_equal_separate_launches_and_rerun_bit_exact(gpu):
     """The fused layers against the same step as separate launches (another kernel and
     summation order for every part: fp32 rounding apart), and re-runs of the plan bit for
