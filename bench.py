@@ -633,6 +633,72 @@ def bench_vae_latent(torch, mt, dev, ws, reps=5, fused=True):
     return dict(us_per_latent=us, launches=launches, audio_ms_per_latent=4 * 882 / 44100 * 1e3)
 
 
+def bench_vae_latent_seq(torch, mt, dev, ws, reps=7):
+    """The VAE latent of bench_vae_latent with its 24-layer stack as one persistent launch:
+    upsample4, the stack at M = 4 rows of one sequence (rmsnorm + qkv, RoPE + cache append +
+    attention over the last 65 keys as an attention item, o +=, rmsnorm + gate|up, down +=:
+    120 items), the spectrum head, istft_frames and istft_emit: 5 launches on one stream
+    (the cooperative launch is not captured in a graph), timed with HIP events on it."""
+    HQ, HKV, CAP, NFFT, HOP, RING = 14, 2, 512, 3528, 882, 8
+    pos0 = 4 * 50
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    h = [torch.randn(H, generator=g, device=dev) for _ in range(3)]
+    frames = torch.zeros(4, H, device=dev)
+    qkv = torch.zeros(4, QKV, device=dev)
+    att = torch.zeros(4, HQ * 64, device=dev)
+    mlp = torch.zeros(4, INTER, device=dev)
+    spec = torch.zeros(4, NFFT + 2, device=dev)
+    head_w = (torch.randn(NFFT + 2, H, generator=g, device=dev) * 0.02).half()
+    head_b = (torch.randn(NFFT + 2, generator=g, device=dev) * 0.02).half()
+    caches = [(torch.randn(HKV, CAP, 64, generator=g, device=dev).half(),
+               torch.randn(HKV, CAP, 64, generator=g, device=dev).half()) for _ in ws]
+    i = torch.arange(32, device=dev, dtype=torch.float32)
+    invf = (1.0 / torch.pow(torch.tensor(1e6, device=dev), 2.0 * i / 64.0)).float()
+    t = torch.arange(NFFT, device=dev, dtype=torch.float64)
+    window = (0.5 - 0.5 * torch.cos(2 * torch.pi * t / NFFT)).float()
+    cos_table = torch.cos(2 * torch.pi * t / NFFT).float()
+    ring = torch.zeros(RING, NFFT, device=dev)
+    pcm = torch.zeros(4 * HOP, device=dev)
+    pos_d = torch.arange(pos0, pos0 + 4, device=dev, dtype=torch.int32)
+    items = []
+    for p, (kc, vc) in zip(ws, caches):
+        items.append(mt.op(frames, p["qkv"], qkv, 4, bias=p["qkv_b"], norm=p["norm1"]))
+        items.append(mt.attn_op(qkv, 4, HQ, HKV, pos_d, kc, vc, CAP, 0, invf, att, window=65))
+        items.append(mt.op(att, p["o"], frames, 4, flags=mt.GemvFlags.accumulate))
+        items.append(mt.op(frames, p["gate"], mlp, 4, flags=mt.GemvFlags.siluGate, w2=p["up"], norm=p["norm2"]))
+        items.append(mt.op(mlp, p["down"], frames, 4, flags=mt.GemvFlags.accumulate))
+    seq = mt.Seq(items)
+    cs = torch.cuda.Stream(device=dev)
+    s = cs.cuda_stream
+
+    def step():
+        mt.upsample4(h[0], h[1], h[2], frames, stream=s)
+        seq.run(s)
+        mt.linear(frames, head_w, spec, 4, bias=head_b, stream=s)
+        mt.istft_frames(spec, 4, NFFT, cos_table, window, ring, 4 * 50, RING, stream=s)
+        mt.istft_emit(ring, window, NFFT, HOP, 4 * 50 * HOP, 4 * HOP, 4 * 50 + 3, RING, pcm, stream=s)
+
+    times = []
+    with torch.cuda.stream(cs):
+        step()
+        torch.cuda.synchronize()
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            step()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+    seq.check()
+    kern = seq.kernel
+    seq.close()
+    return dict(us_per_latent=1e3 * sorted(times)[len(times) // 2], launches=5, items=len(items),
+                kernel="decode-layer kernel" if kern == mt.SEQ_DECODE_LAYER else "general sequence kernel",
+                audio_ms_per_latent=4 * HOP / 44100 * 1e3)
+
+
 def graph_us_replay(torch, graph, stream, rounds=5) -> float:
     """Median replay time (us) of an already captured graph on `stream`, HIP events on it."""
     times = []
@@ -911,6 +977,9 @@ def main() -> int:
         log("VAE decode of one latent (24-layer stack at M = 4, head, ISTFT; graph replay)")
         line["vae_latent"] = {k: (round(v, 3) if isinstance(v, float) else v)
                               for k, v in bench_vae_latent(torch, mt, dev, ws).items()}
+        log("VAE decode of one latent with the layer stack as one persistent launch")
+        line["vae_latent_persistent"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                         for k, v in bench_vae_latent_seq(torch, mt, dev, ws).items()}
         log("LLM decode step paired with a VAE latent on two streams, and serial")
         line["llm_vae_paired"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                   for k, v in bench_paired(torch, mt, dev, ws).items()}

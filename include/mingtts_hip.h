@@ -239,9 +239,13 @@ int mt_seq_create(const mt_linear_op *ops, uint32_t n_ops, mt_seq **out);
  * cache_len) (window 0 = unlimited; a pos[b] >= cache_len appends nothing), with scores
  * scaled by `scale`; out row b (stride ldo) gets the hq heads of 64.  qkv rows are
  * [q (hq*64) | k (hkv*64) | v (hkv*64)] at stride ldq; they are read, not modified (the
- * rotated q stays inside the kernel).  Requirements: as mt_rope_cache_decode and
- * mt_attention_decode; B <= 8; the caches of the sequence's attention items must not
- * overlap each other or any linear's x or y.
+ * rotated q stays inside the kernel).  With cache_stride 0 and B > 1 the rows are
+ * instead B consecutive positions of one sequence sharing one cache, pos[b] = pos[0] + b
+ * (mt_rope_attention's rows, as the VAE decoder's layers issue them): row b appends its k
+ * and v at pos[b] and attends over [max(0, pos[b] + 1 - window), pos[b]], rows 0 .. b - 1's
+ * new keys included.  Requirements: as mt_rope_cache_decode and mt_attention_decode (or
+ * mt_rope_attention for rows of one sequence); B <= 8; the caches of the sequence's
+ * attention items must not overlap each other or any linear's x or y.
  */
 typedef struct mt_attn_op {
     const float *qkv;

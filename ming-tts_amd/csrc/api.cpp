@@ -217,8 +217,10 @@ int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out
                 !aligned(a.v_cache, 16) || a.cache_stride % 8)
                 return set_error(MT_EINVAL, "%s: qkv, out and the caches must be 16-byte aligned with 16-byte row strides",
                                  who);
-            if (a.B > 1 && a.cache_stride < static_cast<uint64_t>(a.hkv) * a.cache_len * 64)
-                return set_error(MT_EINVAL, "%s: cache_stride smaller than one cache", who);
+            // Stride 0 with B > 1: rows of one sequence sharing one cache; otherwise one cache a row.
+            if (a.B > 1 && a.cache_stride != 0 && a.cache_stride < static_cast<uint64_t>(a.hkv) * a.cache_len * 64)
+                return set_error(MT_EINVAL, "%s: cache_stride smaller than one cache (0 for rows of one sequence)",
+                                 who);
         } else if (items[i].kind == MT_SEQ_LINEAR) {
             const mt_linear_op &o = items[i].linear;
             LinearArgs a;

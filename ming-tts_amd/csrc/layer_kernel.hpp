@@ -474,8 +474,8 @@ template <int WT, int M, bool ATT>
 __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
                                                            uint32_t *sync, const uint32_t *tags, uint32_t tag_bytes) {
     typedef LayCtx<WT, M> X;
-    // The x staging; with attention items also their scratch (5120 floats).
-    constexpr uint32_t XS = ATT && 2 * X::PLANE < 10240 ? 10240u : 2 * X::PLANE;
+    // The x staging; with attention items also their scratch (7168 floats).
+    constexpr uint32_t XS = ATT && 2 * X::PLANE < 14336 ? 14336u : 2 * X::PLANE;
     __shared__ __attribute__((aligned(16))) uint16_t xs[XS];
     __shared__ __attribute__((aligned(16))) float p_qkv[LCls<LC_QKV, M>::PART];
     __shared__ __attribute__((aligned(16))) float p_o[LCls<LC_O, M>::PART];

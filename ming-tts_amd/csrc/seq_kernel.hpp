@@ -354,12 +354,16 @@ __device__ __forceinline__ float wave_sum_bfly(float v) { return group_sum(v, 64
 //     k are rotated (NeoX pairs i, i + 32, angle = pos * inv_freq[i]); k and v, rounded to
 //     the cache type, are appended at pos by the first head of each kv group and used for
 //     key pos from LDS by every head, so no workgroup waits for another's cache write.
+//   - Rows of one sequence (a shared cache: cache_stride 0 with more than one row, at
+//     positions pos[0] + b, as mt_rope_attention's rows): row b also takes the keys at
+//     pos[0] .. pos - 1 from rows 0 .. b - 1 of the activations (rotated and rounded the same
+//     way), since those rows' items append them concurrently; older keys come from the cache.
 //   - Scores: the 8 lanes of a key group sum their dims by shuffles; each thread keeps a
 //     running maximum, the sum of exp(score - max) and the p-weighted v sum of its keys
 //     (rescaled when the maximum grows).  At the end the workgroup maximum rescales every
 //     thread's part, and the parts meet in LDS in a fixed order.
 // The head's output row is stored as tagged words (and to the user buffer when final).
-// NW: the workgroup's waves (8 key groups each).  Uses lds (floats) as scratch: 5120 words.
+// NW: the workgroup's waves (8 key groups each).  Uses lds (floats) as scratch: 7168 words.
 template <int CT, int NW = CW>
 __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t h, __amdgpu_buffer_rsrc_t rsrc,
                                             uint32_t parity, float *lds, bool &gave_up, uint32_t *sync) {
@@ -375,14 +379,20 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     constexpr int WV = CT == DT_F32 ? 2 : 1;   // 16-byte loads per 8 elements
     const uint32_t hq = o.heads & 0xFFFFu, hkv = o.heads >> 16;
     const uint32_t kvh = h / (hq / hkv);
-    float *sraw = lds;          // [192] q | k | v of the row, as read
+    float *sraw = lds;          // [64] q of the row, as read
     float *sq = lds + 192;      // [64] rotated q
-    float *skv = lds + 256;     // [128] k (rotated) | v at key pos, rounded to the cache type
     float *red = lds + 384;     // [16] wave maxima, then wave sums of the softmax denominators
     float *part = lds + 512;    // [64][64] p.v parts of the key groups
     float *part2 = lds + 4608;  // [8][64] sums of eight key groups
+    float *kvraw = lds + 5120;  // [8][128] k | v of the rows whose keys come from the activations
+    float *skv = lds + 6144;    // [8][128] those keys: k rotated | v, rounded to the cache type
 
     const uint32_t pos = gld(o.pos + b);
+    // Keys at positions pos0 .. pos come from rows 0 .. nnew - 1 of the activations: the row
+    // itself, or with a shared cache rows 0 .. b of the sequence.
+    const bool shared = o.cache_stride == 0 && o.M > 1;
+    const uint32_t pos0 = shared ? gld(o.pos) : pos;
+    const uint32_t nnew = shared ? b + 1 : 1u;
     const bool append = pos < o.cache_len;
     // Keys [j0, len): len = pos + 1 (the new key at pos comes from LDS), or the whole cache
     // when pos is past it.
@@ -428,13 +438,23 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     };
     chunk_loads(0);
 
-    // q head h, k and v heads kvh of row b: 48 chunks of 4 words.
-    if (tid < 48) {
-        const uint32_t pt = tid >> 4, c4 = 4 * (tid & 15);
-        const uint32_t col = (pt == 0 ? h * 64 : pt == 1 ? (hq + kvh) * 64 : (hq + hkv + kvh) * 64) + c4;
+    // q head h of row b (16 chunks of 4 words), then k and v heads kvh of each row the keys
+    // pos0 .. pos come from (32 chunks a row).
+    if (tid < 16 + 32 * nnew) {
+        uint32_t row = b, col;
+        float *dst;
+        if (tid < 16) {
+            col = h * 64 + 4 * tid;
+            dst = sraw + 4 * tid;
+        } else {
+            const uint32_t u = tid - 16, rr = u >> 5, pt = (u >> 4) & 1u, c4 = 4 * (u & 15);
+            row = shared ? rr : b;
+            col = (pt == 0 ? (hq + kvh) * 64 : (hq + hkv + kvh) * 64) + c4;
+            dst = kvraw + rr * 128 + pt * 64 + c4;
+        }
         u32x4 v;
         if (o.xsrc >= 0) {
-            const uint32_t off = (o.xoff + b * o.xld + col) * 4u;
+            const uint32_t off = (o.xoff + row * o.xld + col) * 4u;
             v = ldtag4(rsrc, off);
             uint32_t spins = 0;
             while (!tagged4(v, parity) && !gave_up) {
@@ -448,31 +468,37 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
             }
             v &= ~1u;
         } else {
-            v = gld(reinterpret_cast<const u32x4 *>(static_cast<const float *>(o.x) + static_cast<size_t>(b) * o.ldx + col));
+            v = gld(reinterpret_cast<const u32x4 *>(static_cast<const float *>(o.x) + static_cast<size_t>(row) * o.ldx + col));
         }
-        *reinterpret_cast<u32x4 *>(sraw + pt * 64 + c4) = v;
+        *reinterpret_cast<u32x4 *>(dst) = v;
     }
     __syncthreads();
     if (tid < 32) {
         const uint32_t i = tid;
-        const float angle = static_cast<float>(pos) * gld(o.inv_freq + i);
+        const float f = gld(o.inv_freq + i);
+        const float angle = static_cast<float>(pos) * f;
         const float c = cosf(angle), s = sinf(angle);
         const float q0 = sraw[i], q1 = sraw[i + 32];
         sq[i] = q0 * c - q1 * s;
         sq[i + 32] = q1 * c + q0 * s;
-        const float k0 = sraw[64 + i], k1 = sraw[96 + i];
-        const float r0 = cache_round<CT>(k0 * c - k1 * s), r1 = cache_round<CT>(k1 * c + k0 * s);
-        const float v0 = cache_round<CT>(sraw[128 + i]), v1 = cache_round<CT>(sraw[160 + i]);
-        skv[i] = r0;
-        skv[i + 32] = r1;
-        skv[64 + i] = v0;
-        skv[96 + i] = v1;
+        for (uint32_t rr = 0; rr < nnew; rr++) {
+            const float ar = static_cast<float>(pos0 + rr) * f;  // the row's own key: angle
+            const float cr = cosf(ar), sr = sinf(ar);
+            const float *kr = kvraw + rr * 128;
+            const float k0 = kr[i], k1 = kr[32 + i];
+            float *d = skv + rr * 128;
+            d[i] = cache_round<CT>(k0 * cr - k1 * sr);
+            d[i + 32] = cache_round<CT>(k1 * cr + k0 * sr);
+            d[64 + i] = cache_round<CT>(kr[64 + i]);
+            d[96 + i] = cache_round<CT>(kr[96 + i]);
+        }
         if (append && h % (hq / hkv) == 0) {
+            const float *d = skv + (nnew - 1) * 128;  // the row's own key
             const size_t dst = cbase + (static_cast<size_t>(kvh) * o.cache_len + pos) * 64;
-            cache_store<CT>(const_cast<uint16_t *>(o.w), dst + i, r0);
-            cache_store<CT>(const_cast<uint16_t *>(o.w), dst + i + 32, r1);
-            cache_store<CT>(const_cast<uint16_t *>(o.w2), dst + i, v0);
-            cache_store<CT>(const_cast<uint16_t *>(o.w2), dst + i + 32, v1);
+            cache_store<CT>(const_cast<uint16_t *>(o.w), dst + i, d[i]);
+            cache_store<CT>(const_cast<uint16_t *>(o.w), dst + i + 32, d[i + 32]);
+            cache_store<CT>(const_cast<uint16_t *>(o.w2), dst + i, d[64 + i]);
+            cache_store<CT>(const_cast<uint16_t *>(o.w2), dst + i + 32, d[96 + i]);
         }
     }
     __syncthreads();
@@ -490,11 +516,13 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
             const int t = c0 + kq + KG * u;
             if (t < nk) {  // the 8 lanes of a key group agree
                 float kf[8], vf[8];
-                if (j0 + t == pos) {
+                const uint32_t p = j0 + static_cast<uint32_t>(t);
+                if (p >= pos0) {  // a key from the activations
+                    const uint32_t rr = min(p - pos0, nnew - 1);
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
-                        kf[e] = skv[8 * r + e];
-                        vf[e] = skv[64 + 8 * r + e];
+                        kf[e] = skv[rr * 128 + 8 * r + e];
+                        vf[e] = skv[rr * 128 + 64 + 8 * r + e];
                     }
                 } else {
                     unpack(kraw[u], kf);
@@ -627,6 +655,13 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
             const SeqOp on = sdesc[next ? i + 1 : i];
             const SeqTiles sn = stile[next ? i + 1 : i];
             const WaveTiles wtn = swt[next ? i + 1 : i][w];
+            // The items' scratch is the next linear's staging: the 256 elements past its M K in
+            // each half, which its MFMAs read against zero weights when K is not a multiple of
+            // their blocks, are cleared (a scratch word's halves may read as a NaN).
+            if (g < items && next && on.kind == SEQ_LINEAR && tid < 64) {
+                const uint32_t e0 = on.M * on.K + 8 * (tid & 31);
+                *reinterpret_cast<u32x4 *>(&xs[tid >> 5][e0]) = u32x4{0u, 0u, 0u, 0u};
+            }
             gain_request(on, next, gr);
             if (wtn.n <= 2) tile_loads<2>(on, sn, wtn, An);
             else if (wtn.n <= 6) tile_loads<6>(on, sn, wtn, An);
