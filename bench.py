@@ -193,7 +193,7 @@ def bench_decode_seq(torch, mt, dev, ws, steps, warmup, M=2):
     nbytes = sum(op_bytes(o) for o in ops)
     flops = sum(op_flops(o) for o in ops)
     res = dict(groups=seq.groups, bytes=nbytes, flops=flops, times_ms=times, ops=len(ops),
-               kernel=("mt::layer_kernel<1, 2> (fp16 weights, M = 2, the Qwen2-0.5B decode-layer kernel)"
+               kernel=("mt::layer_kernel<1, 2, false> (fp16 weights, M = 2, the Qwen2-0.5B decode-layer kernel)"
                        if seq.kernel == mt.SEQ_DECODE_LAYER else
                        "mt::seq_kernel<1, 2, false> (fp16 weights, M = 2, linears only)")
                + "; one launch per decode step")
