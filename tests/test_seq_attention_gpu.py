@@ -95,6 +95,7 @@ def _setup(layers, B, cap, seed, cache_np, gpu, pos):
     (24, 2, 512, np.float16, 0, [100, 511]),      # 24 layers; the last cache slot
     (2, 2, 128, np.float32, 64, [127, 130]),      # fp32 cache, window 64, row 1 past the cache
     (3, 1, 256, np.float16, 0, [0]),              # one row at position 0 (one key)
+    (3, 4, 256, np.float16, 0, [10, 200, 255, 77]),   # four independent sequences (M = 4)
 ])
 def test_layers_match_fp64_oracle(gpu, layers, B, cap, cache_np, window, pos):
     say(f"seq+attention layers={layers} B={B} cap={cap} cache={np.dtype(cache_np).name} window={window} pos={pos}")

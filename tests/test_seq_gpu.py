@@ -14,14 +14,14 @@ pytestmark = pytest.mark.gpu
 H, QKV, INTER = 896, 1152, 4864
 
 
-def make_stack(layers: int, M: int, seed: int, device):
-    """Per-layer fp16 weights ~ N(0, 0.02^2) (qkv with bias, o, gate, up, down) and RMSNorm
-    gains ~ 1 + N(0, 0.1^2), seeded per layer from the SplitMix64 normal stream."""
+def make_stack(layers: int, M: int, seed: int, device, wt=O.F16):
+    """Per-layer 16-bit weights of type wt ~ N(0, 0.02^2) (qkv with bias, o, gate, up, down)
+    and RMSNorm gains ~ 1 + N(0, 0.1^2), seeded per layer from the SplitMix64 normal stream."""
     ws = []
     for l in range(layers):
         n = QKV * H + QKV + H * H + 2 * INTER * H + H * INTER
         z = O.gaussian(seed * 1000 + l, n, 0.02)
-        bits, _ = O.round16(z, O.F16)
+        bits, _ = O.round16(z, wt)
         o = 0
         parts = {}
         for name, size, shape in (("qkv", QKV * H, (QKV, H)), ("qkv_b", QKV, (QKV,)), ("o", H * H, (H, H)),
@@ -30,9 +30,9 @@ def make_stack(layers: int, M: int, seed: int, device):
             parts[name] = bits[o:o + size].reshape(shape)
             o += size
         gains = 1.0 + O.gaussian(seed * 1000 + 500 + l, 2 * H, 0.1)
-        parts["norm1"], _ = O.round16(gains[:H], O.F16)
-        parts["norm2"], _ = O.round16(gains[H:], O.F16)
-        parts["dev"] = {k: dev16(v, O.F16, device) for k, v in parts.items()}
+        parts["norm1"], _ = O.round16(gains[:H], wt)
+        parts["norm2"], _ = O.round16(gains[H:], wt)
+        parts["dev"] = {k: dev16(v, wt, device) for k, v in parts.items()}
         ws.append(parts)
     x0 = O.gaussian(seed + 7, M * H)
     return ws, x0.reshape(M, H)
@@ -52,18 +52,18 @@ def chain_ops(ws, M, resid, qkv, mlp):
     return ops
 
 
-def oracle_chain(ws, x0, M):
+def oracle_chain(ws, x0, M, wt=O.F16):
     """The same chain in fp64 per op, activations stored as fp32 between ops (as on the GPU)."""
     resid = x0.astype(np.float32).copy()
     qkv = mlp = None
     for p in ws:
-        qkv = O.linear_np64(O.rmsnorm_f64(resid, p["norm1"], O.F16), p["qkv"], None, O.F16, p["qkv_b"], None,
+        qkv = O.linear_np64(O.rmsnorm_f64(resid, p["norm1"], wt), p["qkv"], None, wt, p["qkv_b"], None,
                             0).astype(np.float32)
-        resid = O.linear_f64(np.ascontiguousarray(qkv[:, :H]), p["o"], None, O.F16, None, resid, M, H, H,
+        resid = O.linear_f64(np.ascontiguousarray(qkv[:, :H]), p["o"], None, wt, None, resid, M, H, H,
                              O.ACCUM).astype(np.float32)
-        mlp = O.linear_np64(O.rmsnorm_f64(resid, p["norm2"], O.F16), p["gate"], p["up"], O.F16, None, None,
+        mlp = O.linear_np64(O.rmsnorm_f64(resid, p["norm2"], wt), p["gate"], p["up"], wt, None, None,
                             O.SILU_GATE).astype(np.float32)
-        resid = O.linear_f64(mlp, p["down"], None, O.F16, None, resid, M, H, INTER, O.ACCUM).astype(np.float32)
+        resid = O.linear_f64(mlp, p["down"], None, wt, None, resid, M, H, INTER, O.ACCUM).astype(np.float32)
     return resid, qkv, mlp
 
 
@@ -131,6 +131,36 @@ def test_decode_layer_kernel_matches_general_kernel(gpu, layers, M):
         assert O.normwise_rel_err(g, want[j]) <= 1e-3, what
         if 1 in outs:
             assert O.normwise_rel_err(g, outs[1][j].astype(np.float64)) <= 1e-5, what
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_decode_layer_kernel_with_bf16_weights(gpu, M):
+    """The reference's checkpoints hold bf16 weights (Weights.swift): the decode-layer kernel's
+    bf16 instantiation (bf16 MFMA, the hi + lo split of x in bf16) against the fp64 chain on
+    the same bf16 weights and, at M <= 2, against the general kernel."""
+    ws, x0 = make_stack(3, M, 61 + M, gpu, wt=O.BF16)
+    resid, qkv, mlp = buffers(M, x0, gpu)
+    ops = chain_ops(ws, M, resid, qkv, mlp)
+    outs = {}
+    for mode in ((0, 1) if M <= 2 else (0,)):
+        old = mt.set_tuning(mt.TUNE_SEQ_LAYER, mode)
+        try:
+            seq = mt.Seq(ops)
+        finally:
+            mt.set_tuning(mt.TUNE_SEQ_LAYER, old)
+        say(f"seq bf16 M={M} mode {mode} kernel {seq.kernel}")
+        assert seq.kernel == (mt.SEQ_DECODE_LAYER if mode == 0 else mt.SEQ_GENERAL)
+        resid.copy_(torch.from_numpy(x0))
+        seq.run()
+        torch.cuda.synchronize()
+        seq.check()
+        seq.close()
+        outs[mode] = [t.cpu().numpy().copy() for t in (resid, qkv, mlp)]
+    want = oracle_chain(ws, x0, M, wt=O.BF16)
+    for j, what in enumerate(("resid", "qkv", "mlp")):
+        assert O.normwise_rel_err(outs[0][j], want[j]) <= 1e-3, what
+        if 1 in outs:
+            assert O.normwise_rel_err(outs[0][j], outs[1][j].astype(np.float64)) <= 1e-5, what
 
 
 def test_seq_deterministic_and_equal_to_per_op_launches(gpu):
