@@ -42,41 +42,44 @@ __device__ __forceinline__ void store1(void *base, size_t off, float v) {
     else static_cast<_Float16 *>(base)[off] = static_cast<_Float16>(v);
 }
 
-// Grid (ceil(slots / 2), rows); 64 threads: lane & 31 is the rotation pair, lane >> 5 picks
-// one of two head slots.  Slots: hq query heads, hkv key heads, hkv value heads.
+// One 256-thread workgroup per row: lane t & 31 is the rotation pair i, and the eight groups
+// of 32 lanes take the row's head slots (hq query heads, hkv key heads, hkv value heads) in
+// turn, so a lane forms cos and sin of its pair's angle (pos * inv_freq[i]) once for all the
+// heads it rotates, and each group reads and writes a head's 64 words in two coalesced
+// 128-byte halves.
 template <int CT>
-__global__ __launch_bounds__(64) void rope_cache_kernel(float *qkv, uint32_t ldq, uint32_t hq, uint32_t hkv,
-                                                        uint32_t pos0, const uint32_t *pos_arr, void *kc,
-                                                        void *vc, uint32_t cache_len, uint64_t cache_stride,
-                                                        const float *inv_freq) {
-    const uint32_t i = threadIdx.x & 31;
-    const uint32_t slot = blockIdx.x * 2 + (threadIdx.x >> 5);
-    const uint32_t m = blockIdx.y;
-    if (slot >= hq + 2 * hkv) return;
+__global__ __launch_bounds__(256) void rope_cache_kernel(float *qkv, uint32_t ldq, uint32_t hq, uint32_t hkv,
+                                                         uint32_t pos0, const uint32_t *pos_arr, void *kc,
+                                                         void *vc, uint32_t cache_len, uint64_t cache_stride,
+                                                         const float *inv_freq) {
+    const uint32_t i = threadIdx.x & 31, grp = threadIdx.x >> 5;
+    const uint32_t m = blockIdx.x;
     const uint32_t pos = pos_arr ? pos_arr[m] : pos0 + m;
     const uint64_t cbase = pos_arr ? static_cast<uint64_t>(m) * cache_stride : 0;
-    float *row = qkv + static_cast<size_t>(m) * ldq + static_cast<size_t>(slot) * 64;
     // A device-side position past the cache (only possible through pos_arr, which the host
     // cannot see) appends nothing; the query heads are still rotated.
-    if (slot >= hq && pos >= cache_len) return;
-    if (slot >= hq + hkv) {
-        const size_t dst = cbase + (static_cast<size_t>(slot - hq - hkv) * cache_len + pos) * 64;
-        store1<CT>(vc, dst + i, row[i]);
-        store1<CT>(vc, dst + i + 32, row[i + 32]);
-        return;
-    }
+    const bool append = pos < cache_len;
     const float angle = static_cast<float>(pos) * inv_freq[i];
     const float c = cosf(angle), s = sinf(angle);
-    const float x0 = row[i], x1 = row[i + 32];
-    const float r0 = x0 * c - x1 * s;
-    const float r1 = x1 * c + x0 * s;
-    if (slot < hq) {
-        row[i] = r0;
-        row[i + 32] = r1;
-    } else {
-        const size_t dst = cbase + (static_cast<size_t>(slot - hq) * cache_len + pos) * 64;
-        store1<CT>(kc, dst + i, r0);
-        store1<CT>(kc, dst + i + 32, r1);
+    float *row = qkv + static_cast<size_t>(m) * ldq;
+    for (uint32_t slot = grp; slot < hq + 2 * hkv; slot += 8) {
+        const float x0 = row[slot * 64 + i], x1 = row[slot * 64 + i + 32];
+        float r0, r1;
+        rope_rotate(x0, x1, c, s, r0, r1);
+        if (slot < hq) {
+            row[slot * 64 + i] = r0;
+            row[slot * 64 + i + 32] = r1;
+        } else if (!append) {
+            continue;
+        } else if (slot < hq + hkv) {
+            const size_t dst = cbase + (static_cast<size_t>(slot - hq) * cache_len + pos) * 64;
+            store1<CT>(kc, dst + i, r0);
+            store1<CT>(kc, dst + i + 32, r1);
+        } else {
+            const size_t dst = cbase + (static_cast<size_t>(slot - hq - hkv) * cache_len + pos) * 64;
+            store1<CT>(vc, dst + i, x0);
+            store1<CT>(vc, dst + i + 32, x1);
+        }
     }
 }
 
@@ -269,8 +272,8 @@ __global__ __launch_bounds__(ATT_THREADS) void rope_attention_kernel(float *qkv,
         const float c = cosf(angle), sn = sinf(angle);
         float *row = qkv + static_cast<size_t>(m) * ldq + static_cast<size_t>(h) * 64;
         const float x0 = row[i], x1 = row[i + 32];
-        const float r0 = x0 * c - x1 * sn;
-        const float r1 = x1 * c + x0 * sn;
+        float r0, r1;
+        rope_rotate(x0, x1, c, sn, r0, r1);
         row[i] = r0;
         row[i + 32] = r1;
         qs[i] = r0;
@@ -282,8 +285,8 @@ __global__ __launch_bounds__(ATT_THREADS) void rope_attention_kernel(float *qkv,
         const float angle = static_cast<float>(pos) * inv_freq[i];
         const float c = cosf(angle), sn = sinf(angle);
         const float x0 = row[i], x1 = row[i + 32];
-        const float r0 = x0 * c - x1 * sn;
-        const float r1 = x1 * c + x0 * sn;
+        float r0, r1;
+        rope_rotate(x0, x1, c, sn, r0, r1);
         const float *vrow = row + static_cast<size_t>(hkv) * 64;
         float k0 = r0, k1 = r1, v0 = vrow[i], v1 = vrow[i + 32];
         if constexpr (CT == DT_F16) {  // as the fp16 cache holds them
@@ -419,12 +422,12 @@ int launch_rope_attention(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, 
 int launch_rope_cache(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
                       const uint32_t *pos_arr, void *kc, void *vc, int ct, uint32_t cache_len,
                       uint64_t cache_stride, const float *inv_freq, hipStream_t stream) {
-    dim3 grid((hq + 2 * hkv + 1) / 2, rows);
+    const dim3 grid(rows);
     if (ct == DT_F32)
-        hipLaunchKernelGGL(rope_cache_kernel<DT_F32>, grid, dim3(64), 0, stream, qkv, ldq, hq, hkv, pos0, pos_arr,
+        hipLaunchKernelGGL(rope_cache_kernel<DT_F32>, grid, dim3(256), 0, stream, qkv, ldq, hq, hkv, pos0, pos_arr,
                            kc, vc, cache_len, cache_stride, inv_freq);
     else
-        hipLaunchKernelGGL(rope_cache_kernel<DT_F16>, grid, dim3(64), 0, stream, qkv, ldq, hq, hkv, pos0, pos_arr,
+        hipLaunchKernelGGL(rope_cache_kernel<DT_F16>, grid, dim3(256), 0, stream, qkv, ldq, hq, hkv, pos0, pos_arr,
                            kc, vc, cache_len, cache_stride, inv_freq);
     return check_launch("rope_cache");
 }

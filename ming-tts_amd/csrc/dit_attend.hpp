@@ -30,7 +30,9 @@ __device__ __forceinline__ void dit_rope_table(float freq, uint32_t S, float (&c
 
 // x_transformers interleaved rotary pair: (x, y) -> (x c - y s, y c + x s).
 __device__ __forceinline__ float2 dit_rope_pair(float2 v, float c, float s) {
-    return make_float2(v.x * c - v.y * s, v.y * c + v.x * s);
+    // The contraction written out, as rope_rotate does, so both kernels that inline this get
+    // the same bits.
+    return make_float2(fmaf(-v.y, s, v.x * c), fmaf(v.x, s, v.y * c));
 }
 
 // The lane's operands of one item: its q pair and the k and v pairs of the S keys.

@@ -89,6 +89,14 @@ __device__ __forceinline__ float octet_sum(float v) {
     return v + dpp_mov<0x141>(v);  // row_half_mirror
 }
 
+// NeoX rotation of the pair (x0, x1) by the angle whose cosine and sine are c and s: r0 =
+// x0 c - x1 s, r1 = x1 c + x0 s, with the contraction written out (the product x0 c or x1 c
+// rounded, then one fused multiply-add), so every kernel that rotates a pair gets its bits.
+__device__ __forceinline__ void rope_rotate(float x0, float x1, float c, float s, float &r0, float &r1) {
+    r0 = fmaf(-x1, s, x0 * c);
+    r1 = fmaf(x0, s, x1 * c);
+}
+
 // Sum over aligned groups of `width` lanes (8, 16, 32 or 64), the same bits in every lane of
 // a group: quad swaps and the half-row mirror on DPP (8), the row mirror (16), then
 // exchanges between rows.

@@ -479,16 +479,17 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
         const float angle = static_cast<float>(pos) * f;
         const float c = cosf(angle), s = sinf(angle);
         const float q0 = sraw[i], q1 = sraw[i + 32];
-        sq[i] = q0 * c - q1 * s;
-        sq[i + 32] = q1 * c + q0 * s;
+        rope_rotate(q0, q1, c, s, sq[i], sq[i + 32]);
         for (uint32_t rr = 0; rr < nnew; rr++) {
             const float ar = static_cast<float>(pos0 + rr) * f;  // the row's own key: angle
             const float cr = cosf(ar), sr = sinf(ar);
             const float *kr = kvraw + rr * 128;
             const float k0 = kr[i], k1 = kr[32 + i];
             float *d = skv + rr * 128;
-            d[i] = cache_round<CT>(k0 * cr - k1 * sr);
-            d[i + 32] = cache_round<CT>(k1 * cr + k0 * sr);
+            float r0, r1;
+            rope_rotate(k0, k1, cr, sr, r0, r1);
+            d[i] = cache_round<CT>(r0);
+            d[i + 32] = cache_round<CT>(r1);
             d[64 + i] = cache_round<CT>(kr[64 + i]);
             d[96 + i] = cache_round<CT>(kr[96 + i]);
         }

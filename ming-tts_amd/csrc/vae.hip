@@ -9,7 +9,7 @@
 // cos table; out = sum of overlapping frames / sum of their window^2.
 //
 // Layout on gfx950:
-//   - upsample4: one thread per (frame row, feature);
+//   - upsample4: one thread per feature, writing its four frame rows;
 //   - istft_frames: one 256-thread workgroup per (frame, 512 output samples): the frame's
 //     bins (re, im) and the cos table sit in LDS; a thread computes samples t and N - t in one
 //     pass over the bins, since cos(2 pi k (N - t) / N) = cos(2 pi k t / N) and the sine terms
@@ -25,18 +25,18 @@ namespace {
 
 constexpr int ISTFT_NMAX = 4096;   // nfft limit of the LDS tables
 
+// One thread per feature writes all four frame rows from one read of prev, cur and next.
 __global__ __launch_bounds__(256) void upsample4_kernel(const float *prev, const float *cur, const float *next,
                                                         float *frames, uint32_t ldf, uint32_t hidden, uint32_t has_prev,
                                                         uint32_t has_next) {
-    const uint32_t c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
     if (c >= hidden) return;
     const float h = cur[c];
-    float v;
-    if (r == 0) v = has_prev ? 0.625f * h + 0.375f * prev[c] : h;
-    else if (r == 1) v = has_prev ? 0.875f * h + 0.125f * prev[c] : h;
-    else if (r == 2) v = has_next ? 0.875f * h + 0.125f * next[c] : h;
-    else v = has_next ? 0.625f * h + 0.375f * next[c] : h;
-    frames[static_cast<size_t>(r) * ldf + c] = v;
+    const float p = has_prev ? prev[c] : h, n = has_next ? next[c] : h;
+    frames[c] = has_prev ? 0.625f * h + 0.375f * p : h;
+    frames[static_cast<size_t>(ldf) + c] = has_prev ? 0.875f * h + 0.125f * p : h;
+    frames[2 * static_cast<size_t>(ldf) + c] = has_next ? 0.875f * h + 0.125f * n : h;
+    frames[3 * static_cast<size_t>(ldf) + c] = has_next ? 0.625f * h + 0.375f * n : h;
 }
 
 // Samples t and N - t of frame blockIdx.y for t in [blockIdx.x * 512 / 2 ..): thread j takes
@@ -111,7 +111,7 @@ int mt_upsample4(const float *prev, const float *cur, const float *next, float *
     if (hidden == 0) return MT_OK;
     if (!cur || !frames) return set_error(MT_EINVAL, "mt_upsample4: null pointer");
     if (ldf < hidden) return set_error(MT_EINVAL, "mt_upsample4: ldf %u < hidden %u", ldf, hidden);
-    hipLaunchKernelGGL(upsample4_kernel, dim3((hidden + 255) / 256, 4), dim3(256), 0,
+    hipLaunchKernelGGL(upsample4_kernel, dim3((hidden + 255) / 256), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), prev ? prev : cur, cur, next ? next : cur, frames, ldf,
                        hidden, prev ? 1u : 0u, next ? 1u : 0u);
     return check_launch("upsample4");
