@@ -350,6 +350,32 @@ def bench_prefill(torch, mt, dev, ws, M, reps=3):
                 pct_attainable=100 * tflops / attainable, gflop=flops / 1e9, mbytes=nbytes / 1e6)
 
 
+def bench_prefill_chain(torch, mt, dev, ws, M, reps=3):
+    """The prefill chain with the reference's activation types (QwenForward.dispatches at M
+    prompt rows, Qwen.swift:84-91, its linears): fp32 residual and activations, RMSNorm fused
+    into qkv and gate|up, o reading the q part of qkv in place of the attention output, each
+    op consuming the previous op's fp32 output (x split into hi + lo halves of the weights'
+    type on the MFMA GEMM): 96 dependent launches captured in a HIP graph and replayed."""
+    resid = torch.randn(M, H, device=dev)
+    qkv = torch.zeros(M, QKV, device=dev)
+    mlp = torch.zeros(M, INTER, device=dev)
+    ops = decode_ops(mt, ws, M, resid, qkv, mlp)
+    L = mt.load()
+    cs = torch.cuda.Stream(device=dev)
+
+    def stack():
+        for o in ops:
+            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, cs.cuda_stream)
+            if rc:
+                raise RuntimeError(mt.last_error())
+
+    us = graph_us(torch, stack, cs, rounds=reps)
+    flops = sum(op_flops(o) for o in ops)
+    tflops = flops / (us * 1e-6) / 1e12
+    return dict(M=M, us=us, tflops=tflops, pct_mfma_peak=100 * tflops / MFMA_F16_PEAK_TFLOPS, gflop=flops / 1e9,
+                activations="fp32 (hi + lo halves on the MFMA: 2 MFMAs per product)", norms="fused")
+
+
 def bench_attention(torch, mt, dev, reps=200):
     """Batch-2 decode attention, 14 q / 2 kv heads, d 64, fp16 caches of 512, lengths ~ U[32, 512]:
     reps dispatches in one graph (the caches stay cache-resident, as the reference's layer loop
@@ -891,6 +917,11 @@ def main() -> int:
             log(f"prefill stack M={M}")
             out["prefill"].append({k: (round(v, 3) if isinstance(v, float) else v)
                                    for k, v in bench_prefill(torch, mt, dev, ws, M).items()})
+        out["prefill_chain"] = []
+        for M in (64, 256, 512):
+            log(f"prefill chain (fp32 activations, fused norms) M={M}")
+            out["prefill_chain"].append({k: (round(v, 3) if isinstance(v, float) else v)
+                                         for k, v in bench_prefill_chain(torch, mt, dev, ws, M).items()})
         log("DiT head")
         out["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
@@ -962,6 +993,11 @@ def main() -> int:
             log(f"prefill stack M={M}")
             line["prefill"].append({k: (round(v, 3) if isinstance(v, float) else v)
                                     for k, v in bench_prefill(torch, mt, dev, ws, M).items()})
+        line["prefill_chain"] = []
+        for M in (64, 256, 512):
+            log(f"prefill chain (fp32 activations, fused norms) M={M}")
+            line["prefill_chain"].append({k: (round(v, 3) if isinstance(v, float) else v)
+                                          for k, v in bench_prefill_chain(torch, mt, dev, ws, M).items()})
         log("decode attention batch 2")
         line["attention_decode"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                     for k, v in bench_attention(torch, mt, dev).items()}

@@ -167,11 +167,13 @@ enum {
     MT_TUNE_SEQ_GROUPS = 4,      /* workgroups of the persistent sequence kernel (0 = auto) */
     MT_TUNE_SEQ_LAUNCH = 5,      /* 0: cooperative launch (default); 1: ordinary launch, co-residency
                                     then rests on an otherwise idle device (profilers) */
-    MT_TUNE_GEMM_TILE = 6,       /* MFMA GEMM tile (x rows x weight rows) for activations of the
-                                    weights' type: 0 = auto, 1 = 128 x 128, 2 = 64 x 128, 3 = 64 x 64,
-                                    4 = the register-staged kernel that other activation types use */
-    MT_TUNE_GEMM_STAGES = 7,     /* loads of that GEMM: 2..4 = direct-to-LDS stages of 64 k, 1 = two
-                                    register-staged stages into two LDS buffers (0 = auto) */
+    MT_TUNE_GEMM_TILE = 6,       /* MFMA GEMM tile (x rows x weight rows) for fp32 activations and
+                                    activations of the weights' type: 0 = auto, 1 = 128 x 128,
+                                    2 = 64 x 128, 3 = 64 x 64, 4 = the register-staged 64 x 64 kernel
+                                    that the other activation types use, for every type */
+    MT_TUNE_GEMM_STAGES = 7,     /* loads of that GEMM for x of the weights' type: 2..4 = direct-to-LDS
+                                    stages of 64 k, 1 = two register-staged stages into two LDS
+                                    buffers (0 = auto; fp32 x always takes the latter) */
     MT_TUNE_GEMV_MFMA = 8,       /* the MFMA kernel that stages x once per 16 output features: 0 =
                                     for 3..16 rows (default; 3..8 with a fused norm), 1 = never
                                     (lane-group GEMV up to 8 rows, GEMM above), 2 = up to 64 rows of

@@ -282,7 +282,8 @@ gemm_fn pick_x(int xt, bool gated, bool norm) {
 }  // namespace
 
 int launch_gemm(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed) {
-    if (xt == wt && a.norm == nullptr && tuning().gemm_tile != 4) return launch_gemm_tiled(a, wt, stream, fixed);
+    if (((xt == wt && a.norm == nullptr) || xt == DT_F32) && tuning().gemm_tile != 4)
+        return launch_gemm_tiled(a, xt, wt, stream, fixed);
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool norm = a.norm != nullptr;
     gemm_fn fn = wt == DT_BF16 ? pick_x<DT_BF16>(xt, gated, norm) : pick_x<DT_F16>(xt, gated, norm);

@@ -165,14 +165,16 @@ int device_cus();
 // synchronising the stream, so it is not for use under graph capture once it must grow.
 int stream_workspace(hipStream_t stream, size_t part_bytes, uint32_t counters, void **part, uint32_t **cnt);
 
-// Pipelined MFMA GEMM for activations of the weights' type.
+// Pipelined MFMA GEMM for activations of the weights' type, or fp32 (split into hi + lo).
 struct TiledPlan {
     int shape;                // index of the (bm, bn) tile shape
     uint32_t bm, bn;          // x rows and weight rows per tile
     uint32_t tiles_m, tiles_n, splits, kps;
-    int stages;               // LDS pipeline depth (64-k stages)
+    int stages;               // LDS pipeline depth (64-k stages; 1: two register-staged buffers)
 };
-TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, int shape_override, int splitk_override);
-int launch_gemm_tiled(const LinearArgs &a, int wt, hipStream_t stream, const FixedWs *fixed = nullptr);
+TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, int shape_override, int splitk_override,
+                     bool split);
+// x of the weights' type without a norm, or fp32 x with or without one (a.norm).
+int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed = nullptr);
 
 }  // namespace mt

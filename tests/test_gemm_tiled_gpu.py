@@ -1,14 +1,15 @@
-"""The pipelined MFMA GEMM (activations of the weights' type) under every tile shape and
-forced split-K count, on ragged shapes, against the oracle's fp32 reference loop and fp64
-recomputation; split-K runs are re-run to show the arrival counters re-arm and the
-partial sums are added in a fixed order (bit-identical results)."""
+"""The pipelined MFMA GEMM under every tile shape and forced split-K count, on ragged shapes,
+against the oracle's fp32 reference loop and fp64 recomputation: activations of the weights'
+type, and fp32 activations split into hi + lo planes (with and without the fused RMSNorm);
+split-K runs are re-run to show the arrival counters re-arm and the partial sums are added
+in a fixed order (bit-identical results)."""
 import numpy as np
 import pytest
 import torch
 
 import mingtts as mt
 import oracle as O
-from _gpu_util import assert_linear_parity, expected, run_linear, say
+from _gpu_util import assert_linear_parity, dev16, expected, run_linear, say
 
 pytestmark = pytest.mark.gpu
 
@@ -93,6 +94,75 @@ def test_bf16(gpu, shape):
     c = _case(M + 3 * N + K, M, N, K, flags, bias, O.BF16)
     got, xu = _with_tuning(0, 0, lambda: run_linear(c, O.BF16, gpu))
     assert_linear_parity(got, *expected(c, xu), K, f"bf16 {_ids(shape)}")
+
+
+# fp32 x split into hi + lo halves represents x to 2^-22 (fp16) / 2^-17 (bf16) relative, so the
+# products stay within fp32 accumulation error of fp64; x rounded to 16 bits alone would sit
+# near 3e-4 and fail this bound.
+SPLIT_TOL = 2e-5
+
+
+@pytest.mark.parametrize("wt", [O.F16, O.BF16], ids=["wf16", "wbf16"])
+@pytest.mark.parametrize("splits", [0, 3])
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_fp32_activations_split_into_hi_and_lo(gpu, shape, tile, splits, wt):
+    M, N, K, flags, bias = shape
+    if flags & O.SILU_GATE and tile == 3:
+        pytest.skip("a gated tile always has 128 weight rows")
+    say(f"tiled fp32 x w{wt} tile={tile} splits={splits} {_ids(shape)}")
+    c = _case(M * 13 + N + K + wt, M, N, K, flags, bias, wt)
+    # Larger x gives the lo half more to carry; with bf16 halves (2^-17) unit-scale x keeps a
+    # gated product inside the reference's per-element tolerance.
+    c["x"] = c["x"] * np.float32(3.0 if wt == O.F16 else 1.0)
+    got, xu = _with_tuning(tile, splits, lambda: run_linear(c, O.F32, gpu))
+    want32, want64 = expected(c, xu)
+    assert_linear_parity(got, want32, want64, K, f"fp32 x tile {tile} splits {splits} {_ids(shape)}")
+    rel = O.normwise_rel_err(got, want64)
+    assert rel <= SPLIT_TOL, f"fp32 x: normwise {rel:.3g} > {SPLIT_TOL} (lo half lost?)"
+    if splits != 1:
+        again, _ = _with_tuning(tile, splits, lambda: run_linear(c, O.F32, gpu))
+        np.testing.assert_array_equal(again, got)
+
+
+@pytest.mark.parametrize("wt", [O.F16, O.BF16], ids=["wf16", "wbf16"])
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_fp32_activations_with_fused_rmsnorm(gpu, shape, tile, wt):
+    """rmsnorm(x) * gain then the linear, one pass: the row sums of x^2 come from the staged
+    loads and scale the epilogue; under a forced split of 3 each split's partial row sums
+    travel with its partial tile (re-run: bit-identical)."""
+    M, N, K, flags, bias = shape
+    if flags & O.SILU_GATE and tile == 3:
+        pytest.skip("a gated tile always has 128 weight rows")
+    say(f"tiled fp32 x rmsnorm w{wt} tile={tile} {_ids(shape)}")
+    c = _case(M * 17 + N + K + wt, M, N, K, flags, bias, wt)
+    x = c["x"] * np.float32(4.0)
+    gbits, _ = O.round16(1.0 + 0.1 * O.gaussian(4200 + N, K), wt)
+    gated = bool(flags & O.SILU_GATE)
+    x_d = torch.from_numpy(x).to(gpu)
+    y_d = torch.from_numpy(c["y0"].copy()).to(gpu)
+
+    def go():
+        rc = mt.linear_rmsnorm_raw(x_d, O.F32, dev16(gbits, wt, gpu), dev16(c["w"], wt, gpu),
+                                   dev16(c["w2"], wt, gpu) if gated else None, wt,
+                                   dev16(c["bias"], wt, gpu) if c["bias"] is not None else None, y_d,
+                                   M, N, K, K, N, flags | (O.BIAS if bias else 0), 1e-6, None)
+        assert rc == 0, mt.last_error()
+        torch.cuda.synchronize()
+
+    _with_tuning(tile, 3, go)
+    got = y_d.cpu().numpy()
+    y_d.copy_(torch.from_numpy(c["y0"]))
+    _with_tuning(tile, 3, go)
+    np.testing.assert_array_equal(y_d.cpu().numpy(), got)
+    want64 = O.linear_np64(O.rmsnorm_f64(x, gbits, wt), c["w"], c["w2"] if gated else None, wt, c["bias"],
+                           c["y0"], c["flags"])
+    want32 = O.linear_f32(O.rmsnorm_f32(x, gbits, wt), c["w"], c["w2"] if gated else None, wt, c["bias"],
+                          c["y0"], M, N, K, c["flags"])
+    assert_linear_parity(got, want32, want64, K, f"fp32 x rmsnorm tile {tile} {_ids(shape)}")
+    rel = O.normwise_rel_err(got, want64)
+    assert rel <= SPLIT_TOL, f"fp32 x rmsnorm: normwise {rel:.3g} > {SPLIT_TOL}"
 
 
 def test_workspace_grows_and_streams_are_independent(gpu):
