@@ -24,7 +24,9 @@
 // 32 k x 16 columns of activations as hi + lo halves of the weights' 16-bit type; see
 // seq_tiles.hpp for the segment interleave):
 //   qkv     S = 2 K-segments per row tile, 8 features, its 14 block steps 2 per wave;
-//   o, down S = 4 (M <= 2) or 2 (M = 4), 16 / S features, block steps split over the 7 waves;
+//   o, down S = 4, 4 features (a workgroup's whole share), block steps split over the 7
+//           waves; at M = 4 the B operand's 16 columns hold rows 0-1 and a second MFMA on
+//           the same weight tile takes rows 2-3 (two column groups);
 //   gate|up S = 1, three row tiles of 8 gate rows and the same features' 8 up rows; the
 //           84 block steps of the three row tiles in runs of 12 per wave.
 // A wave's partial sums go to its own slot of the op class's LDS area; one lane per output
@@ -49,8 +51,10 @@ struct LCls {
     static constexpr bool BIAS = C == LC_QKV;
     static constexpr bool ACC = C == LC_O || C == LC_DOWN;
     static constexpr uint32_t FLAGS = (BIAS ? F_BIAS : 0u) | (ACC ? F_ACCUM : 0u) | (GATED ? F_SILU_GATE : 0u);
-    static constexpr uint32_t S = GATED ? 1u : C == LC_QKV ? 2u : (M <= 2 ? 4u : 2u);
+    static constexpr uint32_t S = GATED ? 1u : C == LC_QKV ? 2u : 4u;
     static constexpr uint32_t LS = S == 4 ? 2u : S == 2 ? 1u : 0u;
+    static constexpr uint32_t CG = (2 * S * M + 15) / 16;  // B column groups (MFMAs per weight tile)
+    static constexpr uint32_t RPG = M / CG;                 // x rows per column group
     static constexpr uint32_t KB = K / 32, KBS = KB / S;
     static constexpr uint32_t FPT = GATED ? 8u : 16u / S;  // features per row tile
     static constexpr uint32_t RT = GATED ? 3u : 1u;         // row tiles
@@ -63,7 +67,8 @@ struct LCls {
     // LDS partial sums: [row tile][x row][virtual row][slot]
     static constexpr uint32_t VR = GATED ? 16u : FPT;
     static constexpr uint32_t PART = RT * M * VR * 8;
-    static_assert(KB % S == 0 && 2 * S * M <= 16 && (!GATED || RT * KBS % 7 == 0), "tiling");
+    static_assert(KB % S == 0 && 2 * S * RPG == (CG == 1 ? 2 * S * M : 16) && RPG * CG == M, "tiling");
+    static_assert((!GATED || RT * KBS % 7 == 0) && (CG == 1 || !GATED), "tiling");
 };
 
 constexpr int LAY_CW = 7;  // waves of a workgroup (the block steps of qkv and o split evenly)
@@ -131,10 +136,11 @@ __device__ __forceinline__ LLane lay_lane(uint32_t r0, uint32_t nr, uint32_t lan
     LLane ll;
     ll.woff = ((r0 + lay_row<C, M>(nr, lane, r.rt)) * L::K + k + r.js * 32) * 2;
     ll.woff2 = L::GATED ? ((r0 + lay_row<C, M>(nr, lane, r.rt + 1 < L::RT ? r.rt + 1 : r.rt)) * L::K + k) * 2 : ll.woff;
-    // B column c: x row m, segment s, half h (c = 2 (m S + s) + h); columns past M S read row 0.
+    // B column c: x row m, segment s, half h (c = 2 (m S + s) + h) of column group 0 (rows
+    // RPG .. 2 RPG - 1 of group 1 sit RPG rows further on); columns past RPG S read row 0.
     const uint32_t c = lane & 15, cc = c >> 1, h = c & 1, s = cc & (L::S - 1);
     uint32_t m = cc >> L::LS;
-    m = m < static_cast<uint32_t>(M) ? m : 0u;
+    m = m < L::RPG ? m : 0u;
     ll.boff = (h * plane + m * L::K + s * L::KBS * 32 + q * 8 + r.js * 32) * 2;
     return ll;
 }
@@ -193,9 +199,11 @@ __device__ __forceinline__ void lay_tiles(const LayCtx<WT, M> &cx, const LayOp &
     }
 }
 
-// Flush of one row tile's accumulator into slot `slot`: part[rt][m][v][slot].
+// Flush of one row tile's accumulator into slot `slot`: part[rt][m][v][slot], x rows m0 + ...
+// (m0: the column group's first row).
 template <int M, int C>
-__device__ __forceinline__ void lay_flush(const f32x4 acc, float *part, uint32_t rt, uint32_t slot, uint32_t lane) {
+__device__ __forceinline__ void lay_flush(const f32x4 acc, float *part, uint32_t rt, uint32_t slot, uint32_t lane,
+                                          uint32_t m0 = 0) {
     typedef LCls<C, M> L;
     float *pp = part + rt * (M * L::VR * 8) + slot;
     const uint32_t c = lane & 15, qd = lane >> 4;
@@ -219,7 +227,7 @@ __device__ __forceinline__ void lay_flush(const f32x4 acc, float *part, uint32_t
             q[8] = e1;
         }
     } else {  // S == 4: rows 4 qd + i: virtual row qd, segment i
-        const uint32_t sc = (c >> 1) & 3, m = c >> 3;
+        const uint32_t sc = (c >> 1) & 3, m = m0 + (c >> 3);
         const float e = dpp_oct(sc == 0 ? acc[0] : sc == 1 ? acc[1] : sc == 2 ? acc[2] : acc[3]);
         if ((c & 7) == 0 && m < static_cast<uint32_t>(M)) pp[(m * L::VR + qd) * 8] = e;
     }
@@ -232,16 +240,19 @@ __device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A
     typedef LCls<C, M> L;
     constexpr LRange r = lay_range<C, M>(W);
     const char *bp = reinterpret_cast<const char *>(cx.xs) + cx.ln[C].boff;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;
+    constexpr uint32_t GOFF = L::RPG * L::K * 2;  // bytes from column group 0's rows to group 1's
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc, accg = acc;
 #pragma unroll
     for (uint32_t k = r.kb; k < r.ke; k++) {  // block js + k of row tile rt, or k - ks of rt + 1
-        const u32x4 bv = *reinterpret_cast<const u32x4 *>(
-            k < r.ks ? bp + k * 64 : bp + (static_cast<int>(k - r.ks) - static_cast<int>(r.js)) * 64);
+        const char *b = k < r.ks ? bp + k * 64 : bp + (static_cast<int>(k - r.ks) - static_cast<int>(r.js)) * 64;
+        const u32x4 bv = *reinterpret_cast<const u32x4 *>(b);
         if (k < r.ks) acc = mfma16<WT>(A[k], bv, acc);
         else acc2 = mfma16<WT>(A[k], bv, acc2);
+        if constexpr (L::CG == 2) accg = mfma16<WT>(A[k], *reinterpret_cast<const u32x4 *>(b + GOFF), accg);
     }
     lay_flush<M, C>(acc, cx.part[C], r.rt, W, cx.lane);
     if constexpr (r.ks < L::TA) lay_flush<M, C>(acc2, cx.part[C], r.rt + 1, W, cx.lane);
+    if constexpr (L::CG == 2) lay_flush<M, C>(accg, cx.part[C], r.rt, W, cx.lane, L::RPG);
 }
 
 // One op of class C (descriptor d; ops[i] holds its full descriptor for an external x): A
