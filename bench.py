@@ -588,6 +588,54 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
                 attention="inside the out projection" if fused else "separate launch")
 
 
+def bench_aggregator(torch, mt, dev, reps=5):
+    """The aggregator stage of one generation step (MingEngine.encodeStep, Engine.swift:405-410):
+    the cls row and x_embedder (1024 x 64) of the new latent, the 8-block DiT (hidden 1024, 16
+    heads) at batch 1 x seq 2 (M = 2, attention inside the out projection), the final norm +
+    896 x 1024 linear of row 0: 34 launches, bf16 weights ~ N(0, 0.02^2), captured in a HIP
+    graph and replayed."""
+    HID, HEADS, LAT, BLOCKS = 1024, 16, 64, 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+
+    def w(*shape, scale=0.02):
+        return (torch.randn(*shape, generator=g, device=dev) * scale).bfloat16()
+
+    def gain(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=dev)).bfloat16()
+
+    blocks = [dict(n1=gain(HID), qkv=w(3 * HID, HID), qkv_b=w(3 * HID), out=w(HID, HID), out_b=w(HID), n2=gain(HID),
+                   ff1=w(4 * HID, HID), ff1_b=w(4 * HID), ff2=w(HID, 4 * HID), ff2_b=w(HID)) for _ in range(BLOCKS)]
+    fin_n, fin_w, fin_b = gain(HID), w(H, HID), w(H)
+    xw, xb = w(HID, LAT, scale=0.05), w(HID, scale=0.05)
+    i = torch.arange(32, device=dev, dtype=torch.float32)
+    invf = (1.0 / torch.pow(torch.tensor(1e4, device=dev), 2.0 * i / 64.0)).float()
+    cls = torch.randn(HID, device=dev)
+    latent = torch.randn(1, LAT, device=dev)
+    x = torch.zeros(2, HID, device=dev)
+    qkv = torch.zeros(2, 3 * HID, device=dev)
+    ff = torch.zeros(2, 4 * HID, device=dev)
+    out = torch.zeros(1, H, device=dev)
+    cs = torch.cuda.Stream(device=dev)
+
+    def stage():
+        s = cs.cuda_stream
+        x[0].copy_(cls)
+        mt.linear(latent, xw, x[1:], 1, bias=xb, stream=s)
+        for p in blocks:
+            mt.linear(x, p["qkv"], qkv, 2, bias=p["qkv_b"], norm=p["n1"], stream=s)
+            mt.dit_attention_linear(qkv, 1, 2, HEADS, invf, p["out"], x, flags=mt.GemvFlags.accumulate, bias=p["out_b"],
+                                    stream=s)
+            mt.linear(x, p["ff1"], ff, 2, flags=mt.GemvFlags.gelu, bias=p["ff1_b"], norm=p["n2"], stream=s)
+            mt.linear(ff, p["ff2"], x, 2, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=s)
+        mt.linear(x, fin_w, out, 1, bias=fin_b, norm=fin_n, stream=s)
+
+    us = graph_us(torch, stage, cs, rounds=reps)
+    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
+    return dict(us_per_generation_step=us, launches=1 + 1 + 4 * BLOCKS + 1, weight_mb=wbytes / 1e6,
+                gbs_algorithmic=wbytes / (us * 1e-6) / 1e9)
+
+
 def vae_latent_graph(torch, mt, dev, ws, fused=True):
     """The VAE latent of bench_vae_latent captured in a HIP graph on its own stream; returns
     (graph, stream, launches, the tensors the graph reads and writes, to be kept alive while
@@ -926,6 +974,8 @@ def main() -> int:
         out["dit_head"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_dit(torch, mt, dev).items()}
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
         out["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
+        log("aggregator stage of one generation step (8 DiT blocks at M = 2, graph replay)")
+        out["aggregator"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_aggregator(torch, mt, dev).items()}
         if args.vs_blas:
             log("per-op graph replay: mt_linear vs hipBLASLt")
             out["per_op_graph_replay"] = bench_gemm_ops(torch, mt, dev, ws)
@@ -1010,6 +1060,8 @@ def main() -> int:
         line["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
         line["flow_step_separate_attention"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                                 for k, v in bench_flow_step(torch, mt, dev, fused=False).items()}
+        log("aggregator stage of one generation step (8 DiT blocks at M = 2, graph replay)")
+        line["aggregator"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_aggregator(torch, mt, dev).items()}
         log("VAE decode of one latent (24-layer stack at M = 4, head, ISTFT; graph replay)")
         line["vae_latent"] = {k: (round(v, 3) if isinstance(v, float) else v)
                               for k, v in bench_vae_latent(torch, mt, dev, ws).items()}

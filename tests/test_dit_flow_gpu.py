@@ -311,3 +311,69 @@ def test_flow_ode_loop_matches_fp64_chain(gpu):
         assert np.all(np.isfinite(g)), what
         rel = O.normwise_rel_err(g, want)
         assert rel <= 1e-3, f"{what}: normwise {rel:.3g}"
+
+
+def oracle_dit_stack(blocks, x0, B, S, invf):
+    """DiTForward.encode's block loop (DiT.swift:41-49) at B x S rows, fp64 per op with fp32
+    activations between ops."""
+    x = x0.astype(np.float32).copy()
+    M = B * S
+    for p in blocks:
+        qkv = O.linear_np64(O.rmsnorm_f64(x, p["norm1"], O.BF16), p["qkv"], None, O.BF16, p["qkv_b"], None,
+                            O.BIAS).astype(np.float32)
+        att = O.dit_attention_f64(qkv, B, S, HEADS, invf).astype(np.float32)
+        x = O.linear_f64(att, p["out"], None, O.BF16, p["out_b"], x, M, HID, HID, O.ACCUM).astype(np.float32)
+        ff = O.linear_np64(O.rmsnorm_f64(x, p["norm2"], O.BF16), p["ff1"], None, O.BF16, p["ff1_b"], None,
+                           O.BIAS | O.GELU).astype(np.float32)
+        x = O.linear_f64(ff, p["ff2"], None, O.BF16, p["ff2_b"], x, M, HID, 4 * HID, O.ACCUM).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("P", [1, 3])
+def test_aggregator_stage_matches_fp64(gpu, P):
+    """The aggregator (linear_proj_audio): one latent per generation step (MingEngine.encodeStep,
+    Engine.swift:405-410: row 0 the cls embedding, row 1 x_embedder(latent), the 8-block DiT at
+    batch 1 x seq 2, the final norm + 896 x 1024 linear of row 0), or a clone prompt's P
+    reference latents at once (Engine.swift:234-250: rows [cls, x_embedder(latent_p)] per
+    latent at row stride 2 hidden, batch P x seq 2, the final layer of every row), against the
+    fp64 chain."""
+    rng = np.random.default_rng(51 + P)
+    blocks = dit_weights(8, 51 + P)
+    bf = lambda *shape, s=0.02: O.round16(rng.standard_normal(shape).astype(np.float32) * np.float32(s), O.BF16)[0]
+    xw, xb = bf(HID, LAT, s=0.05), bf(HID, s=0.05)
+    fin_norm = O.round16((1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32), O.BF16)[0]
+    fin_w, fin_b = bf(896, HID), bf(896)
+    cls = rng.standard_normal(HID).astype(np.float32)
+    latents = rng.standard_normal((P, LAT)).astype(np.float32)
+    invf = invf_1e4()
+    M = 2 * P
+    out_rows = 1 if P == 1 else M
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    b16 = lambda a: dev16(a, O.BF16, gpu)
+    dw = [{k: b16(v) for k, v in p.items()} for p in blocks]
+    x = t(np.tile(cls, (M, 1)))
+    qkv = torch.zeros(M, 3 * HID, device=gpu)
+    ff = torch.zeros(M, 4 * HID, device=gpu)
+    out = torch.zeros(out_rows, 896, device=gpu)
+    invf_d = t(invf)
+    say(f"aggregator: {P} latent(s), x_embedder, 8 DiT blocks at batch {P} x seq 2, final layer of {out_rows} row(s)")
+    # x_embedder(latent_p) into row 2 p + 1 (row stride 2 hidden), over the cls rows.
+    mt.linear(t(latents), b16(xw), x[1:], P, bias=b16(xb), ldy=2 * HID)
+    for d in dw:
+        mt.linear(x, d["qkv"], qkv, M, bias=d["qkv_b"], norm=d["norm1"])
+        mt.dit_attention_linear(qkv, P, 2, HEADS, invf_d, d["out"], x, flags=mt.GemvFlags.accumulate, bias=d["out_b"])
+        mt.linear(x, d["ff1"], ff, M, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"])
+        mt.linear(ff, d["ff2"], x, M, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])
+    mt.linear(x, b16(fin_w), out, out_rows, bias=b16(fin_b), norm=b16(fin_norm))
+    torch.cuda.synchronize()
+
+    x0 = np.tile(cls, (M, 1)).astype(np.float32)
+    x0[1::2] = O.linear_np64(latents, xw, None, O.BF16, xb, None, O.BIAS).astype(np.float32)
+    want_x = oracle_dit_stack(blocks, x0, P, 2, invf)
+    want_out = O.linear_np64(O.rmsnorm_f64(want_x[:out_rows], fin_norm, O.BF16), fin_w, None, O.BF16, fin_b, None,
+                             O.BIAS)
+    for got, want, what in ((x, want_x, "hidden"), (out, want_out, "LLM row(s)")):
+        g = got.cpu().numpy()
+        assert np.all(np.isfinite(g)), what
+        rel = O.normwise_rel_err(g, want)
+        assert rel <= 1e-3, f"{what}: normwise {rel:.3g}"
