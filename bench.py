@@ -364,8 +364,12 @@ def bench_prefill_chain(torch, mt, dev, ws, M, reps=3):
     cs = torch.cuda.Stream(device=dev)
 
     def stack():
+        s = cs.cuda_stream
         for o in ops:
-            rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, cs.cuda_stream)
+            if o.norm:
+                rc = L.mt_linear_rmsnorm(o.x, o.xt, o.norm, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
+            else:
+                rc = L.mt_linear(o.x, o.xt, o.w, o.w2, o.wt, o.bias, o.y, o.p, s)
             if rc:
                 raise RuntimeError(mt.last_error())
 
@@ -929,11 +933,12 @@ def main() -> int:
     ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
-    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill"], default="all",
+    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain"], default="all",
                     help="decode: only the linear decode step; layer: it and the decode step with attention; "
                          "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
-                         "gemm: only the prefill and DiT GEMM stacks; prefill: only the prefill stack at --rows")
-    ap.add_argument("--rows", type=int, default=512, help="with --only prefill: the prompt rows M")
+                         "gemm: only the prefill and DiT GEMM stacks; prefill: only the prefill stack at --rows; "
+                         "chain: only the fp32-activation prefill chain at --rows")
+    ap.add_argument("--rows", type=int, default=512, help="with --only prefill or chain: the prompt rows M")
     ap.add_argument("--vs-blas", action="store_true",
                     help="with --only gemm: also time each prefill linear alone (graph replay) "
                          "next to hipBLASLt on the same shapes")
@@ -958,6 +963,11 @@ def main() -> int:
         log(f"prefill stack M={args.rows}")
         print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
                           for k, v in bench_prefill(torch, mt, dev, ws, args.rows).items()}), flush=True)
+        return 0
+    if args.only == "chain":
+        log(f"prefill chain (fp32 activations, fused norms) M={args.rows}")
+        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
+                          for k, v in bench_prefill_chain(torch, mt, dev, ws, args.rows).items()}), flush=True)
         return 0
     if args.only == "gemm":
         out = {"prefill": [], "dit_head": None}

@@ -106,20 +106,36 @@ __device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t G) {
 }
 
 // hi = round(x), lo = round(x - hi) in type T (round to nearest even), for 8 values packed in
-// pairs.
+// pairs.  x - hi is exact in fp32, so with fp16 halves each lo is one mixed-precision fma
+// (fp32 x minus the fp16 hi, rounded to fp16 into the pair's low or high half) after one
+// packed conversion for the pair's hi: 3 instructions a pair.  bf16 has no mixed fma: the
+// pair's hi is widened back and subtracted.
+typedef float f32x2t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2t __attribute__((ext_vector_type(2)));
 template <int T>
-__device__ __forceinline__ uint32_t round16x(float x) {
-    if constexpr (T == DT_BF16) return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
-    else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t &hi, uint32_t &lo) {
+    if constexpr (T == DT_BF16) {
+        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2t{x0, x1}, bf16x2t));
+        hi = h;
+        lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2t{x0 - bf16_lo(h), x1 - bf16_hi(h)}, bf16x2t));
+    } else {
+        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2t{x0, x1}, f16x2t));
+        uint32_t l;
+        asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(l) : "v"(x0), "v"(h));
+        asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(l) : "v"(x1), "v"(h));
+        hi = h;
+        lo = l;
+    }
 }
 template <int T>
 __device__ __forceinline__ void split8(const float (&x)[8], u32x4t &hi, u32x4t &lo) {
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        const uint32_t h0 = round16x<T>(x[2 * e]), h1 = round16x<T>(x[2 * e + 1]);
-        hi[e] = h0 | (h1 << 16);
-        lo[e] = round16x<T>(x[2 * e] - dec1<T>(static_cast<uint16_t>(h0))) |
-                (round16x<T>(x[2 * e + 1] - dec1<T>(static_cast<uint16_t>(h1))) << 16);
+        uint32_t h, l;
+        split2<T>(x[2 * e], x[2 * e + 1], h, l);
+        hi[e] = h;
+        lo[e] = l;
     }
 }
 
@@ -166,7 +182,7 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     static_assert(NE % (4 * NT) == 0, "partial tiles move as float4 per thread");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LBYTES];
     __shared__ uint32_t last_flag;
-    __shared__ __attribute__((aligned(16))) float row_ss[NORM ? BM : 4];  // rows' sums of x^2 (NORM)
+    __shared__ __attribute__((aligned(16))) float row_ss[NORM ? BM : 4];  // rows' sums of x^2, then scales (NORM)
     float *ctile = reinterpret_cast<float *>(lds);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -363,8 +379,17 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
                     for (int e = 0; e < 8; e++) ss[j] = fmaf(x[e], x[e], ss[j]);
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        x[2 * e] *= dec_lo<WT>(r.g[e]);
-                        x[2 * e + 1] *= dec_hi<WT>(r.g[e]);
+                        if constexpr (WT == DT_F16) {  // x times the fp16 gain in one mixed fma each
+                            float p0, p1;
+                            asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(p0) : "v"(x[2 * e]), "v"(r.g[e]));
+                            asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+                                : "=v"(p1) : "v"(x[2 * e + 1]), "v"(r.g[e]));
+                            x[2 * e] = p0;
+                            x[2 * e + 1] = p1;
+                        } else {
+                            x[2 * e] *= dec_lo<WT>(r.g[e]);
+                            x[2 * e + 1] *= dec_hi<WT>(r.g[e]);
+                        }
                     }
                 }
                 u32x4t hi, lo;
@@ -402,11 +427,12 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
             }
         }
         if constexpr (NORM) {
-            // Row sums over the 8 threads of a row (an aligned lane octet): this split's part.
+            // Row sums over the 8 threads of a row (an aligned lane octet): this split's part,
+            // or with K whole the row's scale.
 #pragma unroll
             for (int j = 0; j < IA; j++) {
                 const float t = octet_sum(ss[j]);
-                if (kc == 0) row_ss[(tid + NT * j) >> 3] = t;
+                if (kc == 0) row_ss[(tid + NT * j) >> 3] = a.splits > 1 ? t : 1.0f / sqrtf(t / static_cast<float>(K) + a.eps);
             }
         }
     } else if constexpr (P == 1) {
@@ -608,7 +634,11 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
             *reinterpret_cast<f32x4t *>(ctile + row * CLD + n) = sum[u];
         }
         if constexpr (NORM) {
-            if (tid < BM / 4) *reinterpret_cast<f32x4t *>(row_ss + 4 * tid) = rsum;
+            if (tid < BM / 4) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) rsum[e] = 1.0f / sqrtf(rsum[e] / static_cast<float>(K) + a.eps);
+                *reinterpret_cast<f32x4t *>(row_ss + 4 * tid) = rsum;  // the rows' scales
+            }
         }
         __syncthreads();
     }
@@ -638,9 +668,8 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
             float c = ctile[m * CLD + n];
             float c2 = GATED ? ctile[(BM + m) * CLD + n] : 0.0f;
             if constexpr (NORM) {
-                const float sc = 1.0f / sqrtf(row_ss[m] / static_cast<float>(K) + a.eps);
-                c *= sc;
-                c2 *= sc;
+                c *= row_ss[m];  // the row's scale by now
+                c2 *= row_ss[m];
             }
             float v = epilogue(c, c2, bv, flags);
             if (flags & F_ACCUM) v += yo[i];
