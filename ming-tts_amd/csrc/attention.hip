@@ -6,12 +6,12 @@
 //
 // Attention layout on gfx950: one 256-thread workgroup per (query row, head) item.
 //   - scores: groups of 8 lanes own one key (lane r of a group reads dims 8r..8r+7, so a
-//     wave reads 8 whole key rows per load instruction), 32 keys per pass, eight passes'
-//     keys requested before any is used, the 8 partial dots meet on DPP; scores land
-//     in LDS (at most 4096 keys);
+//     wave reads 8 whole key rows per load instruction), 32 keys per pass, sixteen passes'
+//     keys requested before any is used (a decode step's keys, up to 512, in one round trip),
+//     the 8 partial dots meet on DPP; scores land in LDS (at most 4096 keys);
 //   - softmax: block max and block sum through LDS;
 //   - p.v: 16 lanes cover the 64 dims of one V row (4 dims each, one coalesced row per
-//     16 lanes), 16 key phases per workgroup, eight rows per lane requested at a time,
+//     16 lanes), 16 key phases per workgroup, 32 rows per lane requested at a time,
 //     partial sums meet in LDS in a fixed order.
 // Batched decode (mt_attention_decode) is the same kernel with a per-row cache base and
 // the row's query position read from a device array.
@@ -153,10 +153,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
         qf[0] = a.x; qf[1] = a.y; qf[2] = a.z; qf[3] = a.w;
         qf[4] = b.x; qf[5] = b.y; qf[6] = b.z; qf[7] = b.w;
     }
-    // Eight passes of 32 keys per round, all requested before any is used (keys past the
+    // Sixteen passes of 32 keys per round, all requested before any is used (keys past the
     // end re-read the last key and are skipped).
     float mx = -INFINITY;
-    constexpr int KP = ATT_THREADS / 8, KU = 8;
+    constexpr int KP = ATT_THREADS / 8, KU = 16;
     for (int t0 = tid >> 3; t0 < nk; t0 += KU * KP) {
         Raw8<CT> kr[KU];
 #pragma unroll
@@ -199,10 +199,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
     sum = (red[0] + red[1]) + (red[2] + red[3]);
 
     // p . v: 16 lanes per V row (4 dims each), 16 key phases, keys t = ks, ks + 16, ... in
-    // order; eight rows per round requested before any is used (rows past the end re-read
+    // order; 32 rows per round requested before any is used (rows past the end re-read
     // the last row and are skipped).
     const int d4 = tid & 15, ks = tid >> 4;
-    constexpr int VU = 8;
+    constexpr int VU = 32;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int t0 = ks; t0 < nk; t0 += 16 * VU) {
         float4 v[VU];
@@ -309,13 +309,13 @@ __global__ __launch_bounds__(ATT_THREADS) void rope_attention_kernel(float *qkv,
     }
     __syncthreads();
 
-    // Scores: the cache's keys in rounds of eight passes, then the chunk's keys from LDS.
+    // Scores: the cache's keys in rounds of sixteen passes, then the chunk's keys from LDS.
     const int r = tid & 7;
     float qf[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) qf[e] = qs[8 * r + e];
     float mx = -INFINITY;
-    constexpr int KP = ATT_THREADS / 8, KU = 8;
+    constexpr int KP = ATT_THREADS / 8, KU = 16;
     for (int t0 = tid >> 3; t0 < nc; t0 += KU * KP) {
         Raw8<CT> kr[KU];
 #pragma unroll
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(ATT_THREADS) void rope_attention_kernel(float *qkv,
 
     // p . v in attention_kernel's order (keys ks, ks + 16, ... of each phase).
     const int d4 = tid & 15, ks = tid >> 4;
-    constexpr int VU = 8;
+    constexpr int VU = 32;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int t0 = ks; t0 < nk; t0 += 16 * VU) {
         float4 v[VU];

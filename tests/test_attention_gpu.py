@@ -115,6 +115,42 @@ def test_decode_window_and_length_edges(gpu):
             assert ex <= 0, f"window {window} b={b} index {i} got {g} want {w}"
 
 
+@pytest.mark.parametrize("ct,cap,window", [(np.float32, 512, 0), (np.float16, 512, 65), (np.float16, 2048, 0),
+                                           (np.float32, 4096, 200), (np.float16, 4096, 0)])
+def test_decode_lengths_caches_and_windows(gpu, ct, cap, window):
+    """mt_attention_decode over 8 sequences whose lengths straddle the kernel's 32-key score
+    passes and 512-key rounds (0, 1, 63 .. 129, the cache's end) on caches of 512 to 4096
+    positions, with and without a window; a sequence without keys gets zeros.  Against the
+    fp64 oracle on the stored cache values; a second run gives the same bits."""
+    lens = np.array([0, 1, 63, 64, 65, 129, cap - 1, cap], np.uint32)
+    B = len(lens)
+    z = O.gaussian(cap + window, B * HKV * cap * 64 * 2 + B * HQ * 64)
+    kc0 = z[:B * HKV * cap * 64].reshape(B, HKV, cap, 64).astype(ct)
+    vc0 = z[B * HKV * cap * 64:2 * B * HKV * cap * 64].reshape(B, HKV, cap, 64).astype(ct)
+    q = z[2 * B * HKV * cap * 64:].reshape(B, HQ * 64)
+    kc = torch.from_numpy(kc0.copy()).to(gpu)
+    vc = torch.from_numpy(vc0.copy()).to(gpu)
+    qd = torch.from_numpy(q.copy()).to(gpu)
+    lens_d = torch.from_numpy(lens.astype(np.int32)).to(gpu)
+    runs = []
+    for r in range(2):
+        out = torch.full((B, HQ * 64), 7.0, device=gpu)
+        say(f"decode lengths ct={np.dtype(ct).name} cap={cap} window={window} run {r}")
+        mt.attention_decode(qd, HQ * 64, B, HQ, HKV, lens_d, window, kc, vc, cap, HKV * cap * 64, out, HQ * 64, 0.125)
+        torch.cuda.synchronize()
+        runs.append(out.cpu().numpy().reshape(B, HQ, 64))
+    np.testing.assert_array_equal(runs[0], runs[1])
+    got = runs[0]
+    for b in range(B):
+        if lens[b] == 0:
+            np.testing.assert_array_equal(got[b], np.zeros((HQ, 64), np.float32))
+            continue
+        want = O.attention_f64(q[b].reshape(HQ, 64), kc0[b].astype(np.float64), vc0[b].astype(np.float64),
+                               int(lens[b]) - 1, window, 0.125)
+        ex, i, g, w = O.worst_violation(got[b], want, 2e-5)
+        assert ex <= 0, f"len {lens[b]} index {i} got {g} want {w}"
+
+
 @pytest.mark.parametrize("ct,M,pos0,window,cap", [
     (torch.float16, 4, 200, 65, 512),    # one VAE latent's sliding-window rows
     (torch.float32, 4, 200, 65, 512),
