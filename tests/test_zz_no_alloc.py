@@ -1,8 +1,9 @@
 """mt_linear_static (the allocation-free mt_linear): through the C ABI, on linears whose K is
-split (the pipelined GEMM and the small-row MFMA kernel, whose partial sums then live in the
-library's fixed device array), against mt_linear on the same inputs -- bit for bit, since the
-kernels and their summation order are the same -- on consecutive calls, each later one
-smaller, so a call that found the array dirty from the one before would show it."""
+split (the pipelined GEMM, with 16-bit and with fp32 x, and the small-row MFMA kernel, whose
+partial sums then live in the library's fixed device array), against mt_linear on the same
+inputs -- bit for bit, since the kernels and their summation order are the same -- on
+consecutive calls, each later one smaller, so a call that found the array dirty from the one
+before would show it."""
 import numpy as np
 import pytest
 import torch
@@ -33,6 +34,7 @@ def _case(M, N, K, xt, seed, gpu):
 @pytest.mark.parametrize("rounds", [2])
 def test_static_linear_matches_mt_linear(gpu, rounds):
     cases = [(64, 896, 4864, mt.F16, mt.KERNEL_GEMM),        # pipelined GEMM, K split
+             (64, 896, 4864, mt.F32, mt.KERNEL_GEMM),        # its fp32-x (hi + lo) path, K split in 8
              (6, 1024, 4096, mt.F32, mt.KERNEL_GEMV_MFMA),   # small-row MFMA kernel, K split
              (3, 512, 1024, mt.F32, mt.KERNEL_GEMV_MFMA)]    # smaller again
     for r in range(rounds):
