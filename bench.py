@@ -508,7 +508,7 @@ def bench_gemm_ops(torch, mt, dev, ws, reps=5):
     return rows
 
 
-def bench_flow_step(torch, mt, dev, reps=5, fused=True):
+def flow_step_graph(torch, mt, dev, fused=True):
     """The flow stage of one generation step at the reference's flow-head shape
     (MingEngine.encodeStep, Engine.swift:387-402; DiTForward.encode, DiT.swift:35-52): the
     cond embedder (896 -> 1024, M = 1), then 10 ODE steps of the EPSS schedule with sway
@@ -517,8 +517,9 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
     blocks (hidden 1024, 16 heads, batch 2 x seq 3 = 6 rows: rmsnorm+qkv 3072x1024,
     dit_attention, out 1024x1024 +=, rmsnorm+ff1 4096x1024 GELU, ff2 1024x4096 +=), the final
     rmsnorm + 64x1024 linear and flow_euler with dt = t[k+1] - t[k]: 431 launches, bf16
-    weights ~ N(0, 0.02^2), captured in a HIP graph and replayed.  With ``fused`` each block's
-    attention runs inside its out projection (mt_dit_attention_linear): 351 launches."""
+    weights ~ N(0, 0.02^2), captured in a HIP graph on its own stream.  With ``fused`` each
+    block's attention runs inside its out projection (mt_dit_attention_linear): 351 launches.
+    Returns (graph, stream, launches, weight bytes per ODE step, the tensors to keep alive)."""
     HID, HEADS, LAT, BLOCKS, STEPS = 1024, 16, 64, 8, 10
     g = torch.Generator(device=dev)
     g.manual_seed(5)
@@ -578,6 +579,15 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
+    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
+    keep = (blocks, fin_n, fin_w, fin_b, xw, xb, cb, invf, y, hist, cemb, z, cond_w, cond_b, temb, x, qkv, att, ff, pred)
+    return graph, cs, 1 + STEPS * (3 + (4 if fused else 5) * BLOCKS), wbytes, keep
+
+
+def bench_flow_step(torch, mt, dev, reps=5, fused=True):
+    """The flow stage of flow_step_graph, replayed: the best of `reps` replays, each bracketed
+    by HIP events on the replay stream."""
+    graph, _, launches, wbytes, keep = flow_step_graph(torch, mt, dev, fused)
     ev = Events(torch)
     best = None
     for _ in range(reps):
@@ -585,9 +595,9 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True):
         graph.replay()
         ms = ev.stop_ms()
         best = ms if best is None else min(best, ms)
-    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
-    return dict(us_per_generation_step=best * 1e3, us_per_ode_step=best * 1e3 / STEPS,
-                launches=1 + STEPS * (3 + (4 if fused else 5) * BLOCKS), weight_mb_per_ode_step=wbytes / 1e6,
+    del graph
+    return dict(us_per_generation_step=best * 1e3, us_per_ode_step=best * 1e3 / 10,
+                launches=launches, weight_mb_per_ode_step=wbytes / 1e6,
                 schedule="EPSS 10 steps, sway -1",
                 attention="inside the out projection" if fused else "separate launch")
 
