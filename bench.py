@@ -943,11 +943,13 @@ def main() -> int:
     ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
-    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain"], default="all",
+    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention"],
+                    default="all",
                     help="decode: only the linear decode step; layer: it and the decode step with attention; "
                          "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
                          "gemm: only the prefill and DiT GEMM stacks; prefill: only the prefill stack at --rows; "
-                         "chain: only the fp32-activation prefill chain at --rows")
+                         "chain: only the fp32-activation prefill chain at --rows; vae: only the VAE latent "
+                         "(graph of launches, then with the persistent stack); attention: only the decode attention")
     ap.add_argument("--rows", type=int, default=512, help="with --only prefill or chain: the prompt rows M")
     ap.add_argument("--vs-blas", action="store_true",
                     help="with --only gemm: also time each prefill linear alone (graph replay) "
@@ -966,6 +968,8 @@ def main() -> int:
     if args.only == "copy":
         print(json.dumps(bench_copy(torch, dev)), flush=True)
         return 0
+    if args.seq_launch == "plain":
+        mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 1)
     log("generating 24 layers of fp16 weights")
     ws = make_layers(torch, dev)
     torch.cuda.synchronize()
@@ -973,6 +977,17 @@ def main() -> int:
         log(f"prefill stack M={args.rows}")
         print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
                           for k, v in bench_prefill(torch, mt, dev, ws, args.rows).items()}), flush=True)
+        return 0
+    if args.only == "vae":
+        log("VAE latent: graph of launches, then with the layer stack as one persistent launch")
+        out = {"vae_latent": bench_vae_latent(torch, mt, dev, ws), "vae_latent_persistent": bench_vae_latent_seq(torch, mt, dev, ws)}
+        print(json.dumps({k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                          for k, v in out.items()}), flush=True)
+        return 0
+    if args.only == "attention":
+        log("decode attention, batch 2")
+        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_attention(torch, mt, dev).items()}),
+              flush=True)
         return 0
     if args.only == "chain":
         log(f"prefill chain (fp32 activations, fused norms) M={args.rows}")
@@ -1002,8 +1017,6 @@ def main() -> int:
         print(json.dumps(out), flush=True)
         return 0
 
-    if args.seq_launch == "plain":
-        mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 1)
     log(f"decode step (persistent sequence, {args.seq_launch} launch): {args.warmup} warmup + {args.steps} timed")
     d = bench_decode_seq(torch, mt, dev, ws, args.steps, args.warmup)
     t = sorted(d["times_ms"])

@@ -10,10 +10,14 @@
 //
 // Layout on gfx950:
 //   - upsample4: one thread per feature, writing its four frame rows;
-//   - istft_frames: one 256-thread workgroup per (frame, 512 output samples): the frame's
-//     bins (re, im) and the cos table sit in LDS; a thread computes samples t and N - t in one
-//     pass over the bins, since cos(2 pi k (N - t) / N) = cos(2 pi k t / N) and the sine terms
-//     only change sign, which halves the table reads and multiply-adds of the reference loop;
+//   - istft_frames: one 512-thread workgroup per (frame, 32 samples t and their mirrors N - t):
+//     the frame's bins (re, im) and the cos table sit in LDS; a lane computes samples t and
+//     N - t in one pass over the bins, since cos(2 pi k (N - t) / N) = cos(2 pi k t / N) and the
+//     sine terms only change sign, which halves the table reads and multiply-adds of the
+//     reference loop; the 16 half-waves take 16 ranges of the bins, and the bins and the table
+//     sit in LDS as (re, im) and (cos, sin) pairs, one 8-byte read each per bin (the reference
+//     walks all bins in one dependent chain: 28 workgroups of such chains took 78 us for a
+//     latent's 4 frames);
 //   - istft_emit: one thread per output sample.
 #include "mt_device.hpp"
 #include "mt_internal.hpp"
@@ -39,40 +43,64 @@ __global__ __launch_bounds__(256) void upsample4_kernel(const float *prev, const
     frames[3 * static_cast<size_t>(ldf) + c] = has_next ? 0.625f * h + 0.375f * n : h;
 }
 
-// Samples t and N - t of frame blockIdx.y for t in [blockIdx.x * 512 / 2 ..): thread j takes
-// t = blockIdx.x * 256 + j (t <= N / 2) and its mirror N - t.
-__global__ __launch_bounds__(256) void istft_frames_kernel(const float *spec, uint32_t ld_spec, const float *cos_table,
-                                                           const float *window, float *ring_frames, uint32_t nfft,
-                                                           uint32_t frame0, uint32_t ring) {
-    __shared__ float re[ISTFT_NMAX / 2 + 1];
-    __shared__ float im[ISTFT_NMAX / 2 + 1];
-    __shared__ float ctab[ISTFT_NMAX];
-    const uint32_t N = nfft, bins = N / 2 + 1, f = blockIdx.y;
+// Samples t and N - t of frame blockIdx.y for the 32 t = blockIdx.x * 32 + (tid % 32) (t <=
+// N / 2): the 16 half-waves r = tid / 32 each sum the bins of range r of 1 .. N/2 - 1 (the
+// index k t mod N advanced by t per bin, so no division and no chain through the table
+// reads), and the 16 partial sums meet in LDS in range order.  The bins sit in LDS as (re, im)
+// pairs and the table as (cos a, sin a) pairs, so a bin costs one uniform and one gathered
+// 8-byte read.
+constexpr int ISTFT_T = 32;     // samples (and their mirrors) per workgroup
+constexpr int ISTFT_R = 16;     // bin ranges: one per half-wave
+__global__ __launch_bounds__(ISTFT_T * ISTFT_R) void istft_frames_kernel(const float *spec, uint32_t ld_spec,
+                                                                        const float *cos_table, const float *window,
+                                                                        float *ring_frames, uint32_t nfft, uint32_t frame0,
+                                                                        uint32_t ring) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    __shared__ f2 bin[ISTFT_NMAX / 2 + 1];   // (re, im)
+    __shared__ f2 cs[ISTFT_NMAX];            // (cos 2 pi i / N, sin 2 pi i / N)
+    __shared__ float part[ISTFT_R][2][ISTFT_T];
+    constexpr uint32_t NT = ISTFT_T * ISTFT_R;
+    const uint32_t N = nfft, bins = N / 2 + 1, f = blockIdx.y, tid = threadIdx.x;
     const float *row = spec + static_cast<size_t>(f) * ld_spec;
-    for (uint32_t k = threadIdx.x; k < bins; k += 256) {
+    for (uint32_t k = tid; k < bins; k += NT) {
         const float mag = fminf(expf(row[k]), 100.0f);
         const float ph = row[bins + k];
-        re[k] = mag * cosf(ph);
-        im[k] = mag * sinf(ph);
+        bin[k] = f2{mag * cosf(ph), mag * sinf(ph)};
     }
-    for (uint32_t k = threadIdx.x; k < N; k += 256) ctab[k] = cos_table[k];
-    __syncthreads();
-    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
-    if (t > N / 2) return;
-    // sum over k = 1 .. N/2 - 1 of re[k] cos(2 pi k t / N) and im[k] sin(2 pi k t / N), the
-    // sine read from the cos table a quarter turn on: sin(a) = cos(a + 3 pi / 2).
+    // The sine is read from the cos table a quarter turn on: sin(a) = cos(a + 3 pi / 2).
     const uint32_t quarter3 = 3 * (N / 4);
-    uint32_t idx = 0;
-    float sc = 0.0f, ss = 0.0f;
-    for (uint32_t k = 1; k < N / 2; k++) {
-        idx += t;
-        if (idx >= N) idx -= N;
-        uint32_t sidx = idx + quarter3;
-        if (sidx >= N) sidx -= N;
-        sc = fmaf(re[k], ctab[idx], sc);
-        ss = fmaf(im[k], ctab[sidx], ss);
+    for (uint32_t i = tid; i < N; i += NT) {
+        const uint32_t j = i + quarter3;
+        cs[i] = f2{cos_table[i], cos_table[j >= N ? j - N : j]};
     }
-    const float base = re[0] + ((t & 1) ? -re[N / 2] : re[N / 2]);  // N even: t and N - t share parity
+    __syncthreads();
+    const uint32_t tq = tid % ISTFT_T, r = tid / ISTFT_T;
+    const uint32_t t = blockIdx.x * ISTFT_T + tq;
+    const uint32_t tt = t <= N / 2 ? t : 0u;  // lanes past N / 2 sum for t = 0 and store nothing
+    const uint32_t nk = N / 2 - 1, k0 = 1 + r * nk / ISTFT_R, k1 = 1 + (r + 1) * nk / ISTFT_R;
+    uint32_t idx = ((k0 - 1) * tt) % N;
+    float sc = 0.0f, ss = 0.0f;
+#pragma unroll 4
+    for (uint32_t k = k0; k < k1; k++) {
+        idx += tt;
+        if (idx >= N) idx -= N;
+        const f2 b = bin[k], c = cs[idx];
+        sc = fmaf(b.x, c.x, sc);
+        ss = fmaf(b.y, c.y, ss);
+    }
+    part[r][0][tq] = sc;
+    part[r][1][tq] = ss;
+    __syncthreads();
+    if (r != 0 || t > N / 2) return;
+    sc = part[0][0][tq];
+    ss = part[0][1][tq];
+#pragma unroll
+    for (uint32_t q = 1; q < ISTFT_R; q++) {
+        sc += part[q][0][tq];
+        ss += part[q][1][tq];
+    }
+    const f2 b0 = bin[0], bh = bin[N / 2];
+    const float base = b0.x + ((t & 1) ? -bh.x : bh.x);  // N even: t and N - t share parity
     const float scale = 1.0f / static_cast<float>(N);
     float *out = ring_frames + static_cast<size_t>((frame0 + f) % ring) * N;
     out[t] = (base + 2.0f * (sc - ss)) * scale * window[t];
@@ -125,8 +153,8 @@ int mt_istft_frames(const float *spec, uint32_t ld_spec, uint32_t count, uint32_
         return set_error(MT_EINVAL, "mt_istft_frames: nfft %u must be a multiple of 4 in 8..%d", nfft, ISTFT_NMAX);
     if (ld_spec < nfft + 2) return set_error(MT_EINVAL, "mt_istft_frames: ld_spec %u < nfft + 2", ld_spec);
     if (ring == 0 || count > ring) return set_error(MT_EINVAL, "mt_istft_frames: %u frames for a ring of %u", count, ring);
-    const dim3 grid((nfft / 2 + 1 + 255) / 256, count);
-    hipLaunchKernelGGL(istft_frames_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), spec, ld_spec,
+    const dim3 grid((nfft / 2 + 1 + ISTFT_T - 1) / ISTFT_T, count);
+    hipLaunchKernelGGL(istft_frames_kernel, grid, dim3(ISTFT_T * ISTFT_R), 0, reinterpret_cast<hipStream_t>(stream), spec, ld_spec,
                        cos_table, window, ring_frames, nfft, frame0, ring);
     return check_launch("istft_frames");
 }
