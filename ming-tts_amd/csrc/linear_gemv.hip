@@ -3,7 +3,7 @@
 //
 // Reference kernel replaced: gemv_kernel<MR> (Shaders.swift:47-108) and, for 3..8 rows,
 // gemm8_kernel (Shaders.swift:188-283).  One wave64 holds 64 / L output features; the
-// workgroup is 256 threads, or fewer when that leaves the grid short of workgroups.
+// workgroup size is the one that leaves the busiest CU the fewest features.
 #include "gemv_core.hpp"
 #include "mt_internal.hpp"
 
@@ -79,10 +79,20 @@ int launch_gemv(const LinearArgs &a, int xt, int wt, hipStream_t stream, int ove
     const int mr = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : 8;
     const int l2 = gemv_lanes_log2(a.K, override_lanes, a.M);
     const int L = 1 << l2;
-    // 256 threads per workgroup unless that leaves fewer than 512 workgroups; never below
-    // one wave (64 threads).
+    // The workgroup size (64..256 threads) that puts the fewest output features on the
+    // busiest CU (ties: the larger size): with 4864 features of 16 lanes on 256 CUs, 128-thread
+    // workgroups leave 2 or 3 (16 or 24 features) per CU, 64-thread ones 4 or 5 (at most 20).
+    const int cus = device_cus() > 0 ? device_cus() : 256;
     int threads = 256;
-    while (threads > 64 && (a.N + (threads / L) - 1) / (threads / L) < 512) threads >>= 1;
+    long best = -1;
+    for (int t = 256; t >= 64; t >>= 1) {
+        const long per = t / L, wgs = (static_cast<long>(a.N) + per - 1) / per;
+        const long load = (wgs + cus - 1) / cus * per;
+        if (best < 0 || load < best) {
+            best = load;
+            threads = t;
+        }
+    }
     const int per_group = threads / L;
     dim3 grid((a.N + per_group - 1) / per_group, (a.M + mr - 1) / mr);
     gemv_fn fn = pick(mr, wt, xt, gated, norm);
