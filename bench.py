@@ -516,9 +516,10 @@ def flow_step_graph(torch, mt, dev, fused=True):
     (precomputed once by the time MLP, Engine.swift:186-198, outside the timed region), 8 DiT
     blocks (hidden 1024, 16 heads, batch 2 x seq 3 = 6 rows: rmsnorm+qkv 3072x1024,
     dit_attention, out 1024x1024 +=, rmsnorm+ff1 4096x1024 GELU, ff2 1024x4096 +=), the final
-    rmsnorm + 64x1024 linear and flow_euler with dt = t[k+1] - t[k]: 431 launches, bf16
+    rmsnorm + 64x1024 linear and flow_euler with dt = t[k+1] - t[k], each step's Euler update
+    fused with the next step's flow_assemble (mt_flow_euler_assemble): 422 launches, bf16
     weights ~ N(0, 0.02^2), captured in a HIP graph on its own stream.  With ``fused`` each
-    block's attention runs inside its out projection (mt_dit_attention_linear): 351 launches.
+    block's attention runs inside its out projection (mt_dit_attention_linear): 342 launches.
     Returns (graph, stream, launches, weight bytes per ODE step, the tensors to keep alive)."""
     HID, HEADS, LAT, BLOCKS, STEPS = 1024, 16, 64, 8, 10
     g = torch.Generator(device=dev)
@@ -553,8 +554,8 @@ def flow_step_graph(torch, mt, dev, fused=True):
 
     def step():
         mt.linear(z, cond_w, cemb, 1, bias=cond_b, stream=cs.cuda_stream)
+        mt.flow_assemble(y, hist, cemb[0], cb, temb[0], xw, xb, x, stream=cs.cuda_stream)
         for k in range(STEPS):
-            mt.flow_assemble(y, hist, cemb[0], cb, temb[k], xw, xb, x, stream=cs.cuda_stream)
             for p in blocks:
                 mt.linear(x, p["qkv"], qkv, 6, bias=p["qkv_b"], norm=p["n1"], stream=cs.cuda_stream)
                 if fused:
@@ -568,7 +569,11 @@ def flow_step_graph(torch, mt, dev, fused=True):
                           stream=cs.cuda_stream)
                 mt.linear(ff, p["ff2"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=cs.cuda_stream)
             mt.linear(x, fin_w, pred, 6, bias=fin_b, norm=fin_n, stream=cs.cuda_stream)
-            mt.flow_euler(y, pred, 2, 5, 2.0, dts[k], stream=cs.cuda_stream)
+            if k + 1 < STEPS:  # this step's Euler update and the next step's flow input, one launch
+                mt.flow_euler_assemble(y, pred, 2, 5, 2.0, dts[k], hist, cemb[0], cb, temb[k + 1], xw, xb, x,
+                                       stream=cs.cuda_stream)
+            else:
+                mt.flow_euler(y, pred, 2, 5, 2.0, dts[k], stream=cs.cuda_stream)
 
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(cs):
@@ -581,7 +586,7 @@ def flow_step_graph(torch, mt, dev, fused=True):
     torch.cuda.synchronize()
     wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
     keep = (blocks, fin_n, fin_w, fin_b, xw, xb, cb, invf, y, hist, cemb, z, cond_w, cond_b, temb, x, qkv, att, ff, pred)
-    return graph, cs, 1 + STEPS * (3 + (4 if fused else 5) * BLOCKS), wbytes, keep
+    return graph, cs, 2 + STEPS * (2 + (4 if fused else 5) * BLOCKS), wbytes, keep
 
 
 def bench_flow_step(torch, mt, dev, reps=5, fused=True):
@@ -943,7 +948,7 @@ def main() -> int:
     ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
-    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention"],
+    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention", "flow"],
                     default="all",
                     help="decode: only the linear decode step; layer: it and the decode step with attention; "
                          "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
@@ -983,6 +988,13 @@ def main() -> int:
         out = {"vae_latent": bench_vae_latent(torch, mt, dev, ws), "vae_latent_persistent": bench_vae_latent_seq(torch, mt, dev, ws)}
         print(json.dumps({k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                           for k, v in out.items()}), flush=True)
+        return 0
+    if args.only == "flow":
+        log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
+        print(json.dumps({("flow_step" if fused else "flow_step_separate_attention"):
+                          {k: (round(v, 3) if isinstance(v, float) else v)
+                           for k, v in bench_flow_step(torch, mt, dev, fused=fused).items()}
+                          for fused in (True, False)}), flush=True)
         return 0
     if args.only == "attention":
         log("decode attention, batch 2")

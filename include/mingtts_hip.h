@@ -402,6 +402,20 @@ int mt_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, 
                   uint32_t latent_dim, float cfg, float dt, mt_stream_t stream);
 
 /*
+ * mt_flow_euler_assemble -- Encoder.flowEuler of ODE step k followed by Encoder.flowAssemble
+ * of step k + 1 (Kernels.swift:222-246; the ODE loop of Engine.swift:395-402) in one launch:
+ * exactly mt_flow_euler(y, pred, ldp, pred_row, null_row, capture, latent_dim, cfg, dt) then
+ * mt_flow_assemble(y, history, cemb, cond_bias, temb, x_w, x_b, wt, x, ldx, hidden,
+ * latent_dim), the same arithmetic and bits, one workgroup.  No counterpart in the reference
+ * (two dispatches there): it spares one launch per ODE step.  latent_dim a multiple of 8 up
+ * to 2048; x must not overlap y, pred, history or capture.
+ */
+int mt_flow_euler_assemble(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row,
+                           float *capture, float cfg, float dt, const float *history, const float *cemb,
+                           const void *cond_bias, const float *temb, const void *x_w, const void *x_b, mt_dtype wt,
+                           float *x, uint32_t ldx, uint32_t hidden, uint32_t latent_dim, mt_stream_t stream);
+
+/*
  * The audio VAE decoder's tail (VAEDecoder.decodeDispatches, VAEDecoder.swift:81-107).
  *
  * mt_upsample4 -- Encoder.upsample4 (Kernels.swift:247-257, Shaders.swift:700-718): the four

@@ -455,4 +455,21 @@ int mt_flow_euler(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, 
                              reinterpret_cast<hipStream_t>(stream));
 }
 
+int mt_flow_euler_assemble(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row,
+                           float *capture, float cfg, float dt, const float *history, const float *cemb,
+                           const void *cond_bias, const float *temb, const void *x_w, const void *x_b, mt_dtype wt,
+                           float *x, uint32_t ldx, uint32_t hidden, uint32_t latent_dim, mt_stream_t stream) {
+    if (hidden == 0 || latent_dim == 0) return set_error(MT_EINVAL, "mt_flow_euler_assemble: empty hidden or latent");
+    if (wt != MT_BF16 && wt != MT_F16) return set_error(MT_EINVAL, "mt_flow_euler_assemble: weights must be f16 or bf16");
+    if (!y || !pred || !history || !cemb || !cond_bias || !temb || !x_w || !x_b || !x)
+        return set_error(MT_EINVAL, "mt_flow_euler_assemble: null pointer");
+    if (latent_dim % 8 || latent_dim > 2048 || !aligned(x_w, 16))
+        return set_error(MT_EINVAL,
+                         "mt_flow_euler_assemble: latent_dim must be a multiple of 8 up to 2048 and x_w 16-byte aligned");
+    if (ldp < latent_dim) return set_error(MT_EINVAL, "mt_flow_euler_assemble: ldp %u < latent_dim %u", ldp, latent_dim);
+    if (ldx < hidden) return set_error(MT_EINVAL, "mt_flow_euler_assemble: ldx %u < hidden %u", ldx, hidden);
+    return launch_flow_euler_assemble(y, pred, ldp, pred_row, null_row, capture, cfg, dt, history, cemb, cond_bias, temb,
+                                      x_w, x_b, wt, x, ldx, hidden, latent_dim, reinterpret_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

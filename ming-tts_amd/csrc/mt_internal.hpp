@@ -107,6 +107,10 @@ void seq_destroy(SeqPlan *p);
 int seq_groups(const SeqPlan *p);
 int seq_kernel_kind(const SeqPlan *p);
 
+int launch_flow_euler_assemble(float *y, const float *pred, uint32_t ldp, uint32_t pred_row, uint32_t null_row,
+                               float *capture, float cfg, float dt, const float *history, const float *cemb,
+                               const void *cbias, const float *temb, const void *xw, const void *xb, int wt, float *x,
+                               uint32_t ldx, uint32_t hidden, uint32_t latent, hipStream_t stream);
 int launch_rope_cache(float *qkv, uint32_t ldq, uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t pos0,
                       const uint32_t *pos_arr, void *kc, void *vc, int ct, uint32_t cache_len,
                       uint64_t cache_stride, const float *inv_freq, hipStream_t stream);

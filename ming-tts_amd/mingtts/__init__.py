@@ -32,7 +32,7 @@ EXPORTS = (
     "mt_seq_create_items", "mt_seq_run",
     "mt_seq_destroy", "mt_seq_groups", "mt_seq_kernel", "mt_seq_check", "mt_rope_cache", "mt_rope_cache_decode",
     "mt_attention", "mt_attention_decode", "mt_rope_attention", "mt_dit_attention", "mt_dit_attention_linear", "mt_flow_assemble",
-    "mt_flow_euler",
+    "mt_flow_euler", "mt_flow_euler_assemble",
     "mt_upsample4", "mt_istft_frames", "mt_istft_emit", "mt_st_open", "mt_st_close", "mt_st_count", "mt_st_name", "mt_st_find", "mt_arena_create", "mt_arena_tensor",
     "mt_arena_padded", "mt_arena_bytes", "mt_arena_upload", "mt_arena_audit", "mt_arena_destroy",
     "mt_last_error", "mt_version",
@@ -150,6 +150,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.mt_flow_assemble.restype = i32
     L.mt_flow_euler.argtypes = [vp, vp, u32, u32, u32, vp, u32, f32, f32, vp]
     L.mt_flow_euler.restype = i32
+    L.mt_flow_euler_assemble.argtypes = [vp, vp, u32, u32, u32, vp, f32, f32, vp, vp, vp, vp, vp, vp, i32, vp, u32, u32,
+                                         u32, vp]
+    L.mt_flow_euler_assemble.restype = i32
     L.mt_upsample4.argtypes = [vp, vp, vp, vp, u32, u32, vp]
     L.mt_upsample4.restype = i32
     L.mt_istft_frames.argtypes = [vp, u32, u32, u32, vp, vp, vp, u32, u32, vp]
@@ -408,6 +411,16 @@ def flow_euler(y, pred, pred_row, null_row, cfg, dt, capture=None, ldp=None, str
     latent = y.numel()
     check(load().mt_flow_euler(_ptr(y), _ptr(pred), pred.stride(0) if ldp is None else ldp, pred_row, null_row,
                                _ptr(capture), latent, cfg, dt, _stream(stream)))
+
+
+def flow_euler_assemble(y, pred, pred_row, null_row, cfg, dt, history, cemb, cond_bias, temb, x_w, x_b, x,
+                        capture=None, ldp=None, ldx=None, stream=None) -> None:
+    """flow_euler of one ODE step then flow_assemble of the next, in one launch."""
+    hidden, latent = x_w.shape
+    check(load().mt_flow_euler_assemble(_ptr(y), _ptr(pred), pred.stride(0) if ldp is None else ldp, pred_row, null_row,
+                                        _ptr(capture), cfg, dt, _ptr(history), _ptr(cemb), _ptr(cond_bias), _ptr(temb),
+                                        _ptr(x_w), _ptr(x_b), dtype_code(x_w), _ptr(x),
+                                        x.stride(0) if ldx is None else ldx, hidden, latent, _stream(stream)))
 
 
 def upsample4(prev, cur, nxt, frames, ldf=None, stream=None) -> None:

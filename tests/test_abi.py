@@ -202,6 +202,24 @@ def test_dit_attention_linear_rejects_bad_arguments():
     assert call(B=0, M=0) == mt.OK   # empty
 
 
+def test_flow_euler_assemble_rejects_bad_arguments():
+    L = mt.load()
+    A = ALIGNED
+
+    def call(hidden=1024, latent=64, ldp=64, ldx=1024, wt=mt.BF16, xw=W_ADDR, y=A):
+        return L.mt_flow_euler_assemble(y, A, ldp, 2, 5, None, 2.0, 0.0625, A, A, A, A, xw, A, wt, Y_ADDR, ldx,
+                                        hidden, latent, None)
+
+    assert call(hidden=0) == mt.EINVAL and "empty" in mt.last_error()
+    assert call(wt=mt.F32) == mt.EINVAL and "f16 or bf16" in mt.last_error()
+    assert call(y=None) == mt.EINVAL and "null pointer" in mt.last_error()
+    assert call(latent=60, ldp=60) == mt.EINVAL and "multiple of 8" in mt.last_error()
+    assert call(latent=2056, ldp=2056) == mt.EINVAL and "up to 2048" in mt.last_error()
+    assert call(xw=W_ADDR + 2) == mt.EINVAL and "aligned" in mt.last_error()
+    assert call(ldp=32) == mt.EINVAL and "ldp" in mt.last_error()
+    assert call(ldx=1000) == mt.EINVAL and "ldx" in mt.last_error()
+
+
 def test_seq_item_layout_matches_the_header(tmp_path):
     """The ctypes mirrors of mt_attn_op and mt_seq_item have the C compiler's sizes and
     offsets."""

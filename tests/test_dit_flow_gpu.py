@@ -138,6 +138,35 @@ def test_flow_euler(gpu):
             np.testing.assert_array_equal(cap.cpu().numpy(), want_cap.astype(np.float32))
 
 
+@pytest.mark.parametrize("wt,hidden,latent,ldx", [(O.BF16, 1024, 64, 1024), (O.F16, 1000, 72, 1008)])
+def test_flow_euler_assemble_matches_the_two_launches(gpu, wt, hidden, latent, ldx):
+    """mt_flow_euler_assemble = mt_flow_euler then mt_flow_assemble of the next ODE step: y, the
+    six rows of x (row stride ldx) and the captured velocities, bit for bit."""
+    rng = np.random.default_rng(17 + latent)
+    f32 = lambda *shape: rng.standard_normal(shape).astype(np.float32)
+    w16 = lambda *shape, s=0.05: dev16(O.round16(f32(*shape) * np.float32(s), wt)[0], wt, gpu)
+    pred = torch.from_numpy(f32(6, latent)).to(gpu)
+    y0, hist = f32(latent), torch.from_numpy(f32(latent)).to(gpu)
+    cemb, temb = torch.from_numpy(f32(hidden)).to(gpu), torch.from_numpy(f32(hidden)).to(gpu)
+    cbias, xw, xb = w16(hidden, s=1.0), w16(hidden, latent), w16(hidden)
+    outs = []
+    for fused in (False, True):
+        y = torch.from_numpy(y0.copy()).to(gpu)
+        x = torch.zeros(6, ldx, device=gpu)
+        cap = torch.zeros(2 * latent, device=gpu)
+        say(f"flow_euler_assemble fused={fused} w{wt} hidden={hidden} latent={latent}")
+        if fused:
+            mt.flow_euler_assemble(y, pred, 2, 5, 2.0, 0.0625, hist, cemb, cbias, temb, xw, xb, x, capture=cap)
+        else:
+            mt.flow_euler(y, pred, 2, 5, 2.0, 0.0625, capture=cap)
+            mt.flow_assemble(y, hist, cemb, cbias, temb, xw, xb, x)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy() for t in (y, x, cap)])
+    for a, b, what in zip(outs[0], outs[1], ("y", "x", "capture")):
+        np.testing.assert_array_equal(b, a, err_msg=what)
+    assert np.all(outs[1][1][:, hidden:] == 0.0)  # past hidden in each row: untouched
+
+
 HID, HEADS, LAT = 1024, 16, 64
 
 
