@@ -64,18 +64,20 @@ def ensure_built() -> None:
 
 
 class Events:
-    """HIP events on torch's current stream (the stream every launch below uses)."""
+    """HIP events on torch's current stream (the stream every launch below uses), or on
+    `stream`."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, stream=None):
         self.torch = torch
+        self.stream = stream
         self.a = torch.cuda.Event(enable_timing=True)
         self.b = torch.cuda.Event(enable_timing=True)
 
     def start(self):
-        self.a.record()
+        self.a.record(self.stream)
 
     def stop_ms(self) -> float:
-        self.b.record()
+        self.b.record(self.stream)
         self.b.synchronize()
         return self.a.elapsed_time(self.b)
 
@@ -508,7 +510,7 @@ def bench_gemm_ops(torch, mt, dev, ws, reps=5):
     return rows
 
 
-def flow_step_graph(torch, mt, dev, fused=True):
+def flow_step_graph(torch, mt, dev, fused=True, persistent=False):
     """The flow stage of one generation step at the reference's flow-head shape
     (MingEngine.encodeStep, Engine.swift:387-402; DiTForward.encode, DiT.swift:35-52): the
     cond embedder (896 -> 1024, M = 1), then 10 ODE steps of the EPSS schedule with sway
@@ -520,6 +522,9 @@ def flow_step_graph(torch, mt, dev, fused=True):
     fused with the next step's flow_assemble (mt_flow_euler_assemble): 422 launches, bf16
     weights ~ N(0, 0.02^2), captured in a HIP graph on its own stream.  With ``fused`` each
     block's attention runs inside its out projection (mt_dit_attention_linear): 342 launches.
+    With ``persistent`` each ODE step's 8 blocks are one launch of the DiT-block kernel
+    (mt_seq_create_items with DiT attention items): 32 launches, run on the stream (a
+    cooperative launch is not captured), so `graph` is then the stage's function.
     Returns (graph, stream, launches, weight bytes per ODE step, the tensors to keep alive)."""
     HID, HEADS, LAT, BLOCKS, STEPS = 1024, 16, 64, 8, 10
     g = torch.Generator(device=dev)
@@ -550,13 +555,23 @@ def flow_step_graph(torch, mt, dev, fused=True):
     pred = torch.zeros(6, LAT, device=dev)
     cs = torch.cuda.Stream(device=dev)
     dts = [float(sched[k + 1] - sched[k]) for k in range(STEPS)]
+    seq = None
+    if persistent:
+        items = []
+        for p in blocks:
+            items += [mt.op(x, p["qkv"], qkv, 6, bias=p["qkv_b"], norm=p["n1"]),
+                      mt.dit_attn_op(qkv, 2, 3, HEADS, invf, att),
+                      mt.op(att, p["out"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["out_b"]),
+                      mt.op(x, p["ff1"], ff, 6, flags=mt.GemvFlags.gelu, bias=p["ff1_b"], norm=p["n2"]),
+                      mt.op(ff, p["ff2"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"])]
+        seq = mt.Seq(items)
     torch.cuda.synchronize()
 
     def step():
         mt.linear(z, cond_w, cemb, 1, bias=cond_b, stream=cs.cuda_stream)
         mt.flow_assemble(y, hist, cemb[0], cb, temb[0], xw, xb, x, stream=cs.cuda_stream)
         for k in range(STEPS):
-            for p in blocks:
+            for p in ([] if persistent else blocks):
                 mt.linear(x, p["qkv"], qkv, 6, bias=p["qkv_b"], norm=p["n1"], stream=cs.cuda_stream)
                 if fused:
                     mt.dit_attention_linear(qkv, 2, 3, HEADS, invf, p["out"], x, flags=mt.GemvFlags.accumulate,
@@ -568,6 +583,8 @@ def flow_step_graph(torch, mt, dev, fused=True):
                 mt.linear(x, p["ff1"], ff, 6, flags=mt.GemvFlags.gelu, bias=p["ff1_b"], norm=p["n2"],
                           stream=cs.cuda_stream)
                 mt.linear(ff, p["ff2"], x, 6, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=cs.cuda_stream)
+            if persistent:
+                seq.run(stream=cs.cuda_stream)
             mt.linear(x, fin_w, pred, 6, bias=fin_b, norm=fin_n, stream=cs.cuda_stream)
             if k + 1 < STEPS:  # this step's Euler update and the next step's flow input, one launch
                 mt.flow_euler_assemble(y, pred, 2, 5, 2.0, dts[k], hist, cemb[0], cb, temb[k + 1], xw, xb, x,
@@ -575,6 +592,14 @@ def flow_step_graph(torch, mt, dev, fused=True):
             else:
                 mt.flow_euler(y, pred, 2, 5, 2.0, dts[k], stream=cs.cuda_stream)
 
+    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
+    keep = (blocks, fin_n, fin_w, fin_b, xw, xb, cb, invf, y, hist, cemb, z, cond_w, cond_b, temb, x, qkv, att, ff, pred,
+            seq)
+    if persistent:
+        step()
+        torch.cuda.synchronize()
+        seq.check()
+        return step, cs, 2 + STEPS * 3, wbytes, keep
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(cs):
         step()
@@ -584,27 +609,32 @@ def flow_step_graph(torch, mt, dev, fused=True):
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
-    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
-    keep = (blocks, fin_n, fin_w, fin_b, xw, xb, cb, invf, y, hist, cemb, z, cond_w, cond_b, temb, x, qkv, att, ff, pred)
     return graph, cs, 2 + STEPS * (2 + (4 if fused else 5) * BLOCKS), wbytes, keep
 
 
-def bench_flow_step(torch, mt, dev, reps=5, fused=True):
-    """The flow stage of flow_step_graph, replayed: the best of `reps` replays, each bracketed
-    by HIP events on the replay stream."""
-    graph, _, launches, wbytes, keep = flow_step_graph(torch, mt, dev, fused)
-    ev = Events(torch)
+def bench_flow_step(torch, mt, dev, reps=5, fused=True, persistent=False):
+    """The flow stage of flow_step_graph, replayed (or, persistent, run on its stream): the best
+    of `reps` runs, each bracketed by HIP events on that stream."""
+    graph, cs, launches, wbytes, keep = flow_step_graph(torch, mt, dev, fused, persistent)
+    ev = Events(torch, cs) if persistent else Events(torch)
     best = None
     for _ in range(reps):
         ev.start()
-        graph.replay()
+        if persistent:
+            graph()
+        else:
+            graph.replay()
         ms = ev.stop_ms()
         best = ms if best is None else min(best, ms)
+    if persistent:
+        torch.cuda.synchronize()
+        keep[-1].check()
     del graph
     return dict(us_per_generation_step=best * 1e3, us_per_ode_step=best * 1e3 / 10,
                 launches=launches, weight_mb_per_ode_step=wbytes / 1e6,
                 schedule="EPSS 10 steps, sway -1",
-                attention="inside the out projection" if fused else "separate launch")
+                blocks="one DiT-block kernel launch per ODE step" if persistent else "a launch per linear",
+                attention="inside the out projection" if fused or persistent else "separate launch")
 
 
 def bench_aggregator(torch, mt, dev, reps=5):
@@ -991,10 +1021,12 @@ def main() -> int:
         return 0
     if args.only == "flow":
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
-        print(json.dumps({("flow_step" if fused else "flow_step_separate_attention"):
-                          {k: (round(v, 3) if isinstance(v, float) else v)
-                           for k, v in bench_flow_step(torch, mt, dev, fused=fused).items()}
-                          for fused in (True, False)}), flush=True)
+        out = {}
+        for name, kw in (("flow_step_persistent", dict(persistent=True)), ("flow_step", dict(fused=True)),
+                         ("flow_step_separate_attention", dict(fused=False))):
+            out[name] = {k: (round(v, 3) if isinstance(v, float) else v)
+                         for k, v in bench_flow_step(torch, mt, dev, **kw).items()}
+        print(json.dumps(out), flush=True)
         return 0
     if args.only == "attention":
         log("decode attention, batch 2")

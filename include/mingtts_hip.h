@@ -32,6 +32,10 @@
  *   (mt_seq_create_items) Encoder.attention of one Sources/MingTTS/Engine/Qwen.swift:86-87
  *                        decode layer, inside the
  *                        sequence
+ *   mt_dit_attn_op       Encoder.ditAttention of   Sources/MingTTS/Engine/Kernels.swift:208-220,
+ *   (mt_seq_create_items) DiTForward.encode's      Sources/MingTTS/Engine/DiT.swift:35-52
+ *                        blocks, inside the
+ *                        sequence
  *   mt_rope_cache        Encoder.ropeCache         Sources/MingTTS/Engine/Kernels.swift:180-191
  *   mt_attention         Encoder.attention         Sources/MingTTS/Engine/Kernels.swift:193-206
  *   mt_rope_attention    Encoder.ropeCache +       Sources/MingTTS/Engine/Kernels.swift:180-206,
@@ -265,15 +269,40 @@ typedef struct mt_attn_op {
     float scale;
 } mt_attn_op;
 
-enum { MT_SEQ_LINEAR = 0, MT_SEQ_ATTENTION = 1 };
+/*
+ * The DiT's full attention of mt_dit_attention as an item of a sequence (Encoder.ditAttention,
+ * Kernels.swift:208-220; DiTForward.encode, DiT.swift:35-52): B sequences of S rows, H heads of
+ * 64, interleaved RoPE at positions 0 .. S - 1, scores scaled by `scale`; qkv rows [q | k | v]
+ * (H*64 each) at stride ldq, out rows (H*64) at stride ldo.  It runs only in the DiT-block
+ * kernel (mt_seq_kernel = MT_SEQ_DIT_BLOCK), where every workgroup computes it while staging
+ * the out projection's activations.
+ */
+typedef struct mt_dit_attn_op {
+    const float *qkv;
+    uint32_t ldq, B, S, H;
+    const float *inv_freq;  /* 32 floats: 1 / theta^(2i / 64) */
+    float *out;
+    uint32_t ldo;
+    float scale;
+} mt_dit_attn_op;
+
+enum { MT_SEQ_LINEAR = 0, MT_SEQ_ATTENTION = 1, MT_SEQ_DIT_ATTENTION = 2 };
 typedef struct mt_seq_item {
-    int32_t kind;          /* MT_SEQ_LINEAR: `linear` is the op; MT_SEQ_ATTENTION: `attn` */
+    int32_t kind;          /* MT_SEQ_LINEAR: `linear` is the op; MT_SEQ_ATTENTION: `attn`;
+                              MT_SEQ_DIT_ATTENTION: `dit` */
     mt_linear_op linear;
     mt_attn_op attn;
+    mt_dit_attn_op dit;
 } mt_seq_item;
 /* mt_seq_create over a list of linears and attention items: the whole decode layer
  * (QwenForward.dispatches, Qwen.swift:84-91) as one persistent launch.  An attention
- * item's output is an activation like a linear's (a later linear reads it as x). */
+ * item's output is an activation like a linear's (a later linear reads it as x).
+ * DiT attention items are taken in one pattern only: DiT blocks at the flow head's shape
+ * (DiTForward.encode, DiT.swift:35-52), each rmsnorm+qkv 3072 x 1024 + bias, the DiT
+ * attention (B 2, S 3, H 16) of that qkv, out 1024 x 1024 + bias += reading the attention's
+ * output, rmsnorm+ff1 4096 x 1024 + bias GELU, ff2 1024 x 4096 + bias +=, at M = 6 rows, every
+ * attention item with the same inv_freq and scale, on a device with 256 CUs (one workgroup
+ * each); anything else with a DiT attention item returns MT_ENOTSUP. */
 int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out);
 int mt_seq_run(mt_seq *seq, mt_stream_t stream);
 int mt_seq_destroy(mt_seq *seq);
@@ -282,9 +311,11 @@ int mt_seq_groups(const mt_seq *seq);
 /* The kernel the plan runs: MT_SEQ_DECODE_LAYER when its linears repeat the Qwen2-0.5B
  * decode layer of QwenForward.dispatches (Qwen.swift:84-91; qkv 1152 x 896 + bias with the
  * first RMSNorm, o 896 x 896 +=, gate|up 2 x 4864 x 896 SiLU-gate with the second RMSNorm,
- * down 896 x 4864 +=) at 1, 2 or 4 rows, with no attention items; MT_SEQ_GENERAL otherwise
- * (or under MT_TUNE_SEQ_LAYER = 1).  Both compute the same sequence. */
-enum { MT_SEQ_GENERAL = 0, MT_SEQ_DECODE_LAYER = 1 };
+ * down 896 x 4864 +=) at 1, 2 or 4 rows, with or without decode attention items;
+ * MT_SEQ_DIT_BLOCK for the DiT blocks described at mt_seq_create_items; MT_SEQ_GENERAL
+ * otherwise (or under MT_TUNE_SEQ_LAYER = 1, which refuses DiT attention items).  All compute
+ * the same sequence. */
+enum { MT_SEQ_GENERAL = 0, MT_SEQ_DECODE_LAYER = 1, MT_SEQ_DIT_BLOCK = 2 };
 int mt_seq_kernel(const mt_seq *seq);
 /* Synchronous health check of a plan after its runs completed: MT_EHIP if a dataflow wait
  * of a run gave up after its spin bound (co-residency was lost), MT_ERANGE if an fp16-weight

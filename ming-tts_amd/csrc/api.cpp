@@ -221,6 +221,15 @@ int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out
             if (a.B > 1 && a.cache_stride != 0 && a.cache_stride < static_cast<uint64_t>(a.hkv) * a.cache_len * 64)
                 return set_error(MT_EINVAL, "%s: cache_stride smaller than one cache (0 for rows of one sequence)",
                                  who);
+        } else if (items[i].kind == MT_SEQ_DIT_ATTENTION) {
+            const mt_dit_attn_op &a = items[i].dit;
+            if (a.B == 0 || a.S == 0 || a.H == 0 || a.S > 8 || a.B * a.S > 8)
+                return set_error(MT_EINVAL, "%s: a DiT attention item takes B, S, H >= 1, S <= 8 and B S <= 8", who);
+            if (!a.qkv || !a.inv_freq || !a.out) return set_error(MT_EINVAL, "%s: null pointer", who);
+            if (a.ldq < 3 * a.H * 64 || a.ldo < a.H * 64)
+                return set_error(MT_EINVAL, "%s: ldq < 3 H * 64 or ldo < H * 64", who);
+            if (!aligned(a.qkv, 16) || a.ldq % 4 || !aligned(a.out, 16) || a.ldo % 4)
+                return set_error(MT_EINVAL, "%s: qkv and out must be 16-byte aligned with 16-byte row strides", who);
         } else if (items[i].kind == MT_SEQ_LINEAR) {
             const mt_linear_op &o = items[i].linear;
             LinearArgs a;
@@ -234,21 +243,25 @@ int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out
     }
     // Plan at a workgroup count: the dataflow form (hazards the reordering could break),
     // then the kernel: the decode-layer kernel when the ops repeat the Qwen2-0.5B decode
-    // layer and the count fits its tiling, else the general kernel within its limits.
-    auto plan_at = [&](int g, std::vector<SeqOp> &d, int &w, bool &layer) {
+    // layer and the count fits its tiling, the DiT-block kernel for the flow head's DiT
+    // blocks, else the general kernel within its limits.
+    auto plan_at = [&](int g, std::vector<SeqOp> &d, int &w, int &k) {
         int r = seq_plan(items, n_items, g, d, w);
         if (r) return r;
-        layer = g_tuning.seq_layer == 0 && layer_pattern(d.data(), n_items, g);
-        return layer ? MT_OK : seq_general_limits(items, n_items, g);
+        const bool special = g_tuning.seq_layer == 0;
+        k = special && layer_pattern(d.data(), n_items, g)  ? MT_SEQ_DECODE_LAYER
+            : special && dit_pattern(d.data(), n_items, g) ? MT_SEQ_DIT_BLOCK
+                                                            : MT_SEQ_GENERAL;
+        return k != MT_SEQ_GENERAL ? MT_OK : seq_general_limits(items, n_items, g);
     };
     // Plan once with the expected workgroup count before touching the device, so a sequence
     // no kernel can take is rejected without a GPU; re-plan for the device's counts.
     std::vector<SeqOp> dev;
     int wt = DT_F16;
-    bool layer = false;
+    int kind = MT_SEQ_GENERAL;
     const int want = g_tuning.seq_groups;
     const int guess = want > 0 ? want : 256;
-    int rc = plan_at(guess, dev, wt, layer);
+    int rc = plan_at(guess, dev, wt, kind);
     if (rc) return rc;
     if (n_items == 0) return set_error(MT_EINVAL, "mt_seq_create: empty sequence");
     int groups = 0, preferred = 0;
@@ -257,18 +270,18 @@ int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out
     // The preferred count when the plan fits it, else every workgroup the device holds.
     std::vector<SeqOp> d2;
     int wt2 = DT_F16;
-    bool layer2 = false;
-    if (plan_at(preferred, d2, wt2, layer2) == MT_OK) {
+    int kind2 = MT_SEQ_GENERAL;
+    if (plan_at(preferred, d2, wt2, kind2) == MT_OK) {
         groups = preferred;
     } else {
-        rc = plan_at(groups, d2, wt2, layer2);
+        rc = plan_at(groups, d2, wt2, kind2);
         if (rc) return rc;
     }
     dev.swap(d2);
     wt = wt2;
-    layer = layer2;
+    kind = kind2;
     SeqPlan *plan = nullptr;
-    rc = seq_create(dev.data(), n_items, wt, groups, layer, &plan);
+    rc = seq_create(dev.data(), n_items, wt, groups, kind, &plan);
     if (rc) return rc;
     *out = reinterpret_cast<mt_seq *>(plan);
     return MT_OK;

@@ -35,23 +35,33 @@
 // tiling holds for 224 <= G <= 256 (the host checks it).
 #pragma once
 
+#include "dit_attend.hpp"
 #include "seq_kernel.hpp"
 
 namespace mt {
 
-enum : int { LC_QKV = 0, LC_O = 1, LC_GU = 2, LC_DOWN = 3 };
+// Op classes: the Qwen2-0.5B decode layer's four, and the four linears of a DiT block (the
+// DiT-block kernel below).  A kernel runs one set of four; SLOT indexes its per-class state.
+enum : int { LC_QKV = 0, LC_O = 1, LC_GU = 2, LC_DOWN = 3, LC_DQKV = 4, LC_DO = 5, LC_FF1 = 6, LC_FF2 = 7 };
 
 // Compile-time shape and tiling of op class C at M rows.
 template <int C, int M>
 struct LCls {
-    static constexpr uint32_t N = C == LC_QKV ? LAY_QKV : C == LC_GU ? LAY_I : LAY_H;
-    static constexpr uint32_t K = C == LC_DOWN ? LAY_I : LAY_H;
+    static constexpr bool DIT = C >= LC_DQKV;
+    static constexpr int SLOT = C & 3;
+    static constexpr uint32_t N = C == LC_QKV ? LAY_QKV : C == LC_GU ? LAY_I : C == LC_DQKV ? DIT_QKV
+                                : C == LC_FF1 ? DIT_FF : DIT ? DIT_H : LAY_H;
+    static constexpr uint32_t K = C == LC_DOWN ? LAY_I : C == LC_FF2 ? DIT_FF : DIT ? DIT_H : LAY_H;
     static constexpr bool GATED = C == LC_GU;
-    static constexpr bool NORM = C == LC_QKV || C == LC_GU;
-    static constexpr bool BIAS = C == LC_QKV;
-    static constexpr bool ACC = C == LC_O || C == LC_DOWN;
-    static constexpr uint32_t FLAGS = (BIAS ? F_BIAS : 0u) | (ACC ? F_ACCUM : 0u) | (GATED ? F_SILU_GATE : 0u);
-    static constexpr uint32_t S = GATED ? 1u : C == LC_QKV ? 2u : 4u;
+    static constexpr bool NORM = C == LC_QKV || C == LC_GU || C == LC_DQKV || C == LC_FF1;
+    static constexpr bool BIAS = C == LC_QKV || DIT;
+    static constexpr bool ACC = C == LC_O || C == LC_DOWN || C == LC_DO || C == LC_FF2;
+    static constexpr bool GELU = C == LC_FF1;
+    // x is the DiT attention of the block's qkv, computed by the workgroup while staging.
+    static constexpr bool ATTX = C == LC_DO;
+    static constexpr uint32_t FLAGS =
+        (BIAS ? F_BIAS : 0u) | (ACC ? F_ACCUM : 0u) | (GATED ? F_SILU_GATE : 0u) | (GELU ? F_GELU : 0u);
+    static constexpr uint32_t S = GATED || C == LC_DQKV || C == LC_FF1 ? 1u : C == LC_QKV ? 2u : 4u;
     static constexpr uint32_t LS = S == 4 ? 2u : S == 2 ? 1u : 0u;
     static constexpr uint32_t CG = (2 * S * M + 15) / 16;  // B column groups (MFMAs per weight tile)
     static constexpr uint32_t RPG = M / CG;                 // x rows per column group
@@ -67,7 +77,7 @@ struct LCls {
     // LDS partial sums: [row tile][x row][virtual row][slot]
     static constexpr uint32_t VR = GATED ? 16u : FPT;
     static constexpr uint32_t PART = RT * M * VR * 8;
-    static_assert(KB % S == 0 && 2 * S * RPG == (CG == 1 ? 2 * S * M : 16) && RPG * CG == M, "tiling");
+    static_assert(KB % S == 0 && 2 * S * RPG == (CG == 1 ? 2 * S * M : 16) && RPG * CG == M && CG <= 3, "tiling");
     static_assert((!GATED || RT * KBS % 7 == 0) && (CG == 1 || !GATED), "tiling");
 };
 
@@ -150,11 +160,15 @@ template <int WT, int M>
 struct LayCtx {
     static constexpr uint32_t PLANE = M * LAY_I + 64;  // hi / lo planes of the x staging (elements)
     uint16_t *xs;    // [2][PLANE] staged x of the current op
-    float *part[4];  // per class: [row tile][x row][virtual row][8 slots]
-    float *ssw[4];   // per norm class: [M][8 slots] sums of x^2
+    float *part[4];  // per class slot: [row tile][x row][virtual row][8 slots]
+    float *ssw[4];   // per norm class slot: [M][8 slots] sums of x^2
     LLane ln[4];
     uint32_t r0[4], nr[4];
-    uint32_t tid, lane, w, parity;
+    uint32_t tid, lane, w, parity, g;
+    // DiT-block kernel: the lane's RoPE pair's cos / sin at positions 0 .. S - 1 and the
+    // attention's score scale.
+    float rc[DIT_MAXS], rs[DIT_MAXS];
+    float ascale;
     bool up;         // gate|up: the lane's tile rows are W2's
     __amdgpu_buffer_rsrc_t rsrc;
     uint32_t *tags;
@@ -171,8 +185,8 @@ __device__ __forceinline__ void lay_tiles_w(const LayCtx<WT, M> &cx, const uint1
     static_assert(K1 <= L::TA && L::TA <= NN, "tile registers");
     constexpr LRange r = lay_range<C, M>(W);
     const uint16_t *base = (L::GATED && cx.up) ? w2 : w;
-    const char *p = reinterpret_cast<const char *>(base) + cx.ln[C].woff;
-    const char *p2 = reinterpret_cast<const char *>(base) + cx.ln[C].woff2;
+    const char *p = reinterpret_cast<const char *>(base) + cx.ln[L::SLOT].woff;
+    const char *p2 = reinterpret_cast<const char *>(base) + cx.ln[L::SLOT].woff2;
 #pragma unroll
     for (uint32_t k = K0; k < K1; k++) {
         const char *a = k < r.ks ? p + k * 64 : p2 + (k - r.ks) * 64;
@@ -239,20 +253,119 @@ template <int WT, int M, int C, int W, int NA>
 __device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A)[NA]) {
     typedef LCls<C, M> L;
     constexpr LRange r = lay_range<C, M>(W);
-    const char *bp = reinterpret_cast<const char *>(cx.xs) + cx.ln[C].boff;
-    constexpr uint32_t GOFF = L::RPG * L::K * 2;  // bytes from column group 0's rows to group 1's
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc, accg = acc;
+    const char *bp = reinterpret_cast<const char *>(cx.xs) + cx.ln[L::SLOT].boff;
+    constexpr uint32_t GOFF = L::RPG * L::K * 2;  // bytes from one column group's rows to the next's
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc, accg = acc, accg2 = acc;
 #pragma unroll
     for (uint32_t k = r.kb; k < r.ke; k++) {  // block js + k of row tile rt, or k - ks of rt + 1
         const char *b = k < r.ks ? bp + k * 64 : bp + (static_cast<int>(k - r.ks) - static_cast<int>(r.js)) * 64;
         const u32x4 bv = *reinterpret_cast<const u32x4 *>(b);
         if (k < r.ks) acc = mfma16<WT>(A[k], bv, acc);
         else acc2 = mfma16<WT>(A[k], bv, acc2);
-        if constexpr (L::CG == 2) accg = mfma16<WT>(A[k], *reinterpret_cast<const u32x4 *>(b + GOFF), accg);
+        if constexpr (L::CG >= 2) accg = mfma16<WT>(A[k], *reinterpret_cast<const u32x4 *>(b + GOFF), accg);
+        if constexpr (L::CG >= 3) accg2 = mfma16<WT>(A[k], *reinterpret_cast<const u32x4 *>(b + 2 * GOFF), accg2);
     }
-    lay_flush<M, C>(acc, cx.part[C], r.rt, W, cx.lane);
-    if constexpr (r.ks < L::TA) lay_flush<M, C>(acc2, cx.part[C], r.rt + 1, W, cx.lane);
-    if constexpr (L::CG == 2) lay_flush<M, C>(accg, cx.part[C], r.rt, W, cx.lane, L::RPG);
+    float *part = cx.part[L::SLOT];
+    lay_flush<M, C>(acc, part, r.rt, W, cx.lane);
+    if constexpr (r.ks < L::TA) lay_flush<M, C>(acc2, part, r.rt + 1, W, cx.lane);
+    if constexpr (L::CG >= 2) lay_flush<M, C>(accg, part, r.rt, W, cx.lane, L::RPG);
+    if constexpr (L::CG >= 3) lay_flush<M, C>(accg2, part, r.rt, W, cx.lane, 2 * L::RPG);
+}
+
+// The DiT attention that a DiT block's out projection stages as its x (DiT-block kernel; the
+// arithmetic of dit_attend.hpp): half wave hw of the 14 takes the (sequence, head) groups hw,
+// hw + 14 and hw + 28 of the B H = 32, lane p the interleaved-RoPE pair 2p, 2p + 1 of the q, k
+// and v of the group's S rows.  Each workgroup computes all of it from the block's tagged qkv
+// (read once), so the attention adds no exchange between workgroups.
+constexpr uint32_t DIT_GROUPS = DIT_B * DIT_HEADS, DIT_HW = LAY_THREADS / 32;
+constexpr uint32_t DIT_GR = (DIT_GROUPS + DIT_HW - 1) / DIT_HW;  // groups a half wave takes
+constexpr uint32_t DIT_T = 3 * DIT_S;                             // q, k and v pairs of a group
+static_assert(DIT_GR * DIT_T <= 32, "one stale bit per pair");
+
+__device__ __forceinline__ u32x2 ldtag2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, SC1);
+}
+__device__ __forceinline__ bool tagged2(const u32x2 a, uint32_t parity) {
+    return parity ? (a.x & a.y & 1u) != 0 : ((a.x | a.y) & 1u) == 0;
+}
+// Byte offset in the tag buffer of pair t of group gi (t < S: q of row t; then the S k rows,
+// then the S v rows); d.xoff / d.xld locate the block's qkv output.
+__device__ __forceinline__ uint32_t dit_att_off(const LayOp &d, uint32_t gi, uint32_t t, uint32_t p) {
+    const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, part = t / DIT_S, row = b * DIT_S + t % DIT_S;
+    return (d.xoff + row * d.xld + part * (DIT_HEADS * 64) + h * 64 + 2 * p) * 4u;
+}
+template <int WT, int M>
+__device__ __forceinline__ void dit_att_request(const LayCtx<WT, M> &cx, const LayOp &d, u32x2 (&a)[DIT_GR][DIT_T]) {
+    const uint32_t hw = cx.tid >> 5, p = cx.tid & 31;
+#pragma unroll
+    for (uint32_t r = 0; r < DIT_GR; r++) {
+        const uint32_t gi = hw + DIT_HW * r;
+#pragma unroll
+        for (uint32_t t = 0; t < DIT_T; t++)  // past the groups: an offset outside the buffer reads 0
+            a[r][t] = ldtag2(cx.rsrc, gi < DIT_GROUPS ? dit_att_off(d, gi, t, p) : 0xFFFFFFF0u);
+    }
+}
+// Waits for the requested pairs, then computes each group's S query rows and stages them
+// (hi + lo) as x of the out projection (K = H 64); `item` is the attention item, whose user
+// output workgroup 0 writes when it is the region's last write.
+template <int WT, int M, uint32_t K>
+__device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d, const SeqOp &item,
+                                              u32x2 (&a)[DIT_GR][DIT_T]) {
+    const uint32_t hw = cx.tid >> 5, p = cx.tid & 31;
+    uint32_t stale = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < DIT_GR; r++)
+#pragma unroll
+        for (uint32_t t = 0; t < DIT_T; t++)
+            if (hw + DIT_HW * r < DIT_GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * DIT_T + t);
+    uint32_t spins = 0;
+    while (stale && !cx.gave_up) {
+        if (++spins > SPIN_LIMIT) {
+            cx.gave_up = true;
+            raise_flag(cx.sync, SYNC_TIMEOUT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (uint32_t r = 0; r < DIT_GR; r++)
+#pragma unroll
+            for (uint32_t t = 0; t < DIT_T; t++)
+                if ((stale >> (r * DIT_T + t)) & 1u) a[r][t] = ldtag2(cx.rsrc, dit_att_off(d, hw + DIT_HW * r, t, p));
+        stale = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < DIT_GR; r++)
+#pragma unroll
+            for (uint32_t t = 0; t < DIT_T; t++)
+                if (hw + DIT_HW * r < DIT_GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * DIT_T + t);
+    }
+    const bool write_out = item.final_out != 0 && cx.g == 0;
+    bool range_ok = true;
+#pragma unroll
+    for (uint32_t r = 0; r < DIT_GR; r++) {
+        const uint32_t gi = hw + DIT_HW * r;
+        if (gi >= DIT_GROUPS) continue;  // the whole half wave together
+        const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, col = h * 64 + 2 * p;
+        auto pair = [&](uint32_t t) { return make_float2(untag(a[r][t].x), untag(a[r][t].y)); };
+        DitItem it;
+#pragma unroll
+        for (uint32_t j = 0; j < DIT_MAXS; j++) {
+            it.k[j] = j < DIT_S ? pair(DIT_S + j) : make_float2(0.0f, 0.0f);
+            it.v[j] = j < DIT_S ? pair(2 * DIT_S + j) : make_float2(0.0f, 0.0f);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < DIT_S; i++) {
+            it.q = pair(i);
+            const float2 o = dit_item_attend(it, i, DIT_S, cx.rc, cx.rs, cx.ascale);
+            const uint32_t row = b * DIT_S + i;
+            const uint32_t hi = pack2<WT>(o.x, o.y);
+            const uint32_t lo = pack2<WT>(o.x - dec_lo<WT>(hi), o.y - dec_hi<WT>(hi));
+            *reinterpret_cast<uint32_t *>(cx.xs + row * K + col) = hi;
+            *reinterpret_cast<uint32_t *>(cx.xs + LayCtx<WT, M>::PLANE + row * K + col) = lo;
+            if constexpr (WT == DT_F16) range_ok = range_ok && fmaxf(fabsf(o.x), fabsf(o.y)) <= 65504.0f;
+            if (write_out) *reinterpret_cast<float2 *>(item.y + static_cast<size_t>(row) * item.ldy + col) = o;
+        }
+    }
+    if (!range_ok) raise_flag(cx.sync, SYNC_RANGE);
 }
 
 // One op of class C (descriptor d; ops[i] holds its full descriptor for an external x): A
@@ -272,14 +385,16 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     constexpr bool EARLY = L::NORM && M <= 2;
     static_assert(NB < 16, "a batch fits the explicit wait below");
     const uint32_t tid = cx.tid, lane = cx.lane;
-    const uint32_t r0 = cx.r0[C], nr = cx.nr[C];
+    const uint32_t r0 = cx.r0[L::SLOT], nr = cx.nr[L::SLOT];
     const bool xext = (d.flags & LAY_XEXT) != 0;
 
-    // Activations: chunk e = tid + 448 r is 4 k of x row e / K4.
+    // Activations: chunk e = tid + 448 r is 4 k of x row e / K4 (or the DiT attention's qkv).
     u32x4 xv[L::XR];
     u32x2 gv[L::XR];
+    u32x2 att[L::ATTX ? DIT_GR : 1][DIT_T];
+    if constexpr (L::ATTX) dit_att_request(cx, d, att);
 #pragma unroll
-    for (uint32_t r = 0; r < L::XR; r++) {
+    for (uint32_t r = 0; r < (L::ATTX ? 0u : L::XR); r++) {
         const uint32_t e = tid + 448 * r;
         const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
         const bool ok = e < L::NCH;
@@ -315,78 +430,82 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
         yw = ld32(yext ? reinterpret_cast<const uint32_t *>(d.y) + static_cast<size_t>(om) * d.ldy + n
                        : cx.tags + d.yoff + om * d.yld + n);
 
-    // Wait for the activations; stale chunks are requested again, all at once per round.
-    if (!xext) {
-        uint32_t stale = 0;
-#pragma unroll
-        for (uint32_t r = 0; r < L::XR; r++)
-            if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
-        uint32_t spins = 0;
-        while (stale && !cx.gave_up) {
-            if (++spins > SPIN_LIMIT) {
-                cx.gave_up = true;
-                raise_flag(cx.sync, SYNC_TIMEOUT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (uint32_t r = 0; r < L::XR; r++) {
-                if ((stale >> r) & 1u) {
-                    const uint32_t e = tid + 448 * r;
-                    const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
-                    xv[r] = ldtag4(cx.rsrc, (d.xoff + m * d.xld + k) * 4u);
-                }
-            }
-            stale = 0;
+    if constexpr (L::ATTX) {
+        dit_att_stage<WT, M, L::K>(cx, d, ops[i - 1], att);
+    } else {
+        // Wait for the activations; stale chunks are requested again, all at once per round.
+        if (!xext) {
+            uint32_t stale = 0;
 #pragma unroll
             for (uint32_t r = 0; r < L::XR; r++)
                 if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
-        }
-    }
-    if constexpr (EARLY) issue();
-    // Convert into the staging: tag bit cleared, x^2 summed per row, gain applied, split
-    // into hi + lo halves of the weights' type.
-    const uint32_t clear = xext ? ~0u : ~1u;
-    float ss[M];
+            uint32_t spins = 0;
+            while (stale && !cx.gave_up) {
+                if (++spins > SPIN_LIMIT) {
+                    cx.gave_up = true;
+                    raise_flag(cx.sync, SYNC_TIMEOUT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-    for (int mm = 0; mm < M; mm++) ss[mm] = 0.0f;
-    bool range_ok = true;
+                for (uint32_t r = 0; r < L::XR; r++) {
+                    if ((stale >> r) & 1u) {
+                        const uint32_t e = tid + 448 * r;
+                        const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+                        xv[r] = ldtag4(cx.rsrc, (d.xoff + m * d.xld + k) * 4u);
+                    }
+                }
+                stale = 0;
 #pragma unroll
-    for (uint32_t r = 0; r < L::XR; r++) {
-        const uint32_t e = tid + 448 * r;
-        if (e < L::NCH) {
-            const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
-            float x[4];
-            x[0] = __uint_as_float(xv[r].x & clear);
-            x[1] = __uint_as_float(xv[r].y & clear);
-            x[2] = __uint_as_float(xv[r].z & clear);
-            x[3] = __uint_as_float(xv[r].w & clear);
-            if constexpr (L::NORM) {
-                float t = x[0] * x[0];
-                t = fmaf(x[1], x[1], t);
-                t = fmaf(x[2], x[2], t);
-                t = fmaf(x[3], x[3], t);
-#pragma unroll
-                for (int mm = 0; mm < M; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
-                x[0] *= dec_lo<WT>(gv[r].x);
-                x[1] *= dec_hi<WT>(gv[r].x);
-                x[2] *= dec_lo<WT>(gv[r].y);
-                x[3] *= dec_hi<WT>(gv[r].y);
+                for (uint32_t r = 0; r < L::XR; r++)
+                    if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
             }
-            if constexpr (WT == DT_F16)
-                range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
-            u32x2 hi, lo;
-            split4p<WT>(x, hi, lo);
-            *reinterpret_cast<u32x2 *>(cx.xs + m * L::K + k) = hi;
-            *reinterpret_cast<u32x2 *>(cx.xs + LayCtx<WT, M>::PLANE + m * L::K + k) = lo;
         }
-    }
-    if (!range_ok) raise_flag(cx.sync, SYNC_RANGE);
-    if constexpr (L::NORM) {
+        if constexpr (EARLY) issue();
+        // Convert into the staging: tag bit cleared, x^2 summed per row, gain applied, split
+        // into hi + lo halves of the weights' type.
+        const uint32_t clear = xext ? ~0u : ~1u;
+        float ss[M];
 #pragma unroll
-        for (int mm = 0; mm < M; mm++) {
-            const float t = wave_sum(ss[mm]);
-            if (lane == 0) cx.ssw[C][mm * 8 + cx.w] = t;
+        for (int mm = 0; mm < M; mm++) ss[mm] = 0.0f;
+        bool range_ok = true;
+#pragma unroll
+        for (uint32_t r = 0; r < L::XR; r++) {
+            const uint32_t e = tid + 448 * r;
+            if (e < L::NCH) {
+                const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+                float x[4];
+                x[0] = __uint_as_float(xv[r].x & clear);
+                x[1] = __uint_as_float(xv[r].y & clear);
+                x[2] = __uint_as_float(xv[r].z & clear);
+                x[3] = __uint_as_float(xv[r].w & clear);
+                if constexpr (L::NORM) {
+                    float t = x[0] * x[0];
+                    t = fmaf(x[1], x[1], t);
+                    t = fmaf(x[2], x[2], t);
+                    t = fmaf(x[3], x[3], t);
+#pragma unroll
+                    for (int mm = 0; mm < M; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
+                    x[0] *= dec_lo<WT>(gv[r].x);
+                    x[1] *= dec_hi<WT>(gv[r].x);
+                    x[2] *= dec_lo<WT>(gv[r].y);
+                    x[3] *= dec_hi<WT>(gv[r].y);
+                }
+                if constexpr (WT == DT_F16)
+                    range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
+                u32x2 hi, lo;
+                split4p<WT>(x, hi, lo);
+                *reinterpret_cast<u32x2 *>(cx.xs + m * L::K + k) = hi;
+                *reinterpret_cast<u32x2 *>(cx.xs + LayCtx<WT, M>::PLANE + m * L::K + k) = lo;
+            }
+        }
+        if (!range_ok) raise_flag(cx.sync, SYNC_RANGE);
+        if constexpr (L::NORM) {
+#pragma unroll
+            for (int mm = 0; mm < M; mm++) {
+                const float t = wave_sum(ss[mm]);
+                if (lane == 0) cx.ssw[L::SLOT][mm * 8 + cx.w] = t;
+            }
         }
     }
     __syncthreads();  // x staged
@@ -410,7 +529,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     // Outputs: the 8 slots summed in slot order, norm scale, epilogue, tagged store.
     if (live) {
         auto total = [&](uint32_t rt, uint32_t v) {
-            const float *p = cx.part[C] + ((rt * M + om) * L::VR + v) * 8;
+            const float *p = cx.part[L::SLOT] + ((rt * M + om) * L::VR + v) * 8;
             const f32x4 a = *reinterpret_cast<const f32x4 *>(p);
             const f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
             return ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
@@ -423,7 +542,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
             a1 = total(0, of);
         }
         if constexpr (L::NORM) {
-            const float *sp = cx.ssw[C] + om * 8;
+            const float *sp = cx.ssw[L::SLOT] + om * 8;
             const f32x4 a = *reinterpret_cast<const f32x4 *>(sp);
             const f32x4 b = *reinterpret_cast<const f32x4 *>(sp + 4);
             const float t = ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
@@ -603,6 +722,119 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
             lay_tiles<WT, M, LC_QKV, Q1, LQ::TA>(cx, dq, PQ);
             lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[nx + 1 + A], PO);
         });
+    }
+    // The last workgroup out advances the epoch for the next run.
+    if (cx.tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(sync + SYNC_EXIT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == G - 1) {
+            __hip_atomic_store(sync + SYNC_EXIT, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(sync + SYNC_EPOCH, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// The DiT-block kernel: n_ops = 5 L ops, L DiT blocks of the flow head (dit_pattern: qkv,
+// DiT attention, out, ff1, ff2 at M = 6 on DIT_G workgroups, the host checks them), the
+// packed descriptors after the op descriptors.  The attention item is not a step of its own:
+// each workgroup computes it while staging the out projection's x (dit_att_stage).  Tiling at
+// 256 workgroups: qkv 12 and ff1 16 features a workgroup (S = 1, one row tile, 32 block steps
+// as 5 a wave), out and ff2 4 features (S = 4, three B column groups of two rows).  Each op
+// requests the weight tiles of the op two steps on (qkv: ff1, out: ff2, ff1: the next block's
+// qkv, ff2: the next block's out) behind its output stores.
+template <int WT>
+__global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
+                                                               uint32_t *sync, const uint32_t *tags,
+                                                               uint32_t tag_bytes) {
+    constexpr int M = DIT_B * DIT_S;
+    typedef LayCtx<WT, M> X;
+    typedef LCls<LC_DQKV, M> LQ;
+    typedef LCls<LC_DO, M> LO;
+    typedef LCls<LC_FF1, M> LF;
+    typedef LCls<LC_FF2, M> LD;
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2 * X::PLANE];
+    __shared__ __attribute__((aligned(16))) float p_q[LQ::PART];
+    __shared__ __attribute__((aligned(16))) float p_o[LO::PART];
+    __shared__ __attribute__((aligned(16))) float p_f[LF::PART];
+    __shared__ __attribute__((aligned(16))) float p_d[LD::PART];
+    __shared__ __attribute__((aligned(16))) float s_q[M * 8];
+    __shared__ __attribute__((aligned(16))) float s_f[M * 8];
+    const LayOp *__restrict__ lops = reinterpret_cast<const LayOp *>(ops + n_ops);
+
+    X cx;
+    cx.xs = xs;
+    cx.part[LQ::SLOT] = p_q;
+    cx.part[LO::SLOT] = p_o;
+    cx.part[LF::SLOT] = p_f;
+    cx.part[LD::SLOT] = p_d;
+    cx.ssw[LQ::SLOT] = s_q;
+    cx.ssw[LF::SLOT] = s_f;
+    cx.ssw[LO::SLOT] = s_q;
+    cx.ssw[LD::SLOT] = s_f;
+    cx.tid = threadIdx.x;
+    cx.lane = cx.tid & 63;
+    cx.w = __builtin_amdgcn_readfirstlane(cx.tid >> 6);
+    cx.sync = sync;
+    cx.tags = const_cast<uint32_t *>(tags);
+    cx.gave_up = false;
+    const uint32_t g = blockIdx.x, G = gridDim.x;
+    cx.g = g;
+    const uint32_t Ns[4] = {LQ::N, LO::N, LF::N, LD::N};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        cx.r0[c] = static_cast<uint32_t>(static_cast<uint64_t>(g) * Ns[c] / G);
+        cx.nr[c] = static_cast<uint32_t>(static_cast<uint64_t>(g + 1) * Ns[c] / G) - cx.r0[c];
+    }
+    {
+        LRange rq{}, ro{}, rf{}, rd{};
+        switch (cx.w) {
+#define DIT_RANGES(W)                      \
+    case W:                                \
+        rq = lay_range<LC_DQKV, M>(W);     \
+        ro = lay_range<LC_DO, M>(W);       \
+        rf = lay_range<LC_FF1, M>(W);      \
+        rd = lay_range<LC_FF2, M>(W);      \
+        break;
+            DIT_RANGES(0) DIT_RANGES(1) DIT_RANGES(2) DIT_RANGES(3) DIT_RANGES(4) DIT_RANGES(5)
+            default: DIT_RANGES(6)
+#undef DIT_RANGES
+        }
+        cx.ln[LQ::SLOT] = lay_lane<LC_DQKV, M>(cx.r0[LQ::SLOT], cx.nr[LQ::SLOT], cx.lane, rq, X::PLANE);
+        cx.ln[LO::SLOT] = lay_lane<LC_DO, M>(cx.r0[LO::SLOT], cx.nr[LO::SLOT], cx.lane, ro, X::PLANE);
+        cx.ln[LF::SLOT] = lay_lane<LC_FF1, M>(cx.r0[LF::SLOT], cx.nr[LF::SLOT], cx.lane, rf, X::PLANE);
+        cx.ln[LD::SLOT] = lay_lane<LC_FF2, M>(cx.r0[LD::SLOT], cx.nr[LD::SLOT], cx.lane, rd, X::PLANE);
+        cx.up = false;
+    }
+    // Slots no compute wave writes stay zero.
+    for (uint32_t e = cx.tid; e < LQ::PART; e += LAY_THREADS) p_q[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < LO::PART; e += LAY_THREADS) p_o[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < LF::PART; e += LAY_THREADS) p_f[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < LD::PART; e += LAY_THREADS) p_d[e] = 0.0f;
+    for (uint32_t e = cx.tid; e < M * 8; e += LAY_THREADS) s_q[e] = s_f[e] = 0.0f;
+    const uint32_t epoch = __hip_atomic_load(sync + SYNC_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    cx.parity = epoch & 1u;
+    cx.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(tags), 0, static_cast<int>(tag_bytes), BUF_DWORD3);
+    // The attention's rotation table (every item shares the first one's frequencies and scale).
+    const SeqOp &a0 = ops[1];
+    dit_rope_table(gld(a0.inv_freq + (cx.tid & 31)), DIT_S, cx.rc, cx.rs);
+    cx.ascale = a0.eps;
+
+    u32x4 PQ[LQ::TA], PO[LO::TA], PF[LF::TA], PD[LD::TA];
+    const uint32_t L = n_ops / 5;
+    if (L > 0) {
+        lay_tiles<WT, M, LC_DQKV, 0, LQ::TA>(cx, lops[0], PQ);
+        lay_tiles<WT, M, LC_DO, 0, LO::TA>(cx, lops[2], PO);
+    }
+    __syncthreads();
+    for (uint32_t l = 0; l < L; l++) {
+        // The last block's requests for a next block read block 0's weights again (unused), so
+        // every op requests the same number of tiles.
+        const uint32_t i = 5 * l, nx = l + 1 < L ? i + 5 : 0;
+        const uint32_t io = i + 2, i1 = i + 3, i2 = i + 4;  // out, ff1, ff2 (i + 1: the attention)
+        lay_step<WT, M, LC_DQKV, 0>(cx, ops, i, lops[i], PQ, [&]() { lay_tiles<WT, M, LC_FF1, 0, LF::TA>(cx, lops[i1], PF); });
+        lay_step<WT, M, LC_DO, 0>(cx, ops, io, lops[io], PO, [&]() { lay_tiles<WT, M, LC_FF2, 0, LD::TA>(cx, lops[i2], PD); });
+        lay_step<WT, M, LC_FF1, 0>(cx, ops, i1, lops[i1], PF, [&]() { lay_tiles<WT, M, LC_DQKV, 0, LQ::TA>(cx, lops[nx], PQ); });
+        lay_step<WT, M, LC_FF2, 0>(cx, ops, i2, lops[i2], PD,
+                                   [&]() { lay_tiles<WT, M, LC_DO, 0, LO::TA>(cx, lops[nx + 2], PO); });
     }
     // The last workgroup out advances the epoch for the next run.
     if (cx.tid == 0) {

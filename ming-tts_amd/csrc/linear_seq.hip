@@ -13,7 +13,8 @@ struct SeqPlan {
     int groups = 0;
     int device = 0;
     seq_fn fn = nullptr;
-    bool layer = false;  // runs the decode-layer kernel (packed descriptors follow the ops)
+    bool layer = false;  // runs the decode-layer or DiT-block kernel (packed descriptors follow the ops)
+    int kind = MT_SEQ_GENERAL;
     int threads = SEQ_THREADS;
 };
 
@@ -38,7 +39,7 @@ int seq_limits(int *groups_out, int *preferred_out) {
     return MT_OK;
 }
 
-int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, bool layer, SeqPlan **out) {
+int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, int kind, SeqPlan **out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(MT_EHIP, "mt_seq_create: hipGetDevice: %s", hipGetErrorString(e));
@@ -56,7 +57,12 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, bool layer, SeqPl
         if (ops[i].M != m_all) m_all = 0;
     bool attn = false;
     for (uint32_t i = 0; i < n_ops; i++) attn = attn || ops[i].kind == SEQ_ATTN;
-    if (layer) {
+    p->kind = kind;
+    if (kind == MT_SEQ_DIT_BLOCK) {
+        p->fn = dit_block_kernel_fn(wt);
+        p->layer = true;
+        p->threads = LAY_THREADS;
+    } else if (kind == MT_SEQ_DECODE_LAYER) {
         p->fn = layer_kernel_fn(wt, m_all, attn);
         p->layer = true;
         p->threads = LAY_THREADS;
@@ -113,6 +119,12 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, bool layer, SeqPl
                 d.tag = static_cast<uint32_t>(o.tag - p->d_tags);
                 d.eps = o.eps;
                 d.flags = (o.xsrc < 0 ? LAY_XEXT : 0u) | (o.ysrc < 0 ? LAY_YEXT : 0u) | (o.final_out ? LAY_FINAL : 0u);
+                // A linear whose x is a DiT attention item's output computes that attention
+                // itself: its x is the item's qkv.
+                if (o.kind == SEQ_LINEAR && o.xsrc >= 0 && ops[o.xsrc].kind == SEQ_DIT) {
+                    d.xoff = ops[o.xsrc].xoff;
+                    d.xld = ops[o.xsrc].xld;
+                }
             }
             e = hipMemcpy(p->d_ops + n_ops, lay.data(), sizeof(LayOp) * n_ops, hipMemcpyHostToDevice);
         }
@@ -164,7 +176,7 @@ int seq_check(SeqPlan *p) {
 
 int seq_groups(const SeqPlan *p) { return p->groups; }
 
-int seq_kernel_kind(const SeqPlan *p) { return p->layer ? MT_SEQ_DECODE_LAYER : MT_SEQ_GENERAL; }
+int seq_kernel_kind(const SeqPlan *p) { return p->kind; }
 
 void seq_destroy(SeqPlan *p) {
     if (!p) return;

@@ -71,7 +71,9 @@ struct SeqOp {
     int32_t pad;
 };
 static_assert(sizeof(SeqOp) % 16 == 0, "SeqOp is staged into LDS in 16-byte pieces");
-enum : int32_t { SEQ_LINEAR = 0, SEQ_ATTN = 1 };
+// A DiT attention item (kind SEQ_DIT): x the qkv rows (M = B S rows, K = 3 H 64), y the output
+// (N = H 64), eps the score scale, heads = H | S << 16, inv_freq its 32 RoPE frequencies.
+enum : int32_t { SEQ_LINEAR = 0, SEQ_ATTN = 1, SEQ_DIT = 2 };
 struct SeqPlan;
 // Limits of the persistent sequence kernel: threads per workgroup, output features per
 // workgroup per op, and the LDS areas of its waves.
@@ -100,7 +102,15 @@ int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups);
 // 896 x 4864 accumulating) at one M of 1, 2 or 4, with `groups` in the decode-layer
 // kernel's range?
 bool layer_pattern(const SeqOp *ops, uint32_t n, int groups);
-int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, bool layer, SeqPlan **out);
+// The DiT blocks of the flow head (DiTForward.encode, DiT.swift:35-52) the DiT-block kernel is
+// specialised for: per block rmsnorm+qkv 3072 x 1024 + bias, DiT attention (B 2, S 3, H 16) of
+// that qkv, out 1024 x 1024 + bias += of the attention's output, rmsnorm+ff1 4096 x 1024 + bias
+// GELU, ff2 1024 x 4096 + bias +=, at M = 6, on exactly DIT_G workgroups.
+constexpr uint32_t DIT_H = 1024, DIT_QKV = 3072, DIT_FF = 4096, DIT_B = 2, DIT_S = 3, DIT_HEADS = 16;
+constexpr int DIT_G = 256;
+bool dit_pattern(const SeqOp *ops, uint32_t n, int groups);
+// The kernel of a plan: MT_SEQ_GENERAL, MT_SEQ_DECODE_LAYER or MT_SEQ_DIT_BLOCK.
+int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, int kind, SeqPlan **out);
 int seq_run(SeqPlan *p, hipStream_t stream);
 int seq_check(SeqPlan *p);
 void seq_destroy(SeqPlan *p);

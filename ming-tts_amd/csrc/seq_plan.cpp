@@ -114,6 +114,23 @@ int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp
             d.inv_freq = a.inv_freq;
             d.cache_stride = a.cache_stride;
             d.cache_t = a.cache_t;
+        } else if (items[i].kind == MT_SEQ_DIT_ATTENTION) {
+            const mt_dit_attn_op &a = items[i].dit;
+            const uint32_t rows = a.B * a.S, N = a.H * 64;
+            xv[i] = View{reinterpret_cast<const char *>(a.qkv), static_cast<uint64_t>(a.ldq) * 4, uint64_t(3 * N) * 4, rows};
+            yv[i] = View{reinterpret_cast<const char *>(a.out), static_cast<uint64_t>(a.ldo) * 4, uint64_t(N) * 4, rows};
+            d.kind = SEQ_DIT;
+            d.x = a.qkv;
+            d.xt = MT_F32;
+            d.ldx = a.ldq;
+            d.y = a.out;
+            d.ldy = a.ldo;
+            d.M = rows;
+            d.N = N;
+            d.K = 3 * N;
+            d.eps = a.scale;
+            d.heads = a.H | (a.S << 16);
+            d.inv_freq = a.inv_freq;
         } else {
             const mt_linear_op &o = items[i].linear;
             const mt_gemv_params &p = o.p;
@@ -173,10 +190,11 @@ int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp
             // When x spans all heads of an attention item whose own x spans all of a linear
             // producer's features (q, k and v heads), those heads consumed every feature of
             // that producer: every workgroup has finished it.  (The attention item itself
-            // runs on a few workgroups; its own x reads prove nothing.)
+            // runs on a few workgroups; its own x reads prove nothing.)  A DiT attention item
+            // is computed by every workgroup from all of its qkv, the same argument.
             if (d.kind == SEQ_LINEAR && d.xcol == 0 && d.K == src.N) {
                 if (src.kind == SEQ_LINEAR && src.N >= static_cast<uint32_t>(groups)) db = std::max(db, d.xsrc);
-                if (src.kind == SEQ_ATTN && src.xsrc >= 0) {
+                if ((src.kind == SEQ_ATTN || src.kind == SEQ_DIT) && src.xsrc >= 0) {
                     const SeqOp &pp = out[src.xsrc];
                     if (pp.kind == SEQ_LINEAR && src.xcol == 0 && src.K == pp.N && pp.N >= static_cast<uint32_t>(groups))
                         db = std::max(db, src.xsrc);
@@ -219,6 +237,12 @@ int seq_plan(const mt_seq_item *items, uint32_t n, int groups, std::vector<SeqOp
 
 int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups) {
     for (uint32_t i = 0; i < n; i++) {
+        if (items[i].kind == MT_SEQ_DIT_ATTENTION)
+            return set_error(MT_ENOTSUP,
+                             "mt_seq_create: op %u: a DiT attention item runs only in the DiT-block kernel (blocks "
+                             "of qkv 3072 x 1024, attention B 2 S 3 H 16, out, ff1 4096 x 1024 GELU, ff2 at M = 6 on "
+                             "%d workgroups)",
+                             i, DIT_G);
         if (items[i].kind != MT_SEQ_LINEAR) continue;
         const mt_linear_op &o = items[i].linear;
         const mt_gemv_params &p = o.p;
@@ -285,6 +309,40 @@ bool layer_pattern(const SeqOp *ops, uint32_t n, int groups) {
         if (o.kind != SEQ_LINEAR || o.M != M || o.N != c.N || o.K != c.K || o.flags != c.flags ||
             (o.norm != nullptr) != c.norm || ((o.flags & F_BIAS) != 0) != (o.bias != nullptr))
             return false;
+    }
+    return true;
+}
+
+bool dit_pattern(const SeqOp *ops, uint32_t n, int groups) {
+    if (n == 0 || n % 5 || groups != DIT_G) return false;
+    struct Want {
+        uint32_t N, K, flags;
+        bool norm;
+    };
+    const Want want[5] = {{DIT_QKV, DIT_H, F_BIAS, true},
+                          {0, 0, 0, false},
+                          {DIT_H, DIT_H, F_BIAS | F_ACCUM, false},
+                          {DIT_FF, DIT_H, F_BIAS | F_GELU, true},
+                          {DIT_H, DIT_FF, F_BIAS | F_ACCUM, false}};
+    const uint32_t M = DIT_B * DIT_S;
+    for (uint32_t i = 0; i < n; i++) {
+        const SeqOp &o = ops[i];
+        const uint32_t j = i % 5;
+        if (o.M != M) return false;
+        if (j == 1) {
+            // The attention reads all of this block's qkv output; every item shares the first
+            // one's frequencies and scale (the kernel builds its rotation table once).
+            if (o.kind != SEQ_DIT || o.heads != (DIT_HEADS | (DIT_S << 16)) || o.xsrc != static_cast<int32_t>(i - 1) ||
+                o.xcol != 0 || o.inv_freq != ops[1].inv_freq || o.eps != ops[1].eps)
+                return false;
+            continue;
+        }
+        const Want &c = want[j];
+        if (o.kind != SEQ_LINEAR || o.N != c.N || o.K != c.K || o.flags != c.flags || (o.norm != nullptr) != c.norm ||
+            o.bias == nullptr)
+            return false;
+        // The out projection reads exactly the attention's output (it computes it itself).
+        if (j == 2 && (o.xsrc != static_cast<int32_t>(i - 1) || o.xcol != 0)) return false;
     }
     return true;
 }

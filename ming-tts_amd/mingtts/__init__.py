@@ -24,7 +24,7 @@ OK, EHIP, ENOMEM, EINVAL, ERANGE, ENOTSUP = 0, -5, -12, -22, -34, -95
 KERNEL_GEMV, KERNEL_GEMM, KERNEL_GEMV_MFMA = 1, 2, 3
 (TUNE_GEMV_ROWS_MAX, TUNE_GEMV_LANES, TUNE_GEMM_SPLITK, TUNE_SEQ_GROUPS, TUNE_SEQ_LAUNCH, TUNE_GEMM_TILE,
  TUNE_GEMM_STAGES, TUNE_GEMV_MFMA, TUNE_SEQ_LAYER) = 1, 2, 3, 4, 5, 6, 7, 8, 9
-SEQ_GENERAL, SEQ_DECODE_LAYER = 0, 1
+SEQ_GENERAL, SEQ_DECODE_LAYER, SEQ_DIT_BLOCK = 0, 1, 2
 
 # Every symbol include/mingtts_hip.h declares.
 EXPORTS = (
@@ -80,12 +80,19 @@ class AttnOp(ctypes.Structure):
                 ("scale", ctypes.c_float)]
 
 
-SEQ_LINEAR, SEQ_ATTENTION = 0, 1
+class DitAttnOp(ctypes.Structure):
+    """mt_dit_attn_op: the DiT's full attention (mt_dit_attention) as an item of a sequence."""
+    _fields_ = [("qkv", ctypes.c_void_p), ("ldq", ctypes.c_uint32), ("B", ctypes.c_uint32), ("S", ctypes.c_uint32),
+                ("H", ctypes.c_uint32), ("inv_freq", ctypes.c_void_p), ("out", ctypes.c_void_p),
+                ("ldo", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+SEQ_LINEAR, SEQ_ATTENTION, SEQ_DIT_ATTENTION = 0, 1, 2
 
 
 class SeqItem(ctypes.Structure):
-    """mt_seq_item: a linear or an attention item of a sequence."""
-    _fields_ = [("kind", ctypes.c_int32), ("linear", LinearOp), ("attn", AttnOp)]
+    """mt_seq_item: a linear, a decode attention or a DiT attention item of a sequence."""
+    _fields_ = [("kind", ctypes.c_int32), ("linear", LinearOp), ("attn", AttnOp), ("dit", DitAttnOp)]
 
 
 class StEntry(ctypes.Structure):
@@ -281,7 +288,7 @@ def set_tuning(key: int, value: int) -> int:
 
 class Seq:
     """A persistent sequence plan (mt_seq_*) of linears (``LinearOp``) and, optionally,
-    decode attention items (``AttnOp``)."""
+    decode attention items (``AttnOp``) or DiT attention items (``DitAttnOp``)."""
 
     def __init__(self, ops: Sequence):
         h = ctypes.c_void_p()
@@ -294,6 +301,9 @@ class Seq:
                 if isinstance(o, AttnOp):
                     items[i].kind = SEQ_ATTENTION
                     items[i].attn = o
+                elif isinstance(o, DitAttnOp):
+                    items[i].kind = SEQ_DIT_ATTENTION
+                    items[i].dit = o
                 else:
                     items[i].kind = SEQ_LINEAR
                     items[i].linear = o
@@ -314,7 +324,7 @@ class Seq:
     @property
     def kernel(self) -> int:
         """SEQ_DECODE_LAYER when the plan runs the kernel specialised for Qwen2-0.5B decode
-        layers, else SEQ_GENERAL."""
+        layers, SEQ_DIT_BLOCK for the flow head's DiT blocks, else SEQ_GENERAL."""
         return check(load().mt_seq_kernel(self.handle))
 
     def close(self) -> None:
@@ -339,6 +349,13 @@ def op(x, w, y, M, flags=0, w2=None, bias=None, ldx=None, ldy=None, xt=None, wt=
                     GemvParams(M, N, K, x.stride(0) if ldx is None else ldx, y.stride(0) if ldy is None else ldy,
                                flags, eps if norm is not None else 0.0),
                     dtype_code(x) if xt is None else xt, dtype_code(w) if wt is None else wt)
+
+
+def dit_attn_op(qkv, B, S, H, inv_freq, out, ldq=None, ldo=None, scale=0.125) -> DitAttnOp:
+    """An mt_dit_attn_op over torch tensors: B sequences of S rows of qkv ([B S, 3 H 64] at
+    stride ldq), out [B S, H 64]."""
+    return DitAttnOp(_ptr(qkv), qkv.stride(0) if ldq is None else ldq, B, S, H, _ptr(inv_freq), _ptr(out),
+                     out.stride(0) if ldo is None else ldo, scale)
 
 
 def attn_op(qkv, B, hq, hkv, pos, kc, vc, cache_len, cache_stride, inv_freq, out, ldq=None, ldo=None,

@@ -221,19 +221,23 @@ def test_flow_euler_assemble_rejects_bad_arguments():
 
 
 def test_seq_item_layout_matches_the_header(tmp_path):
-    """The ctypes mirrors of mt_attn_op and mt_seq_item have the C compiler's sizes and
-    offsets."""
+    """The ctypes mirrors of mt_attn_op, mt_dit_attn_op and mt_seq_item have the C compiler's
+    sizes and offsets."""
     import ctypes
     src = tmp_path / "layout.c"
     src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "mingtts_hip.h"\n'
-                   'int main(void) { printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(mt_attn_op), '
+                   'int main(void) { printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(mt_attn_op), '
                    'offsetof(mt_attn_op, cache_stride), offsetof(mt_attn_op, scale), sizeof(mt_seq_item), '
-                   'offsetof(mt_seq_item, linear), offsetof(mt_seq_item, attn), sizeof(mt_linear_op)); return 0; }\n')
+                   'offsetof(mt_seq_item, linear), offsetof(mt_seq_item, attn), sizeof(mt_linear_op), '
+                   'sizeof(mt_dit_attn_op), offsetof(mt_dit_attn_op, inv_freq), offsetof(mt_dit_attn_op, scale), '
+                   'offsetof(mt_seq_item, dit)); return 0; }\n')
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
     got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [ctypes.sizeof(mt.AttnOp), mt.AttnOp.cache_stride.offset, mt.AttnOp.scale.offset,
-            ctypes.sizeof(mt.SeqItem), mt.SeqItem.linear.offset, mt.SeqItem.attn.offset, ctypes.sizeof(mt.LinearOp)]
+            ctypes.sizeof(mt.SeqItem), mt.SeqItem.linear.offset, mt.SeqItem.attn.offset, ctypes.sizeof(mt.LinearOp),
+            ctypes.sizeof(mt.DitAttnOp), mt.DitAttnOp.inv_freq.offset, mt.DitAttnOp.scale.offset,
+            mt.SeqItem.dit.offset]
     assert got == want
 
 
@@ -243,6 +247,8 @@ def _items(ops):
     for i, o in enumerate(ops):
         if isinstance(o, mt.AttnOp):
             items[i].kind, items[i].attn = mt.SEQ_ATTENTION, o
+        elif isinstance(o, mt.DitAttnOp):
+            items[i].kind, items[i].dit = mt.SEQ_DIT_ATTENTION, o
         else:
             items[i].kind, items[i].linear = mt.SEQ_LINEAR, o
     return items
@@ -288,3 +294,52 @@ def test_seq_attention_items_are_checked_before_the_device():
     items[0].kind = 7
     assert L.mt_seq_create_items(items, 1, ctypes.byref(h)) == mt.EINVAL
     assert "unknown kind" in mt.last_error()
+
+
+def test_dit_attention_items_are_checked_before_the_device():
+    """DiT attention items: argument errors are MT_EINVAL; a sequence with one outside the
+    DiT-block pattern (shape, wiring, frequencies, the general kernel forced) is MT_ENOTSUP,
+    both before any device call; the pattern itself gets as far as the device query."""
+    import ctypes
+    L = mt.load()
+    h = ctypes.c_void_p()
+    X, QKV, ATT, FF, INV, INV2 = (k << 22 for k in (1, 2, 3, 4, 5, 6))
+    W, B16 = 64 << 22, 96 << 22
+
+    def lin(x, y, N, K, flags, norm=True):
+        return mt.LinearOp(x, W, None, B16, B16 if norm else None, y,
+                           mt.GemvParams(6, N, K, K, N, flags | mt.GemvFlags.bias, 1e-6 if norm else 0.0),
+                           mt.F32, mt.BF16)
+
+    def dit(**kw):
+        a = dict(qkv=QKV, ldq=3072, B=2, S=3, H=16, inv_freq=INV, out=ATT, ldo=1024, scale=0.125)
+        a.update(kw)
+        return mt.DitAttnOp(*(a[f[0]] for f in mt.DitAttnOp._fields_))
+
+    def block(att=None, out_x=ATT, ff1_flags=mt.GemvFlags.gelu):
+        return [lin(X, QKV, 3072, 1024, 0), dit() if att is None else att,
+                lin(out_x, X, 1024, 1024, mt.GemvFlags.accumulate, norm=False),
+                lin(X, FF, 4096, 1024, ff1_flags), lin(FF, X, 1024, 4096, mt.GemvFlags.accumulate, norm=False)]
+
+    good = block() + block()
+    rc = L.mt_seq_create_items(_items(good), len(good), ctypes.byref(h))
+    assert rc not in (mt.EINVAL, mt.ENOTSUP), mt.last_error()   # planned; the device query fails here
+    for bad, needle in ((dit(B=0), "B, S, H >= 1"), (dit(S=9), "S <= 8"), (dit(B=3, S=3), "B S <= 8"),
+                        (dit(inv_freq=None), "null pointer"), (dit(ldq=2048), "ldq"),
+                        (dit(out=ATT + 4), "16-byte aligned")):
+        ops = block(att=bad)
+        assert L.mt_seq_create_items(_items(ops), len(ops), ctypes.byref(h)) == mt.EINVAL, needle
+        assert needle in mt.last_error(), mt.last_error()
+    for ops in (block(ff1_flags=0),                                  # ff1 without GELU
+                block(att=dit(scale=0.25)) + block(),                # scales differ between items
+                block() + block(att=dit(inv_freq=INV2)),             # frequencies differ between items
+                block()[:4]):                                        # not whole blocks
+        assert L.mt_seq_create_items(_items(ops), len(ops), ctypes.byref(h)) == mt.ENOTSUP
+        assert "DiT-block kernel" in mt.last_error(), mt.last_error()
+    ops = block(att=dit(H=8))                                        # not the flow head's heads: out reads
+    assert L.mt_seq_create_items(_items(ops), len(ops), ctypes.byref(h)) == mt.ENOTSUP   # past its output
+    mt.set_tuning(mt.TUNE_SEQ_LAYER, 1)
+    try:
+        assert L.mt_seq_create_items(_items(good), len(good), ctypes.byref(h)) == mt.ENOTSUP
+    finally:
+        mt.set_tuning(mt.TUNE_SEQ_LAYER, 0)
