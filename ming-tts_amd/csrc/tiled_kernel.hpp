@@ -88,9 +88,12 @@ __device__ __forceinline__ f32x16t mfma32x(u32x4t a, u32x4t b, f32x16t c) {
                                                       0, 0, 0);
 }
 
-// One wave-wide direct load: lane l's 16 bytes at gaddr land at LDS byte lds + 16 l.
+// One wave-wide direct load: lane l's 16 bytes at gaddr land at LDS byte lds + 16 l (lds
+// wave-uniform; the compiler sets m0 from it).
 __device__ __forceinline__ void dma16(uint32_t lds, const void *gaddr) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gaddr) : "memory", "m0");
+    __builtin_amdgcn_global_load_lds(
+        reinterpret_cast<const __attribute__((address_space(1))) void *>(reinterpret_cast<uintptr_t>(gaddr)),
+        reinterpret_cast<__attribute__((address_space(3))) void *>(lds), 16, 0, 0);
 }
 
 template <int N>
