@@ -637,12 +637,14 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True, persistent=False):
                 attention="inside the out projection" if fused or persistent else "separate launch")
 
 
-def bench_aggregator(torch, mt, dev, reps=5):
+def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
     """The aggregator stage of one generation step (MingEngine.encodeStep, Engine.swift:405-410):
     the cls row and x_embedder (1024 x 64) of the new latent, the 8-block DiT (hidden 1024, 16
     heads) at batch 1 x seq 2 (M = 2, attention inside the out projection), the final norm +
-    896 x 1024 linear of row 0: 34 launches, bf16 weights ~ N(0, 0.02^2), captured in a HIP
-    graph and replayed."""
+    896 x 1024 linear of row 0: 35 launches, bf16 weights ~ N(0, 0.02^2), captured in a HIP
+    graph and replayed.  With ``persistent`` the 8 blocks are one launch of the DiT-block
+    kernel (DiT attention items): 4 launches, run on the stream (a cooperative launch is not
+    captured), the median of `reps` runs between HIP events."""
     HID, HEADS, LAT, BLOCKS = 1024, 16, 64, 8
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -666,12 +668,25 @@ def bench_aggregator(torch, mt, dev, reps=5):
     ff = torch.zeros(2, 4 * HID, device=dev)
     out = torch.zeros(1, H, device=dev)
     cs = torch.cuda.Stream(device=dev)
+    seq = None
+    if persistent:
+        att = torch.zeros(2, HID, device=dev)
+        items = []
+        for p in blocks:
+            items += [mt.op(x, p["qkv"], qkv, 2, bias=p["qkv_b"], norm=p["n1"]),
+                      mt.dit_attn_op(qkv, 1, 2, HEADS, invf, att),
+                      mt.op(att, p["out"], x, 2, flags=mt.GemvFlags.accumulate, bias=p["out_b"]),
+                      mt.op(x, p["ff1"], ff, 2, flags=mt.GemvFlags.gelu, bias=p["ff1_b"], norm=p["n2"]),
+                      mt.op(ff, p["ff2"], x, 2, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"])]
+        seq = mt.Seq(items)
 
     def stage():
         s = cs.cuda_stream
         x[0].copy_(cls)
         mt.linear(latent, xw, x[1:], 1, bias=xb, stream=s)
-        for p in blocks:
+        if persistent:
+            seq.run(stream=s)
+        for p in ([] if persistent else blocks):
             mt.linear(x, p["qkv"], qkv, 2, bias=p["qkv_b"], norm=p["n1"], stream=s)
             mt.dit_attention_linear(qkv, 1, 2, HEADS, invf, p["out"], x, flags=mt.GemvFlags.accumulate, bias=p["out_b"],
                                     stream=s)
@@ -679,10 +694,25 @@ def bench_aggregator(torch, mt, dev, reps=5):
             mt.linear(ff, p["ff2"], x, 2, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=s)
         mt.linear(x, fin_w, out, 1, bias=fin_b, norm=fin_n, stream=s)
 
-    us = graph_us(torch, stage, cs, rounds=reps)
+    if persistent:
+        with torch.cuda.stream(cs):
+            stage()
+            torch.cuda.synchronize()
+            ev = Events(torch, cs)
+            times = []
+            for _ in range(reps):
+                ev.start()
+                stage()
+                times.append(ev.stop_ms() * 1e3)
+        seq.check()
+        us = sorted(times)[len(times) // 2]
+        seq.close()
+    else:
+        us = graph_us(torch, stage, cs, rounds=reps)
     wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
-    return dict(us_per_generation_step=us, launches=1 + 1 + 4 * BLOCKS + 1, weight_mb=wbytes / 1e6,
-                gbs_algorithmic=wbytes / (us * 1e-6) / 1e9)
+    return dict(us_per_generation_step=us, launches=1 + 1 + (1 if persistent else 4 * BLOCKS) + 1,
+                weight_mb=wbytes / 1e6, gbs_algorithmic=wbytes / (us * 1e-6) / 1e9,
+                blocks="one DiT-block kernel launch" if persistent else "a launch per linear")
 
 
 def vae_latent_graph(torch, mt, dev, ws, fused=True):
@@ -1021,7 +1051,8 @@ def main() -> int:
         return 0
     if args.only == "flow":
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
-        out = {}
+        out = {"aggregator": bench_aggregator(torch, mt, dev),
+               "aggregator_persistent": bench_aggregator(torch, mt, dev, persistent=True)}
         for name, kw in (("flow_step_persistent", dict(persistent=True)), ("flow_step", dict(fused=True)),
                          ("flow_step_separate_attention", dict(fused=False))):
             out[name] = {k: (round(v, 3) if isinstance(v, float) else v)
@@ -1139,6 +1170,9 @@ def main() -> int:
                                                 for k, v in bench_flow_step(torch, mt, dev, fused=False).items()}
         log("aggregator stage of one generation step (8 DiT blocks at M = 2, graph replay)")
         line["aggregator"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_aggregator(torch, mt, dev).items()}
+        log("aggregator stage with the 8 DiT blocks as one persistent launch")
+        line["aggregator_persistent"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                         for k, v in bench_aggregator(torch, mt, dev, persistent=True).items()}
         log("VAE decode of one latent (24-layer stack at M = 4, head, ISTFT; graph replay)")
         line["vae_latent"] = {k: (round(v, 3) if isinstance(v, float) else v)
                               for k, v in bench_vae_latent(torch, mt, dev, ws).items()}

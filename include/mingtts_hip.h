@@ -299,8 +299,9 @@ typedef struct mt_seq_item {
  * item's output is an activation like a linear's (a later linear reads it as x).
  * DiT attention items are taken in one pattern only: DiT blocks at the flow head's shape
  * (DiTForward.encode, DiT.swift:35-52), each rmsnorm+qkv 3072 x 1024 + bias, the DiT
- * attention (B 2, S 3, H 16) of that qkv, out 1024 x 1024 + bias += reading the attention's
- * output, rmsnorm+ff1 4096 x 1024 + bias GELU, ff2 1024 x 4096 + bias +=, at M = 6 rows, every
+ * attention (H 16; B 2 x S 3 = 6 rows as in the flow loop, or B 1 x S 2 = 2 rows as in the
+ * aggregator) of that qkv, out 1024 x 1024 + bias += reading the attention's output,
+ * rmsnorm+ff1 4096 x 1024 + bias GELU, ff2 1024 x 4096 + bias +=, at M = B S rows, every
  * attention item with the same inv_freq and scale, on a device with 256 CUs (one workgroup
  * each); anything else with a DiT attention item returns MT_ENOTSUP. */
 int mt_seq_create_items(const mt_seq_item *items, uint32_t n_items, mt_seq **out);

@@ -273,14 +273,18 @@ __device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A
 }
 
 // The DiT attention that a DiT block's out projection stages as its x (DiT-block kernel; the
-// arithmetic of dit_attend.hpp): half wave hw of the 14 takes the (sequence, head) groups hw,
-// hw + 14 and hw + 28 of the B H = 32, lane p the interleaved-RoPE pair 2p, 2p + 1 of the q, k
-// and v of the group's S rows.  Each workgroup computes all of it from the block's tagged qkv
-// (read once), so the attention adds no exchange between workgroups.
-constexpr uint32_t DIT_GROUPS = DIT_B * DIT_HEADS, DIT_HW = LAY_THREADS / 32;
-constexpr uint32_t DIT_GR = (DIT_GROUPS + DIT_HW - 1) / DIT_HW;  // groups a half wave takes
-constexpr uint32_t DIT_T = 3 * DIT_S;                             // q, k and v pairs of a group
-static_assert(DIT_GR * DIT_T <= 32, "one stale bit per pair");
+// arithmetic of dit_attend.hpp), for B sequences of S rows at M = B S: (2, 3) in the flow
+// loop, (1, 2) in the aggregator.  Half wave hw of the 14 takes the (sequence, head) groups hw,
+// hw + 14, ... of the B H, lane p the interleaved-RoPE pair 2p, 2p + 1 of the q, k and v of the
+// group's S rows.  Each workgroup computes all of it from the block's tagged qkv (read once),
+// so the attention adds no exchange between workgroups.
+template <int M>
+struct DitAtt {
+    static constexpr uint32_t S = M == 6 ? 3u : 2u, B = M / S;
+    static constexpr uint32_t GROUPS = B * DIT_HEADS, HW = LAY_THREADS / 32;
+    static constexpr uint32_t GR = (GROUPS + HW - 1) / HW;  // groups a half wave takes
+    static constexpr uint32_t T = 3 * S;                     // q, k and v pairs of a group
+};
 
 __device__ __forceinline__ u32x2 ldtag2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, SC1);
@@ -290,19 +294,24 @@ __device__ __forceinline__ bool tagged2(const u32x2 a, uint32_t parity) {
 }
 // Byte offset in the tag buffer of pair t of group gi (t < S: q of row t; then the S k rows,
 // then the S v rows); d.xoff / d.xld locate the block's qkv output.
+template <int M>
 __device__ __forceinline__ uint32_t dit_att_off(const LayOp &d, uint32_t gi, uint32_t t, uint32_t p) {
-    const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, part = t / DIT_S, row = b * DIT_S + t % DIT_S;
+    constexpr uint32_t S = DitAtt<M>::S;
+    const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, part = t / S, row = b * S + t % S;
     return (d.xoff + row * d.xld + part * (DIT_HEADS * 64) + h * 64 + 2 * p) * 4u;
 }
 template <int WT, int M>
-__device__ __forceinline__ void dit_att_request(const LayCtx<WT, M> &cx, const LayOp &d, u32x2 (&a)[DIT_GR][DIT_T]) {
+__device__ __forceinline__ void dit_att_request(const LayCtx<WT, M> &cx, const LayOp &d,
+                                                u32x2 (&a)[DitAtt<M>::GR][DitAtt<M>::T]) {
+    typedef DitAtt<M> D;
+    static_assert(D::B * D::S == M && D::GR * D::T <= 32, "DiT attention shape; one stale bit per pair");
     const uint32_t hw = cx.tid >> 5, p = cx.tid & 31;
 #pragma unroll
-    for (uint32_t r = 0; r < DIT_GR; r++) {
-        const uint32_t gi = hw + DIT_HW * r;
+    for (uint32_t r = 0; r < D::GR; r++) {
+        const uint32_t gi = hw + D::HW * r;
 #pragma unroll
-        for (uint32_t t = 0; t < DIT_T; t++)  // past the groups: an offset outside the buffer reads 0
-            a[r][t] = ldtag2(cx.rsrc, gi < DIT_GROUPS ? dit_att_off(d, gi, t, p) : 0xFFFFFFF0u);
+        for (uint32_t t = 0; t < D::T; t++)  // past the groups: an offset outside the buffer reads 0
+            a[r][t] = ldtag2(cx.rsrc, gi < D::GROUPS ? dit_att_off<M>(d, gi, t, p) : 0xFFFFFFF0u);
     }
 }
 // Waits for the requested pairs, then computes each group's S query rows and stages them
@@ -310,14 +319,15 @@ __device__ __forceinline__ void dit_att_request(const LayCtx<WT, M> &cx, const L
 // output workgroup 0 writes when it is the region's last write.
 template <int WT, int M, uint32_t K>
 __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d, const SeqOp &item,
-                                              u32x2 (&a)[DIT_GR][DIT_T]) {
+                                              u32x2 (&a)[DitAtt<M>::GR][DitAtt<M>::T]) {
+    typedef DitAtt<M> D;
     const uint32_t hw = cx.tid >> 5, p = cx.tid & 31;
     uint32_t stale = 0;
 #pragma unroll
-    for (uint32_t r = 0; r < DIT_GR; r++)
+    for (uint32_t r = 0; r < D::GR; r++)
 #pragma unroll
-        for (uint32_t t = 0; t < DIT_T; t++)
-            if (hw + DIT_HW * r < DIT_GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * DIT_T + t);
+        for (uint32_t t = 0; t < D::T; t++)
+            if (hw + D::HW * r < D::GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * D::T + t);
     uint32_t spins = 0;
     while (stale && !cx.gave_up) {
         if (++spins > SPIN_LIMIT) {
@@ -327,36 +337,36 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
         }
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (uint32_t r = 0; r < DIT_GR; r++)
+        for (uint32_t r = 0; r < D::GR; r++)
 #pragma unroll
-            for (uint32_t t = 0; t < DIT_T; t++)
-                if ((stale >> (r * DIT_T + t)) & 1u) a[r][t] = ldtag2(cx.rsrc, dit_att_off(d, hw + DIT_HW * r, t, p));
+            for (uint32_t t = 0; t < D::T; t++)
+                if ((stale >> (r * D::T + t)) & 1u) a[r][t] = ldtag2(cx.rsrc, dit_att_off<M>(d, hw + D::HW * r, t, p));
         stale = 0;
 #pragma unroll
-        for (uint32_t r = 0; r < DIT_GR; r++)
+        for (uint32_t r = 0; r < D::GR; r++)
 #pragma unroll
-            for (uint32_t t = 0; t < DIT_T; t++)
-                if (hw + DIT_HW * r < DIT_GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * DIT_T + t);
+            for (uint32_t t = 0; t < D::T; t++)
+                if (hw + D::HW * r < D::GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * D::T + t);
     }
     const bool write_out = item.final_out != 0 && cx.g == 0;
     bool range_ok = true;
 #pragma unroll
-    for (uint32_t r = 0; r < DIT_GR; r++) {
-        const uint32_t gi = hw + DIT_HW * r;
-        if (gi >= DIT_GROUPS) continue;  // the whole half wave together
+    for (uint32_t r = 0; r < D::GR; r++) {
+        const uint32_t gi = hw + D::HW * r;
+        if (gi >= D::GROUPS) continue;  // the whole half wave together
         const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, col = h * 64 + 2 * p;
         auto pair = [&](uint32_t t) { return make_float2(untag(a[r][t].x), untag(a[r][t].y)); };
         DitItem it;
 #pragma unroll
         for (uint32_t j = 0; j < DIT_MAXS; j++) {
-            it.k[j] = j < DIT_S ? pair(DIT_S + j) : make_float2(0.0f, 0.0f);
-            it.v[j] = j < DIT_S ? pair(2 * DIT_S + j) : make_float2(0.0f, 0.0f);
+            it.k[j] = j < D::S ? pair(D::S + j) : make_float2(0.0f, 0.0f);
+            it.v[j] = j < D::S ? pair(2 * D::S + j) : make_float2(0.0f, 0.0f);
         }
 #pragma unroll
-        for (uint32_t i = 0; i < DIT_S; i++) {
+        for (uint32_t i = 0; i < D::S; i++) {
             it.q = pair(i);
-            const float2 o = dit_item_attend(it, i, DIT_S, cx.rc, cx.rs, cx.ascale);
-            const uint32_t row = b * DIT_S + i;
+            const float2 o = dit_item_attend(it, i, D::S, cx.rc, cx.rs, cx.ascale);
+            const uint32_t row = b * D::S + i;
             const uint32_t hi = pack2<WT>(o.x, o.y);
             const uint32_t lo = pack2<WT>(o.x - dec_lo<WT>(hi), o.y - dec_hi<WT>(hi));
             *reinterpret_cast<uint32_t *>(cx.xs + row * K + col) = hi;
@@ -391,7 +401,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     // Activations: chunk e = tid + 448 r is 4 k of x row e / K4 (or the DiT attention's qkv).
     u32x4 xv[L::XR];
     u32x2 gv[L::XR];
-    u32x2 att[L::ATTX ? DIT_GR : 1][DIT_T];
+    u32x2 att[L::ATTX ? DitAtt<M>::GR : 1][DitAtt<M>::T];
     if constexpr (L::ATTX) dit_att_request(cx, d, att);
 #pragma unroll
     for (uint32_t r = 0; r < (L::ATTX ? 0u : L::XR); r++) {
@@ -733,19 +743,19 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
     }
 }
 
-// The DiT-block kernel: n_ops = 5 L ops, L DiT blocks of the flow head (dit_pattern: qkv,
-// DiT attention, out, ff1, ff2 at M = 6 on DIT_G workgroups, the host checks them), the
-// packed descriptors after the op descriptors.  The attention item is not a step of its own:
-// each workgroup computes it while staging the out projection's x (dit_att_stage).  Tiling at
-// 256 workgroups: qkv 12 and ff1 16 features a workgroup (S = 1, one row tile, 32 block steps
-// as 5 a wave), out and ff2 4 features (S = 4, three B column groups of two rows).  Each op
+// The DiT-block kernel: n_ops = 5 L ops, L DiT blocks of the flow head's shape (dit_pattern:
+// qkv, DiT attention, out, ff1, ff2 at M = 6 (batch 2 x seq 3, the flow loop) or M = 2 (1 x 2,
+// the aggregator) on DIT_G workgroups, the host checks them), the packed descriptors after
+// the op descriptors.  The attention item is not a step of its own: each workgroup computes it
+// while staging the out projection's x (dit_att_stage).  Tiling at 256 workgroups: qkv 12 and
+// ff1 16 features a workgroup (S = 1, one row tile, 32 block steps as 5 a wave), out and ff2 4
+// features (S = 4; at M = 6 three B column groups of two rows).  Each op
 // requests the weight tiles of the op two steps on (qkv: ff1, out: ff2, ff1: the next block's
 // qkv, ff2: the next block's out) behind its output stores.
-template <int WT>
+template <int WT, int M>
 __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__restrict__ ops, uint32_t n_ops,
                                                                uint32_t *sync, const uint32_t *tags,
                                                                uint32_t tag_bytes) {
-    constexpr int M = DIT_B * DIT_S;
     typedef LayCtx<WT, M> X;
     typedef LCls<LC_DQKV, M> LQ;
     typedef LCls<LC_DO, M> LO;
@@ -815,7 +825,7 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
     cx.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(tags), 0, static_cast<int>(tag_bytes), BUF_DWORD3);
     // The attention's rotation table (every item shares the first one's frequencies and scale).
     const SeqOp &a0 = ops[1];
-    dit_rope_table(gld(a0.inv_freq + (cx.tid & 31)), DIT_S, cx.rc, cx.rs);
+    dit_rope_table(gld(a0.inv_freq + (cx.tid & 31)), DitAtt<M>::S, cx.rc, cx.rs);
     cx.ascale = a0.eps;
 
     u32x4 PQ[LQ::TA], PO[LO::TA], PF[LF::TA], PD[LD::TA];

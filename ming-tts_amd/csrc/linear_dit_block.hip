@@ -3,9 +3,9 @@
 
 namespace mt {
 
-seq_fn dit_block_kernel_fn(int wt) {
-    if (wt == DT_BF16) return dit_block_kernel<DT_BF16>;
-    if (wt == DT_F16) return dit_block_kernel<DT_F16>;
+seq_fn dit_block_kernel_fn(int wt, uint32_t M) {
+    if (M == 6) return wt == DT_BF16 ? dit_block_kernel<DT_BF16, 6> : dit_block_kernel<DT_F16, 6>;
+    if (M == 2) return wt == DT_BF16 ? dit_block_kernel<DT_BF16, 2> : dit_block_kernel<DT_F16, 2>;
     return nullptr;
 }
 

@@ -59,7 +59,7 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, int kind, SeqPlan
     for (uint32_t i = 0; i < n_ops; i++) attn = attn || ops[i].kind == SEQ_ATTN;
     p->kind = kind;
     if (kind == MT_SEQ_DIT_BLOCK) {
-        p->fn = dit_block_kernel_fn(wt);
+        p->fn = dit_block_kernel_fn(wt, m_all);
         p->layer = true;
         p->threads = LAY_THREADS;
     } else if (kind == MT_SEQ_DECODE_LAYER) {

@@ -103,10 +103,11 @@ int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups);
 // kernel's range?
 bool layer_pattern(const SeqOp *ops, uint32_t n, int groups);
 // The DiT blocks of the flow head (DiTForward.encode, DiT.swift:35-52) the DiT-block kernel is
-// specialised for: per block rmsnorm+qkv 3072 x 1024 + bias, DiT attention (B 2, S 3, H 16) of
-// that qkv, out 1024 x 1024 + bias += of the attention's output, rmsnorm+ff1 4096 x 1024 + bias
-// GELU, ff2 1024 x 4096 + bias +=, at M = 6, on exactly DIT_G workgroups.
-constexpr uint32_t DIT_H = 1024, DIT_QKV = 3072, DIT_FF = 4096, DIT_B = 2, DIT_S = 3, DIT_HEADS = 16;
+// specialised for: per block rmsnorm+qkv 3072 x 1024 + bias, DiT attention (H 16) of that qkv,
+// out 1024 x 1024 + bias += of the attention's output, rmsnorm+ff1 4096 x 1024 + bias GELU, ff2
+// 1024 x 4096 + bias +=, at B 2 x S 3 = 6 rows (the flow loop) or B 1 x S 2 = 2 rows (the
+// aggregator), on exactly DIT_G workgroups.
+constexpr uint32_t DIT_H = 1024, DIT_QKV = 3072, DIT_FF = 4096, DIT_HEADS = 16;
 constexpr int DIT_G = 256;
 bool dit_pattern(const SeqOp *ops, uint32_t n, int groups);
 // The kernel of a plan: MT_SEQ_GENERAL, MT_SEQ_DECODE_LAYER or MT_SEQ_DIT_BLOCK.

@@ -967,6 +967,6 @@ seq_fn seq_attn_kernel(int wt, bool m2);
 // The decode-layer kernel (linear_layer.hip) for weights wt at M rows (1, 2 or 4), or null.
 seq_fn layer_kernel_fn(int wt, uint32_t M, bool att);
 seq_fn layer_attn_kernel_fn(int wt, uint32_t M);
-seq_fn dit_block_kernel_fn(int wt);
+seq_fn dit_block_kernel_fn(int wt, uint32_t M);
 
 }  // namespace mt

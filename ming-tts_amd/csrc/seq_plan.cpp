@@ -240,7 +240,7 @@ int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups) {
         if (items[i].kind == MT_SEQ_DIT_ATTENTION)
             return set_error(MT_ENOTSUP,
                              "mt_seq_create: op %u: a DiT attention item runs only in the DiT-block kernel (blocks "
-                             "of qkv 3072 x 1024, attention B 2 S 3 H 16, out, ff1 4096 x 1024 GELU, ff2 at M = 6 on "
+                             "of qkv 3072 x 1024, attention H 16 at B 2 S 3 or B 1 S 2, out, ff1 4096 x 1024 GELU, ff2 on "
                              "%d workgroups)",
                              i, DIT_G);
         if (items[i].kind != MT_SEQ_LINEAR) continue;
@@ -324,7 +324,9 @@ bool dit_pattern(const SeqOp *ops, uint32_t n, int groups) {
                           {DIT_H, DIT_H, F_BIAS | F_ACCUM, false},
                           {DIT_FF, DIT_H, F_BIAS | F_GELU, true},
                           {DIT_H, DIT_FF, F_BIAS | F_ACCUM, false}};
-    const uint32_t M = DIT_B * DIT_S;
+    // (B, S) = (2, 3) in the flow loop, (1, 2) in the aggregator: the row count fixes both.
+    const uint32_t M = ops[0].M, S = M == 6 ? 3u : 2u;
+    if (M != 6 && M != 2) return false;
     for (uint32_t i = 0; i < n; i++) {
         const SeqOp &o = ops[i];
         const uint32_t j = i % 5;
@@ -332,7 +334,7 @@ bool dit_pattern(const SeqOp *ops, uint32_t n, int groups) {
         if (j == 1) {
             // The attention reads all of this block's qkv output; every item shares the first
             // one's frequencies and scale (the kernel builds its rotation table once).
-            if (o.kind != SEQ_DIT || o.heads != (DIT_HEADS | (DIT_S << 16)) || o.xsrc != static_cast<int32_t>(i - 1) ||
+            if (o.kind != SEQ_DIT || o.heads != (DIT_HEADS | (S << 16)) || o.xsrc != static_cast<int32_t>(i - 1) ||
                 o.xcol != 0 || o.inv_freq != ops[1].inv_freq || o.eps != ops[1].eps)
                 return false;
             continue;

@@ -257,38 +257,41 @@ def test_flow_step_matches_fp64_chain(gpu, fused):
         assert rel <= 1e-3, f"{what}: normwise {rel:.3g}"
 
 
-def dit_block_items(dw, x, qkv, att, ff, invf_d):
-    """The items of DiTForward.encode's blocks (DiT.swift:35-52) over the six flow rows x, as a
+def dit_block_items(dw, x, qkv, att, ff, invf_d, B=2, S=3):
+    """The items of DiTForward.encode's blocks (DiT.swift:35-52) over the B S rows x, as a
     persistent sequence: per block rmsnorm+qkv, the DiT attention, out +=, rmsnorm+ff1 GELU,
     ff2 +=."""
+    M = B * S
     items = []
     for d in dw:
-        items += [mt.op(x, d["qkv"], qkv, 6, bias=d["qkv_b"], norm=d["norm1"]),
-                  mt.dit_attn_op(qkv, 2, 3, HEADS, invf_d, att),
-                  mt.op(att, d["out"], x, 6, flags=mt.GemvFlags.accumulate, bias=d["out_b"]),
-                  mt.op(x, d["ff1"], ff, 6, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"]),
-                  mt.op(ff, d["ff2"], x, 6, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])]
+        items += [mt.op(x, d["qkv"], qkv, M, bias=d["qkv_b"], norm=d["norm1"]),
+                  mt.dit_attn_op(qkv, B, S, HEADS, invf_d, att),
+                  mt.op(att, d["out"], x, M, flags=mt.GemvFlags.accumulate, bias=d["out_b"]),
+                  mt.op(x, d["ff1"], ff, M, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"]),
+                  mt.op(ff, d["ff2"], x, M, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])]
     return items
 
 
-@pytest.mark.parametrize("blocks_n", [1, 8])
-def test_dit_blocks_as_one_persistent_launch(gpu, blocks_n):
-    """The DiT blocks of one ODE step as one launch of the DiT-block kernel: the hidden rows
-    within 1e-3 (normwise) of the fp64 chain and within 1e-5 of the same blocks as separate
-    launches; the last attention item's output written; two runs in a row give the same bits."""
+@pytest.mark.parametrize("B,S,blocks_n", [(2, 3, 1), (2, 3, 8), (1, 2, 1), (1, 2, 8)])
+def test_dit_blocks_as_one_persistent_launch(gpu, B, S, blocks_n):
+    """The DiT blocks of one ODE step (B 2 x S 3) or of the aggregator (B 1 x S 2) as one
+    launch of the DiT-block kernel: the hidden rows within 1e-3 (normwise) of the fp64 chain
+    and within 1e-5 of the same blocks as separate launches; the last attention item's output
+    written; two runs in a row give the same bits."""
+    M = B * S
     rng = np.random.default_rng(51)
     blocks = dit_weights(blocks_n, 51)
-    x0 = rng.standard_normal((6, HID)).astype(np.float32)
+    x0 = rng.standard_normal((M, HID)).astype(np.float32)
     invf = invf_1e4()
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
     dw = [{k: dev16(v, O.BF16, gpu) for k, v in p.items()} for p in blocks]
     x = t(x0.copy())
-    qkv = torch.zeros(6, 3 * HID, device=gpu)
-    att = torch.zeros(6, HID, device=gpu)
-    ff = torch.zeros(6, 4 * HID, device=gpu)
+    qkv = torch.zeros(M, 3 * HID, device=gpu)
+    att = torch.zeros(M, HID, device=gpu)
+    ff = torch.zeros(M, 4 * HID, device=gpu)
     invf_d = t(invf)
-    say(f"DiT-block kernel: {blocks_n} blocks at M = 6")
-    seq = mt.Seq(dit_block_items(dw, x, qkv, att, ff, invf_d))
+    say(f"DiT-block kernel: {blocks_n} blocks at B {B} x S {S}")
+    seq = mt.Seq(dit_block_items(dw, x, qkv, att, ff, invf_d, B, S))
     assert seq.kernel == mt.SEQ_DIT_BLOCK and seq.groups == 256
     runs = []
     for _ in range(2):
@@ -302,11 +305,11 @@ def test_dit_blocks_as_one_persistent_launch(gpu, blocks_n):
     # the same blocks as separate launches
     xs = t(x0.copy())
     for d in dw:
-        mt.linear(xs, d["qkv"], qkv, 6, bias=d["qkv_b"], norm=d["norm1"])
-        mt.dit_attention(qkv, 2, 3, HEADS, invf_d, att)
-        mt.linear(att, d["out"], xs, 6, flags=mt.GemvFlags.accumulate, bias=d["out_b"])
-        mt.linear(xs, d["ff1"], ff, 6, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"])
-        mt.linear(ff, d["ff2"], xs, 6, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])
+        mt.linear(xs, d["qkv"], qkv, M, bias=d["qkv_b"], norm=d["norm1"])
+        mt.dit_attention(qkv, B, S, HEADS, invf_d, att)
+        mt.linear(att, d["out"], xs, M, flags=mt.GemvFlags.accumulate, bias=d["out_b"])
+        mt.linear(xs, d["ff1"], ff, M, flags=mt.GemvFlags.gelu, bias=d["ff1_b"], norm=d["norm2"])
+        mt.linear(ff, d["ff2"], xs, M, flags=mt.GemvFlags.accumulate, bias=d["ff2_b"])
     torch.cuda.synchronize()
     assert O.normwise_rel_err(got, xs.cpu().numpy()) <= 1e-5
     assert O.normwise_rel_err(got_att, att.cpu().numpy()) <= 1e-5
@@ -315,11 +318,11 @@ def test_dit_blocks_as_one_persistent_launch(gpu, blocks_n):
     for p in blocks:
         q = O.linear_np64(O.rmsnorm_f64(want, p["norm1"], O.BF16), p["qkv"], None, O.BF16, p["qkv_b"], None,
                           O.BIAS).astype(np.float32)
-        a = O.dit_attention_f64(q, 2, 3, HEADS, invf).astype(np.float32)
-        want = O.linear_f64(a, p["out"], None, O.BF16, p["out_b"], want, 6, HID, HID, O.ACCUM).astype(np.float32)
+        a = O.dit_attention_f64(q, B, S, HEADS, invf).astype(np.float32)
+        want = O.linear_f64(a, p["out"], None, O.BF16, p["out_b"], want, M, HID, HID, O.ACCUM).astype(np.float32)
         f = O.linear_np64(O.rmsnorm_f64(want, p["norm2"], O.BF16), p["ff1"], None, O.BF16, p["ff1_b"], None,
                           O.BIAS | O.GELU).astype(np.float32)
-        want = O.linear_f64(f, p["ff2"], None, O.BF16, p["ff2_b"], want, 6, HID, 4 * HID, O.ACCUM).astype(np.float32)
+        want = O.linear_f64(f, p["ff2"], None, O.BF16, p["ff2_b"], want, M, HID, 4 * HID, O.ACCUM).astype(np.float32)
     rel = O.normwise_rel_err(got, want)
     assert rel <= 1e-3, f"normwise {rel:.3g}"
     seq.close()
