@@ -306,9 +306,9 @@ def test_dit_attention_items_are_checked_before_the_device():
     X, QKV, ATT, FF, INV, INV2 = (k << 22 for k in (1, 2, 3, 4, 5, 6))
     W, B16 = 64 << 22, 96 << 22
 
-    def lin(x, y, N, K, flags, norm=True):
+    def lin(x, y, N, K, flags, norm=True, M=6):
         return mt.LinearOp(x, W, None, B16, B16 if norm else None, y,
-                           mt.GemvParams(6, N, K, K, N, flags | mt.GemvFlags.bias, 1e-6 if norm else 0.0),
+                           mt.GemvParams(M, N, K, K, N, flags | mt.GemvFlags.bias, 1e-6 if norm else 0.0),
                            mt.F32, mt.BF16)
 
     def dit(**kw):
@@ -324,6 +324,15 @@ def test_dit_attention_items_are_checked_before_the_device():
     good = block() + block()
     rc = L.mt_seq_create_items(_items(good), len(good), ctypes.byref(h))
     assert rc not in (mt.EINVAL, mt.ENOTSUP), mt.last_error()   # planned; the device query fails here
+    # the aggregator's shape, batch 1 x seq 2
+    agg = [lin(X, QKV, 3072, 1024, 0, M=2), dit(B=1, S=2), lin(ATT, X, 1024, 1024, mt.GemvFlags.accumulate, False, 2),
+           lin(X, FF, 4096, 1024, mt.GemvFlags.gelu, M=2), lin(FF, X, 1024, 4096, mt.GemvFlags.accumulate, False, 2)]
+    rc = L.mt_seq_create_items(_items(agg), len(agg), ctypes.byref(h))
+    assert rc not in (mt.EINVAL, mt.ENOTSUP), mt.last_error()
+    odd = [lin(X, QKV, 3072, 1024, 0, M=4), dit(B=2, S=2), lin(ATT, X, 1024, 1024, mt.GemvFlags.accumulate, False, 4),
+           lin(X, FF, 4096, 1024, mt.GemvFlags.gelu, M=4), lin(FF, X, 1024, 4096, mt.GemvFlags.accumulate, False, 4)]
+    assert L.mt_seq_create_items(_items(odd), len(odd), ctypes.byref(h)) == mt.ENOTSUP   # B 2 x S 2: no kernel
+    assert "DiT-block kernel" in mt.last_error(), mt.last_error()
     for bad, needle in ((dit(B=0), "B, S, H >= 1"), (dit(S=9), "S <= 8"), (dit(B=3, S=3), "B S <= 8"),
                         (dit(inv_freq=None), "null pointer"), (dit(ldq=2048), "ldq"),
                         (dit(out=ATT + 4), "16-byte aligned")):
