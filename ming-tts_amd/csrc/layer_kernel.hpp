@@ -61,18 +61,25 @@ struct LCls {
     static constexpr bool ATTX = C == LC_DO;
     static constexpr uint32_t FLAGS =
         (BIAS ? F_BIAS : 0u) | (ACC ? F_ACCUM : 0u) | (GATED ? F_SILU_GATE : 0u) | (GELU ? F_GELU : 0u);
-    static constexpr uint32_t S = GATED || C == LC_DQKV || C == LC_FF1 ? 1u : C == LC_QKV ? 2u : 4u;
+    // down is split over K between the two workgroups of a pair (g, g ^ 1): each owns the
+    // pair's features over its half of K, and reads only that half of x.  Its outputs are
+    // two tagged planes (the residual plus the first half's sums; the second half's sums),
+    // which the next qkv (x, X2) and o (old y, Y2) add as they read them.
+    static constexpr uint32_t KSPLIT = C == LC_DOWN ? 2u : 1u;
+    static constexpr uint32_t KX = K / KSPLIT;              // k a workgroup stages and sums
+    static constexpr bool X2 = C == LC_QKV, Y2 = C == LC_O;  // may read down's two planes
+    static constexpr uint32_t S = GATED || C == LC_DQKV || C == LC_FF1 ? 1u : C == LC_QKV || C == LC_DOWN ? 2u : 4u;
     static constexpr uint32_t LS = S == 4 ? 2u : S == 2 ? 1u : 0u;
     static constexpr uint32_t CG = (2 * S * M + 15) / 16;  // B column groups (MFMAs per weight tile)
     static constexpr uint32_t RPG = M / CG;                 // x rows per column group
-    static constexpr uint32_t KB = K / 32, KBS = KB / S;
+    static constexpr uint32_t KB = KX / 32, KBS = KB / S;
     static constexpr uint32_t FPT = GATED ? 8u : 16u / S;  // features per row tile
     static constexpr uint32_t RT = GATED ? 3u : 1u;         // row tiles
     static constexpr uint32_t NMAX = FPT * RT;              // features a workgroup can own
     // Tiles a compute wave loads: gate|up's RT KBS tiles split evenly over the 7 compute waves;
     // otherwise the most block steps any wave has.
     static constexpr uint32_t TA = GATED ? RT * KBS / 7 : (KBS + 6) / 7;
-    static constexpr uint32_t K4 = K / 4, NCH = M * K4;     // 16-byte x chunks of the op
+    static constexpr uint32_t K4 = KX / 4, NCH = M * K4;    // 16-byte x chunks of the op
     static constexpr uint32_t XR = (NCH + 447) / 448;       // x chunks per compute thread
     // LDS partial sums: [row tile][x row][virtual row][slot]
     static constexpr uint32_t VR = GATED ? 16u : FPT;
@@ -88,7 +95,8 @@ constexpr int LAY_THREADS = LAY_CW * 64;
 // The fields of one op the kernel reads, packed for one scalar load (built by the plan
 // compiler next to the op descriptors).  Tagged positions are word offsets into the plan's
 // tag buffer.
-enum : uint32_t { LAY_XEXT = 1, LAY_YEXT = 2, LAY_FINAL = 4 };
+// LAY_X2 / LAY_Y2: x / the old y is down's output, two tagged planes M LAY_H words apart.
+enum : uint32_t { LAY_XEXT = 1, LAY_YEXT = 2, LAY_FINAL = 4, LAY_X2 = 8, LAY_Y2 = 16 };
 struct LayOp {
     const uint16_t *w;     // weights (gate|up: the gate rows)
     const uint16_t *p2;    // gate|up: W2 (the up rows); qkv: the bias
@@ -139,10 +147,11 @@ __device__ __forceinline__ uint32_t lay_row(uint32_t nr, uint32_t lane, uint32_t
     return f < nr ? f : nr - 1;  // padding rows repeat the last feature (their sums are not used)
 }
 template <int C, int M>
-__device__ __forceinline__ LLane lay_lane(uint32_t r0, uint32_t nr, uint32_t lane, const LRange &r, uint32_t plane) {
+__device__ __forceinline__ LLane lay_lane(uint32_t r0, uint32_t nr, uint32_t lane, const LRange &r, uint32_t plane,
+                                          uint32_t kh = 0) {
     typedef LCls<C, M> L;
     const uint32_t a = lane & 15, q = lane >> 4;
-    const uint32_t k = (L::GATED ? 0u : (a & (L::S - 1)) * L::KBS * 32) + q * 8;
+    const uint32_t k = kh + (L::GATED ? 0u : (a & (L::S - 1)) * L::KBS * 32) + q * 8;
     LLane ll;
     ll.woff = ((r0 + lay_row<C, M>(nr, lane, r.rt)) * L::K + k + r.js * 32) * 2;
     ll.woff2 = L::GATED ? ((r0 + lay_row<C, M>(nr, lane, r.rt + 1 < L::RT ? r.rt + 1 : r.rt)) * L::K + k) * 2 : ll.woff;
@@ -151,7 +160,7 @@ __device__ __forceinline__ LLane lay_lane(uint32_t r0, uint32_t nr, uint32_t lan
     const uint32_t c = lane & 15, cc = c >> 1, h = c & 1, s = cc & (L::S - 1);
     uint32_t m = cc >> L::LS;
     m = m < L::RPG ? m : 0u;
-    ll.boff = (h * plane + m * L::K + s * L::KBS * 32 + q * 8 + r.js * 32) * 2;
+    ll.boff = (h * plane + m * L::KX + s * L::KBS * 32 + q * 8 + r.js * 32) * 2;
     return ll;
 }
 
@@ -165,6 +174,7 @@ struct LayCtx {
     LLane ln[4];
     uint32_t r0[4], nr[4];
     uint32_t tid, lane, w, parity, g;
+    uint32_t kh, half;  // down: this workgroup's half of K (its first k, and 0 / 1)
     // DiT-block kernel: the lane's RoPE pair's cos / sin at positions 0 .. S - 1 and the
     // attention's score scale.
     float rc[DIT_MAXS], rs[DIT_MAXS];
@@ -254,7 +264,7 @@ __device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A
     typedef LCls<C, M> L;
     constexpr LRange r = lay_range<C, M>(W);
     const char *bp = reinterpret_cast<const char *>(cx.xs) + cx.ln[L::SLOT].boff;
-    constexpr uint32_t GOFF = L::RPG * L::K * 2;  // bytes from one column group's rows to the next's
+    constexpr uint32_t GOFF = L::RPG * L::KX * 2;  // bytes from one column group's rows to the next's
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc, accg = acc, accg2 = acc;
 #pragma unroll
     for (uint32_t k = r.kb; k < r.ke; k++) {  // block js + k of row tile rt, or k - ks of rt + 1
@@ -397,9 +407,13 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     const uint32_t tid = cx.tid, lane = cx.lane;
     const uint32_t r0 = cx.r0[L::SLOT], nr = cx.nr[L::SLOT];
     const bool xext = (d.flags & LAY_XEXT) != 0;
+    // down reads its half of K; x from down's two planes is read from both.
+    const uint32_t kx0 = L::KSPLIT > 1 ? cx.kh : 0u;
+    const bool x2 = L::X2 && (d.flags & LAY_X2) != 0;
+    constexpr uint32_t PL = M * LAY_H;  // words between down's planes
 
     // Activations: chunk e = tid + 448 r is 4 k of x row e / K4 (or the DiT attention's qkv).
-    u32x4 xv[L::XR];
+    u32x4 xv[L::XR], xv2[L::X2 ? L::XR : 1];
     u32x2 gv[L::XR];
     u32x2 att[L::ATTX ? DitAtt<M>::GR : 1][DitAtt<M>::T];
     if constexpr (L::ATTX) dit_att_request(cx, d, att);
@@ -409,12 +423,14 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
         const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
         const bool ok = e < L::NCH;
         if (!xext) {
-            xv[r] = ldtag4(cx.rsrc, ok ? (d.xoff + m * d.xld + k) * 4u : 0xFFFFFFF0u);
+            xv[r] = ldtag4(cx.rsrc, ok ? (d.xoff + m * d.xld + kx0 + k) * 4u : 0xFFFFFFF0u);
+            if constexpr (L::X2)
+                if (x2) xv2[r] = ldtag4(cx.rsrc, ok ? (d.xoff + PL + m * d.xld + k) * 4u : 0xFFFFFFF0u);
         } else {  // x from the user buffer (the sequence's first op)
             const SeqOp &o = ops[i];
             xv[r] = u32x4{0u, 0u, 0u, 0u};
             if (ok) {
-                const size_t off = static_cast<size_t>(m) * o.ldx + k;
+                const size_t off = static_cast<size_t>(m) * o.ldx + kx0 + k;
                 if (o.xt == DT_F32) {
                     xv[r] = gld(reinterpret_cast<const u32x4 *>(static_cast<const float *>(o.x) + off));
                 } else {
@@ -434,21 +450,32 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     const bool live = of < nr;
     const uint32_t n = r0 + (live ? of : 0u);
     const bool yext = (d.flags & LAY_YEXT) != 0;
-    uint32_t braw = 0, yw = 0;
+    uint32_t braw = 0, yw = 0, yw2 = 0;
+    const bool y2 = L::Y2 && (d.flags & LAY_Y2) != 0;
     if constexpr (L::BIAS) braw = gld(d.p2 + n);
     if constexpr (L::ACC)  // old y: a tagged word, or the user's y; one load either way (no branch)
         yw = ld32(yext ? reinterpret_cast<const uint32_t *>(d.y) + static_cast<size_t>(om) * d.ldy + n
                        : cx.tags + d.yoff + om * d.yld + n);
+    if constexpr (L::Y2)
+        if (y2) yw2 = ld32(cx.tags + d.yoff + PL + om * d.yld + n);
 
     if constexpr (L::ATTX) {
         dit_att_stage<WT, M, L::K>(cx, d, ops[i - 1], att);
     } else {
         // Wait for the activations; stale chunks are requested again, all at once per round.
         if (!xext) {
-            uint32_t stale = 0;
+            static_assert(L::XR <= 16, "stale bits: 16 per plane");
+            auto stale_bits = [&]() {
+                uint32_t st = 0;
 #pragma unroll
-            for (uint32_t r = 0; r < L::XR; r++)
-                if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
+                for (uint32_t r = 0; r < L::XR; r++) {
+                    if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) st |= 1u << r;
+                    if constexpr (L::X2)
+                        if (x2 && tid + 448 * r < L::NCH && !tagged4(xv2[r], cx.parity)) st |= 1u << (16 + r);
+                }
+                return st;
+            };
+            uint32_t stale = stale_bits();
             uint32_t spins = 0;
             while (stale && !cx.gave_up) {
                 if (++spins > SPIN_LIMIT) {
@@ -459,16 +486,13 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
                 __builtin_amdgcn_s_sleep(1);
 #pragma unroll
                 for (uint32_t r = 0; r < L::XR; r++) {
-                    if ((stale >> r) & 1u) {
-                        const uint32_t e = tid + 448 * r;
-                        const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
-                        xv[r] = ldtag4(cx.rsrc, (d.xoff + m * d.xld + k) * 4u);
-                    }
+                    const uint32_t e = tid + 448 * r;
+                    const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+                    if ((stale >> r) & 1u) xv[r] = ldtag4(cx.rsrc, (d.xoff + m * d.xld + kx0 + k) * 4u);
+                    if constexpr (L::X2)
+                        if ((stale >> (16 + r)) & 1u) xv2[r] = ldtag4(cx.rsrc, (d.xoff + PL + m * d.xld + k) * 4u);
                 }
-                stale = 0;
-#pragma unroll
-                for (uint32_t r = 0; r < L::XR; r++)
-                    if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) stale |= 1u << r;
+                stale = stale_bits();
             }
         }
         if constexpr (EARLY) issue();
@@ -489,6 +513,14 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
                 x[1] = __uint_as_float(xv[r].y & clear);
                 x[2] = __uint_as_float(xv[r].z & clear);
                 x[3] = __uint_as_float(xv[r].w & clear);
+                if constexpr (L::X2) {
+                    if (x2) {  // the residual: down's first plane + its second, in that order
+                        x[0] += untag(xv2[r].x);
+                        x[1] += untag(xv2[r].y);
+                        x[2] += untag(xv2[r].z);
+                        x[3] += untag(xv2[r].w);
+                    }
+                }
                 if constexpr (L::NORM) {
                     float t = x[0] * x[0];
                     t = fmaf(x[1], x[1], t);
@@ -505,8 +537,8 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
                     range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
                 u32x2 hi, lo;
                 split4p<WT>(x, hi, lo);
-                *reinterpret_cast<u32x2 *>(cx.xs + m * L::K + k) = hi;
-                *reinterpret_cast<u32x2 *>(cx.xs + LayCtx<WT, M>::PLANE + m * L::K + k) = lo;
+                *reinterpret_cast<u32x2 *>(cx.xs + m * L::KX + k) = hi;
+                *reinterpret_cast<u32x2 *>(cx.xs + LayCtx<WT, M>::PLANE + m * L::KX + k) = lo;
             }
         }
         if (!range_ok) raise_flag(cx.sync, SYNC_RANGE);
@@ -566,26 +598,51 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
             bias = dec1<WT>(static_cast<uint16_t>(braw));
         }
         float v = epilogue(a1, a2, bias, L::FLAGS);
+        // Wait for a tagged word at byte offset off to carry the run's parity.
+        auto await_word = [&](uint32_t &word, uint32_t off) {
+            uint32_t spins = 0;
+            while ((word & 1u) != cx.parity && !cx.gave_up) {
+                if (++spins > SPIN_LIMIT) {
+                    cx.gave_up = true;
+                    raise_flag(cx.sync, SYNC_TIMEOUT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                word = ldtag1(cx.rsrc, off);
+            }
+        };
+        // down's second half adds no old y: its plane holds its own sums.
+        const bool second = L::KSPLIT > 1 && cx.half != 0;
         if constexpr (L::ACC) {
-            if (!yext) {
-                const uint32_t yoff = (d.yoff + om * d.yld + n) * 4u;
-                uint32_t spins = 0;
-                while ((yw & 1u) != cx.parity && !cx.gave_up) {
-                    if (++spins > SPIN_LIMIT) {
-                        cx.gave_up = true;
-                        raise_flag(cx.sync, SYNC_TIMEOUT);
-                        break;
+            if (!second) {
+                if (!yext) await_word(yw, (d.yoff + om * d.yld + n) * 4u);
+                float old = __uint_as_float(yext ? yw : yw & ~1u);
+                if constexpr (L::Y2) {
+                    if (y2) {
+                        await_word(yw2, (d.yoff + PL + om * d.yld + n) * 4u);
+                        old += untag(yw2);
                     }
-                    __builtin_amdgcn_s_sleep(1);
-                    yw = ldtag1(cx.rsrc, yoff);
+                }
+                v += old;
+            }
+        }
+        const uint32_t t = d.tag + (second ? PL : 0u) + om * L::N + n;
+        st_tag(cx.tags + t, v, cx.parity);
+        if (d.flags & LAY_FINAL) {
+            float out = v;
+            if constexpr (L::KSPLIT > 1) {
+                // The user's value is what the next layer would read: the first plane plus
+                // this one, written by the second half once the first half's word is current.
+                if (second) {
+                    uint32_t w0 = ldtag1(cx.rsrc, (t - PL) * 4u);
+                    await_word(w0, (t - PL) * 4u);
+                    out = untag(w0) + untag(__float_as_uint(v));  // the stored word's value
                 }
             }
-            v += __uint_as_float(yext ? yw : yw & ~1u);
+            if (L::KSPLIT == 1 || second)
+                *reinterpret_cast<__attribute__((address_space(1))) float *>(
+                    reinterpret_cast<uintptr_t>(d.y + static_cast<size_t>(om) * d.ldy + n)) = out;
         }
-        st_tag(cx.tags + d.tag + om * L::N + n, v, cx.parity);
-        if (d.flags & LAY_FINAL)
-            *reinterpret_cast<__attribute__((address_space(1))) float *>(
-                reinterpret_cast<uintptr_t>(d.y + static_cast<size_t>(om) * d.ldy + n)) = v;
     }
     // Otherwise later ops' weight tiles go behind this op's output stores: they drain while
     // the next op's activations are being produced by the other workgroups.
@@ -645,9 +702,13 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
     const uint32_t Ns[4] = {LAY_QKV, LAY_H, LAY_I, LAY_H};
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        cx.r0[c] = static_cast<uint32_t>(static_cast<uint64_t>(g) * Ns[c] / G);
-        cx.nr[c] = static_cast<uint32_t>(static_cast<uint64_t>(g + 1) * Ns[c] / G) - cx.r0[c];
+        // down: pair g >> 1 of the G / 2 (G is even) owns the features, half g & 1 of K
+        const uint32_t u = c == LC_DOWN ? g >> 1 : g, U = c == LC_DOWN ? G >> 1 : G;
+        cx.r0[c] = static_cast<uint32_t>(static_cast<uint64_t>(u) * Ns[c] / U);
+        cx.nr[c] = static_cast<uint32_t>(static_cast<uint64_t>(u + 1) * Ns[c] / U) - cx.r0[c];
     }
+    cx.half = g & 1u;
+    cx.kh = cx.half * LCls<LC_DOWN, M>::KX;
     {
         LRange rq{}, ro{}, rg{}, rd{};
         switch (cx.w) {
@@ -665,7 +726,7 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
         cx.ln[LC_QKV] = lay_lane<LC_QKV, M>(cx.r0[LC_QKV], cx.nr[LC_QKV], cx.lane, rq, X::PLANE);
         cx.ln[LC_O] = lay_lane<LC_O, M>(cx.r0[LC_O], cx.nr[LC_O], cx.lane, ro, X::PLANE);
         cx.ln[LC_GU] = lay_lane<LC_GU, M>(cx.r0[LC_GU], cx.nr[LC_GU], cx.lane, rg, X::PLANE);
-        cx.ln[LC_DOWN] = lay_lane<LC_DOWN, M>(cx.r0[LC_DOWN], cx.nr[LC_DOWN], cx.lane, rd, X::PLANE);
+        cx.ln[LC_DOWN] = lay_lane<LC_DOWN, M>(cx.r0[LC_DOWN], cx.nr[LC_DOWN], cx.lane, rd, X::PLANE, cx.kh);
         cx.up = (cx.lane & 15) >= 8;
     }
     // Slots no compute wave writes (slot 7, and gate|up's row tiles a wave does not reach) stay zero.
@@ -788,6 +849,8 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
     cx.gave_up = false;
     const uint32_t g = blockIdx.x, G = gridDim.x;
     cx.g = g;
+    cx.half = 0;
+    cx.kh = 0;
     const uint32_t Ns[4] = {LQ::N, LO::N, LF::N, LD::N};
 #pragma unroll
     for (int c = 0; c < 4; c++) {

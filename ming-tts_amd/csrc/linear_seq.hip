@@ -43,9 +43,17 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, int kind, SeqPlan
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(MT_EHIP, "mt_seq_create: hipGetDevice: %s", hipGetErrorString(e));
-    // Each op's tagged output starts 16-byte aligned.
+    // The decode-layer kernel splits each layer's down over K between workgroup pairs: its
+    // output is two planes (the layer's last op: every 4th op, every 5th with attention).
+    bool any_attn = false;
+    for (uint32_t i = 0; i < n_ops; i++) any_attn = any_attn || ops[i].kind == SEQ_ATTN;
+    const uint32_t per = any_attn ? 5 : 4;
+    for (uint32_t i = 0; i < n_ops; i++) ops[i].planes = kind == MT_SEQ_DECODE_LAYER && i % per == per - 1 ? 2 : 1;
+    // Each op's tagged output starts 16-byte aligned (planes M N words apart; M N is a
+    // multiple of 4 for every split op).
     size_t tag_words = 0;
-    for (uint32_t i = 0; i < n_ops; i++) tag_words += (static_cast<size_t>(ops[i].M) * ops[i].N + 3) & ~size_t(3);
+    for (uint32_t i = 0; i < n_ops; i++)
+        tag_words += (static_cast<size_t>(ops[i].M) * ops[i].N * ops[i].planes + 3) & ~size_t(3);
     if (tag_words * 4 > 0x7FFFFFF0u) return set_error(MT_ENOTSUP, "mt_seq_create: the ops' outputs exceed 2 GiB");
     SeqPlan *p = new SeqPlan();
     p->n_ops = n_ops;
@@ -85,7 +93,7 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, int kind, SeqPlan
         size_t off = 0;
         for (uint32_t i = 0; i < n_ops; i++) {
             ops[i].tag = p->d_tags + off;
-            off += (static_cast<size_t>(ops[i].M) * ops[i].N + 3) & ~size_t(3);
+            off += (static_cast<size_t>(ops[i].M) * ops[i].N * ops[i].planes + 3) & ~size_t(3);
         }
         // Tagged sources as offsets into the tag buffer (no dependent lookups on the device).
         for (uint32_t i = 0; i < n_ops; i++) {
@@ -118,7 +126,9 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, int kind, SeqPlan
                 d.ldy = o.ldy;
                 d.tag = static_cast<uint32_t>(o.tag - p->d_tags);
                 d.eps = o.eps;
-                d.flags = (o.xsrc < 0 ? LAY_XEXT : 0u) | (o.ysrc < 0 ? LAY_YEXT : 0u) | (o.final_out ? LAY_FINAL : 0u);
+                d.flags = (o.xsrc < 0 ? LAY_XEXT : 0u) | (o.ysrc < 0 ? LAY_YEXT : 0u) | (o.final_out ? LAY_FINAL : 0u) |
+                          (o.xsrc >= 0 && ops[o.xsrc].planes == 2 ? LAY_X2 : 0u) |
+                          (o.ysrc >= 0 && ops[o.ysrc].planes == 2 ? LAY_Y2 : 0u);
                 // A linear whose x is a DiT attention item's output computes that attention
                 // itself: its x is the item's qkv.
                 if (o.kind == SEQ_LINEAR && o.xsrc >= 0 && ops[o.xsrc].kind == SEQ_DIT) {

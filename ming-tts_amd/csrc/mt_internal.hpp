@@ -68,7 +68,7 @@ struct SeqOp {
     const float *inv_freq;  // 32 RoPE frequencies
     uint64_t cache_stride;  // elements between row b's caches and row b + 1's
     int32_t cache_t;        // cache element type
-    int32_t pad;
+    int32_t planes;         // tagged output planes: 2 for the decode-layer kernel's down (split over K), else 1
 };
 static_assert(sizeof(SeqOp) % 16 == 0, "SeqOp is staged into LDS in 16-byte pieces");
 // A DiT attention item (kind SEQ_DIT): x the qkv rows (M = B S rows, K = 3 H 64), y the output

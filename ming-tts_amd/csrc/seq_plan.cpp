@@ -281,7 +281,8 @@ int seq_general_limits(const mt_seq_item *items, uint32_t n, int groups) {
 }
 
 bool layer_pattern(const SeqOp *ops, uint32_t n, int groups) {
-    if (n < 2 || groups < LAY_GMIN || groups > LAY_GMAX) return false;
+    // An even count: down runs on workgroup pairs.
+    if (n < 2 || groups < LAY_GMIN || groups > LAY_GMAX || groups % 2) return false;
     const uint32_t M = ops[0].M;
     if (M != 1 && M != 2 && M != 4) return false;
     // With attention items every layer is qkv, attention, o, gate|up, down; the item's rows are
