@@ -24,15 +24,21 @@
 // 32 k x 16 columns of activations as hi + lo halves of the weights' 16-bit type; see
 // seq_tiles.hpp for the segment interleave):
 //   qkv     S = 2 K-segments per row tile, 8 features, its 14 block steps 2 per wave;
-//   o, down S = 4, 4 features (a workgroup's whole share), block steps split over the 7
+//   o       S = 4, 4 features (a workgroup's whole share), block steps split over the 7
 //           waves; at M = 4 the B operand's 16 columns hold rows 0-1 and a second MFMA on
 //           the same weight tile takes rows 2-3 (two column groups);
 //   gate|up S = 1, three row tiles of 8 gate rows and the same features' 8 up rows; the
-//           84 block steps of the three row tiles in runs of 12 per wave.
+//           84 block steps of the three row tiles in runs of 12 per wave;
+//   down    split over K between the two workgroups of a pair: S = 2 over the workgroup's
+//           half of K (2432), 8 features (the pair's share), its 76 block steps split over
+//           the 7 waves; it stages and reads only its half of x.  Its output is two tagged
+//           planes, the first half's sums plus the residual and the second half's sums, added
+//           in that order by the next qkv (its x) and o (its old y); the second half writes a
+//           final user output once the first half's word is current.
 // A wave's partial sums go to its own slot of the op class's LDS area; one lane per output
 // adds the 8 slots in slot order (slots no wave writes stay zero), so results are the same
-// on every run.  A workgroup owns features [g N / G, (g + 1) N / G) of every op, which the
-// tiling holds for 224 <= G <= 256 (the host checks it).
+// on every run.  A workgroup owns features [g N / G, (g + 1) N / G) of every op (down: pair
+// g / 2 of G / 2), which the tiling holds for even 224 <= G <= 256 (the host checks it).
 #pragma once
 
 #include "dit_attend.hpp"
