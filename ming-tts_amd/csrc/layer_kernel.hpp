@@ -402,13 +402,15 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
 // holds up this op's stores unless it drains during the conversion and the MFMAs.  The
 // normed ops (qkv, gate|up) at M <= 2 issue theirs early: the norm's reductions give them
 // the longest window (decode step at M = 2: 421 -> 395.5 us; M = 1: 389 -> 341 us, A/B on
-// one box).  Early batches from o or at M = 4 measured slower (o: +28 us at M = 2; M = 4:
-// +40 to +110 us), so they stay behind the stores.
-template <int WT, int M, int C, uint32_t NB, int NA, class ISSUE>
+// one box).  down, split over K, does too in plans without attention items (ATTK false; M =
+// 2: 370 -> 367 us; with them 490 -> 498 us, so not there).  Early batches from o or
+// at M = 4 measured slower (o: +28 us at M = 2; M = 4: +40 to +110 us), so they stay behind
+// the stores.
+template <int WT, int M, int C, uint32_t NB, bool ATTK = false, int NA, class ISSUE>
 __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restrict__ ops, uint32_t i, const LayOp &d,
                                          const u32x4 (&A)[NA], ISSUE &&issue) {
     typedef LCls<C, M> L;
-    constexpr bool EARLY = L::NORM && M <= 2;
+    constexpr bool EARLY = (L::NORM || (C == LC_DOWN && !ATTK)) && M <= 2;
     static_assert(NB < 16, "a batch fits the explicit wait below");
     const uint32_t tid = cx.tid, lane = cx.lane;
     const uint32_t r0 = cx.r0[L::SLOT], nr = cx.nr[L::SLOT];
@@ -794,7 +796,7 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
             lay_tiles<WT, M, LC_QKV, 0, Q1>(cx, lops[nx], PQ);
         });
         dq = lops[nx];
-        lay_step<WT, M, LC_DOWN, NBD>(cx, ops, id, dn, PD, [&]() {
+        lay_step<WT, M, LC_DOWN, NBD, ATT>(cx, ops, id, dn, PD, [&]() {
             lay_tiles<WT, M, LC_GU, 0, G1>(cx, lops[nx + 2 + A], PG);
             lay_tiles<WT, M, LC_QKV, Q1, LQ::TA>(cx, dq, PQ);
             lay_tiles<WT, M, LC_O, 0, LO::TA>(cx, lops[nx + 1 + A], PO);
