@@ -637,14 +637,13 @@ def bench_flow_step(torch, mt, dev, reps=5, fused=True, persistent=False):
                 attention="inside the out projection" if fused or persistent else "separate launch")
 
 
-def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
+def aggregator_stage(torch, mt, dev, persistent=False):
     """The aggregator stage of one generation step (MingEngine.encodeStep, Engine.swift:405-410):
     the cls row and x_embedder (1024 x 64) of the new latent, the 8-block DiT (hidden 1024, 16
     heads) at batch 1 x seq 2 (M = 2, attention inside the out projection), the final norm +
-    896 x 1024 linear of row 0: 35 launches, bf16 weights ~ N(0, 0.02^2), captured in a HIP
-    graph and replayed.  With ``persistent`` the 8 blocks are one launch of the DiT-block
-    kernel (DiT attention items): 4 launches, run on the stream (a cooperative launch is not
-    captured), the median of `reps` runs between HIP events."""
+    896 x 1024 linear of row 0: 35 launches, bf16 weights ~ N(0, 0.02^2).  With ``persistent``
+    the 8 blocks are one launch of the DiT-block kernel (DiT attention items): 4 launches.
+    Returns (stage(stream handle), plan or None, launches, weight bytes)."""
     HID, HEADS, LAT, BLOCKS = 1024, 16, 64, 8
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -666,11 +665,10 @@ def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
     x = torch.zeros(2, HID, device=dev)
     qkv = torch.zeros(2, 3 * HID, device=dev)
     ff = torch.zeros(2, 4 * HID, device=dev)
+    att = torch.zeros(2, HID, device=dev)
     out = torch.zeros(1, H, device=dev)
-    cs = torch.cuda.Stream(device=dev)
     seq = None
     if persistent:
-        att = torch.zeros(2, HID, device=dev)
         items = []
         for p in blocks:
             items += [mt.op(x, p["qkv"], qkv, 2, bias=p["qkv_b"], norm=p["n1"]),
@@ -680,8 +678,7 @@ def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
                       mt.op(ff, p["ff2"], x, 2, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"])]
         seq = mt.Seq(items)
 
-    def stage():
-        s = cs.cuda_stream
+    def stage(s):
         x[0].copy_(cls)
         mt.linear(latent, xw, x[1:], 1, bias=xb, stream=s)
         if persistent:
@@ -693,6 +690,21 @@ def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
             mt.linear(x, p["ff1"], ff, 2, flags=mt.GemvFlags.gelu, bias=p["ff1_b"], norm=p["n2"], stream=s)
             mt.linear(ff, p["ff2"], x, 2, flags=mt.GemvFlags.accumulate, bias=p["ff2_b"], stream=s)
         mt.linear(x, fin_w, out, 1, bias=fin_b, norm=fin_n, stream=s)
+
+    stage.keep = (blocks, fin_n, fin_w, fin_b, xw, xb, invf, cls, latent, x, qkv, ff, att, out)
+    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
+    return stage, seq, 1 + 1 + (1 if persistent else 4 * BLOCKS) + 1, wbytes
+
+
+def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
+    """The aggregator stage (aggregator_stage): as a HIP graph of 35 launches replayed, or, with
+    ``persistent``, 4 launches run on the stream (a cooperative launch is not captured), the
+    median of `reps` runs between HIP events."""
+    stage_fn, seq, launches, wbytes = aggregator_stage(torch, mt, dev, persistent)
+    cs = torch.cuda.Stream(device=dev)
+
+    def stage():
+        stage_fn(cs.cuda_stream)
 
     if persistent:
         with torch.cuda.stream(cs):
@@ -709,8 +721,7 @@ def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
         seq.close()
     else:
         us = graph_us(torch, stage, cs, rounds=reps)
-    wbytes = sum(sum(t.numel() * 2 for t in p.values()) for p in blocks) + (fin_w.numel() + xw.numel()) * 2
-    return dict(us_per_generation_step=us, launches=1 + 1 + (1 if persistent else 4 * BLOCKS) + 1,
+    return dict(us_per_generation_step=us, launches=launches,
                 weight_mb=wbytes / 1e6, gbs_algorithmic=wbytes / (us * 1e-6) / 1e9,
                 blocks="one DiT-block kernel launch" if persistent else "a launch per linear")
 
@@ -786,12 +797,11 @@ def bench_vae_latent(torch, mt, dev, ws, reps=5, fused=True):
     return dict(us_per_latent=us, launches=launches, audio_ms_per_latent=4 * 882 / 44100 * 1e3)
 
 
-def bench_vae_latent_seq(torch, mt, dev, ws, reps=7):
-    """The VAE latent of bench_vae_latent with its 24-layer stack as one persistent launch:
-    upsample4, the stack at M = 4 rows of one sequence (rmsnorm + qkv, RoPE + cache append +
-    attention over the last 65 keys as an attention item, o +=, rmsnorm + gate|up, down +=:
-    120 items), the spectrum head, istft_frames and istft_emit: 5 launches on one stream
-    (the cooperative launch is not captured in a graph), timed with HIP events on it."""
+def vae_latent_seq_stage(torch, mt, dev, ws):
+    """The VAE latent with its 24-layer stack as one persistent launch: upsample4, the stack at
+    M = 4 rows of one sequence (rmsnorm + qkv, RoPE + cache append + attention over the last
+    65 keys as an attention item, o +=, rmsnorm + gate|up, down +=: 120 items), the spectrum
+    head, istft_frames and istft_emit: 5 launches.  Returns (step(stream handle), plan)."""
     HQ, HKV, CAP, NFFT, HOP, RING = 14, 2, 512, 3528, 882, 8
     pos0 = 4 * 50
     g = torch.Generator(device=dev)
@@ -822,15 +832,30 @@ def bench_vae_latent_seq(torch, mt, dev, ws, reps=7):
         items.append(mt.op(frames, p["gate"], mlp, 4, flags=mt.GemvFlags.siluGate, w2=p["up"], norm=p["norm2"]))
         items.append(mt.op(mlp, p["down"], frames, 4, flags=mt.GemvFlags.accumulate))
     seq = mt.Seq(items)
-    cs = torch.cuda.Stream(device=dev)
-    s = cs.cuda_stream
+    keep = (h, frames, qkv, att, mlp, spec, head_w, head_b, caches, invf, window, cos_table, ring, pcm, pos_d, items)
 
-    def step():
+    def step(s):
         mt.upsample4(h[0], h[1], h[2], frames, stream=s)
         seq.run(s)
         mt.linear(frames, head_w, spec, 4, bias=head_b, stream=s)
         mt.istft_frames(spec, 4, NFFT, cos_table, window, ring, 4 * 50, RING, stream=s)
         mt.istft_emit(ring, window, NFFT, HOP, 4 * 50 * HOP, 4 * HOP, 4 * 50 + 3, RING, pcm, stream=s)
+
+    step.keep = keep
+    return step, seq
+
+
+def bench_vae_latent_seq(torch, mt, dev, ws, reps=7):
+    """The VAE latent of bench_vae_latent with its 24-layer stack as one persistent launch
+    (vae_latent_seq_stage): 5 launches on one stream (the cooperative launch is not captured
+    in a graph), timed with HIP events on it."""
+    HOP = 882
+    run, seq = vae_latent_seq_stage(torch, mt, dev, ws)
+    cs = torch.cuda.Stream(device=dev)
+    s = cs.cuda_stream
+
+    def step():
+        run(s)
 
     times = []
     with torch.cuda.stream(cs):
@@ -847,9 +872,109 @@ def bench_vae_latent_seq(torch, mt, dev, ws, reps=7):
     seq.check()
     kern = seq.kernel
     seq.close()
-    return dict(us_per_latent=1e3 * sorted(times)[len(times) // 2], launches=5, items=len(items),
+    return dict(us_per_latent=1e3 * sorted(times)[len(times) // 2], launches=5, items=120,
                 kernel="decode-layer kernel" if kern == mt.SEQ_DECODE_LAYER else "general sequence kernel",
                 audio_ms_per_latent=4 * HOP / 44100 * 1e3)
+
+
+def llm_token_stage(torch, mt, dev, ws, M=1, cap=512):
+    """The llm stage's token (MingEngine.encodeStep, Engine.swift:381-385): the 24 decode layers
+    with attention at the reference's single row (QwenForward.dispatches with rows 1,
+    Qwen.swift:72-97) as one persistent launch of 120 items, the final RMSNorm of that row
+    (Qwen.swift:94) and the stop head (2 x 896 + bias, Engine.swift:385).  Returns
+    (stage(stream handle), plan)."""
+    import numpy as np
+    HQ, HKV = 14, 2
+    lens = np.random.default_rng(1).integers(32, cap + 1, M).astype(np.int32)
+    pos = torch.from_numpy(lens - 1).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    caches = [(torch.randn(M, HKV, cap, 64, generator=g, device=dev).half(),
+               torch.randn(M, HKV, cap, 64, generator=g, device=dev).half()) for _ in ws]
+    i = torch.arange(32, device=dev, dtype=torch.float32)
+    inv_freq = (1.0 / torch.pow(torch.tensor(1e6, device=dev), 2.0 * i / 64.0)).float()
+    resid = torch.randn(M, H, generator=g, device=dev)
+    qkv = torch.zeros(M, QKV, device=dev)
+    att = torch.zeros(M, HQ * 64, device=dev)
+    mlp = torch.zeros(M, INTER, device=dev)
+    z = torch.zeros(M, H, device=dev)
+    final_norm = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).half()
+    stop_w = (0.02 * torch.randn(2, H, generator=g, device=dev)).half()
+    stop_b = (0.02 * torch.randn(2, generator=g, device=dev)).half()
+    logits = torch.zeros(M, 2, device=dev)
+    items = []
+    for p, (kc, vc) in zip(ws, caches):
+        items.append(mt.op(resid, p["qkv"], qkv, M, bias=p["qkv_b"], norm=p["norm1"]))
+        items.append(mt.attn_op(qkv, M, HQ, HKV, pos, kc, vc, cap, HKV * cap * 64, inv_freq, att))
+        items.append(mt.op(att, p["o"], resid, M, flags=mt.GemvFlags.accumulate))
+        items.append(mt.op(resid, p["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=p["up"], norm=p["norm2"]))
+        items.append(mt.op(mlp, p["down"], resid, M, flags=mt.GemvFlags.accumulate))
+    seq = mt.Seq(items)
+
+    def stage(s):
+        seq.run(s)
+        mt.rmsnorm(resid, final_norm, z, rows=M, stream=s)
+        mt.linear(z, stop_w, logits, M, bias=stop_b, stream=s)
+
+    stage.keep = (caches, pos, inv_freq, resid, qkv, att, mlp, z, final_norm, stop_w, stop_b, logits, items)
+    return stage, seq
+
+
+# The reference's per-stage GPU times of one generation step on its Apple GPU (bf16 weights,
+# fp32 activations), .claude/skills/verify/features/bench.md:25, in us.
+REF_STEP_US = {"llm": 5240.0, "flow": 8930.0, "agg": 840.0, "total": 15010.0}
+
+
+def bench_generation_step(torch, mt, dev, ws, reps=5):
+    """One whole generation step after the prefill (MingEngine.encodeStep, Engine.swift:377-415),
+    stage by stage as the reference's StepRecorder times it (Engine.swift:30-85), on one stream
+    with HIP events between the stages:
+      llm:  llm_token_stage (24 decode layers with attention at M = 1 in one launch, final
+            norm, stop head);
+      vae:  the VAE frames of an older latent (vae_latent_seq_stage).  The reference encodes
+            them beside the llm token on a concurrent encoder (Engine.swift:383-384), so its
+            "llm" figure covers both; here they run one after the other;
+      flow: the cond embedder and 10 EPSS ODE steps of the 8-block DiT at M = 6
+            (flow_step_graph, a HIP graph of 342 launches);
+      agg:  the aggregator with its 8 DiT blocks as one launch (aggregator_stage).
+    The median of `reps` runs per stage, after one untimed run."""
+    llm, llm_seq = llm_token_stage(torch, mt, dev, ws)
+    vae, vae_seq = vae_latent_seq_stage(torch, mt, dev, ws)
+    flow_graph, cs, flow_launches, _, flow_keep = flow_step_graph(torch, mt, dev, fused=True)
+    agg, agg_seq, agg_launches, _ = aggregator_stage(torch, mt, dev, persistent=True)
+    s = cs.cuda_stream
+    names = ("llm", "vae", "flow", "agg")
+    times = {n: [] for n in names}
+    with torch.cuda.stream(cs):
+        for r in range(reps + 1):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+            ev[0].record(cs)
+            llm(s)
+            ev[1].record(cs)
+            vae(s)
+            ev[2].record(cs)
+            flow_graph.replay()
+            ev[3].record(cs)
+            agg(s)
+            ev[4].record(cs)
+            ev[4].synchronize()
+            if r:
+                for j, n in enumerate(names):
+                    times[n].append(1e3 * ev[j].elapsed_time(ev[j + 1]))
+    for q in (llm_seq, vae_seq, agg_seq):
+        q.check()
+        q.close()
+    med = {n: sorted(t)[len(t) // 2] for n, t in times.items()}
+    out = {f"{n}_us": med[n] for n in names}
+    out["llm_with_vae_us"] = med["llm"] + med["vae"]
+    out["total_us"] = sum(med.values())
+    out["launches"] = {"llm": 3, "vae": 5, "flow": flow_launches, "agg": agg_launches}
+    out["reference_us"] = {"llm_with_vae": REF_STEP_US["llm"], "flow": REF_STEP_US["flow"], "agg": REF_STEP_US["agg"],
+                           "total": REF_STEP_US["total"],
+                           "source": "Apple M-series GPU, .claude/skills/verify/features/bench.md:25"}
+    out["llm_rows"] = 1
+    del flow_graph, flow_keep
+    return out
 
 
 def graph_us_replay(torch, graph, stream, rounds=5) -> float:
@@ -1008,13 +1133,15 @@ def main() -> int:
     ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
-    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention", "flow"],
+    ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention", "flow",
+                                       "step"],
                     default="all",
                     help="decode: only the linear decode step; layer: it and the decode step with attention; "
                          "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
                          "gemm: only the prefill and DiT GEMM stacks; prefill: only the prefill stack at --rows; "
                          "chain: only the fp32-activation prefill chain at --rows; vae: only the VAE latent "
-                         "(graph of launches, then with the persistent stack); attention: only the decode attention")
+                         "(graph of launches, then with the persistent stack); attention: only the decode attention; "
+                         "step: only one whole generation step, stage by stage")
     ap.add_argument("--rows", type=int, default=512, help="with --only prefill or chain: the prompt rows M")
     ap.add_argument("--vs-blas", action="store_true",
                     help="with --only gemm: also time each prefill linear alone (graph replay) "
@@ -1058,6 +1185,11 @@ def main() -> int:
             out[name] = {k: (round(v, 3) if isinstance(v, float) else v)
                          for k, v in bench_flow_step(torch, mt, dev, **kw).items()}
         print(json.dumps(out), flush=True)
+        return 0
+    if args.only == "step":
+        log("one generation step: llm token, VAE latent, flow stage, aggregator")
+        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
+                          for k, v in bench_generation_step(torch, mt, dev, ws).items()}), flush=True)
         return 0
     if args.only == "attention":
         log("decode attention, batch 2")
@@ -1179,6 +1311,9 @@ def main() -> int:
         log("VAE decode of one latent with the layer stack as one persistent launch")
         line["vae_latent_persistent"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                          for k, v in bench_vae_latent_seq(torch, mt, dev, ws).items()}
+        log("one generation step, stage by stage (llm token, VAE latent, flow, aggregator)")
+        line["generation_step"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                   for k, v in bench_generation_step(torch, mt, dev, ws).items()}
         log("LLM decode step paired with a VAE latent on two streams, and serial")
         line["llm_vae_paired"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                   for k, v in bench_paired(torch, mt, dev, ws).items()}

@@ -707,6 +707,7 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
     cx.tags = const_cast<uint32_t *>(tags);
     cx.gave_up = false;
     const uint32_t g = blockIdx.x, G = gridDim.x;
+    cx.g = g;
     const uint32_t Ns[4] = {LAY_QKV, LAY_H, LAY_I, LAY_H};
 #pragma unroll
     for (int c = 0; c < 4; c++) {

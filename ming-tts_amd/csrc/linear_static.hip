@@ -24,10 +24,6 @@ static __device__ __align__(256) uint8_t scratch[STATIC_BYTES];
 
 namespace {
 
-__global__ void zero_words(uint32_t *p, uint32_t n) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
-}
-
 std::mutex g_mu;
 void *g_ptr[64];  // the array's address on each device, set at the device's first call
 
@@ -44,12 +40,9 @@ int static_scratch(hipStream_t stream, FixedWs &ws) {
             hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
             if (e != hipSuccess || !p)
                 return set_error(MT_EHIP, "mt_linear_static: hipGetSymbolAddress: %s", hipGetErrorString(e));
-            // Device globals start zero; the counters are cleared once more here by a kernel (a
-            // memset could land in a graph the caller is capturing), on the caller's stream,
-            // ahead of the call's own launch.
-            hipLaunchKernelGGL(zero_words, dim3(16), dim3(256), 0, stream, static_cast<uint32_t *>(p), STATIC_COUNTERS);
-            e = hipGetLastError();
-            if (e != hipSuccess) return set_error(MT_EHIP, "mt_linear_static: clearing the counters: %s", hipGetErrorString(e));
+            // The array starts zero (a device global) and every launch leaves its counters zero,
+            // so no clear is issued: one here could still be running on this stream while
+            // another stream's first call already counts tiles in.
             g_ptr[dev] = p;
         }
         p = g_ptr[dev];

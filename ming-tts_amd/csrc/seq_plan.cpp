@@ -311,6 +311,16 @@ bool layer_pattern(const SeqOp *ops, uint32_t n, int groups) {
             (o.norm != nullptr) != c.norm || ((o.flags & F_BIAS) != 0) != (o.bias != nullptr))
             return false;
     }
+    // Dataflow: this kernel splits each down over K, so its output is two tagged planes, and
+    // only a qkv reading it as x or an o reading it as the old y adds the second plane.  Any
+    // other in-plan reader of a down output would read the first half's sums alone.
+    auto is_down = [&](int32_t src) { return src >= 0 && static_cast<uint32_t>(src) % per == per - 1; };
+    for (uint32_t i = 0; i < n; i++) {
+        const uint32_t j = i % per;
+        const bool qkv = j == 0, o_proj = j == (att ? 2u : 1u);
+        if (is_down(ops[i].xsrc) && !(qkv && ops[i].kind == SEQ_LINEAR)) return false;
+        if (is_down(ops[i].ysrc) && !o_proj) return false;
+    }
     return true;
 }
 
@@ -346,6 +356,14 @@ bool dit_pattern(const SeqOp *ops, uint32_t n, int groups) {
             return false;
         // The out projection reads exactly the attention's output (it computes it itself).
         if (j == 2 && (o.xsrc != static_cast<int32_t>(i - 1) || o.xcol != 0)) return false;
+    }
+    // Nothing but that out projection may read a DiT attention item: the kernel never writes
+    // the items' outputs to the tagged buffer, so another reader would wait for them forever.
+    for (uint32_t i = 0; i < n; i++) {
+        const int32_t xs = ops[i].xsrc, ys = ops[i].ysrc;
+        if (xs >= 0 && static_cast<uint32_t>(xs) % 5 == 1 && !(i % 5 == 2 && static_cast<uint32_t>(xs) == i - 1))
+            return false;
+        if (ys >= 0 && static_cast<uint32_t>(ys) % 5 == 1) return false;
     }
     return true;
 }

@@ -258,3 +258,38 @@ def test_linear_after_early_attention_item_reads_no_stale_scratch(gpu):
         want = O.linear_f64(np.ascontiguousarray(a[:, :K]), wb, None, O.F16, None, None, B, N, K, 0)
         assert O.normwise_rel_err(got, want) <= 1e-5
     seq.close()
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_token_with_final_norm_and_stop_head_matches_fp64(gpu, B):
+    """The llm stage's token (Engine.swift:381-385): the decode layers with attention in one
+    launch, then the final RMSNorm of the last hidden rows (Qwen.swift:94) and the stop head, a
+    2 x 896 linear with bias (Engine.swift:385), against the fp64 chain of the same token."""
+    layers, cap = 4, 512
+    pos = [441, 338][:B]
+    say(f"token + final norm + stop head B={B}")
+    ws, x0, kcs, vcs, k0, v0, resid, qkv, att, mlp, pos_d, invf, invf_d = _setup(layers, B, cap, 61, np.float16, gpu, pos)
+    fin = 1.0 + O.gaussian(63, H, 0.1)
+    fin_bits, _ = O.round16(fin, O.F16)
+    stop = O.gaussian(64, 2 * H + 2, 0.02)
+    stop_bits, _ = O.round16(stop, O.F16)
+    stop_w, stop_b = stop_bits[:2 * H].reshape(2, H), stop_bits[2 * H:]
+    from _gpu_util import dev16
+    fin_d, stop_w_d, stop_b_d = dev16(fin_bits, O.F16, gpu), dev16(stop_w, O.F16, gpu), dev16(stop_b, O.F16, gpu)
+    z = torch.zeros(B, H, device=gpu)
+    logits = torch.zeros(B, 2, device=gpu)
+    seq = mt.Seq(layer_items(ws, B, resid, qkv, att, mlp, kcs, vcs, pos_d, invf_d, cap))
+    seq.run()
+    mt.rmsnorm(resid, fin_d, z, rows=B)
+    mt.linear(z, stop_w_d, logits, B, bias=stop_b_d)
+    torch.cuda.synchronize()
+    seq.check()
+    seq.close()
+    want_r = oracle_layers(ws, x0, B, k0, v0, pos, invf, 0, np.float16)[0]
+    want_z = O.rmsnorm_f64(want_r, fin_bits, O.F16).astype(np.float32)
+    want_l = O.linear_np64(want_z, stop_w, None, O.F16, stop_b, None, 0)
+    for got, want, what in ((z, want_z, "final norm"), (logits, want_l, "stop logits")):
+        g = got.cpu().numpy()
+        assert np.all(np.isfinite(g)), what
+        rel = O.normwise_rel_err(g, want)
+        assert rel <= 1e-3, f"{what}: normwise {rel:.3g}"

@@ -133,6 +133,47 @@ def test_decode_layer_kernel_matches_general_kernel(gpu, layers, M):
             assert O.normwise_rel_err(g, outs[1][j].astype(np.float64)) <= 1e-5, what
 
 
+def test_layer_shapes_with_other_dataflow_run_the_general_kernel(gpu):
+    """A plan with the decode layer's shapes whose downs accumulate into a buffer of their own
+    (each layer's down reads the previous down's output as its old y, while o accumulates
+    into the residual): the decode-layer kernel splits down over K into two planes that only
+    qkv's x and o's old y add, so the plan compiler must give this plan to the general
+    kernel, whose result matches the fp64 chain of the same dataflow."""
+    M, layers = 2, 3
+    ws, x0 = make_stack(layers, M, 71, gpu)
+    resid, qkv, mlp = buffers(M, x0, gpu)
+    side0 = O.gaussian(73, M * H).reshape(M, H).astype(np.float32)
+    side = torch.from_numpy(side0.copy()).to(gpu)
+    ops = []
+    for p in ws:
+        d = p["dev"]
+        ops.append(mt.op(resid, d["qkv"], qkv, M, bias=d["qkv_b"], norm=d["norm1"]))
+        ops.append(mt.op(qkv, d["o"], resid, M, flags=mt.GemvFlags.accumulate, ldx=QKV))
+        ops.append(mt.op(resid, d["gate"], mlp, M, flags=mt.GemvFlags.siluGate, w2=d["up"], norm=d["norm2"]))
+        ops.append(mt.op(mlp, d["down"], side, M, flags=mt.GemvFlags.accumulate))
+    seq = mt.Seq(ops)
+    say(f"seq other-dataflow layers={layers} M={M} kernel {seq.kernel}")
+    assert seq.kernel == mt.SEQ_GENERAL
+    seq.run()
+    torch.cuda.synchronize()
+    seq.check()
+    seq.close()
+    r, s = x0.astype(np.float32).copy(), side0.copy()
+    q = m = None
+    for p in ws:
+        q = O.linear_np64(O.rmsnorm_f64(r, p["norm1"], O.F16), p["qkv"], None, O.F16, p["qkv_b"], None,
+                          0).astype(np.float32)
+        r = O.linear_f64(np.ascontiguousarray(q[:, :H]), p["o"], None, O.F16, None, r, M, H, H,
+                         O.ACCUM).astype(np.float32)
+        m = O.linear_np64(O.rmsnorm_f64(r, p["norm2"], O.F16), p["gate"], p["up"], O.F16, None, None,
+                          O.SILU_GATE).astype(np.float32)
+        s = O.linear_f64(m, p["down"], None, O.F16, None, s, M, H, INTER, O.ACCUM).astype(np.float32)
+    for got, want, what in ((resid, r, "resid"), (side, s, "side"), (qkv, q, "qkv"), (mlp, m, "mlp")):
+        g = got.cpu().numpy()
+        assert np.all(np.isfinite(g)), what
+        assert O.normwise_rel_err(g, want) <= 1e-3, what
+
+
 @pytest.mark.parametrize("M", [1, 2, 4])
 def test_decode_layer_kernel_with_bf16_weights(gpu, M):
     """The reference's checkpoints hold bf16 weights (Weights.swift): the decode-layer kernel's
