@@ -303,6 +303,110 @@ def bench_gemv_single(torch, mt, dev, M=1, rounds=5):
                 pool_copies=copies, timing="graph replay of one dispatch per pool slice")
 
 
+# The decode-time linear shapes the reference's GEMV bench times (GemvBench.swift:18-36):
+# (label, M, N, K, flags, gated).
+GEMV_BENCH_SHAPES = [
+    ("llm qkv", 1, 1152, 896, 0, False), ("llm o", 1, 896, 896, 2, False), ("llm gate|up", 1, 4864, 896, 8, True),
+    ("llm down", 1, 896, 4864, 2, False), ("agg qkv", 2, 3072, 1024, 0, False), ("agg out", 2, 1024, 1024, 2, False),
+    ("agg ff1", 2, 4096, 1024, 4, False), ("agg ff2", 2, 1024, 4096, 2, False), ("vae qkv", 4, 1152, 896, 0, False),
+    ("vae o", 4, 896, 896, 2, False), ("vae gate|up", 4, 4864, 896, 8, True), ("vae down", 4, 896, 4864, 2, False),
+    ("vae head", 4, 3530, 896, 0, False), ("flow qkv", 6, 3072, 1024, 0, False), ("flow out", 6, 1024, 1024, 2, False),
+    ("flow ff1", 6, 4096, 1024, 4, False), ("flow ff2", 6, 1024, 4096, 2, False),
+]
+
+
+def bench_gemv_shapes(torch, mt, dev, rounds=3):
+    """The reference's GEMV bench (GemvBench.swift:18-36, 96-157) on MI355X: each decode-time
+    linear shape as a graph of back-to-back dispatches, each reading the next slice of a
+    >= 1 GiB fp16 weight pool (no cache level serves a weight twice), fp32 x and y as the
+    reference's activations; per shape the median replay / dispatches."""
+    L = mt.load()
+    cs = torch.cuda.Stream(device=dev)
+    out = []
+    for label, M, N, K, flags, gated in GEMV_BENCH_SHAPES:
+        per = N * K * (2 if gated else 1)
+        copies = (1 << 30) // (per * 2) + 1
+        pool = torch.empty(copies, per, device=dev, dtype=torch.float16)
+        pool.normal_(0.0, 0.02)
+        x = torch.randn(M, K, device=dev)
+        y = torch.zeros(M, N, device=dev)
+        p = mt.GemvParams(M, N, K, K, N, flags, 0.0)
+
+        def run():
+            for i in range(copies):
+                w = pool[i].data_ptr()
+                rc = L.mt_linear(x.data_ptr(), mt.F32, w, w + N * K * 2 if gated else None, mt.F16, None,
+                                 y.data_ptr(), p, cs.cuda_stream)
+                if rc:
+                    raise RuntimeError(mt.last_error())
+
+        us = graph_us(torch, run, cs, rounds) / copies
+        nbytes = shape_bytes(M, N, K, flags)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append(dict(shape=label, M=M, N=N, K=K, us_per_dispatch=us, gbs=gbs,
+                        pct_of_hbm_peak=100 * gbs / HBM_PEAK_GBS, family=int(mt.linear_kernel(M, N, K, mt.F32, mt.F16))))
+        del pool
+    torch.cuda.synchronize()
+    return out
+
+
+def bench_prefill_parts(torch, mt, dev, ws, M=174, cap=512, reps=3):
+    """The reference's prefill bench (QwenBench.swift:114-129): the prompt's M = 174 rows through
+    the 24 layers with the reference's types (fp32 activations, fp16 weights), as the whole
+    layer sequence (rmsnorm + qkv, rope_cache, causal attention from position 0, o +=,
+    rmsnorm + gate|up, down +=: 144 launches) and each part alone over the 24 layers' weights,
+    every figure a HIP-graph replay."""
+    HQ, HKV = 14, 2
+    resid = torch.randn(M, H, device=dev)
+    qkv = torch.zeros(M, QKV, device=dev)
+    att = torch.zeros(M, HQ * 64, device=dev)
+    mlp = torch.zeros(M, INTER, device=dev)
+    caches = [(torch.zeros(HKV, cap, 64, device=dev).half(), torch.zeros(HKV, cap, 64, device=dev).half()) for _ in ws]
+    i = torch.arange(32, device=dev, dtype=torch.float32)
+    invf = (1.0 / torch.pow(torch.tensor(1e6, device=dev), 2.0 * i / 64.0)).float()
+    cs = torch.cuda.Stream(device=dev)
+    F = mt.GemvFlags
+
+    def qkv_part(p, s):
+        mt.linear(resid, p["qkv"], qkv, M, bias=p["qkv_b"], norm=p["norm1"], stream=s)
+
+    def rope_part(c, s):
+        mt.rope_cache(qkv, QKV, M, HQ, HKV, 0, c[0], c[1], cap, invf, stream=s)
+
+    def attn_part(c, s):
+        mt.attention(qkv, QKV, M, HQ, HKV, 0, 0, c[0], c[1], cap, att, HQ * 64, stream=s)
+
+    def o_part(p, s):
+        mt.linear(att, p["o"], resid, M, flags=F.accumulate, stream=s)
+
+    def gu_part(p, s):
+        mt.linear(resid, p["gate"], mlp, M, flags=F.siluGate, w2=p["up"], norm=p["norm2"], stream=s)
+
+    def down_part(p, s):
+        mt.linear(mlp, p["down"], resid, M, flags=F.accumulate, stream=s)
+
+    def layers(parts):
+        def run():
+            s = cs.cuda_stream
+            for p, c in zip(ws, caches):
+                for name, fn in parts:
+                    fn(c if name in ("rope_cache", "attention") else p, s)
+        return run
+
+    seq_parts = [("rmsnorm+qkv", qkv_part), ("rope_cache", rope_part), ("attention", attn_part), ("o+res", o_part),
+                 ("rmsnorm+gate|up", gu_part), ("down+res", down_part)]
+    whole = graph_us(torch, layers(seq_parts), cs, rounds=reps)
+    parts = {}
+    for name, fn in seq_parts:
+        us = graph_us(torch, layers([(name, fn)]), cs, rounds=reps)
+        parts[name] = dict(us_per_dispatch=us / len(ws), us_per_step=us)
+    lin = {"rmsnorm+qkv": (QKV, H, 1), "o+res": (H, H, 1), "rmsnorm+gate|up": (INTER, H, 2), "down+res": (H, INTER, 1)}
+    flops = sum(2 * M * n * k * g for n, k, g in lin.values()) * len(ws)
+    return dict(M=M, layer_sequence_us=whole, launches=6 * len(ws), parts=parts,
+                linear_tflops=flops / (sum(parts[k]["us_per_step"] for k in lin) * 1e-6) / 1e12,
+                activations="fp32 (the reference's), fp16 weights, fp16 K/V cache")
+
+
 def bench_prefill(torch, mt, dev, ws, M, reps=3):
     """The 24-layer backbone GEMMs at M rows, fp16 activations, fp32 outputs: 96 launches,
     captured in a HIP graph and replayed, as the reference encodes them into one command
@@ -1134,14 +1238,15 @@ def main() -> int:
                     help="launch of the persistent decode kernel: cooperative (default) or ordinary "
                          "(for profilers that cannot follow a cooperative launch)")
     ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention", "flow",
-                                       "step"],
+                                       "step", "refshapes"],
                     default="all",
                     help="decode: only the linear decode step; layer: it and the decode step with attention; "
                          "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
                          "gemm: only the prefill and DiT GEMM stacks; prefill: only the prefill stack at --rows; "
                          "chain: only the fp32-activation prefill chain at --rows; vae: only the VAE latent "
                          "(graph of launches, then with the persistent stack); attention: only the decode attention; "
-                         "step: only one whole generation step, stage by stage")
+                         "step: only one whole generation step, stage by stage; refshapes: only the reference "
+                         "benches' shapes (the 17 GEMV bench shapes, the 174-row prefill per part)")
     ap.add_argument("--rows", type=int, default=512, help="with --only prefill or chain: the prompt rows M")
     ap.add_argument("--vs-blas", action="store_true",
                     help="with --only gemm: also time each prefill linear alone (graph replay) "
@@ -1186,6 +1291,13 @@ def main() -> int:
                          for k, v in bench_flow_step(torch, mt, dev, **kw).items()}
         print(json.dumps(out), flush=True)
         return 0
+    if args.only == "refshapes":
+        log("the reference GEMV bench's 17 decode shapes, rotated 1 GiB pools")
+        out = {"gemv_bench_shapes": bench_gemv_shapes(torch, mt, dev)}
+        log("prefill at the reference bench's 174 prompt rows, whole layers and per part")
+        out["prefill_174"] = bench_prefill_parts(torch, mt, dev, ws)
+        print(json.dumps(out), flush=True)
+        return 0
     if args.only == "step":
         log("one generation step: llm token, VAE latent, flow stage, aggregator")
         print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
@@ -1218,6 +1330,8 @@ def main() -> int:
         out["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
         log("aggregator stage of one generation step (8 DiT blocks at M = 2, graph replay)")
         out["aggregator"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_aggregator(torch, mt, dev).items()}
+        log("prefill at the reference bench's 174 prompt rows, whole layers and per part")
+        out["prefill_174"] = bench_prefill_parts(torch, mt, dev, ws)
         if args.vs_blas:
             log("per-op graph replay: mt_linear vs hipBLASLt")
             out["per_op_graph_replay"] = bench_gemm_ops(torch, mt, dev, ws)
@@ -1288,6 +1402,10 @@ def main() -> int:
             log(f"prefill chain (fp32 activations, fused norms) M={M}")
             line["prefill_chain"].append({k: (round(v, 3) if isinstance(v, float) else v)
                                           for k, v in bench_prefill_chain(torch, mt, dev, ws, M).items()})
+        log("prefill at the reference bench's 174 prompt rows, whole layers and per part")
+        line["prefill_174"] = bench_prefill_parts(torch, mt, dev, ws)
+        log("the reference GEMV bench's 17 decode shapes, rotated 1 GiB pools")
+        line["gemv_bench_shapes"] = bench_gemv_shapes(torch, mt, dev)
         log("decode attention batch 2")
         line["attention_decode"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                     for k, v in bench_attention(torch, mt, dev).items()}
