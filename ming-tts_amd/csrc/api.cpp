@@ -150,8 +150,8 @@ int mt_set_tuning(int key, int value) {
         return set_error(MT_EINVAL, "mt_set_tuning: the small-M kernel choice is 0, 1 or 2, got %d", value);
     if (key == MT_TUNE_GEMM_STAGES && value > 4)
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMM pipeline depth is 1..4, got %d", value);
-    if (key == MT_TUNE_GEMM_TILE && value > 4)
-        return set_error(MT_EINVAL, "mt_set_tuning: the GEMM tile choice is 0..4, got %d", value);
+    if (key == MT_TUNE_GEMM_TILE && value > 5)
+        return set_error(MT_EINVAL, "mt_set_tuning: the GEMM tile choice is 0..5, got %d", value);
     if (key == MT_TUNE_GEMV_ROWS_MAX && value > 8)
         return set_error(MT_EINVAL, "mt_set_tuning: the GEMV takes at most 8 rows per block, got %d", value);
     return slot->exchange(value < 0 ? def : value, std::memory_order_relaxed);

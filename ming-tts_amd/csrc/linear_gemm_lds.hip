@@ -6,6 +6,7 @@
 // Reference kernel replaced: gemm_kernel<32,64,32,4> (Shaders.swift:297-410).
 #include <algorithm>
 
+#include "ring_kernel.hpp"
 #include "tiled_kernel.hpp"
 
 namespace mt {
@@ -81,6 +82,12 @@ size_t tiled_partial_bytes(const TiledPlan &p, bool gated, bool norm) {
     return static_cast<size_t>(p.tiles_m) * p.tiles_n * p.splits * ne * sizeof(float);
 }
 
+// The gated ring kernel (ring_kernel.hpp) takes a SiLU-gated linear of x of the weights' type
+// from this many rows on (auto tile choice): its 96-feature tiles then fill the chip in one wave
+// (204 tiles at M = 512 on 256 CUs), where the 64-feature tiles need two (gate|up at M = 512:
+// 20.6 against 25.0 us); below it the 64-feature tiles are faster.
+constexpr uint32_t RING_GATED_MIN_M = 384;
+
 int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
     const bool split = xt == DT_F32, norm = a.norm != nullptr;
@@ -88,6 +95,22 @@ int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, c
     const int cus = device_cus();
     if (cus <= 0) return set_error(MT_EHIP, "gemm: cannot query the device");
     const int tile = tuning().gemm_tile, splitk = tuning().gemm_splitk, stages_override = tuning().gemm_stages;
+    if (gated && !split && (tile == 5 || (tile == 0 && splitk == 0 && a.M >= RING_GATED_MIN_M))) {
+        ring::RingArgs r;
+        r.x = static_cast<const uint16_t *>(a.x);
+        r.w = a.w;
+        r.w2 = a.w2;
+        r.bias = a.bias;
+        r.y = a.y;
+        r.M = a.M; r.N = a.N; r.K = a.K; r.ldx = a.ldx; r.ldy = a.ldy; r.flags = a.flags;
+        r.tiles_m = (a.M + ring::BM - 1) / ring::BM;
+        r.tiles_n = (a.N + ring::FN - 1) / ring::FN;
+        const uint64_t G = static_cast<uint64_t>(r.tiles_m) * r.tiles_n;
+        if (G == 0 || G > 0x7FFFFFFFu) return set_error(MT_EINVAL, "gemm: %llu ring tiles", static_cast<unsigned long long>(G));
+        hipLaunchKernelGGL(pick_ring_gated(wt), dim3(static_cast<uint32_t>(G)), dim3(ring::NT), 0, stream, r);
+        return check_launch("gemm (ring)");
+    }
+    if (tile == 5) return set_error(MT_EINVAL, "gemm: tile 5 (the gated ring kernel) takes a SiLU-gated linear of x of the weights' type");
     TiledPlan p = tiled_plan(a.M, a.N, a.K, gated, cus, tile, splitk, split);
     if (stages_override >= 1 && !split) p.stages = stages_override;
     if (p.bm == 0) return set_error(MT_EINVAL, "gemm: tile shape %d does not apply to this linear", tile);

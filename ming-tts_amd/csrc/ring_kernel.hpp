@@ -1,0 +1,240 @@
+// Ring GEMM for the SiLU-gated prefill linear (gate|up) with x of the weights' 16-bit type, at
+// M large enough that its output tiles fill the chip (mt_linear routes M >= 384 here).
+//
+// Reference kernel replaced: gemm_kernel<32,64,32,4> with the SiLU-gate epilogue
+// (Shaders.swift:297-410), as QwenForward.dispatches calls it for gate|up (Qwen.swift:90).
+//
+// y[m][n] = epilogue(sum_k x[m][k] w[n][k], sum_k x[m][k] w2[n][k]) on one 512-thread workgroup
+// per tile of 128 x rows and 96 features (192 weight rows: 32-row blocks of W and W2 for the
+// same 32 features, alternating), so 2 x 4864 features at M = 512 make 204 tiles, one wave of
+// workgroups on 256 CUs, where 64-feature tiles (304) would need two.
+//   - One workgroup per CU (120 KB of LDS): a ring of three 64-k stages (40 KB each: the
+//     tile's 128 x rows, then its 192 weight rows, 128 bytes a row) filled with direct-to-LDS
+//     loads (global_load_lds_dwordx4).  The prologue fills all three; iteration s waits for
+//     stage s + 1 with an exact vmcnt, meets at a bare s_barrier and refills stage s's slot
+//     with stage s + 3.  __syncthreads would add the compiler's workgroup fence, which waits
+//     for every load in flight (vmcnt(0)) and so drains the ring at each stage.
+//   - Chunk c of row r of a stage sits in slot c ^ (r & 7) ^ ((r >> 3) & 1): the operand reads
+//     (32 rows of one chunk per half-wave) are free of bank conflicts.
+//   - Eight waves, two per SIMD: waves 0-3 multiply the 16-k steps 0-1 of every stage, waves
+//     4-7 steps 2-3 (the other wave of a SIMD hides a wave's LDS reads).  Wave w owns x rows
+//     32 (w & 3) .. + 31 against all 192 weight rows: six 32 x 32 accumulators on
+//     v_mfma_f32_32x32x16, the gate and up sums of a feature in the same lane.  After the loop
+//     the second group hands its sums to the first through LDS (a fixed order: first + second).
+//   - The epilogue runs from registers: lane l holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
+//     of each block, so each store writes two 128-byte row segments.  The old y (accumulate) is
+//     requested while the groups' sums meet.
+//   - Rows past M or N and k past K are loaded from a zero block; rows past M or N are not
+//     stored.  The workgroup -> tile order gives each XCD a contiguous run of tiles (the x-row
+//     tiles of one weight tile first), which share weight rows in that XCD's L2.
+#pragma once
+
+#include "tiled_kernel.hpp"
+
+namespace mt {
+namespace ring {
+
+using tiled::f32x16t;
+using tiled::u32x4t;
+using tiled::f32x4t;
+
+constexpr int BM = 128, BN = 192, FN = 96;  // x rows, weight rows, features per tile
+constexpr int NS = 3;                        // LDS stages of 64 k
+constexpr int NT = 512, NW = 8;              // threads, waves
+constexpr int R = BM + BN;                   // rows of a stage
+constexpr int SB = R * 128;                  // bytes of a stage
+constexpr int LPW = R / (8 * NW);            // direct loads per wave per stage
+constexpr int WNT = BN / 32;                 // 32-row weight blocks: g0 u0 g1 u1 g2 u2
+constexpr int RED = 4 * WNT * 4096;          // the k groups' hand-over (bytes)
+constexpr int LDS_BYTES = NS * SB > RED ? NS * SB : RED;
+static_assert(LPW * 8 * NW == R && LDS_BYTES <= 160 * 1024 && (NS - 1) * LPW <= 63, "ring shape");
+
+// Loaded in place of any 16-byte chunk outside the operands (one per code object).
+static __device__ __attribute__((aligned(16))) uint32_t g_zero_ring[4];
+
+struct RingArgs {
+    const uint16_t *x, *w, *w2, *bias;
+    float *y;
+    uint32_t M, N, K, ldx, ldy, flags;
+    uint32_t tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ void bar() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int WT>
+__global__ __launch_bounds__(NT) void ring_gated_kernel(RingArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kh = wave >> 2, wm = wave & 3;
+
+    const uint32_t t = tiled::xcd_order(blockIdx.x, gridDim.x);
+    const uint32_t tm = t % a.tiles_m, tn = t / a.tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * FN;
+    const uint32_t M = a.M, N = a.N, K = a.K;
+    const uint32_t nsteps = (K + 63) / 64;
+
+    // Direct loads: instruction i of this wave fills stage rows 8 (wave + NW i) .. + 7, the lane
+    // slot lane & 7 of row 8 (wave + NW i) + lane / 8 with chunk (lane & 7) ^ g(row).
+    const char *src[LPW];
+    bool rowok[LPW];
+    uint32_t ci[LPW];
+    const uint32_t lds0 =
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(lds)));
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const int r = 8 * (wave + NW * i) + (lane >> 3);
+        ci[i] = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1);
+        const uint16_t *base;
+        uint32_t row, lim;
+        size_t ld;
+        if (r < BM) {
+            base = a.x; row = m0 + r; lim = M; ld = a.ldx;
+        } else {
+            const int j = r - BM, b = j >> 5;
+            base = (b & 1) ? a.w2 : a.w;
+            row = n0 + 32 * (b >> 1) + (j & 31);
+            lim = N; ld = K;
+        }
+        rowok[i] = row < lim;
+        src[i] = reinterpret_cast<const char *>(base + static_cast<size_t>(rowok[i] ? row : 0) * ld + 8 * ci[i]);
+    }
+    const char *zero = reinterpret_cast<const char *>(g_zero_ring);
+    auto issue = [&](uint32_t s) {
+        const uint32_t k = s * 64;
+#pragma unroll
+        for (int i = 0; i < LPW; i++) {
+            const char *g = (rowok[i] && k + 8 * ci[i] < K) ? src[i] + 2 * static_cast<size_t>(k) : zero;
+            tiled::dma16(__builtin_amdgcn_readfirstlane(lds0 + (s % NS) * SB + (wave + NW * i) * 1024), g);
+        }
+    };
+    // This wave's part of a stage has landed once at most `ahead` later stages are in flight.
+    auto wait_ahead = [&](uint32_t ahead) {
+        if (ahead >= 2) tiled::wait_vm<2 * LPW>();
+        else if (ahead == 1) tiled::wait_vm<LPW>();
+        else tiled::wait_vm<0>();
+    };
+
+    // Operand reads: row (l & 31) of a 32-row block, chunk 2 q + (l >> 5) of the stage (q = this
+    // group's 16-k step), slot chunk ^ g(l & 31).
+    const int fr = lane & 31, fh = lane >> 5;
+    const uint32_t gsw = (fr & 7) ^ ((fr >> 3) & 1);
+    const uint32_t cofs0 = ((2 * (2 * kh) + fh) ^ gsw) << 4, cofs1 = ((2 * (2 * kh + 1) + fh) ^ gsw) << 4;
+    const uint32_t aoff = (32 * wm + fr) * 128;
+    uint32_t boff[WNT];
+#pragma unroll
+    for (int j = 0; j < WNT; j++) boff[j] = (BM + 32 * j + fr) * 128;
+
+    f32x16t acc[WNT];
+#pragma unroll
+    for (int j = 0; j < WNT; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+    struct Fr {
+        u32x4t a[2], b[2][WNT];
+    };
+    auto rd = [&](Fr &f, uint32_t slot) {
+        const uint8_t *st = lds + slot * SB;
+        f.a[0] = *reinterpret_cast<const u32x4t *>(st + aoff + cofs0);
+        f.a[1] = *reinterpret_cast<const u32x4t *>(st + aoff + cofs1);
+#pragma unroll
+        for (int j = 0; j < WNT; j++) {
+            f.b[0][j] = *reinterpret_cast<const u32x4t *>(st + boff[j] + cofs0);
+            f.b[1][j] = *reinterpret_cast<const u32x4t *>(st + boff[j] + cofs1);
+        }
+    };
+    auto mma = [&](const Fr &f) {
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int j = 0; j < WNT; j++) acc[j] = tiled::mfma32x<WT>(f.a[q], f.b[q][j], acc[j]);
+    };
+
+    const uint32_t flags = a.flags;
+    float bv[WNT / 2];
+#pragma unroll
+    for (int p = 0; p < WNT / 2; p++) {
+        const uint32_t n = n0 + 32 * p + fr;
+        bv[p] = (flags & F_BIAS) && n < N ? dec1<WT>(a.bias[n]) : 0.0f;
+    }
+
+    if (nsteps > 0) {
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+            if (static_cast<uint32_t>(s) < nsteps) issue(s);
+        wait_ahead(min(static_cast<uint32_t>(NS - 1), nsteps - 1));
+        bar();
+        Fr f;
+        rd(f, 0);
+        for (uint32_t s = 0; s < nsteps; s++) {
+            mma(f);
+            if (s + 1 < nsteps) {
+                // stages issued so far: 0 .. min(s + NS - 1, nsteps - 1)
+                wait_ahead(min(s + NS - 1, nsteps - 1) - (s + 1));
+                bar();  // stage s + 1 is in; every wave has read stage s, whose slot takes s + NS
+                if (s + NS < nsteps) issue(s + NS);
+                rd(f, (s + 1) % NS);
+            }
+        }
+    }
+
+    // The old y of this lane's outputs (accumulate), requested before the hand-over.
+    const bool accum = (flags & F_ACCUM) != 0;
+    float yo[16][WNT / 2];
+    if (kh == 0 && accum) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t m = m0 + 32 * wm + 8 * (r >> 2) + 4 * fh + (r & 3);
+#pragma unroll
+            for (int p = 0; p < WNT / 2; p++) {
+                const uint32_t n = n0 + 32 * p + fr;
+                yo[r][p] = (m < M && n < N) ? a.y[static_cast<size_t>(m) * a.ldy + n] : 0.0f;
+            }
+        }
+    }
+    // k group 1 hands its sums to group 0 through LDS ([wave & 3][block][reg quad][lane] float4).
+    bar();  // every wave is done with the ring
+    float *red = reinterpret_cast<float *>(lds);
+    if (kh == 1) {
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                *reinterpret_cast<f32x4t *>(red + (((wm * WNT + j) * 4 + u) * 64 + lane) * 4) =
+                    f32x4t{acc[j][4 * u], acc[j][4 * u + 1], acc[j][4 * u + 2], acc[j][4 * u + 3]};
+    }
+    bar();
+    if (kh == 1) return;
+#pragma unroll
+    for (int j = 0; j < WNT; j++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const f32x4t v = *reinterpret_cast<const f32x4t *>(red + (((wm * WNT + j) * 4 + u) * 64 + lane) * 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[j][4 * u + e] += v[e];
+        }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const uint32_t m = m0 + 32 * wm + 8 * (r >> 2) + 4 * fh + (r & 3);
+        float *yr = a.y + static_cast<size_t>(m) * a.ldy;
+#pragma unroll
+        for (int p = 0; p < WNT / 2; p++) {
+            const uint32_t n = n0 + 32 * p + fr;
+            float v = epilogue(acc[2 * p][r], acc[2 * p + 1][r], bv[p], flags);
+            if (accum) v += yo[r][p];
+            if (m < M && n < N) yr[n] = v;
+        }
+    }
+}
+
+typedef void (*ring_fn)(RingArgs);
+
+}  // namespace ring
+
+// The gated ring kernel for weights (and x) of type wt.
+ring::ring_fn pick_ring_gated(int wt);
+
+}  // namespace mt

@@ -207,3 +207,45 @@ def test_nan_rows_past_m_are_not_read(gpu):
     want64 = O.linear_f64(xr[:M], wb, None, O.F16, None, None, M, N, K, 0)
     assert np.all(np.isfinite(got))
     assert O.normwise_rel_err(got, want64) <= 1e-5
+
+
+RING_SHAPES = [  # gated (M, N, K, flags, bias) for the ring kernel of 96-feature tiles
+    (512, 4864, 896, O.SILU_GATE, False),             # gate|up at the prefill's 512 rows
+    (130, 100, 200, O.SILU_GATE, True),               # ragged: rows, features and K past the tiles
+    (384, 300, 136, O.SILU_GATE | O.ACCUM, False),    # K tail inside a stage, accumulate
+    (33, 4864, 896, O.SILU_GATE | O.ACCUM, True),
+    (200, 96, 8, O.SILU_GATE | O.SILU, True),         # K = 8: one chunk of one stage
+    (257, 192, 320, O.SILU_GATE | O.GELU, False),     # GELU after the gate (flag order)
+]
+
+
+@pytest.mark.parametrize("wt", [O.F16, O.BF16], ids=["wf16", "wbf16"])
+@pytest.mark.parametrize("shape", RING_SHAPES, ids=_ids)
+def test_gated_ring_kernel(gpu, shape, wt):
+    """The gated ring kernel (MT_TUNE_GEMM_TILE = 5; the auto choice for gated linears of x of
+    the weights' type from 384 rows on) against the oracle's fp32 loop and fp64, re-run
+    bit-identical; at 512 rows the default routing takes it too and gives the same bits."""
+    M, N, K, flags, bias = shape
+    say(f"ring w{wt} {_ids(shape)}")
+    c = _case(M * 19 + N + K + wt, M, N, K, flags, bias, wt)
+    got, xu = _with_tuning(5, 0, lambda: run_linear(c, wt, gpu))
+    assert_linear_parity(got, *expected(c, xu), K, f"ring w{wt} {_ids(shape)}")
+    again, _ = _with_tuning(5, 0, lambda: run_linear(c, wt, gpu))
+    np.testing.assert_array_equal(again, got)
+    if M >= 384:
+        auto, _ = _with_tuning(0, 0, lambda: run_linear(c, wt, gpu))
+        np.testing.assert_array_equal(auto, got)
+
+
+def test_ring_tile_refuses_ungated_linears(gpu):
+    c = _case(5, 128, 64, 64, 0, False, O.F16)
+    old = mt.set_tuning(mt.TUNE_GEMM_TILE, 5)
+    try:
+        x_d = dev16(O.round16(c["x"], O.F16)[0], O.F16, gpu)
+        w_d = dev16(c["w"], O.F16, gpu)
+        y_d = torch.zeros(128, 64, device=gpu)
+        rc = mt.linear_raw(x_d, O.F16, w_d, None, O.F16, None, y_d, 128, 64, 64, 64, 64, 0)
+    finally:
+        mt.set_tuning(mt.TUNE_GEMM_TILE, old)
+    assert rc == mt.EINVAL, rc
+    assert "ring" in mt.last_error()
