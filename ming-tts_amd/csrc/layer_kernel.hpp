@@ -71,10 +71,14 @@ struct LCls {
     // pair's features over its half of K, and reads only that half of x.  Its outputs are
     // two tagged planes (the residual plus the first half's sums; the second half's sums),
     // which the next qkv (x, X2) and o (old y, Y2) add as they read them.
-    static constexpr uint32_t KSPLIT = C == LC_DOWN ? 2u : 1u;
+    // The DiT block's ff2 (4096 k) is split the same way; the next block's qkv and out add its
+    // two planes.
+    static constexpr uint32_t KSPLIT = C == LC_DOWN || C == LC_FF2 ? 2u : 1u;
     static constexpr uint32_t KX = K / KSPLIT;              // k a workgroup stages and sums
-    static constexpr bool X2 = C == LC_QKV, Y2 = C == LC_O;  // may read down's two planes
-    static constexpr uint32_t S = GATED || C == LC_DQKV || C == LC_FF1 ? 1u : C == LC_QKV || C == LC_DOWN ? 2u : 4u;
+    static constexpr bool X2 = C == LC_QKV || C == LC_DQKV, Y2 = C == LC_O || C == LC_DO;  // may read two planes
+    static constexpr uint32_t PL = M * (DIT ? DIT_H : LAY_H);  // words between a split op's two planes
+    static constexpr uint32_t S = GATED || C == LC_DQKV || C == LC_FF1 ? 1u
+                                : C == LC_QKV || C == LC_DOWN || C == LC_FF2 ? 2u : 4u;
     static constexpr uint32_t LS = S == 4 ? 2u : S == 2 ? 1u : 0u;
     static constexpr uint32_t CG = (2 * S * M + 15) / 16;  // B column groups (MFMAs per weight tile)
     static constexpr uint32_t RPG = M / CG;                 // x rows per column group
@@ -90,7 +94,9 @@ struct LCls {
     // LDS partial sums: [row tile][x row][virtual row][slot]
     static constexpr uint32_t VR = GATED ? 16u : FPT;
     static constexpr uint32_t PART = RT * M * VR * 8;
-    static_assert(KB % S == 0 && 2 * S * RPG == (CG == 1 ? 2 * S * M : 16) && RPG * CG == M && CG <= 3, "tiling");
+    // Column groups after the first start RPG rows further on; a group's 16 columns hold RPG rows
+    // (the columns past 2 S RPG read row 0 and are not flushed).
+    static_assert(KB % S == 0 && 2 * S * RPG <= 16 && (CG == 1 || 2 * S * RPG > 8) && RPG * CG == M && CG <= 3, "tiling");
     static_assert((!GATED || RT * KBS % 7 == 0) && (CG == 1 || !GATED), "tiling");
 };
 
@@ -248,10 +254,10 @@ __device__ __forceinline__ void lay_flush(const f32x4 acc, float *part, uint32_t
             q[24] = e3;
         }
     } else if constexpr (L::S == 2) {  // rows 4 qd + i: virtual row 2 qd + i / 2, segment i % 2
-        const uint32_t sc = (c >> 1) & 1, m = c >> 2;
+        const uint32_t sc = (c >> 1) & 1, mg = c >> 2, m = m0 + mg;
         const float e0 = dpp_quad(sc ? acc[1] : acc[0]);
         const float e1 = dpp_quad(sc ? acc[3] : acc[2]);
-        if ((c & 3) == 0 && m < static_cast<uint32_t>(M)) {
+        if ((c & 3) == 0 && mg < L::RPG && m < static_cast<uint32_t>(M)) {
             float *q = pp + (m * L::VR + 2 * qd) * 8;
             q[0] = e0;
             q[8] = e1;
@@ -416,9 +422,9 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     const uint32_t r0 = cx.r0[L::SLOT], nr = cx.nr[L::SLOT];
     const bool xext = (d.flags & LAY_XEXT) != 0;
     // down reads its half of K; x from down's two planes is read from both.
-    const uint32_t kx0 = L::KSPLIT > 1 ? cx.kh : 0u;
+    const uint32_t kx0 = L::KSPLIT > 1 ? cx.half * L::KX : 0u;
     const bool x2 = L::X2 && (d.flags & LAY_X2) != 0;
-    constexpr uint32_t PL = M * LAY_H;  // words between down's planes
+    constexpr uint32_t PL = L::PL;  // words between a split op's planes
 
     // Activations: chunk e = tid + 448 r is 4 k of x row e / K4 (or the DiT attention's qkv).
     u32x4 xv[L::XR], xv2[L::X2 ? L::XR : 1];
@@ -600,10 +606,14 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
             a1 *= scale;
             a2 *= scale;
         }
+        // A split op's halves are added by its readers, so its epilogue is linear (bias and
+        // the old y only) and the first half alone adds the bias and the old y.
+        static_assert(L::KSPLIT == 1 || (L::FLAGS & ~(F_BIAS | F_ACCUM)) == 0, "a split op's epilogue is linear");
+        const bool second = L::KSPLIT > 1 && cx.half != 0;
         float bias = 0.0f;
         if constexpr (L::BIAS) {
             asm volatile("" : "+v"(braw));
-            bias = dec1<WT>(static_cast<uint16_t>(braw));
+            bias = second ? 0.0f : dec1<WT>(static_cast<uint16_t>(braw));
         }
         float v = epilogue(a1, a2, bias, L::FLAGS);
         // Wait for a tagged word at byte offset off to carry the run's parity.
@@ -619,8 +629,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
                 word = ldtag1(cx.rsrc, off);
             }
         };
-        // down's second half adds no old y: its plane holds its own sums.
-        const bool second = L::KSPLIT > 1 && cx.half != 0;
+        // The second half adds no old y: its plane holds its own sums.
         if constexpr (L::ACC) {
             if (!second) {
                 if (!yext) await_word(yw, (d.yoff + om * d.yld + n) * 4u);
@@ -858,13 +867,15 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
     cx.gave_up = false;
     const uint32_t g = blockIdx.x, G = gridDim.x;
     cx.g = g;
-    cx.half = 0;
-    cx.kh = 0;
+    // ff2: pair g >> 1 of the G / 2 (G is even) owns the features, half g & 1 of K.
+    cx.half = g & 1u;
+    cx.kh = cx.half * LD::KX;
     const uint32_t Ns[4] = {LQ::N, LO::N, LF::N, LD::N};
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        cx.r0[c] = static_cast<uint32_t>(static_cast<uint64_t>(g) * Ns[c] / G);
-        cx.nr[c] = static_cast<uint32_t>(static_cast<uint64_t>(g + 1) * Ns[c] / G) - cx.r0[c];
+        const uint32_t u = c == LD::SLOT ? g >> 1 : g, U = c == LD::SLOT ? G >> 1 : G;
+        cx.r0[c] = static_cast<uint32_t>(static_cast<uint64_t>(u) * Ns[c] / U);
+        cx.nr[c] = static_cast<uint32_t>(static_cast<uint64_t>(u + 1) * Ns[c] / U) - cx.r0[c];
     }
     {
         LRange rq{}, ro{}, rf{}, rd{};
@@ -883,7 +894,7 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
         cx.ln[LQ::SLOT] = lay_lane<LC_DQKV, M>(cx.r0[LQ::SLOT], cx.nr[LQ::SLOT], cx.lane, rq, X::PLANE);
         cx.ln[LO::SLOT] = lay_lane<LC_DO, M>(cx.r0[LO::SLOT], cx.nr[LO::SLOT], cx.lane, ro, X::PLANE);
         cx.ln[LF::SLOT] = lay_lane<LC_FF1, M>(cx.r0[LF::SLOT], cx.nr[LF::SLOT], cx.lane, rf, X::PLANE);
-        cx.ln[LD::SLOT] = lay_lane<LC_FF2, M>(cx.r0[LD::SLOT], cx.nr[LD::SLOT], cx.lane, rd, X::PLANE);
+        cx.ln[LD::SLOT] = lay_lane<LC_FF2, M>(cx.r0[LD::SLOT], cx.nr[LD::SLOT], cx.lane, rd, X::PLANE, cx.kh);
         cx.up = false;
     }
     // Slots no compute wave writes stay zero.

@@ -43,12 +43,14 @@ int seq_create(SeqOp *ops, uint32_t n_ops, int wt, int groups, int kind, SeqPlan
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(MT_EHIP, "mt_seq_create: hipGetDevice: %s", hipGetErrorString(e));
-    // The decode-layer kernel splits each layer's down over K between workgroup pairs: its
-    // output is two planes (the layer's last op: every 4th op, every 5th with attention).
+    // The decode-layer kernel splits each layer's down over K between workgroup pairs, and the
+    // DiT-block kernel each block's ff2: the output is two planes (the layer's or block's last
+    // op: every 4th op, every 5th with attention items).
     bool any_attn = false;
-    for (uint32_t i = 0; i < n_ops; i++) any_attn = any_attn || ops[i].kind == SEQ_ATTN;
+    for (uint32_t i = 0; i < n_ops; i++) any_attn = any_attn || ops[i].kind == SEQ_ATTN || ops[i].kind == SEQ_DIT;
     const uint32_t per = any_attn ? 5 : 4;
-    for (uint32_t i = 0; i < n_ops; i++) ops[i].planes = kind == MT_SEQ_DECODE_LAYER && i % per == per - 1 ? 2 : 1;
+    const bool split = kind == MT_SEQ_DECODE_LAYER || kind == MT_SEQ_DIT_BLOCK;
+    for (uint32_t i = 0; i < n_ops; i++) ops[i].planes = split && i % per == per - 1 ? 2 : 1;
     // Each op's tagged output starts 16-byte aligned (planes M N words apart; M N is a
     // multiple of 4 for every split op).
     size_t tag_words = 0;

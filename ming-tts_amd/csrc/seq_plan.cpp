@@ -359,11 +359,15 @@ bool dit_pattern(const SeqOp *ops, uint32_t n, int groups) {
     }
     // Nothing but that out projection may read a DiT attention item: the kernel never writes
     // the items' outputs to the tagged buffer, so another reader would wait for them forever.
+    // ff2 is split over K into two tagged planes, which only a qkv reading them as x or an out
+    // projection reading them as the old y adds.
     for (uint32_t i = 0; i < n; i++) {
         const int32_t xs = ops[i].xsrc, ys = ops[i].ysrc;
         if (xs >= 0 && static_cast<uint32_t>(xs) % 5 == 1 && !(i % 5 == 2 && static_cast<uint32_t>(xs) == i - 1))
             return false;
         if (ys >= 0 && static_cast<uint32_t>(ys) % 5 == 1) return false;
+        if (xs >= 0 && static_cast<uint32_t>(xs) % 5 == 4 && i % 5 != 0) return false;
+        if (ys >= 0 && static_cast<uint32_t>(ys) % 5 == 4 && i % 5 != 2) return false;
     }
     return true;
 }
