@@ -179,8 +179,11 @@ __device__ __forceinline__ LLane lay_lane(uint32_t r0, uint32_t nr, uint32_t lan
 // Workgroup state shared by the op steps.
 template <int WT, int M>
 struct LayCtx {
-    static constexpr uint32_t PLANE = M * LAY_I + 64;  // hi / lo planes of the x staging (elements)
+    // hi / lo planes of the x staging (elements): down's x; M = 6 runs only the DiT-block
+    // kernel, whose widest staged x is ff2's half of K.
+    static constexpr uint32_t PLANE = M * (M > 4 ? DIT_FF / 2 : LAY_I) + 64;
     uint16_t *xs;    // [2][PLANE] staged x of the current op
+    float *qs;       // DiT-block kernel: the block's qkv [M][DIT_QKV] for its attention
     float *part[4];  // per class slot: [row tile][x row][virtual row][8 slots]
     float *ssw[4];   // per norm class slot: [M][8 slots] sums of x^2
     LLane ln[4];
@@ -296,62 +299,60 @@ __device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A
 
 // The DiT attention that a DiT block's out projection stages as its x (DiT-block kernel; the
 // arithmetic of dit_attend.hpp), for B sequences of S rows at M = B S: (2, 3) in the flow
-// loop, (1, 2) in the aggregator.  Half wave hw of the 14 takes the (sequence, head) groups hw,
-// hw + 14, ... of the B H, lane p the interleaved-RoPE pair 2p, 2p + 1 of the q, k and v of the
-// group's S rows.  Each workgroup computes all of it from the block's tagged qkv (read once),
-// so the attention adds no exchange between workgroups.
+// loop, (1, 2) in the aggregator.  Each workgroup reads the block's whole tagged qkv (M rows of
+// 3 H 64 words) in 16-byte chunks, chunk e = tid + 448 r, as the other ops read their x, and
+// stages it in LDS (cx.qs); then half wave hw of the 14 takes the (sequence, head) groups hw,
+// hw + 14, ... of the B H, lane p the interleaved-RoPE pair 2p, 2p + 1 of the group's q, k and
+// v rows, read from the staging.  So the attention adds no exchange between workgroups, and a
+// lane holds 16-byte chunks (11 at M = 6) rather than every pair of its groups in registers.
 template <int M>
 struct DitAtt {
     static constexpr uint32_t S = M == 6 ? 3u : 2u, B = M / S;
     static constexpr uint32_t GROUPS = B * DIT_HEADS, HW = LAY_THREADS / 32;
     static constexpr uint32_t GR = (GROUPS + HW - 1) / HW;  // groups a half wave takes
-    static constexpr uint32_t T = 3 * S;                     // q, k and v pairs of a group
+    static constexpr uint32_t W = DIT_QKV;                   // words of a qkv row
+    static constexpr uint32_t NCH = M * W / 4;               // 16-byte chunks of the qkv
+    static constexpr uint32_t XA = (NCH + LAY_THREADS - 1) / LAY_THREADS;  // chunks a thread reads
 };
 
-__device__ __forceinline__ u32x2 ldtag2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, SC1);
-}
-__device__ __forceinline__ bool tagged2(const u32x2 a, uint32_t parity) {
-    return parity ? (a.x & a.y & 1u) != 0 : ((a.x | a.y) & 1u) == 0;
-}
-// Byte offset in the tag buffer of pair t of group gi (t < S: q of row t; then the S k rows,
-// then the S v rows); d.xoff / d.xld locate the block's qkv output.
+// Byte offset in the tag buffer of qkv chunk e (d.xoff / d.xld locate the block's qkv output);
+// past the chunks an offset outside the buffer, which reads 0.
 template <int M>
-__device__ __forceinline__ uint32_t dit_att_off(const LayOp &d, uint32_t gi, uint32_t t, uint32_t p) {
-    constexpr uint32_t S = DitAtt<M>::S;
-    const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, part = t / S, row = b * S + t % S;
-    return (d.xoff + row * d.xld + part * (DIT_HEADS * 64) + h * 64 + 2 * p) * 4u;
+__device__ __forceinline__ uint32_t dit_att_off(const LayOp &d, uint32_t e) {
+    typedef DitAtt<M> D;
+    const uint32_t m = e / (D::W / 4), k = (e - m * (D::W / 4)) * 4;
+    return e < D::NCH ? (d.xoff + m * d.xld + k) * 4u : 0xFFFFFFF0u;
 }
 template <int WT, int M>
-__device__ __forceinline__ void dit_att_request(const LayCtx<WT, M> &cx, const LayOp &d,
-                                                u32x2 (&a)[DitAtt<M>::GR][DitAtt<M>::T]) {
-    typedef DitAtt<M> D;
-    static_assert(D::B * D::S == M && D::GR * D::T <= 32, "DiT attention shape; one stale bit per pair");
-    const uint32_t hw = cx.tid >> 5, p = cx.tid & 31;
+__device__ __forceinline__ void dit_att_request(const LayCtx<WT, M> &cx, const LayOp &d, u32x4 (&a)[DitAtt<M>::XA]) {
+    static_assert(DitAtt<M>::B * DitAtt<M>::S == M && DitAtt<M>::XA <= 16, "DiT attention shape; one stale bit per chunk");
 #pragma unroll
-    for (uint32_t r = 0; r < D::GR; r++) {
-        const uint32_t gi = hw + D::HW * r;
-#pragma unroll
-        for (uint32_t t = 0; t < D::T; t++)  // past the groups: an offset outside the buffer reads 0
-            a[r][t] = ldtag2(cx.rsrc, gi < D::GROUPS ? dit_att_off<M>(d, gi, t, p) : 0xFFFFFFF0u);
-    }
+    for (uint32_t r = 0; r < DitAtt<M>::XA; r++) a[r] = ldtag4(cx.rsrc, dit_att_off<M>(d, cx.tid + LAY_THREADS * r));
 }
-// Waits for the requested pairs, then computes each group's S query rows and stages them
-// (hi + lo) as x of the out projection (K = H 64); `item` is the attention item, whose user
-// output workgroup 0 writes when it is the region's last write.
+// Stages each requested chunk in LDS as soon as it is current (a round requests the whole array
+// again, chunks already staged at an offset outside the buffer), then computes each group's S
+// query rows and stages them (hi + lo) as x of the out projection (K = H 64); `item` is the
+// attention item, whose user output workgroup 0 writes when it is the region's last write.
 template <int WT, int M, uint32_t K>
 __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d, const SeqOp &item,
-                                              u32x2 (&a)[DitAtt<M>::GR][DitAtt<M>::T]) {
+                                              u32x4 (&a)[DitAtt<M>::XA]) {
     typedef DitAtt<M> D;
-    const uint32_t hw = cx.tid >> 5, p = cx.tid & 31;
-    uint32_t stale = 0;
+    const uint32_t tid = cx.tid;
+    uint32_t pend = 0;
 #pragma unroll
-    for (uint32_t r = 0; r < D::GR; r++)
-#pragma unroll
-        for (uint32_t t = 0; t < D::T; t++)
-            if (hw + D::HW * r < D::GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * D::T + t);
+    for (uint32_t r = 0; r < D::XA; r++)
+        if (tid + LAY_THREADS * r < D::NCH) pend |= 1u << r;
     uint32_t spins = 0;
-    while (stale && !cx.gave_up) {
+    while (true) {
+#pragma unroll
+        for (uint32_t r = 0; r < D::XA; r++) {
+            if (((pend >> r) & 1u) && tagged4(a[r], cx.parity)) {
+                *reinterpret_cast<f32x4 *>(cx.qs + 4 * (tid + LAY_THREADS * r)) =
+                    f32x4{untag(a[r].x), untag(a[r].y), untag(a[r].z), untag(a[r].w)};
+                pend &= ~(1u << r);
+            }
+        }
+        if (!pend || cx.gave_up) break;
         if (++spins > SPIN_LIMIT) {
             cx.gave_up = true;
             raise_flag(cx.sync, SYNC_TIMEOUT);
@@ -359,17 +360,11 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
         }
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (uint32_t r = 0; r < D::GR; r++)
-#pragma unroll
-            for (uint32_t t = 0; t < D::T; t++)
-                if ((stale >> (r * D::T + t)) & 1u) a[r][t] = ldtag2(cx.rsrc, dit_att_off<M>(d, hw + D::HW * r, t, p));
-        stale = 0;
-#pragma unroll
-        for (uint32_t r = 0; r < D::GR; r++)
-#pragma unroll
-            for (uint32_t t = 0; t < D::T; t++)
-                if (hw + D::HW * r < D::GROUPS && !tagged2(a[r][t], cx.parity)) stale |= 1u << (r * D::T + t);
+        for (uint32_t r = 0; r < D::XA; r++)
+            a[r] = ldtag4(cx.rsrc, (pend >> r) & 1u ? dit_att_off<M>(d, tid + LAY_THREADS * r) : 0xFFFFFFF0u);
     }
+    __syncthreads();  // the qkv staged
+    const uint32_t hw = tid >> 5, p = tid & 31;
     const bool write_out = item.final_out != 0 && cx.g == 0;
     bool range_ok = true;
 #pragma unroll
@@ -377,7 +372,10 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
         const uint32_t gi = hw + D::HW * r;
         if (gi >= D::GROUPS) continue;  // the whole half wave together
         const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, col = h * 64 + 2 * p;
-        auto pair = [&](uint32_t t) { return make_float2(untag(a[r][t].x), untag(a[r][t].y)); };
+        // pair t of the group: t < S the q of row t, then the S k rows, then the S v rows
+        auto pair = [&](uint32_t t) {
+            return *reinterpret_cast<const float2 *>(cx.qs + (b * D::S + t % D::S) * D::W + (t / D::S) * (DIT_HEADS * 64) + col);
+        };
         DitItem it;
 #pragma unroll
         for (uint32_t j = 0; j < DIT_MAXS; j++) {
@@ -416,6 +414,7 @@ template <int WT, int M, int C, uint32_t NB, bool ATTK = false, int NA, class IS
 __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restrict__ ops, uint32_t i, const LayOp &d,
                                          const u32x4 (&A)[NA], ISSUE &&issue) {
     typedef LCls<C, M> L;
+    static_assert(M * L::KX <= LayCtx<WT, M>::PLANE, "x staging");
     constexpr bool EARLY = (L::NORM || (C == LC_DOWN && !ATTK)) && M <= 2;
     static_assert(NB < 16, "a batch fits the explicit wait below");
     const uint32_t tid = cx.tid, lane = cx.lane;
@@ -429,7 +428,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     // Activations: chunk e = tid + 448 r is 4 k of x row e / K4 (or the DiT attention's qkv).
     u32x4 xv[L::XR], xv2[L::X2 ? L::XR : 1];
     u32x2 gv[L::XR];
-    u32x2 att[L::ATTX ? DitAtt<M>::GR : 1][DitAtt<M>::T];
+    u32x4 att[L::ATTX ? DitAtt<M>::XA : 1];
     if constexpr (L::ATTX) dit_att_request(cx, d, att);
 #pragma unroll
     for (uint32_t r = 0; r < (L::ATTX ? 0u : L::XR); r++) {
@@ -476,21 +475,70 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     if constexpr (L::ATTX) {
         dit_att_stage<WT, M, L::K>(cx, d, ops[i - 1], att);
     } else {
-        // Wait for the activations; stale chunks are requested again, all at once per round.
-        if (!xext) {
-            static_assert(L::XR <= 16, "stale bits: 16 per plane");
+        // The conversion into the staging, chunk by chunk: tag bit cleared (down's two planes
+        // added), x^2 summed, gain applied, split into hi + lo halves of the weights' type.
+        // Ops without an early batch convert each chunk as soon as it is current; their rounds
+        // request the whole chunk array again, chunks already staged at an offset outside the
+        // buffer (they read 0 and fetch nothing), so no chunk's old registers are merged with
+        // new ones and the arrays are not held twice over the wait (at M = 6 that spilled 100
+        // registers, whose reloads waited for every weight tile in flight).
+        static_assert(L::XR <= 16, "pending bits");
+        const uint32_t clear = xext ? ~0u : ~1u;
+        float tq[L::NORM ? L::XR : 1];  // x^2 of chunk r (per row below, in chunk order)
+        bool range_ok = true;
+        auto stage = [&](uint32_t r) {
+            const uint32_t e = tid + 448 * r;
+            const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+            float x[4];
+            x[0] = __uint_as_float(xv[r].x & clear);
+            x[1] = __uint_as_float(xv[r].y & clear);
+            x[2] = __uint_as_float(xv[r].z & clear);
+            x[3] = __uint_as_float(xv[r].w & clear);
+            if constexpr (L::X2) {
+                if (x2) {  // the residual: down's first plane + its second, in that order
+                    x[0] += untag(xv2[r].x);
+                    x[1] += untag(xv2[r].y);
+                    x[2] += untag(xv2[r].z);
+                    x[3] += untag(xv2[r].w);
+                }
+            }
+            if constexpr (L::NORM) {
+                float t = x[0] * x[0];
+                t = fmaf(x[1], x[1], t);
+                t = fmaf(x[2], x[2], t);
+                tq[r] = fmaf(x[3], x[3], t);
+                x[0] *= dec_lo<WT>(gv[r].x);
+                x[1] *= dec_hi<WT>(gv[r].x);
+                x[2] *= dec_lo<WT>(gv[r].y);
+                x[3] *= dec_hi<WT>(gv[r].y);
+            }
+            if constexpr (WT == DT_F16)
+                range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
+            u32x2 hi, lo;
+            split4p<WT>(x, hi, lo);
+            *reinterpret_cast<u32x2 *>(cx.xs + m * L::KX + k) = hi;
+            *reinterpret_cast<u32x2 *>(cx.xs + LayCtx<WT, M>::PLANE + m * L::KX + k) = lo;
+        };
+        uint32_t pend = 0;  // chunks in range not staged yet
+#pragma unroll
+        for (uint32_t r = 0; r < L::XR; r++)
+            if (tid + 448 * r < L::NCH) pend |= 1u << r;
+        uint32_t spins = 0;
+        if constexpr (EARLY) {
+            // Every chunk current first (stale ones requested again, all at once per round),
+            // then the batch, then the conversions: the batch drains meanwhile.  These ops run
+            // at M <= 2, where the chunk arrays are small enough to be held over the wait.
             auto stale_bits = [&]() {
                 uint32_t st = 0;
 #pragma unroll
                 for (uint32_t r = 0; r < L::XR; r++) {
-                    if (tid + 448 * r < L::NCH && !tagged4(xv[r], cx.parity)) st |= 1u << r;
+                    if (((pend >> r) & 1u) && !tagged4(xv[r], cx.parity)) st |= 1u << r;
                     if constexpr (L::X2)
-                        if (x2 && tid + 448 * r < L::NCH && !tagged4(xv2[r], cx.parity)) st |= 1u << (16 + r);
+                        if (x2 && ((pend >> r) & 1u) && !tagged4(xv2[r], cx.parity)) st |= 1u << (16 + r);
                 }
                 return st;
             };
-            uint32_t stale = stale_bits();
-            uint32_t spins = 0;
+            uint32_t stale = xext ? 0u : stale_bits();
             while (stale && !cx.gave_up) {
                 if (++spins > SPIN_LIMIT) {
                     cx.gave_up = true;
@@ -508,51 +556,53 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
                 }
                 stale = stale_bits();
             }
+            issue();
+#pragma unroll
+            for (uint32_t r = 0; r < L::XR; r++)
+                if ((pend >> r) & 1u) stage(r);
+        } else {
+            while (true) {
+#pragma unroll
+                for (uint32_t r = 0; r < L::XR; r++) {
+                    bool cur = ((pend >> r) & 1u) != 0;
+                    if (!xext) {
+                        cur = cur && tagged4(xv[r], cx.parity);
+                        if constexpr (L::X2) cur = cur && (!x2 || tagged4(xv2[r], cx.parity));
+                    }
+                    if (cur) {
+                        stage(r);
+                        pend &= ~(1u << r);
+                    }
+                }
+                if (!pend || cx.gave_up) break;
+                if (++spins > SPIN_LIMIT) {
+                    cx.gave_up = true;
+                    raise_flag(cx.sync, SYNC_TIMEOUT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (uint32_t r = 0; r < L::XR; r++) {
+                    const uint32_t e = tid + 448 * r;
+                    const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
+                    const bool want = ((pend >> r) & 1u) != 0;
+                    xv[r] = ldtag4(cx.rsrc, want ? (d.xoff + m * d.xld + kx0 + k) * 4u : 0xFFFFFFF0u);
+                    if constexpr (L::X2)
+                        if (x2) xv2[r] = ldtag4(cx.rsrc, want ? (d.xoff + PL + m * d.xld + k) * 4u : 0xFFFFFFF0u);
+                }
+            }
         }
-        if constexpr (EARLY) issue();
-        // Convert into the staging: tag bit cleared, x^2 summed per row, gain applied, split
-        // into hi + lo halves of the weights' type.
-        const uint32_t clear = xext ? ~0u : ~1u;
         float ss[M];
 #pragma unroll
         for (int mm = 0; mm < M; mm++) ss[mm] = 0.0f;
-        bool range_ok = true;
+        if constexpr (L::NORM) {
 #pragma unroll
-        for (uint32_t r = 0; r < L::XR; r++) {
-            const uint32_t e = tid + 448 * r;
-            if (e < L::NCH) {
-                const uint32_t m = e / L::K4, k = (e - m * L::K4) * 4;
-                float x[4];
-                x[0] = __uint_as_float(xv[r].x & clear);
-                x[1] = __uint_as_float(xv[r].y & clear);
-                x[2] = __uint_as_float(xv[r].z & clear);
-                x[3] = __uint_as_float(xv[r].w & clear);
-                if constexpr (L::X2) {
-                    if (x2) {  // the residual: down's first plane + its second, in that order
-                        x[0] += untag(xv2[r].x);
-                        x[1] += untag(xv2[r].y);
-                        x[2] += untag(xv2[r].z);
-                        x[3] += untag(xv2[r].w);
-                    }
-                }
-                if constexpr (L::NORM) {
-                    float t = x[0] * x[0];
-                    t = fmaf(x[1], x[1], t);
-                    t = fmaf(x[2], x[2], t);
-                    t = fmaf(x[3], x[3], t);
+            for (uint32_t r = 0; r < L::XR; r++) {
+                const uint32_t e = tid + 448 * r, m = e / L::K4;
+                if (e < L::NCH) {
 #pragma unroll
-                    for (int mm = 0; mm < M; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? t : 0.0f;
-                    x[0] *= dec_lo<WT>(gv[r].x);
-                    x[1] *= dec_hi<WT>(gv[r].x);
-                    x[2] *= dec_lo<WT>(gv[r].y);
-                    x[3] *= dec_hi<WT>(gv[r].y);
+                    for (int mm = 0; mm < M; mm++) ss[mm] += m == static_cast<uint32_t>(mm) ? tq[r] : 0.0f;
                 }
-                if constexpr (WT == DT_F16)
-                    range_ok = range_ok && fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))) <= 65504.0f;
-                u32x2 hi, lo;
-                split4p<WT>(x, hi, lo);
-                *reinterpret_cast<u32x2 *>(cx.xs + m * L::KX + k) = hi;
-                *reinterpret_cast<u32x2 *>(cx.xs + LayCtx<WT, M>::PLANE + m * L::KX + k) = lo;
             }
         }
         if (!range_ok) raise_flag(cx.sync, SYNC_RANGE);
@@ -701,6 +751,7 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
 
     X cx;
     cx.xs = xs;
+    cx.qs = nullptr;
     cx.part[LC_QKV] = p_qkv;
     cx.part[LC_O] = p_o;
     cx.part[LC_GU] = p_gu;
@@ -841,6 +892,7 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
     typedef LCls<LC_FF1, M> LF;
     typedef LCls<LC_FF2, M> LD;
     __shared__ __attribute__((aligned(16))) uint16_t xs[2 * X::PLANE];
+    __shared__ __attribute__((aligned(16))) float qs[M * DIT_QKV];
     __shared__ __attribute__((aligned(16))) float p_q[LQ::PART];
     __shared__ __attribute__((aligned(16))) float p_o[LO::PART];
     __shared__ __attribute__((aligned(16))) float p_f[LF::PART];
@@ -851,6 +903,7 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
 
     X cx;
     cx.xs = xs;
+    cx.qs = qs;
     cx.part[LQ::SLOT] = p_q;
     cx.part[LO::SLOT] = p_o;
     cx.part[LF::SLOT] = p_f;
