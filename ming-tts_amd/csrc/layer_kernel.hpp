@@ -190,9 +190,9 @@ struct LayCtx {
     uint32_t r0[4], nr[4];
     uint32_t tid, lane, w, parity, g;
     uint32_t kh, half;  // down: this workgroup's half of K (its first k, and 0 / 1)
-    // DiT-block kernel: the lane's RoPE pair's cos / sin at positions 0 .. S - 1 and the
-    // attention's score scale.
-    float rc[DIT_MAXS], rs[DIT_MAXS];
+    // DiT-block kernel: the attention's RoPE table [cos, sin][pair p < 32][position j < S] and
+    // its score scale.
+    const float *rope;
     float ascale;
     bool up;         // gate|up: the lane's tile rows are W2's
     __amdgpu_buffer_rsrc_t rsrc;
@@ -298,18 +298,17 @@ __device__ __forceinline__ void lay_mma(const LayCtx<WT, M> &cx, const u32x4 (&A
 }
 
 // The DiT attention that a DiT block's out projection stages as its x (DiT-block kernel; the
-// arithmetic of dit_attend.hpp), for B sequences of S rows at M = B S: (2, 3) in the flow
-// loop, (1, 2) in the aggregator.  Each workgroup reads the block's whole tagged qkv (M rows of
-// 3 H 64 words) in 16-byte chunks, chunk e = tid + 448 r, as the other ops read their x, and
-// stages it in LDS (cx.qs); then half wave hw of the 14 takes the (sequence, head) groups hw,
-// hw + 14, ... of the B H, lane p the interleaved-RoPE pair 2p, 2p + 1 of the group's q, k and
-// v rows, read from the staging.  So the attention adds no exchange between workgroups, and a
+// attention of dit_attend.hpp: interleaved RoPE, fp32 scores scaled after the dot, max-subtracted
+// softmax, fp32 p.v, with each dot summed in its own order), for B sequences of S rows at M = B S:
+// (2, 3) in the flow loop, (1, 2) in the aggregator.  Each workgroup reads the block's whole
+// tagged qkv (M rows of 3 H 64 words) in 16-byte chunks, chunk e = tid + 448 r, as the other ops
+// read their x, and stages it in LDS (cx.qs); then each octet of lanes takes a (sequence, head)
+// group, read from the staging.  So the attention adds no exchange between workgroups, and a
 // lane holds 16-byte chunks (11 at M = 6) rather than every pair of its groups in registers.
 template <int M>
 struct DitAtt {
     static constexpr uint32_t S = M == 6 ? 3u : 2u, B = M / S;
-    static constexpr uint32_t GROUPS = B * DIT_HEADS, HW = LAY_THREADS / 32;
-    static constexpr uint32_t GR = (GROUPS + HW - 1) / HW;  // groups a half wave takes
+    static constexpr uint32_t GROUPS = B * DIT_HEADS;
     static constexpr uint32_t W = DIT_QKV;                   // words of a qkv row
     static constexpr uint32_t NCH = M * W / 4;               // 16-byte chunks of the qkv
     static constexpr uint32_t XA = (NCH + LAY_THREADS - 1) / LAY_THREADS;  // chunks a thread reads
@@ -364,35 +363,90 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
             a[r] = ldtag4(cx.rsrc, (pend >> r) & 1u ? dit_att_off<M>(d, tid + LAY_THREADS * r) : 0xFFFFFFF0u);
     }
     __syncthreads();  // the qkv staged
-    const uint32_t hw = tid >> 5, p = tid & 31;
+    // Octet j of wave w < 4 takes group w + 4 j (the groups spread over the four SIMDs, one
+    // round); lane l of it the RoPE pairs 4l .. 4l + 3 (dims 8l .. 8l + 7) of the group's q, k
+    // and v rows.  The S x S scores are summed over the octet together, so their DPP steps
+    // overlap; each query row takes one reciprocal of its softmax sum.
+    static_assert(D::GROUPS <= 32, "one group per octet of waves 0-3");
+    const uint32_t l = cx.lane & 7, gi = cx.w + 4 * (cx.lane >> 3);
     const bool write_out = item.final_out != 0 && cx.g == 0;
     bool range_ok = true;
-#pragma unroll
-    for (uint32_t r = 0; r < D::GR; r++) {
-        const uint32_t gi = hw + D::HW * r;
-        if (gi >= D::GROUPS) continue;  // the whole half wave together
-        const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS, col = h * 64 + 2 * p;
-        // pair t of the group: t < S the q of row t, then the S k rows, then the S v rows
-        auto pair = [&](uint32_t t) {
-            return *reinterpret_cast<const float2 *>(cx.qs + (b * D::S + t % D::S) * D::W + (t / D::S) * (DIT_HEADS * 64) + col);
+    if (cx.w < 4 && gi < D::GROUPS) {
+        const uint32_t b = gi / DIT_HEADS, h = gi % DIT_HEADS;
+        // the lane's 8 dims of row j of part u (0 q, 1 k, 2 v)
+        auto dims = [&](uint32_t u, uint32_t j, float (&v)[8]) {
+            const float *p = cx.qs + (b * D::S + j) * D::W + u * (DIT_HEADS * 64) + h * 64 + 8 * l;
+            const f32x4 a0 = *reinterpret_cast<const f32x4 *>(p), a1 = *reinterpret_cast<const f32x4 *>(p + 4);
+            v[0] = a0[0]; v[1] = a0[1]; v[2] = a0[2]; v[3] = a0[3];
+            v[4] = a1[0]; v[5] = a1[1]; v[6] = a1[2]; v[7] = a1[3];
         };
-        DitItem it;
+        auto rotate = [&](float (&v)[8], uint32_t j) {  // position j
 #pragma unroll
-        for (uint32_t j = 0; j < DIT_MAXS; j++) {
-            it.k[j] = j < D::S ? pair(D::S + j) : make_float2(0.0f, 0.0f);
-            it.v[j] = j < D::S ? pair(2 * D::S + j) : make_float2(0.0f, 0.0f);
+            for (uint32_t pi = 0; pi < 4; pi++) {
+                const uint32_t pp = 4 * l + pi;
+                const float2 r = dit_rope_pair(make_float2(v[2 * pi], v[2 * pi + 1]), cx.rope[pp * D::S + j],
+                                               cx.rope[(32 + pp) * D::S + j]);
+                v[2 * pi] = r.x;
+                v[2 * pi + 1] = r.y;
+            }
+        };
+        float q[D::S][8], k[D::S][8];
+#pragma unroll
+        for (uint32_t j = 0; j < D::S; j++) {
+            dims(0, j, q[j]);
+            dims(1, j, k[j]);
+            rotate(q[j], j);
+            rotate(k[j], j);
         }
+        float sc[D::S][D::S];
+#pragma unroll
+        for (uint32_t i = 0; i < D::S; i++)
+#pragma unroll
+            for (uint32_t j = 0; j < D::S; j++) {
+                float v = q[i][0] * k[j][0];
+#pragma unroll
+                for (uint32_t e = 1; e < 8; e++) v = fmaf(q[i][e], k[j][e], v);
+                sc[i][j] = v;
+            }
+        octet_sums<D::S * D::S>(&sc[0][0]);
+        float vv[D::S][8];
+#pragma unroll
+        for (uint32_t j = 0; j < D::S; j++) dims(2, j, vv[j]);
 #pragma unroll
         for (uint32_t i = 0; i < D::S; i++) {
-            it.q = pair(i);
-            const float2 o = dit_item_attend(it, i, D::S, cx.rc, cx.rs, cx.ascale);
-            const uint32_t row = b * D::S + i;
-            const uint32_t hi = pack2<WT>(o.x, o.y);
-            const uint32_t lo = pack2<WT>(o.x - dec_lo<WT>(hi), o.y - dec_hi<WT>(hi));
-            *reinterpret_cast<uint32_t *>(cx.xs + row * K + col) = hi;
-            *reinterpret_cast<uint32_t *>(cx.xs + LayCtx<WT, M>::PLANE + row * K + col) = lo;
-            if constexpr (WT == DT_F16) range_ok = range_ok && fmaxf(fabsf(o.x), fabsf(o.y)) <= 65504.0f;
-            if (write_out) *reinterpret_cast<float2 *>(item.y + static_cast<size_t>(row) * item.ldy + col) = o;
+            float mx = -INFINITY;
+#pragma unroll
+            for (uint32_t j = 0; j < D::S; j++) {
+                sc[i][j] *= cx.ascale;
+                mx = fmaxf(mx, sc[i][j]);
+            }
+            float sum = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t j = 0; j < D::S; j++) {
+                const float e = expf(sc[i][j] - mx);
+                sum += e;
+#pragma unroll
+                for (uint32_t d2 = 0; d2 < 8; d2++) acc[d2] = fmaf(e, vv[j][d2], acc[d2]);
+            }
+            const float inv = 1.0f / sum;
+            const uint32_t row = b * D::S + i, col = h * 64 + 8 * l;
+            float o[8];
+            uint32_t hv[4], lv[4];
+#pragma unroll
+            for (uint32_t d2 = 0; d2 < 8; d2++) o[d2] = acc[d2] * inv;
+#pragma unroll
+            for (uint32_t pi = 0; pi < 4; pi++) {
+                hv[pi] = pack2<WT>(o[2 * pi], o[2 * pi + 1]);
+                lv[pi] = pack2<WT>(o[2 * pi] - dec_lo<WT>(hv[pi]), o[2 * pi + 1] - dec_hi<WT>(hv[pi]));
+                if constexpr (WT == DT_F16) range_ok = range_ok && fmaxf(fabsf(o[2 * pi]), fabsf(o[2 * pi + 1])) <= 65504.0f;
+            }
+            *reinterpret_cast<u32x4 *>(cx.xs + row * K + col) = u32x4{hv[0], hv[1], hv[2], hv[3]};
+            *reinterpret_cast<u32x4 *>(cx.xs + LayCtx<WT, M>::PLANE + row * K + col) = u32x4{lv[0], lv[1], lv[2], lv[3]};
+            if (write_out) {  // the user's row stride may be any number of floats
+                float *y = item.y + static_cast<size_t>(row) * item.ldy + col;
+#pragma unroll
+                for (uint32_t d2 = 0; d2 < 8; d2++) y[d2] = o[d2];
+            }
         }
     }
     if (!range_ok) raise_flag(cx.sync, SYNC_RANGE);
@@ -752,6 +806,7 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
     X cx;
     cx.xs = xs;
     cx.qs = nullptr;
+    cx.rope = nullptr;
     cx.part[LC_QKV] = p_qkv;
     cx.part[LC_O] = p_o;
     cx.part[LC_GU] = p_gu;
@@ -893,6 +948,7 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
     typedef LCls<LC_FF2, M> LD;
     __shared__ __attribute__((aligned(16))) uint16_t xs[2 * X::PLANE];
     __shared__ __attribute__((aligned(16))) float qs[M * DIT_QKV];
+    __shared__ float rope[2 * 32 * DitAtt<M>::S];
     __shared__ __attribute__((aligned(16))) float p_q[LQ::PART];
     __shared__ __attribute__((aligned(16))) float p_o[LO::PART];
     __shared__ __attribute__((aligned(16))) float p_f[LF::PART];
@@ -904,6 +960,7 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
     X cx;
     cx.xs = xs;
     cx.qs = qs;
+    cx.rope = rope;
     cx.part[LQ::SLOT] = p_q;
     cx.part[LO::SLOT] = p_o;
     cx.part[LF::SLOT] = p_f;
@@ -961,7 +1018,16 @@ __global__ __launch_bounds__(LAY_THREADS) void dit_block_kernel(const SeqOp *__r
     cx.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(tags), 0, static_cast<int>(tag_bytes), BUF_DWORD3);
     // The attention's rotation table (every item shares the first one's frequencies and scale).
     const SeqOp &a0 = ops[1];
-    dit_rope_table(gld(a0.inv_freq + (cx.tid & 31)), DitAtt<M>::S, cx.rc, cx.rs);
+    if (cx.tid < 32) {  // pair tid
+        float c[DIT_MAXS], sn[DIT_MAXS];
+        constexpr uint32_t S = DitAtt<M>::S;
+        dit_rope_table(gld(a0.inv_freq + cx.tid), S, c, sn);
+#pragma unroll
+        for (uint32_t j = 0; j < S; j++) {
+            rope[cx.tid * S + j] = c[j];
+            rope[(32 + cx.tid) * S + j] = sn[j];
+        }
+    }
     cx.ascale = a0.eps;
 
     u32x4 PQ[LQ::TA], PO[LO::TA], PF[LF::TA], PD[LD::TA];

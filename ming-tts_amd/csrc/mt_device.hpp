@@ -89,6 +89,18 @@ __device__ __forceinline__ float octet_sum(float v) {
     return v + dpp_mov<0x141>(v);  // row_half_mirror
 }
 
+// octet_sum of n values at once, value by value the same steps, so the n sums' DPP steps
+// overlap.
+template <int N>
+__device__ __forceinline__ void octet_sums(float *v) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_mov<0xB1>(v[i]);  // quad_perm [1, 0, 3, 2]
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_mov<0x4E>(v[i]);  // quad_perm [2, 3, 0, 1]
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_mov<0x141>(v[i]);  // row_half_mirror
+}
+
 // NeoX rotation of the pair (x0, x1) by the angle whose cosine and sine are c and s: r0 =
 // x0 c - x1 s, r1 = x1 c + x0 s, with the contraction written out (the product x0 c or x1 c
 // rounded, then one fused multiply-add), so every kernel that rotates a pair gets its bits.
