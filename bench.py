@@ -627,8 +627,9 @@ def flow_step_graph(torch, mt, dev, fused=True, persistent=False):
     weights ~ N(0, 0.02^2), captured in a HIP graph on its own stream.  With ``fused`` each
     block's attention runs inside its out projection (mt_dit_attention_linear): 342 launches.
     With ``persistent`` each ODE step's 8 blocks are one launch of the DiT-block kernel
-    (mt_seq_create_items with DiT attention items): 32 launches, run on the stream (a
-    cooperative launch is not captured), so `graph` is then the stage's function.
+    (mt_seq_create_items with DiT attention items): 32 launches, run on the stream (with
+    --seq-launch coop the sequence launch is cooperative, which a graph does not capture; an
+    ordinary one times the same either way), so `graph` is then the stage's function.
     Returns (graph, stream, launches, weight bytes per ODE step, the tensors to keep alive)."""
     HID, HEADS, LAT, BLOCKS, STEPS = 1024, 16, 64, 8, 10
     g = torch.Generator(device=dev)
@@ -802,8 +803,8 @@ def aggregator_stage(torch, mt, dev, persistent=False):
 
 def bench_aggregator(torch, mt, dev, reps=5, persistent=False):
     """The aggregator stage (aggregator_stage): as a HIP graph of 35 launches replayed, or, with
-    ``persistent``, 4 launches run on the stream (a cooperative launch is not captured), the
-    median of `reps` runs between HIP events."""
+    ``persistent``, 4 launches run on the stream (as flow_step_graph runs its persistent
+    stage), the median of `reps` runs between HIP events."""
     stage_fn, seq, launches, wbytes = aggregator_stage(torch, mt, dev, persistent)
     cs = torch.cuda.Stream(device=dev)
 
@@ -951,8 +952,8 @@ def vae_latent_seq_stage(torch, mt, dev, ws):
 
 def bench_vae_latent_seq(torch, mt, dev, ws, reps=7):
     """The VAE latent of bench_vae_latent with its 24-layer stack as one persistent launch
-    (vae_latent_seq_stage): 5 launches on one stream (the cooperative launch is not captured
-    in a graph), timed with HIP events on it."""
+    (vae_latent_seq_stage): 5 launches on one stream (as flow_step_graph runs its persistent
+    stage), timed with HIP events on it."""
     HOP = 882
     run, seq = vae_latent_seq_stage(torch, mt, dev, ws)
     cs = torch.cuda.Stream(device=dev)
@@ -1039,12 +1040,13 @@ def bench_generation_step(torch, mt, dev, ws, reps=5):
             them beside the llm token on a concurrent encoder (Engine.swift:383-384), so its
             "llm" figure covers both; here they run one after the other;
       flow: the cond embedder and 10 EPSS ODE steps of the 8-block DiT at M = 6
-            (flow_step_graph, a HIP graph of 342 launches);
+            (flow_step_graph, persistent: each ODE step's 8 blocks one DiT-block kernel launch,
+            32 launches);
       agg:  the aggregator with its 8 DiT blocks as one launch (aggregator_stage).
     The median of `reps` runs per stage, after one untimed run."""
     llm, llm_seq = llm_token_stage(torch, mt, dev, ws)
     vae, vae_seq = vae_latent_seq_stage(torch, mt, dev, ws)
-    flow_graph, cs, flow_launches, _, flow_keep = flow_step_graph(torch, mt, dev, fused=True)
+    flow, cs, flow_launches, _, flow_keep = flow_step_graph(torch, mt, dev, fused=True, persistent=True)
     agg, agg_seq, agg_launches, _ = aggregator_stage(torch, mt, dev, persistent=True)
     s = cs.cuda_stream
     names = ("llm", "vae", "flow", "agg")
@@ -1057,7 +1059,7 @@ def bench_generation_step(torch, mt, dev, ws, reps=5):
             ev[1].record(cs)
             vae(s)
             ev[2].record(cs)
-            flow_graph.replay()
+            flow()
             ev[3].record(cs)
             agg(s)
             ev[4].record(cs)
@@ -1065,7 +1067,7 @@ def bench_generation_step(torch, mt, dev, ws, reps=5):
             if r:
                 for j, n in enumerate(names):
                     times[n].append(1e3 * ev[j].elapsed_time(ev[j + 1]))
-    for q in (llm_seq, vae_seq, agg_seq):
+    for q in (llm_seq, vae_seq, agg_seq, flow_keep[-1]):
         q.check()
         q.close()
     med = {n: sorted(t)[len(t) // 2] for n, t in times.items()}
@@ -1077,7 +1079,7 @@ def bench_generation_step(torch, mt, dev, ws, reps=5):
                            "total": REF_STEP_US["total"],
                            "source": "Apple M-series GPU, .claude/skills/verify/features/bench.md:25"}
     out["llm_rows"] = 1
-    del flow_graph, flow_keep
+    del flow, flow_keep
     return out
 
 
@@ -1234,9 +1236,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--seq-launch", choices=["coop", "plain"], default="coop",
-                    help="launch of the persistent decode kernel: cooperative (default) or ordinary "
-                         "(for profilers that cannot follow a cooperative launch)")
+    ap.add_argument("--seq-launch", choices=["coop", "plain"], default="plain",
+                    help="launch of the persistent sequence kernels: ordinary (the library's default) "
+                         "or cooperative (co-residency guaranteed, about 17 us later per launch)")
     ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention", "flow",
                                        "step", "refshapes"],
                     default="all",
@@ -1265,8 +1267,7 @@ def main() -> int:
     if args.only == "copy":
         print(json.dumps(bench_copy(torch, dev)), flush=True)
         return 0
-    if args.seq_launch == "plain":
-        mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 1)
+    mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 1 if args.seq_launch == "plain" else 0)
     log("generating 24 layers of fp16 weights")
     ws = make_layers(torch, dev)
     torch.cuda.synchronize()
@@ -1416,6 +1417,9 @@ def main() -> int:
                                  for k, v in bench_dit(torch, mt, dev, cold=True).items()}
         log("flow stage of one generation step (10 ODE steps, 8 DiT blocks, graph replay)")
         line["flow_step"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in bench_flow_step(torch, mt, dev).items()}
+        log("flow stage as one DiT-block kernel launch per ODE step")
+        line["flow_step_persistent"] = {k: (round(v, 3) if isinstance(v, float) else v)
+                                        for k, v in bench_flow_step(torch, mt, dev, persistent=True).items()}
         line["flow_step_separate_attention"] = {k: (round(v, 3) if isinstance(v, float) else v)
                                                 for k, v in bench_flow_step(torch, mt, dev, fused=False).items()}
         log("aggregator stage of one generation step (8 DiT blocks at M = 2, graph replay)")

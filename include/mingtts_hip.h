@@ -169,8 +169,11 @@ enum {
     MT_TUNE_GEMV_LANES = 2,      /* lanes per output feature in the GEMV, 8..64 (0 = auto) */
     MT_TUNE_GEMM_SPLITK = 3,     /* K splits of the pipelined MFMA GEMM (0 = auto) */
     MT_TUNE_SEQ_GROUPS = 4,      /* workgroups of the persistent sequence kernel (0 = auto) */
-    MT_TUNE_SEQ_LAUNCH = 5,      /* 0: cooperative launch (default); 1: ordinary launch, co-residency
-                                    then rests on an otherwise idle device (profilers) */
+    MT_TUNE_SEQ_LAUNCH = 5,      /* 0: cooperative launch; 1: ordinary launch (default), about 17 us
+                                    sooner per launch on MI355X; its workgroups (one a CU) are
+                                    co-resident while no other kernel holds CUs, as on a device
+                                    that runs one stream; a shortfall ends in the bounded waits'
+                                    timeout flag (mt_seq_check), never a hang */
     MT_TUNE_GEMM_TILE = 6,       /* MFMA GEMM tile (x rows x weight rows) for fp32 activations and
                                     activations of the weights' type: 0 = auto, 1 = 128 x 128,
                                     2 = 64 x 128, 3 = 64 x 64, 4 = the register-staged 64 x 64 kernel

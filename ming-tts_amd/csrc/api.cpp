@@ -135,7 +135,7 @@ int mt_set_tuning(int key, int value) {
         case MT_TUNE_GEMV_LANES: slot = &g_tuning.gemv_lanes; def = 0; break;
         case MT_TUNE_GEMM_SPLITK: slot = &g_tuning.gemm_splitk; def = 0; break;
         case MT_TUNE_SEQ_GROUPS: slot = &g_tuning.seq_groups; def = 0; break;
-        case MT_TUNE_SEQ_LAUNCH: slot = &g_tuning.seq_launch; def = 0; break;
+        case MT_TUNE_SEQ_LAUNCH: slot = &g_tuning.seq_launch; def = 1; break;
         case MT_TUNE_GEMM_TILE: slot = &g_tuning.gemm_tile; def = 0; break;
         case MT_TUNE_GEMM_STAGES: slot = &g_tuning.gemm_stages; def = 0; break;
         case MT_TUNE_GEMV_MFMA: slot = &g_tuning.gemv_mfma; def = 0; break;

@@ -30,7 +30,7 @@ struct Tuning {
     std::atomic<int> gemm_stages{0};
     std::atomic<int> gemv_mfma{0};
     std::atomic<int> seq_groups{0};
-    std::atomic<int> seq_launch{0};
+    std::atomic<int> seq_launch{1};
     std::atomic<int> seq_layer{0};
 };
 Tuning &tuning();

@@ -113,8 +113,8 @@ def test_kernel_choice_and_tuning_round_trip():
     assert mt.load().mt_set_tuning(99, 0) == mt.EINVAL
     assert mt.load().mt_set_tuning(mt.TUNE_GEMV_ROWS_MAX, 9) == mt.EINVAL
     assert mt.load().mt_set_tuning(mt.TUNE_SEQ_LAUNCH, 2) == mt.EINVAL
-    assert mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 1) == 0
-    assert mt.set_tuning(mt.TUNE_SEQ_LAUNCH, -1) == 1
+    assert mt.set_tuning(mt.TUNE_SEQ_LAUNCH, 0) == 1   # the ordinary launch is the default
+    assert mt.set_tuning(mt.TUNE_SEQ_LAUNCH, -1) == 0
 
 
 def test_seq_create_validates_every_op_before_the_device():

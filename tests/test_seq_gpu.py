@@ -347,8 +347,8 @@ def test_seq_flags_activations_beyond_fp16_range(gpu):
 
 
 def test_seq_ordinary_launch_matches_cooperative(gpu):
-    """The ordinary-launch mode (for profilers) runs the same plan to the same bits on an idle
-    device."""
+    """The cooperative launch and the ordinary one (the default) run the same plan to the same
+    bits on an idle device."""
     layers, M = 2, 2
     ws, x0 = make_stack(layers, M, 8, gpu)
     resid, qkv, mlp = buffers(M, x0, gpu)
