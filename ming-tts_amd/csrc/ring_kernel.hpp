@@ -20,10 +20,14 @@
 //     4-7 steps 2-3 (the other wave of a SIMD hides a wave's LDS reads).  Wave w owns x rows
 //     32 (w & 3) .. + 31 against all 192 weight rows: six 32 x 32 accumulators on
 //     v_mfma_f32_32x32x16, the gate and up sums of a feature in the same lane.  After the loop
-//     the second group hands its sums to the first through LDS (a fixed order: first + second).
+//     the two groups swap halves of their sums through LDS (added in a fixed order: first group
+//     + second), so all eight waves run the epilogue.
 //   - The epilogue runs from registers: lane l holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
 //     of each block, so each store writes two 128-byte row segments.  The old y (accumulate) is
-//     requested while the groups' sums meet.
+//     requested while the groups' sums meet.  A wave issues about one instruction every four
+//     cycles, so the epilogue's instruction count is its time: the flags are branched on once,
+//     not per output, and SiLU takes the hardware exp2 and reciprocal (8.1 -> 2.2 us of a 24 us
+//     launch at M = 512).
 //   - Rows past M or N and k past K are loaded from a zero block; rows past M or N are not
 //     stored.  The workgroup -> tile order gives each XCD a contiguous run of tiles (the x-row
 //     tiles of one weight tile first), which share weight rows in that XCD's L2.
@@ -63,6 +67,104 @@ __device__ __forceinline__ void bar() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// The epilogue of rarer flag sets (GELU or SiLU after the gate), out of line: inlined 24 times
+// it would multiply the code the common path runs past.
+__device__ __attribute__((noinline)) float epilogue_out_of_line(float acc, float acc2, float b, uint32_t flags) {
+    return epilogue(acc, acc2, b, flags);
+}
+
+// SiLU(g) u = g u / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal (each within 1 ulp):
+// six instructions where expf and an IEEE division take about thirty.
+__device__ __forceinline__ float silu_gate(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
+// The second half of the kernel for k group KH (see the call site): the hand-over through LDS,
+// the epilogue and the stores.  Rows past M or features past N are neither read nor stored.
+template <int WT, int KH>
+__device__ __forceinline__ void finish(const RingArgs &a, const f32x16t (&acc)[WNT], uint8_t *lds, int wm, int lane,
+                                       uint32_t m0, uint32_t n0, const float (&bv)[WNT / 2]) {
+    const int fr = lane & 31, fh = lane >> 5;
+    const uint32_t M = a.M, N = a.N, flags = a.flags;
+    // Accumulator register r of this group's half is x row mb + 8 (r / 4) + r % 4.
+    const uint32_t mb = m0 + 32 * wm + 16 * KH + 4 * fh;
+    // The old y of this half's outputs (accumulate), requested before the hand-over.
+    float yo[8][WNT / 2];
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+#pragma unroll
+        for (int p = 0; p < WNT / 2; p++) yo[r][p] = 0.0f;
+    if (flags & F_ACCUM) {
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const uint32_t m = mb + 8 * (r >> 2) + (r & 3);
+#pragma unroll
+            for (int p = 0; p < WNT / 2; p++) {
+                const uint32_t n = n0 + 32 * p + fr;
+                if (m < M && n < N) yo[r][p] = a.y[static_cast<size_t>(m) * a.ldy + n];
+            }
+        }
+    }
+    // Hand-over area: [wave & 3][giving group][block][register quad of the half][lane] float4.
+    float *red = reinterpret_cast<float *>(lds);
+    auto slot = [&](int giver, int j, int q) { return red + ((((wm * 2 + giver) * WNT + j) * 2 + q) * 64 + lane) * 4; };
+    bar();  // every wave is done with the ring
+    constexpr int GIVE = 8 * (1 - KH), KEEP = 8 * KH;
+#pragma unroll
+    for (int j = 0; j < WNT; j++)
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+            *reinterpret_cast<f32x4t *>(slot(KH, j, q)) = f32x4t{acc[j][GIVE + 4 * q], acc[j][GIVE + 4 * q + 1],
+                                                                 acc[j][GIVE + 4 * q + 2], acc[j][GIVE + 4 * q + 3]};
+    bar();
+    // The sums in a fixed order, group 0's part first.
+    float sm[WNT][8];
+#pragma unroll
+    for (int j = 0; j < WNT; j++)
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const f32x4t v = *reinterpret_cast<const f32x4t *>(slot(1 - KH, j, q));
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float own = acc[j][KEEP + 4 * q + e];
+                sm[j][4 * q + e] = KH == 0 ? own + v[e] : v[e] + own;
+            }
+        }
+    float out[8][WNT / 2];
+    if ((flags & (F_GELU | F_SILU)) == 0) {
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+#pragma unroll
+            for (int p = 0; p < WNT / 2; p++) out[r][p] = silu_gate(sm[2 * p][r] + bv[p], sm[2 * p + 1][r]) + yo[r][p];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+#pragma unroll
+            for (int p = 0; p < WNT / 2; p++)
+                out[r][p] = epilogue_out_of_line(sm[2 * p][r], sm[2 * p + 1][r], bv[p], flags) + yo[r][p];
+    }
+    if (m0 + BM <= M && n0 + FN <= N) {
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            float *yr = a.y + static_cast<size_t>(mb + 8 * (r >> 2) + (r & 3)) * a.ldy + n0 + fr;
+#pragma unroll
+            for (int p = 0; p < WNT / 2; p++) yr[32 * p] = out[r][p];
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const uint32_t m = mb + 8 * (r >> 2) + (r & 3);
+            float *yr = a.y + static_cast<size_t>(m) * a.ldy;
+#pragma unroll
+            for (int p = 0; p < WNT / 2; p++) {
+                const uint32_t n = n0 + 32 * p + fr;
+                if (m < M && n < N) yr[n] = out[r][p];
+            }
+        }
+    }
 }
 
 template <int WT>
@@ -181,53 +283,16 @@ __global__ __launch_bounds__(NT) void ring_gated_kernel(RingArgs a) {
         }
     }
 
-    // The old y of this lane's outputs (accumulate), requested before the hand-over.
-    const bool accum = (flags & F_ACCUM) != 0;
-    float yo[16][WNT / 2];
-    if (kh == 0 && accum) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const uint32_t m = m0 + 32 * wm + 8 * (r >> 2) + 4 * fh + (r & 3);
-#pragma unroll
-            for (int p = 0; p < WNT / 2; p++) {
-                const uint32_t n = n0 + 32 * p + fr;
-                yo[r][p] = (m < M && n < N) ? a.y[static_cast<size_t>(m) * a.ldy + n] : 0.0f;
-            }
-        }
-    }
-    // k group 1 hands its sums to group 0 through LDS ([wave & 3][block][reg quad][lane] float4).
-    bar();  // every wave is done with the ring
-    float *red = reinterpret_cast<float *>(lds);
-    if (kh == 1) {
-#pragma unroll
-        for (int j = 0; j < WNT; j++)
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-                *reinterpret_cast<f32x4t *>(red + (((wm * WNT + j) * 4 + u) * 64 + lane) * 4) =
-                    f32x4t{acc[j][4 * u], acc[j][4 * u + 1], acc[j][4 * u + 2], acc[j][4 * u + 3]};
-    }
-    bar();
-    if (kh == 1) return;
-#pragma unroll
-    for (int j = 0; j < WNT; j++)
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const f32x4t v = *reinterpret_cast<const f32x4t *>(red + (((wm * WNT + j) * 4 + u) * 64 + lane) * 4);
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[j][4 * u + e] += v[e];
-        }
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const uint32_t m = m0 + 32 * wm + 8 * (r >> 2) + 4 * fh + (r & 3);
-        float *yr = a.y + static_cast<size_t>(m) * a.ldy;
-#pragma unroll
-        for (int p = 0; p < WNT / 2; p++) {
-            const uint32_t n = n0 + 32 * p + fr;
-            float v = epilogue(acc[2 * p][r], acc[2 * p + 1][r], bv[p], flags);
-            if (accum) v += yo[r][p];
-            if (m < M && n < N) yr[n] = v;
-        }
-    }
+    // The two k groups' sums meet through LDS, each group finishing half of the accumulator
+    // registers: group kh keeps registers 8 kh .. 8 kh + 7 of every block (x rows 16 kh .. +15
+    // of its 32-row block) and hands the other half to its partner wave.  Both groups then run
+    // the epilogue, 24 outputs a lane.  kh becomes a compile-time constant through the two
+    // instantiations of `finish`, so every register index stays a constant (a kh-dependent index
+    // turns into select chains over all 16 registers).
+    if (kh == 0)
+        finish<WT, 0>(a, acc, lds, wm, lane, m0, n0, bv);
+    else
+        finish<WT, 1>(a, acc, lds, wm, lane, m0, n0, bv);
 }
 
 typedef void (*ring_fn)(RingArgs);
