@@ -75,6 +75,67 @@ __device__ __forceinline__ float epilogue(float acc, float acc2, float b, uint32
     return v;
 }
 
+// The epilogue with its flag set FL fixed at compile time, for kernels that branch on the flags
+// once rather than per output.  SiLU and tanh go through the hardware exp2 and reciprocal (each
+// within 1 ulp): silu(v) = v / (1 + 2^(-v log2 e)), tanh(u) = 1 - 2 / (1 + 2^(2 u log2 e)), a
+// few instructions where expf, tanhf and IEEE division take tens.  Their results differ from
+// epilogue()'s by a few ulp.
+__device__ __forceinline__ float silu_hw(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
+}
+__device__ __forceinline__ float gelu_hw(float x) {
+    const float k = 0.7978845608028654f;
+    float u = k * (x + 0.044715f * x * x * x);
+    u = fminf(fmaxf(u, -15.0f), 15.0f);
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * 2.8853900817779268f));
+    return 0.5f * x * (1.0f + t);
+}
+template <uint32_t FL>
+__device__ __forceinline__ float epilogue_fixed(float acc, float acc2, float b) {
+    float v = acc;
+    if constexpr ((FL & F_BIAS) != 0) v += b;
+    if constexpr ((FL & F_SILU_GATE) != 0) v = silu_hw(v) * acc2;
+    if constexpr ((FL & F_GELU) != 0) v = gelu_hw(v);
+    if constexpr ((FL & F_SILU) != 0) v = silu_hw(v);
+    return v;
+}
+
+// The flag sets the GEMM kernels specialise (every combination of bias, accumulate and the SiLU
+// gate, and bias with GELU); any other set takes the out-of-line epilogue.
+constexpr uint32_t EPI_OTHER = 0x80000000u;
+template <uint32_t V>
+struct FlagSet {
+    static constexpr uint32_t value = V;
+};
+template <typename F>
+__device__ __forceinline__ void with_flag_set(uint32_t flags, F &&f) {
+    switch (flags) {
+        case 0: f(FlagSet<0>{}); break;
+        case F_BIAS: f(FlagSet<F_BIAS>{}); break;
+        case F_ACCUM: f(FlagSet<F_ACCUM>{}); break;
+        case F_BIAS | F_ACCUM: f(FlagSet<F_BIAS | F_ACCUM>{}); break;
+        case F_SILU_GATE: f(FlagSet<F_SILU_GATE>{}); break;
+        case F_SILU_GATE | F_BIAS: f(FlagSet<F_SILU_GATE | F_BIAS>{}); break;
+        case F_SILU_GATE | F_ACCUM: f(FlagSet<F_SILU_GATE | F_ACCUM>{}); break;
+        case F_GELU | F_BIAS: f(FlagSet<F_GELU | F_BIAS>{}); break;
+        default: f(FlagSet<EPI_OTHER>{}); break;
+    }
+}
+__device__ __attribute__((noinline)) inline float epilogue_out_of_line(float acc, float acc2, float b, uint32_t flags) {
+    return epilogue(acc, acc2, b, flags);
+}
+// Epilogue of flag set FL (EPI_OTHER: the runtime flags, out of line), without the accumulate.
+template <uint32_t FL>
+__device__ __forceinline__ float epilogue_set(float acc, float acc2, float b, uint32_t flags) {
+    if constexpr (FL == EPI_OTHER) return epilogue_out_of_line(acc, acc2, b, flags & ~F_ACCUM);
+    else return epilogue_fixed<FL>(acc, acc2, b);
+}
+template <uint32_t FL>
+__device__ __forceinline__ bool accumulates(uint32_t flags) {
+    if constexpr (FL == EPI_OTHER) return (flags & F_ACCUM) != 0;
+    else return (FL & F_ACCUM) != 0;
+}
+
 // One DPP lane move (quad permutes, row shifts and mirrors) of a float.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {

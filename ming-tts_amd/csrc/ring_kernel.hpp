@@ -69,19 +69,6 @@ __device__ __forceinline__ void bar() {
     asm volatile("" ::: "memory");
 }
 
-// The epilogue of rarer flag sets (GELU or SiLU after the gate), out of line: inlined 24 times
-// it would multiply the code the common path runs past.
-__device__ __attribute__((noinline)) float epilogue_out_of_line(float acc, float acc2, float b, uint32_t flags) {
-    return epilogue(acc, acc2, b, flags);
-}
-
-// SiLU(g) u = g u / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal (each within 1 ulp):
-// six instructions where expf and an IEEE division take about thirty.
-__device__ __forceinline__ float silu_gate(float g, float u) {
-    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
-    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
-}
-
 // The second half of the kernel for k group KH (see the call site): the hand-over through LDS,
 // the epilogue and the stores.  Rows past M or features past N are neither read nor stored.
 template <int WT, int KH>
@@ -138,7 +125,7 @@ __device__ __forceinline__ void finish(const RingArgs &a, const f32x16t (&acc)[W
 #pragma unroll
         for (int r = 0; r < 8; r++)
 #pragma unroll
-            for (int p = 0; p < WNT / 2; p++) out[r][p] = silu_gate(sm[2 * p][r] + bv[p], sm[2 * p + 1][r]) + yo[r][p];
+            for (int p = 0; p < WNT / 2; p++) out[r][p] = silu_hw(sm[2 * p][r] + bv[p]) * sm[2 * p + 1][r] + yo[r][p];
     } else {
 #pragma unroll
         for (int r = 0; r < 8; r++)

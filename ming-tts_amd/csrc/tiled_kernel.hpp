@@ -648,37 +648,49 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
 
     // Epilogue from the fp32 tile: consecutive threads take consecutive features of a row, so
     // a thread keeps one feature (its bias requested at entry) over rows tid / FN + (NT / FN) i.
-    // The old y of all its rows is requested before the first is used (lanes past M or N
-    // read y[0]).
+    // The old y of all its rows is requested before the first is used.  The flags are branched
+    // on once (with_flag_set), and a tile inside M x N stores without per-row checks: a wave
+    // issues about one instruction every four cycles, so per-output branches cost microseconds.
     constexpr int EPT = BM * FN / NT, MSTEP = NT / FN;
-    const uint32_t flags = a.flags;
     const int n = en, mr = tid / FN;
     const uint32_t gn = egn;
-    const bool nok = enok;
-    float yo[EPT];
-    if (flags & F_ACCUM) {
+    const bool full = m0 + BM <= M && n0 + FN <= N;
+    const uint32_t flags = a.flags;
+    with_flag_set(flags, [&](auto set) {
+        constexpr uint32_t FL = decltype(set)::value;
+        const bool accum = accumulates<FL>(flags);
+        float yo[EPT];
+#pragma unroll
+        for (int i = 0; i < EPT; i++) yo[i] = 0.0f;
+        if (accum) {  // lanes past M or N read y[0]
+#pragma unroll
+            for (int i = 0; i < EPT; i++) {
+                const uint32_t gm = m0 + mr + MSTEP * i;
+                yo[i] = a.y[full || (gm < M && enok) ? static_cast<size_t>(gm) * a.ldy + gn : 0u];
+            }
+        }
+        float v[EPT];
 #pragma unroll
         for (int i = 0; i < EPT; i++) {
-            const uint32_t gm = m0 + mr + MSTEP * i;
-            yo[i] = a.y[gm < M && nok ? static_cast<size_t>(gm) * a.ldy + gn : 0u];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < EPT; i++) {
-        const int m = mr + MSTEP * i;
-        const uint32_t gm = m0 + m;
-        if (gm < M && nok) {
+            const int m = mr + MSTEP * i;
             float c = ctile[m * CLD + n];
             float c2 = GATED ? ctile[(BM + m) * CLD + n] : 0.0f;
             if constexpr (NORM) {
                 c *= row_ss[m];  // the row's scale by now
                 c2 *= row_ss[m];
             }
-            float v = epilogue(c, c2, bv, flags);
-            if (flags & F_ACCUM) v += yo[i];
-            a.y[static_cast<size_t>(gm) * a.ldy + gn] = v;
+            v[i] = epilogue_set<FL>(c, c2, bv, flags) + yo[i];
         }
-    }
+        float *yc = a.y + static_cast<size_t>(m0 + mr) * a.ldy + gn;
+        if (full) {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) yc[static_cast<size_t>(MSTEP * i) * a.ldy] = v[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < EPT; i++)
+                if (m0 + mr + MSTEP * i < M && enok) yc[static_cast<size_t>(MSTEP * i) * a.ldy] = v[i];
+        }
+    });
 }
 
 typedef void (*tiled_fn)(TiledArgs);
