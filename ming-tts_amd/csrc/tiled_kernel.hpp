@@ -101,6 +101,14 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Workgroup barrier that waits only for this wave's LDS reads (lgkmcnt), not for its loads in
+// flight: __syncthreads adds a fence that the compiler may turn into vmcnt(0).
+__device__ __forceinline__ void tiled_bar() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Workgroup id -> tile order with a contiguous run of ids per XCD (ids are dealt to the
 // 8 XCDs round-robin).
 __device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t G) {
@@ -500,26 +508,69 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
         }
     } else {
         // Stages s + 1 .. s + P - 2 are in flight (or landed) while stage s is multiplied from
-        // registers; stage s + 1's fragments are read from LDS meanwhile.
+        // registers; stage s + 1's fragments are read from LDS meanwhile.  A wave issues about
+        // one instruction every four cycles and a branch costs more, so the steady state (every
+        // iteration issues a stage) runs without conditions: exact waits, direct-load addresses
+        // that step by a fixed stride (rows past M or N step by 0 on the zero block; only a K
+        // tail takes the checked issue), and the two fragment sets alternating by unrolling
+        // instead of being copied.
+        const char *gp[LPW];
+        uint32_t gstride[LPW];
+#pragma unroll
+        for (int i = 0; i < LPW; i++) {
+            gp[i] = rowok[i] ? src[i] : zero;
+            gstride[i] = rowok[i] ? 2u * TBK : 0u;
+        }
+        const uint32_t ldsw = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
+        const bool ktail = (K % TBK) != 0;
+        auto issue_step = [&](uint32_t buf, uint32_t kstep) {
+            if (ktail && kstep + 1 == KT) {
+                issue(buf, kstep);
+                return;
+            }
+#pragma unroll
+            for (int i = 0; i < LPW; i++) dma16(ldsw + buf * SB + NW * i * 1024, gp[i] + static_cast<size_t>(gstride[i]) * kstep);
+        };
 #pragma unroll
         for (int i = 0; i < P - 1; i++)
-            if (static_cast<uint32_t>(i) < nsteps) issue(i, ks0 + i);
+            if (static_cast<uint32_t>(i) < nsteps) issue_step(i, ks0 + i);
         wait_pending(min(static_cast<uint32_t>(P - 2), nsteps - 1));
         __syncthreads();
-        Frags cur, nxt;
-        load(cur, 0);
-        uint32_t buf = 0;  // buffer of stage s
-        for (uint32_t s = 0; s < nsteps; s++) {
-            const uint32_t nb = buf + 1 == P ? 0 : buf + 1;
-            if (s + 1 < nsteps) {
-                wait_pending(min(s + P - 2, nsteps - 1) - (s + 1));
-                __syncthreads();  // stage s + 1 is in; every wave is done reading stage s - 1's buffer
-                if (s + P - 1 < nsteps) issue(buf == 0 ? P - 1 : buf - 1, ks0 + s + P - 1);
-                load(nxt, nb);
-            }
+        Frags fa, fb;
+        load(fa, 0);
+        // Iteration s: stage s + 1 is in once at most P - 3 later stages are in flight; the barrier
+        // also tells that every wave is done reading stage s - 1's buffer, which takes stage
+        // s + P - 1.
+        uint32_t s = 0, bs = 0;  // bs: buffer of stage s
+        auto steady = [&](Frags &cur, Frags &nxt) {
+            const uint32_t b1 = bs + 1 == P ? 0 : bs + 1, bi = bs == 0 ? P - 1 : bs - 1;
+            wait_vm<(P - 3) * LPW>();
+            tiled_bar();
+            issue_step(bi, ks0 + s + P - 1);
+            load(nxt, b1);
             mma(cur);
-            cur = nxt;
-            buf = nb;
+            bs = b1;
+            s++;
+        };
+        while (s + P < nsteps) {  // two steady iterations
+            steady(fa, fb);
+            steady(fb, fa);
+        }
+        if (s + P - 1 < nsteps) {
+            steady(fa, fb);
+            fa = fb;
+        }
+        // The last P - 1 stages: nothing left to issue.
+        for (; s < nsteps; s++) {
+            const uint32_t b1 = bs + 1 == P ? 0 : bs + 1;
+            if (s + 1 < nsteps) {
+                wait_pending(nsteps - 1 - (s + 1));
+                tiled_bar();
+                load(fb, b1);
+            }
+            mma(fa);
+            fa = fb;
+            bs = b1;
         }
     }
     if constexpr (NACC == 2) {
