@@ -251,22 +251,48 @@ __global__ __launch_bounds__(NT) void ring_gated_kernel(RingArgs a) {
     }
 
     if (nsteps > 0) {
+        // Direct loads step by 128 bytes a stage from each lane's source row; a row past M or N
+        // reads row 0 instead of the zero block (its outputs are never stored), so only a K
+        // tail takes the checked issue, and an iteration costs a few uniform branches instead
+        // of per-load selects (a wave issues about one instruction every four cycles).
+        const uint32_t ldsw = __builtin_amdgcn_readfirstlane(lds0 + wave * 1024);
+        const bool ktail = (K % 64) != 0;
+        auto issue_fast = [&](uint32_t s, uint32_t slot) {
+#pragma unroll
+            for (int i = 0; i < LPW; i++) tiled::dma16(ldsw + slot * SB + NW * i * 1024, src[i] + 128 * static_cast<size_t>(s));
+        };
+        // Stages below `fast_end` take the unchecked issue.
+        const uint32_t fast_end = ktail ? nsteps - 1 : nsteps;
 #pragma unroll
         for (int s = 0; s < NS; s++)
-            if (static_cast<uint32_t>(s) < nsteps) issue(s);
+            if (static_cast<uint32_t>(s) < nsteps) {
+                if (static_cast<uint32_t>(s) < fast_end) issue_fast(s, s);
+                else issue(s);
+            }
         wait_ahead(min(static_cast<uint32_t>(NS - 1), nsteps - 1));
         bar();
         Fr f;
         rd(f, 0);
+        // Iteration s: stage s + 1 is in once the stages after it are the only ones in flight;
+        // the barrier also tells that every wave has read stage s, whose slot takes stage s + NS.
+        // One call site of the MFMAs: with a second one (a peeled tail loop) the compiler gave
+        // the accumulators a second register set and spilled.
+        uint32_t slot = 0;  // slot of stage s
         for (uint32_t s = 0; s < nsteps; s++) {
+            const uint32_t next = slot + 1 == NS ? 0 : slot + 1;
             mma(f);
-            if (s + 1 < nsteps) {
-                // stages issued so far: 0 .. min(s + NS - 1, nsteps - 1)
-                wait_ahead(min(s + NS - 1, nsteps - 1) - (s + 1));
-                bar();  // stage s + 1 is in; every wave has read stage s, whose slot takes s + NS
-                if (s + NS < nsteps) issue(s + NS);
-                rd(f, (s + 1) % NS);
+            if (s + NS < nsteps) {
+                tiled::wait_vm<(NS - 2) * LPW>();
+                bar();
+                if (s + NS < fast_end) issue_fast(s + NS, slot);
+                else issue(s + NS);
+                rd(f, next);
+            } else if (s + 1 < nsteps) {
+                wait_ahead(nsteps - 1 - (s + 1));
+                bar();
+                rd(f, next);
             }
+            slot = next;
         }
     }
 
