@@ -38,7 +38,10 @@ tiled_fn pick_tiled(int shape, int stages) {
 //     throughput comes from having one or two workgroups on every CU, not from deeper
 //     pipelines; a workgroup's fixed cost (first stage, epilogue) is about 3 us.
 //   - Not gated: 64 x 64 tiles, 4 stages (64 KB of LDS: two per CU); K is split only when it
-//     is long, into as many parts as keep about two workgroups per CU with >= 8 stages each.
+//     is long: parts of about 16 stages, or of 8 while the tiles alone fill under a third of the
+//     CUs, and at most two workgroups per CU (down, 896 x 4864, graph replay: at M = 256 4 parts
+//     take 12.5 us against 14.7 for 9, at M = 512 4 parts 16.0 against 16.9 for 2; at M = 64 6
+//     parts 11.0 against 11.3 for 4 and 11.7 for 9).
 //   - Gated: 64 x 128 tiles while M <= 64, else 128 x 128; with more tiles than CUs the
 //     double-buffered ring (68 KB) keeps two 128 x 128 workgroups on a CU.
 //   - fp32 activations (split): staged through registers into two LDS buffers, about 0.7 us
@@ -67,7 +70,8 @@ TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, in
     } else if (split) {
         S = std::max(1u, std::min(std::min(2 * ncu / std::max(tiles, 1u), std::max(KT / 4, 1u)), 8u));
     } else if (!gated) {
-        S = std::max(1u, std::min(2 * ncu / std::max(tiles, 1u), KT / 8));
+        const uint32_t t1 = std::max(tiles, 1u);
+        S = std::max(1u, std::min(2 * ncu / t1, std::max(KT / 16, std::min(KT / 8, ncu / (3 * t1)))));
     }
     S = std::max(1u, std::min(S, KT));
     p.kps = (KT + S - 1) / S;
