@@ -30,14 +30,16 @@
 //   - Waves 0-3 and 4-7 form two 2 x 2 grids over the tile, each wave (BM / 2) x (BN / 2);
 //     the first grid multiplies k 0-31 of every stage, the second k 32-63.  Two waves per
 //     SIMD hide each other's LDS reads, and each stage is read from LDS only twice.  The two
-//     grids' sums are added in LDS (first + second, a fixed order) into an fp32 tile that the
-//     epilogue reads row by row, so the stores are coalesced.
+//     grids swap halves of their sums through LDS (added first + second, a fixed order), and
+//     every wave runs the epilogue from its registers; each store covers two 128-byte row
+//     segments.
 //   - Split-K: when the output tiles alone cannot fill the chip, S workgroups share a tile's
-//     K range.  Each writes its fp32 tile to a per-stream workspace with device-coherent
-//     stores, waits for them, and counts itself in at the tile's counter; the workgroup that
-//     arrives last reads the other partial tiles device-coherently (all its loads in flight
-//     at once) and adds the S tiles in split order 0 .. S-1, so the result does not depend on
-//     arrival order.  It then runs the epilogue and re-arms the counter.
+//     K range.  Each writes its partial sums in register order (1 KB per store) to a
+//     per-stream workspace with device-coherent stores, waits for them, and counts itself in
+//     at the tile's counter; the workgroup that arrives last reads the other partials
+//     device-coherently (a batch of splits in flight at once) and adds the S parts in split
+//     order 0 .. S-1, so the result does not depend on arrival order.  It then runs the
+//     epilogue and re-arms the counter.
 //   - Workgroup -> tile order is XCD-aware: consecutive workgroup ids go to different XCDs, so
 //     the id is remapped to give each XCD a contiguous run of tiles (the x-row tiles of one
 //     weight tile first), which then share that XCD's L2.
@@ -49,6 +51,8 @@
 
 #include "mt_device.hpp"
 #include "mt_internal.hpp"
+
+#include <type_traits>
 
 namespace mt {
 namespace tiled {
@@ -165,9 +169,7 @@ struct TileShape {
     static constexpr int LPW = (SPLIT ? BN : BM + BN) / (8 * NW);
     static constexpr int IA = BM * 8 / NT;            // SPLIT: 8-k activation items per thread per stage
     static constexpr int FN = GATED ? 64 : BN;        // output features per tile
-    static constexpr int CLD = FN + 8;                // row stride of the fp32 tile in LDS
-    static constexpr int NCT = GATED ? 2 : 1;         // fp32 tile planes (gated: W and W2 sums)
-    static constexpr int NE = NCT * BM * FN;          // partial-tile elements
+    static constexpr int NE = (GATED ? 2 : 1) * BM * FN;  // partial-tile elements (gated: W and W2 sums)
 };
 // Floats of one split's partial tile in the workspace: the tile, then (normed) its rows'
 // partial sums of x^2.
@@ -183,10 +185,10 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     static_assert(!NORM || SPLIT, "a fused RMSNorm takes fp32 activations");
     typedef TileShape<BM, BN, GATED, KS, SPLIT> TS;
     constexpr int NT = TS::NT, NW = TS::NW, WMT = TS::WMT, WNT = TS::WNT, KKW = TS::KKW, NACC = TS::NACC;
-    constexpr int AR = TS::AR, SB = TS::SB, LPW = TS::LPW, IA = TS::IA, FN = TS::FN, CLD = TS::CLD, NE = TS::NE;
-    constexpr int CBYTES = TS::NCT * BM * CLD * 4;
+    constexpr int AR = TS::AR, SB = TS::SB, LPW = TS::LPW, IA = TS::IA, FN = TS::FN, NE = TS::NE;
+    constexpr int XBYTES = 8 * WMT * WNT * 2 * 64 * 16;  // the k grids' hand-over: [4][2][blocks][2] float4 a lane
     constexpr int NBUF = P == 1 ? 2 : P;  // LDS stages (P == 1: register-staged loads, two LDS buffers)
-    constexpr int LBYTES = NBUF * SB > CBYTES ? NBUF * SB : CBYTES;
+    constexpr int LBYTES = NBUF * SB > XBYTES ? NBUF * SB : XBYTES;
     static_assert(!GATED || BN == 128, "a gated tile is 64 features of W and W2");
     static_assert(LPW * 8 * NW == (SPLIT ? BN : BM + BN) && P >= 1 && P <= 4 && LBYTES <= 160 * 1024, "tile shape");
     static_assert(!SPLIT || (P == 1 && IA * NT == BM * 8), "split staging: two register-staged LDS buffers");
@@ -194,7 +196,6 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LBYTES];
     __shared__ uint32_t last_flag;
     __shared__ __attribute__((aligned(16))) float row_ss[NORM ? BM : 4];  // rows' sums of x^2, then scales (NORM)
-    float *ctile = reinterpret_cast<float *>(lds);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kh = wave >> 2, wm = wave & 1, wn = (wave >> 1) & 1;
@@ -207,13 +208,15 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     const uint32_t m0 = tm * BM;
     const uint32_t n0 = tn * FN;  // first output feature
     const uint32_t M = a.M, N = a.N, K = a.K;
-    // The epilogue's feature (a thread keeps one, see below) and its bias, requested now so
-    // the epilogue does not wait for it.
-    static_assert(NT % FN == 0, "a thread keeps one feature");
-    const int en = tid % FN;
-    const uint32_t egn = n0 + en;
-    const bool enok = egn < N;
-    const float bv = (a.flags & F_BIAS) ? dec1<WT>(a.bias[enok ? egn : 0u]) : 0.0f;
+    // The bias of the lane's output columns (see the epilogue), requested now so the epilogue
+    // does not wait for it: block column j covers features n0 + 32 (wn WNT + j) + lane % 32
+    // (gated: one column, n0 + 32 wn + lane % 32).
+    float bv[WNT];
+#pragma unroll
+    for (int j = 0; j < WNT; j++) {
+        const uint32_t n = n0 + (GATED ? 32 * wn : 32 * (wn * WNT + j)) + (lane & 31);
+        bv[j] = (a.flags & F_BIAS) && n < N ? dec1<WT>(a.bias[n]) : 0.0f;
+    }
     const uint32_t KT = (K + TBK - 1) / TBK;
     const uint32_t ks0 = split * a.kps;
     const uint32_t nsteps = min(ks0 + a.kps, KT) - ks0;
@@ -580,168 +583,191 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
             for (int j = 0; j < WNT; j++) acc[0][i][j] += acc[1][i][j];
     }
 
-    // The fp32 tile: with two k-half grids, the second stores and the first adds.
-    auto cidx = [&](int i, int j, int r) -> int {
-        const int m = 32 * (wm * WMT + i) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int plane = GATED ? j : 0;
-        const int n = (GATED ? 32 * wn : 32 * (wn * WNT + j)) + (lane & 31);
-        return (plane * BM + m) * CLD + n;
-    };
-    __syncthreads();  // the ring is no longer read; the fp32 tile overlays it
-    if (KS == 1 || kh == 1) {
+    // The two k grids' sums meet through LDS, each wave finishing half of its accumulator
+    // registers: the wave of grid kh keeps registers 8 kh .. 8 kh + 7 of every block (rows
+    // 16 kh .. 16 kh + 15 of each 32-row block) and hands the other half to its partner in the
+    // other grid; the sums are first grid + second, a fixed order.  Every wave then runs the
+    // epilogue (or the split-K hand-over) from registers, with no fp32 tile in LDS: lane l
+    // holds rows 8 (r / 4) + 4 (l / 32) + r % 4 of column l % 32, so a store covers two
+    // 128-byte row segments.  kh becomes a compile-time constant through the two
+    // instantiations of `finish`, so every register index stays a constant.
+    constexpr int NB = WMT * WNT;  // 32 x 32 blocks of a wave
+    __syncthreads();  // the ring is no longer read; the hand-over area overlays it
+    float *xch = reinterpret_cast<float *>(lds);
+    const int pos = wave & 3;  // the wave's place in its 2 x 2 grid
+    auto finish = [&](auto khc) {
+        constexpr int KH = decltype(khc)::value;
+        constexpr int GIVE = 8 * (1 - KH), KEEP = 8 * KH;
+        auto slot = [&](int giver, int b, int q) { return xch + ((((pos * 2 + giver) * NB + b) * 2 + q) * 64 + lane) * 4; };
 #pragma unroll
         for (int i = 0; i < WMT; i++)
 #pragma unroll
             for (int j = 0; j < WNT; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) ctile[cidx(i, j, r)] = acc[0][i][j][r];
-    }
-    if constexpr (KS == 2) {
+                for (int q = 0; q < 2; q++)
+                    *reinterpret_cast<f32x4t *>(slot(KH, i * WNT + j, q)) =
+                        f32x4t{acc[0][i][j][GIVE + 4 * q], acc[0][i][j][GIVE + 4 * q + 1], acc[0][i][j][GIVE + 4 * q + 2],
+                               acc[0][i][j][GIVE + 4 * q + 3]};
         __syncthreads();
-        if (kh == 0) {
+        float sm[NB][8];
 #pragma unroll
-            for (int i = 0; i < WMT; i++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
-                for (int j = 0; j < WNT; j++)
+            for (int q = 0; q < 2; q++) {
+                const f32x4t v = *reinterpret_cast<const f32x4t *>(slot(1 - KH, b, q));
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int ci = cidx(i, j, r);
-                        ctile[ci] = acc[0][i][j][r] + ctile[ci];
-                    }
-        }
-    }
-    __syncthreads();
-
-    if (a.splits > 1) {
-        // Partial tile layout: element e = (plane BM + m) FN + n, float4 q = tid + NT u; a
-        // normed tile's BM row sums of x^2 follow (NEP floats per split).
-        constexpr int QPT = NE / 4 / NT;  // float4 per thread
-        constexpr int NEP = partial_floats<BM, BN, GATED, NORM>();
-        static_assert(NEP == NE + (NORM ? BM : 0), "partial layout");
-        const __amdgpu_buffer_rsrc_t rsrc =
-            __builtin_amdgcn_make_buffer_rsrc(a.part, 0, static_cast<int>(a.part_bytes), 0x00020000);
-        auto cq = [&](int q) -> f32x4t {
-            const int e = 4 * q, row = e / FN, n = e % FN;
-            return *reinterpret_cast<const f32x4t *>(ctile + row * CLD + n);
-        };
-        const uint32_t tile_base = tile * a.splits * static_cast<uint32_t>(NEP) * 4u;
-#pragma unroll
-        for (int u = 0; u < QPT; u++) {
-            const int q = tid + NT * u;
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4t, cq(q)), rsrc,
-                                                   tile_base + (split * NEP + 4 * q) * 4u, 0, SC1);
-        }
-        if constexpr (NORM) {
-            if (tid < BM / 4)
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(u32x4t, *reinterpret_cast<const f32x4t *>(row_ss + 4 * tid)), rsrc,
-                    tile_base + (split * NEP + NE + 4 * tid) * 4u, 0, SC1);
-        }
-        wait_vm<0>();
-        __syncthreads();
-        if (tid == 0) {
-            const uint32_t old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_flag = old == a.splits - 1;
-        }
-        __syncthreads();
-        if (!last_flag) return;
-        if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // Sum the S partial tiles in split order, eight float4 loads per thread in flight.
-        constexpr int D = 8 / QPT;  // splits per batch
-        static_assert(QPT <= 8, "partial tile too large for one workgroup");
-        f32x4t sum[QPT];
-#pragma unroll
-        for (int u = 0; u < QPT; u++) sum[u] = f32x4t{0.f, 0.f, 0.f, 0.f};
-        for (uint32_t s0 = 0; s0 < a.splits; s0 += D) {
-            f32x4t v[D][QPT];
-#pragma unroll
-            for (int d = 0; d < D; d++)
-#pragma unroll
-                for (int u = 0; u < QPT; u++) {
-                    const uint32_t sp = s0 + d;
-                    const int q = tid + NT * u;
-                    const uint32_t off = (sp < a.splits && sp != split) ? tile_base + (sp * NEP + 4 * q) * 4u : 0xFFFFFFF0u;
-                    v[d][u] = __builtin_bit_cast(f32x4t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, SC1));
+                for (int e = 0; e < 4; e++) {
+                    const float own = acc[0][b / WNT][b % WNT][KEEP + 4 * q + e];
+                    sm[b][4 * q + e] = KH == 0 ? own + v[e] : v[e] + own;
                 }
-#pragma unroll
-            for (int d = 0; d < D; d++)
-#pragma unroll
-                for (int u = 0; u < QPT; u++) {
-                    const uint32_t sp = s0 + d;
-                    if (sp < a.splits) sum[u] += sp == split ? cq(tid + NT * u) : v[d][u];
-                }
-        }
-        // The rows' sums of x^2 in split order, by the first BM / 4 threads.
-        f32x4t rsum = f32x4t{0.f, 0.f, 0.f, 0.f};
-        if constexpr (NORM) {
-            if (tid < BM / 4) {
-                for (uint32_t sp = 0; sp < a.splits; sp++)
-                    rsum += sp == split ? *reinterpret_cast<const f32x4t *>(row_ss + 4 * tid)
-                                        : __builtin_bit_cast(f32x4t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                         rsrc, tile_base + (sp * NEP + NE + 4 * tid) * 4u, 0, SC1));
             }
-        }
-        __syncthreads();  // every thread has read its own chunks of the tile (and row sums)
-#pragma unroll
-        for (int u = 0; u < QPT; u++) {
-            const int e = 4 * (tid + NT * u), row = e / FN, n = e % FN;
-            *reinterpret_cast<f32x4t *>(ctile + row * CLD + n) = sum[u];
-        }
-        if constexpr (NORM) {
-            if (tid < BM / 4) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) rsum[e] = 1.0f / sqrtf(rsum[e] / static_cast<float>(K) + a.eps);
-                *reinterpret_cast<f32x4t *>(row_ss + 4 * tid) = rsum;  // the rows' scales
-            }
-        }
-        __syncthreads();
-    }
+        // Row of register rr of block row i, and column of block column j (gated: j = 0 the W
+        // sums, j = 1 the W2 sums of the same feature).
+        const int fr = lane & 31, fh = lane >> 5;
+        auto row_of = [&](int i, int rr) { return 32 * (wm * WMT + i) + 16 * KH + 8 * (rr >> 2) + 4 * fh + (rr & 3); };
+        auto col_of = [&](int j) { return GATED ? 32 * wn + fr : 32 * (wn * WNT + j) + fr; };
 
-    // Epilogue from the fp32 tile: consecutive threads take consecutive features of a row, so
-    // a thread keeps one feature (its bias requested at entry) over rows tid / FN + (NT / FN) i.
-    // The old y of all its rows is requested before the first is used.  The flags are branched
-    // on once (with_flag_set), and a tile inside M x N stores without per-row checks: a wave
-    // issues about one instruction every four cycles, so per-output branches cost microseconds.
-    constexpr int EPT = BM * FN / NT, MSTEP = NT / FN;
-    const int n = en, mr = tid / FN;
-    const uint32_t gn = egn;
-    const bool full = m0 + BM <= M && n0 + FN <= N;
-    const uint32_t flags = a.flags;
-    with_flag_set(flags, [&](auto set) {
-        constexpr uint32_t FL = decltype(set)::value;
-        const bool accum = accumulates<FL>(flags);
-        float yo[EPT];
+        if (a.splits > 1) {
+            // Partial tile in register order: float4 q of register half (b, q) of wave w at
+            // ((w NB + b) 2 + q) 64 + lane; a normed tile's BM row sums of x^2 follow (NEP
+            // floats per split).  Each store moves 1 KB of consecutive floats.
+            constexpr int NEP = partial_floats<BM, BN, GATED, NORM>();
+            static_assert(NEP == NE + (NORM ? BM : 0) && NE == NW * NB * 8 * 64, "partial layout");
+            const __amdgpu_buffer_rsrc_t rsrc =
+                __builtin_amdgcn_make_buffer_rsrc(a.part, 0, static_cast<int>(a.part_bytes), 0x00020000);
+            const uint32_t tile_base = tile * a.splits * static_cast<uint32_t>(NEP) * 4u;
+            auto pidx = [&](int b, int q) { return static_cast<uint32_t>((((wave * NB + b) * 2 + q) * 64 + lane) * 4); };
 #pragma unroll
-        for (int i = 0; i < EPT; i++) yo[i] = 0.0f;
-        if (accum) {  // lanes past M or N read y[0]
+            for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int i = 0; i < EPT; i++) {
-                const uint32_t gm = m0 + mr + MSTEP * i;
-                yo[i] = a.y[full || (gm < M && enok) ? static_cast<size_t>(gm) * a.ldy + gn : 0u];
-            }
-        }
-        float v[EPT];
-#pragma unroll
-        for (int i = 0; i < EPT; i++) {
-            const int m = mr + MSTEP * i;
-            float c = ctile[m * CLD + n];
-            float c2 = GATED ? ctile[(BM + m) * CLD + n] : 0.0f;
+                for (int q = 0; q < 2; q++)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4t, f32x4t{sm[b][4 * q], sm[b][4 * q + 1], sm[b][4 * q + 2], sm[b][4 * q + 3]}),
+                        rsrc, tile_base + (split * NEP + pidx(b, q)) * 4u, 0, SC1);
             if constexpr (NORM) {
-                c *= row_ss[m];  // the row's scale by now
-                c2 *= row_ss[m];
+                if (tid < BM / 4)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4t, *reinterpret_cast<const f32x4t *>(row_ss + 4 * tid)), rsrc,
+                        tile_base + (split * NEP + NE + 4 * tid) * 4u, 0, SC1);
             }
-            v[i] = epilogue_set<FL>(c, c2, bv, flags) + yo[i];
-        }
-        float *yc = a.y + static_cast<size_t>(m0 + mr) * a.ldy + gn;
-        if (full) {
+            wait_vm<0>();
+            __syncthreads();
+            if (tid == 0) {
+                const uint32_t old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last_flag = old == a.splits - 1;
+            }
+            __syncthreads();
+            if (!last_flag) return false;
+            if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // Sum the S partial tiles in split order, the other splits' halves requested a batch
+            // of splits at a time.
+            constexpr int D = 16 / (2 * NB) > 0 ? 16 / (2 * NB) : 1;  // splits per batch
+            float tot[NB][8];
 #pragma unroll
-            for (int i = 0; i < EPT; i++) yc[static_cast<size_t>(MSTEP * i) * a.ldy] = v[i];
-        } else {
+            for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int i = 0; i < EPT; i++)
-                if (m0 + mr + MSTEP * i < M && enok) yc[static_cast<size_t>(MSTEP * i) * a.ldy] = v[i];
+                for (int e = 0; e < 8; e++) tot[b][e] = 0.0f;
+            for (uint32_t s0 = 0; s0 < a.splits; s0 += D) {
+                f32x4t v[D][NB][2];
+#pragma unroll
+                for (int d = 0; d < D; d++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++)
+#pragma unroll
+                        for (int q = 0; q < 2; q++) {
+                            const uint32_t sp = s0 + d;
+                            const uint32_t off =
+                                (sp < a.splits && sp != split) ? tile_base + (sp * NEP + pidx(b, q)) * 4u : 0xFFFFFFF0u;
+                            v[d][b][q] = __builtin_bit_cast(f32x4t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, SC1));
+                        }
+#pragma unroll
+                for (int d = 0; d < D; d++) {
+                    const uint32_t sp = s0 + d;
+                    if (sp < a.splits) {
+#pragma unroll
+                        for (int b = 0; b < NB; b++)
+#pragma unroll
+                            for (int e = 0; e < 8; e++) tot[b][e] += sp == split ? sm[b][e] : v[d][b][e >> 2][e & 3];
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) sm[b][e] = tot[b][e];
+            if constexpr (NORM) {
+                // The rows' sums of x^2 in split order, by the first BM / 4 threads, then their
+                // scales.
+                f32x4t rsum = f32x4t{0.f, 0.f, 0.f, 0.f};
+                if (tid < BM / 4) {
+                    for (uint32_t sp = 0; sp < a.splits; sp++)
+                        rsum += sp == split ? *reinterpret_cast<const f32x4t *>(row_ss + 4 * tid)
+                                            : __builtin_bit_cast(f32x4t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                             rsrc, tile_base + (sp * NEP + NE + 4 * tid) * 4u, 0, SC1));
+                }
+                __syncthreads();  // every thread has read its own row sums
+                if (tid < BM / 4) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) rsum[e] = 1.0f / sqrtf(rsum[e] / static_cast<float>(K) + a.eps);
+                    *reinterpret_cast<f32x4t *>(row_ss + 4 * tid) = rsum;  // the rows' scales
+                }
+                __syncthreads();
+            }
         }
-    });
+
+        // Epilogue: the flags are branched on once (with_flag_set), and a tile inside M x N
+        // stores without per-row checks (a wave issues about one instruction every four
+        // cycles, so per-output branches cost microseconds).
+        const bool full = m0 + BM <= M && n0 + FN <= N;
+        const uint32_t flags = a.flags;
+        with_flag_set(flags, [&](auto set) {
+            constexpr uint32_t FL = decltype(set)::value;
+            constexpr int NO = GATED ? WMT : NB;  // output blocks (gated: a W and a W2 block each)
+            const bool accum = accumulates<FL>(flags);
+            float v[NO][8];
+#pragma unroll
+            for (int o = 0; o < NO; o++) {
+                const int i = GATED ? o : o / WNT, j = GATED ? 0 : o % WNT;
+                const uint32_t gn = n0 + col_of(j);
+#pragma unroll
+                for (int rr = 0; rr < 8; rr++) {
+                    const uint32_t gm = m0 + row_of(i, rr);
+                    v[o][rr] = accum ? a.y[full || (gm < M && gn < N) ? static_cast<size_t>(gm) * a.ldy + gn : 0u] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int o = 0; o < NO; o++) {
+                const int i = GATED ? o : o / WNT, j = GATED ? 0 : o % WNT;
+#pragma unroll
+                for (int rr = 0; rr < 8; rr++) {
+                    float c = GATED ? sm[i * WNT][rr] : sm[o][rr];
+                    float c2 = GATED ? sm[i * WNT + 1][rr] : 0.0f;
+                    if constexpr (NORM) {
+                        const float sc = row_ss[row_of(i, rr)];  // the row's scale by now
+                        c *= sc;
+                        c2 *= sc;
+                    }
+                    v[o][rr] += epilogue_set<FL>(c, c2, bv[j], flags);
+                }
+            }
+#pragma unroll
+            for (int o = 0; o < NO; o++) {
+                const int i = GATED ? o : o / WNT, j = GATED ? 0 : o % WNT;
+                const uint32_t gn = n0 + col_of(j);
+                float *yc = a.y + static_cast<size_t>(m0 + row_of(i, 0)) * a.ldy + gn;
+#pragma unroll
+                for (int rr = 0; rr < 8; rr++) {
+                    const uint32_t dr = 8 * (rr >> 2) + (rr & 3);
+                    if (full || (m0 + row_of(i, rr) < M && gn < N)) yc[static_cast<size_t>(dr) * a.ldy] = v[o][rr];
+                }
+            }
+        });
+        return true;
+    };
+    if (kh == 0)
+        finish(std::integral_constant<int, 0>{});
+    else
+        finish(std::integral_constant<int, 1>{});
 }
 
 typedef void (*tiled_fn)(TiledArgs);
