@@ -11,4 +11,9 @@ ring::ring_fn pick_ring_gated(int wt) {
     return wt == DT_BF16 ? ring::ring_gated_kernel<DT_BF16> : ring::ring_gated_kernel<DT_F16>;
 }
 
+ring::ring_fn pick_ring_split(int wt, bool norm) {
+    if (wt == DT_BF16) return norm ? ring::ring_split_kernel<DT_BF16, true> : ring::ring_split_kernel<DT_BF16, false>;
+    return norm ? ring::ring_split_kernel<DT_F16, true> : ring::ring_split_kernel<DT_F16, false>;
+}
+
 }  // namespace mt

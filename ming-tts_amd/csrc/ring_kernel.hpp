@@ -61,6 +61,9 @@ struct RingArgs {
     float *y;
     uint32_t M, N, K, ldx, ldy, flags;
     uint32_t tiles_m, tiles_n;
+    const float *xf;        // ring_split_kernel: fp32 x (x unused)
+    const uint16_t *norm;   // ring_split_kernel: RMSNorm gain [K] (NORM)
+    float eps;
 };
 
 __device__ __forceinline__ void bar() {
@@ -71,9 +74,10 @@ __device__ __forceinline__ void bar() {
 
 // The second half of the kernel for k group KH (see the call site): the hand-over through LDS,
 // the epilogue and the stores.  Rows past M or features past N are neither read nor stored.
-template <int WT, int KH>
+// NORM: each output is scaled by its row's RMSNorm scale rs[row of the tile] before the bias.
+template <int WT, int KH, bool NORM = false>
 __device__ __forceinline__ void finish(const RingArgs &a, const f32x16t (&acc)[WNT], uint8_t *lds, int wm, int lane,
-                                       uint32_t m0, uint32_t n0, const float (&bv)[WNT / 2]) {
+                                       uint32_t m0, uint32_t n0, const float (&bv)[WNT / 2], const float *rs = nullptr) {
     const int fr = lane & 31, fh = lane >> 5;
     const uint32_t M = a.M, N = a.N, flags = a.flags;
     // Accumulator register r of this group's half is x row mb + 8 (r / 4) + r % 4.
@@ -120,6 +124,14 @@ __device__ __forceinline__ void finish(const RingArgs &a, const f32x16t (&acc)[W
                 sm[j][4 * q + e] = KH == 0 ? own + v[e] : v[e] + own;
             }
         }
+    if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const float sc = rs[32 * wm + 16 * KH + 4 * fh + 8 * (r >> 2) + (r & 3)];
+#pragma unroll
+            for (int j = 0; j < WNT; j++) sm[j][r] *= sc;
+        }
+    }
     float out[8][WNT / 2];
     if ((flags & (F_GELU | F_SILU)) == 0) {
 #pragma unroll
@@ -308,11 +320,199 @@ __global__ __launch_bounds__(NT) void ring_gated_kernel(RingArgs a) {
         finish<WT, 1>(a, acc, lds, wm, lane, m0, n0, bv);
 }
 
+// The same tiles for x in fp32 (the reference's activation type), with or without the fused
+// RMSNorm (RingArgs::xf, ::norm, ::eps): x travels through registers, is multiplied by the norm
+// gain, and is staged as hi + lo halves of the weights' type (hi = round(x), lo = round(x - hi):
+// 2^-22 relative with fp16), so each 16-k step takes two MFMAs per weight fragment.  A stage
+// holds the tile's 128 hi rows, its 128 lo rows and its 192 weight rows (56 KB); two stages
+// alternate in LDS, and the next stage's loads travel in registers while a stage multiplies
+// (the compiler sees every load and places exact waits).  The rows' sums of x^2 are summed by
+// the eight threads of a row (a lane octet) and turned into scales before the epilogue.
+constexpr int SX = 2 * BM + BN;          // rows of a split stage (hi, lo, weights)
+constexpr int SSB = SX * 128;            // bytes of a split stage
+constexpr int SIA = BM * 8 / NT;         // 8-k activation items per thread per stage
+constexpr int SWL = BN * 8 / NT;         // 16-byte weight chunks per thread per stage
+static_assert(SIA * NT == BM * 8 && SWL * NT == BN * 8 && 2 * SSB >= RED && 2 * SSB <= 160 * 1024, "split ring shape");
+
+template <int WT, bool NORM>
+__global__ __launch_bounds__(NT) void ring_split_kernel(RingArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SSB];
+    __shared__ __attribute__((aligned(16))) float rs[BM];  // rows' scales (NORM)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kh = wave >> 2, wm = wave & 3;
+    const uint32_t t = tiled::xcd_order(blockIdx.x, gridDim.x);
+    const uint32_t tm = t % a.tiles_m, tn = t / a.tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * FN;
+    const uint32_t M = a.M, N = a.N, K = a.K;
+    const uint32_t nsteps = (K + 63) / 64;
+    const char *zero = reinterpret_cast<const char *>(g_zero_ring);
+    typedef const __attribute__((address_space(1))) u32x4t *gp;
+    auto ld16 = [](const void *p) { return *reinterpret_cast<gp>(reinterpret_cast<uintptr_t>(p)); };
+
+    // Activation item j of this thread: row (tid + NT j) / 8, k 8 (tid % 8) of every stage.
+    const uint32_t kc = tid & 7;
+    const float *xrow[SIA];
+    bool xok[SIA];
+    uint32_t xoff[SIA];  // LDS byte offset of the item's hi chunk in a stage
+#pragma unroll
+    for (int j = 0; j < SIA; j++) {
+        const uint32_t r = (tid + NT * j) >> 3, m = m0 + r;
+        xok[j] = m < M;
+        xrow[j] = a.xf + static_cast<size_t>(xok[j] ? m : 0u) * a.ldx + 8 * kc;
+        xoff[j] = r * 128 + ((kc ^ (r & 7) ^ ((r >> 3) & 1)) << 4);
+    }
+    // Weight chunk i of this thread: stage weight row c / 8 (32-row blocks g0 u0 g1 u1 g2 u2),
+    // slot c % 8, holding chunk (c % 8) ^ g(row) of the row.
+    const char *wsrc[SWL];
+    bool wok[SWL];
+    uint32_t wci[SWL], woff[SWL];
+#pragma unroll
+    for (int i = 0; i < SWL; i++) {
+        const uint32_t c = tid + NT * i, j = c >> 3, b = j >> 5, r = 2 * BM + j;
+        wci[i] = (c & 7) ^ (r & 7) ^ ((r >> 3) & 1);
+        const uint32_t n = n0 + 32 * (b >> 1) + (j & 31);
+        wok[i] = n < N;
+        wsrc[i] = reinterpret_cast<const char *>(((b & 1) ? a.w2 : a.w) + static_cast<size_t>(wok[i] ? n : 0u) * K + 8 * wci[i]);
+        woff[i] = r * 128 + (c & 7) * 16;
+    }
+    struct Stage {
+        u32x4t x[SIA][2], w[SWL], g;
+    };
+    auto gload = [&](Stage &st, uint32_t s) {
+        const uint32_t k = s * 64;
+#pragma unroll
+        for (int i = 0; i < SWL; i++)
+            st.w[i] = __builtin_nontemporal_load(reinterpret_cast<gp>(reinterpret_cast<uintptr_t>(
+                wok[i] && k + 8 * wci[i] < K ? wsrc[i] + 2 * static_cast<size_t>(k) : zero)));
+        const uint32_t kx = k + 8 * kc;
+        const bool kok = kx < K;
+#pragma unroll
+        for (int j = 0; j < SIA; j++) {
+            const bool ok = kok && xok[j];
+            st.x[j][0] = ld16(ok ? static_cast<const void *>(xrow[j] + k) : zero);
+            st.x[j][1] = ld16(ok ? static_cast<const void *>(xrow[j] + k + 4) : zero);
+        }
+        if constexpr (NORM) st.g = ld16(kok ? static_cast<const void *>(a.norm + kx) : zero);
+    };
+    float ss[SIA];
+#pragma unroll
+    for (int j = 0; j < SIA; j++) ss[j] = 0.0f;
+    auto commit = [&](const Stage &st, uint32_t buf) {
+        uint8_t *sb = lds + buf * SSB;
+#pragma unroll
+        for (int i = 0; i < SWL; i++) *reinterpret_cast<u32x4t *>(sb + woff[i]) = st.w[i];
+#pragma unroll
+        for (int j = 0; j < SIA; j++) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[e] = __uint_as_float(st.x[j][0][e]);
+                x[4 + e] = __uint_as_float(st.x[j][1][e]);
+            }
+            if constexpr (NORM) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss[j] = fmaf(x[e], x[e], ss[j]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[2 * e] *= dec_lo<WT>(st.g[e]);
+                    x[2 * e + 1] *= dec_hi<WT>(st.g[e]);
+                }
+            }
+            u32x4t hi, lo;
+            tiled::split8<WT>(x, hi, lo);
+            *reinterpret_cast<u32x4t *>(sb + xoff[j]) = hi;
+            *reinterpret_cast<u32x4t *>(sb + BM * 128 + xoff[j]) = lo;
+        }
+    };
+
+    // Operand reads: row fr of a 32-row block, chunk 2 q + fh of the stage (q: this group's 16-k
+    // step), slot chunk ^ g(fr).
+    const int fr = lane & 31, fh = lane >> 5;
+    const uint32_t gsw = (fr & 7) ^ ((fr >> 3) & 1);
+    const uint32_t cofs0 = ((2 * (2 * kh) + fh) ^ gsw) << 4, cofs1 = ((2 * (2 * kh + 1) + fh) ^ gsw) << 4;
+    const uint32_t aoff = (32 * wm + fr) * 128;
+    f32x16t acc[WNT];
+#pragma unroll
+    for (int j = 0; j < WNT; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+    struct Fr {
+        u32x4t a[2][2], b[2][WNT];  // [16-k step][hi, lo], [16-k step][block]
+    };
+    auto rd = [&](Fr &f, uint32_t buf) {
+        const uint8_t *st = lds + buf * SSB;
+        f.a[0][0] = *reinterpret_cast<const u32x4t *>(st + aoff + cofs0);
+        f.a[0][1] = *reinterpret_cast<const u32x4t *>(st + BM * 128 + aoff + cofs0);
+        f.a[1][0] = *reinterpret_cast<const u32x4t *>(st + aoff + cofs1);
+        f.a[1][1] = *reinterpret_cast<const u32x4t *>(st + BM * 128 + aoff + cofs1);
+#pragma unroll
+        for (int j = 0; j < WNT; j++) {
+            const uint32_t bo = (2 * BM + 32 * j + fr) * 128;
+            f.b[0][j] = *reinterpret_cast<const u32x4t *>(st + bo + cofs0);
+            f.b[1][j] = *reinterpret_cast<const u32x4t *>(st + bo + cofs1);
+        }
+    };
+    auto mma = [&](const Fr &f) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {  // hi then lo on each block; the blocks' MFMAs interleave
+#pragma unroll
+            for (int j = 0; j < WNT; j++) acc[j] = tiled::mfma32x<WT>(f.a[q][0], f.b[q][j], acc[j]);
+#pragma unroll
+            for (int j = 0; j < WNT; j++) acc[j] = tiled::mfma32x<WT>(f.a[q][1], f.b[q][j], acc[j]);
+        }
+    };
+
+    const uint32_t flags = a.flags;
+    float bv[WNT / 2];
+#pragma unroll
+    for (int p = 0; p < WNT / 2; p++) {
+        const uint32_t n = n0 + 32 * p + fr;
+        bv[p] = (flags & F_BIAS) && n < N ? dec1<WT>(a.bias[n]) : 0.0f;
+    }
+
+    if (nsteps > 0) {
+        // Stage s in buffer s % 2; the registers hold stage s + 1 while stage s multiplies.  The
+        // barrier after a commit tells that the stage is in and that every wave has read the
+        // other buffer's fragments (read before its MFMAs), which the next commit overwrites.
+        Stage st;
+        gload(st, 0);
+        commit(st, 0);
+        if (nsteps > 1) gload(st, 1);
+        __syncthreads();
+        Fr f;
+        rd(f, 0);
+        for (uint32_t s = 0; s < nsteps; s++) {
+            mma(f);
+            if (s + 1 < nsteps) {
+                commit(st, (s + 1) & 1);
+                if (s + 2 < nsteps) gload(st, s + 2);
+                __syncthreads();
+                rd(f, (s + 1) & 1);
+            }
+        }
+    }
+    if constexpr (NORM) {
+        // A row's eight threads are an aligned lane octet.
+#pragma unroll
+        for (int j = 0; j < SIA; j++) {
+            const float tsum = octet_sum(ss[j]);
+            if (kc == 0) rs[(tid + NT * j) >> 3] = 1.0f / sqrtf(tsum / static_cast<float>(K) + a.eps);
+        }
+    }
+    // finish's first barrier also publishes the row scales.
+    if (kh == 0)
+        finish<WT, 0, NORM>(a, acc, lds, wm, lane, m0, n0, bv, rs);
+    else
+        finish<WT, 1, NORM>(a, acc, lds, wm, lane, m0, n0, bv, rs);
+}
+
 typedef void (*ring_fn)(RingArgs);
 
 }  // namespace ring
 
 // The gated ring kernel for weights (and x) of type wt.
 ring::ring_fn pick_ring_gated(int wt);
+// The gated ring kernel for fp32 x, weights of type wt, with or without the fused RMSNorm.
+ring::ring_fn pick_ring_split(int wt, bool norm);
 
 }  // namespace mt

@@ -249,3 +249,55 @@ def test_ring_tile_refuses_ungated_linears(gpu):
         mt.set_tuning(mt.TUNE_GEMM_TILE, old)
     assert rc == mt.EINVAL, rc
     assert "ring" in mt.last_error()
+
+
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "rmsnorm"])
+@pytest.mark.parametrize("wt", [O.F16, O.BF16], ids=["wf16", "wbf16"])
+@pytest.mark.parametrize("shape", RING_SHAPES, ids=_ids)
+def test_gated_ring_kernel_fp32_activations(gpu, shape, wt, norm):
+    """The gated ring kernel for fp32 x (hi + lo halves, MT_TUNE_GEMM_TILE = 5; the auto choice
+    for gated linears of fp32 x from 384 rows on), with and without the fused RMSNorm, against
+    the oracle's fp32 loop and fp64 within the split bound; re-run bit-identical, and at 512
+    rows the default routing gives the same bits."""
+    M, N, K, flags, bias = shape
+    say(f"ring fp32 x w{wt} norm={norm} {_ids(shape)}")
+    c = _case(M * 23 + N + K + wt, M, N, K, flags, bias, wt)
+    c["x"] = c["x"] * np.float32(3.0 if wt == O.F16 else 1.0)
+    if not norm:
+        got, xu = _with_tuning(5, 0, lambda: run_linear(c, O.F32, gpu))
+        want32, want64 = expected(c, xu)
+        assert_linear_parity(got, want32, want64, K, f"ring fp32 x {_ids(shape)}")
+        rel = O.normwise_rel_err(got, want64)
+        assert rel <= SPLIT_TOL, f"ring fp32 x: normwise {rel:.3g} > {SPLIT_TOL}"
+        again, _ = _with_tuning(5, 0, lambda: run_linear(c, O.F32, gpu))
+        np.testing.assert_array_equal(again, got)
+        if M >= 384:
+            auto, _ = _with_tuning(0, 0, lambda: run_linear(c, O.F32, gpu))
+            np.testing.assert_array_equal(auto, got)
+        return
+    x = c["x"]
+    gbits, _ = O.round16(1.0 + 0.1 * O.gaussian(4300 + N, K), wt)
+    x_d = torch.from_numpy(x).to(gpu)
+    y_d = torch.from_numpy(c["y0"].copy()).to(gpu)
+
+    def go():
+        rc = mt.linear_rmsnorm_raw(x_d, O.F32, dev16(gbits, wt, gpu), dev16(c["w"], wt, gpu), dev16(c["w2"], wt, gpu), wt,
+                                   dev16(c["bias"], wt, gpu) if c["bias"] is not None else None, y_d,
+                                   M, N, K, K, N, c["flags"], 1e-6, None)
+        assert rc == 0, mt.last_error()
+        torch.cuda.synchronize()
+        return y_d.cpu().numpy().copy()
+
+    got = _with_tuning(5, 0, go)
+    y_d.copy_(torch.from_numpy(c["y0"]))
+    again = _with_tuning(5, 0, go)
+    np.testing.assert_array_equal(again, got)
+    want64 = O.linear_np64(O.rmsnorm_f64(x, gbits, wt), c["w"], c["w2"], wt, c["bias"], c["y0"], c["flags"])
+    want32 = O.linear_f32(O.rmsnorm_f32(x, gbits, wt), c["w"], c["w2"], wt, c["bias"], c["y0"], M, N, K, c["flags"])
+    assert_linear_parity(got, want32, want64, K, f"ring fp32 x rmsnorm {_ids(shape)}")
+    rel = O.normwise_rel_err(got, want64)
+    assert rel <= SPLIT_TOL, f"ring fp32 x rmsnorm: normwise {rel:.3g} > {SPLIT_TOL}"
+    if M >= 384:
+        y_d.copy_(torch.from_numpy(c["y0"]))
+        auto = _with_tuning(0, 0, go)
+        np.testing.assert_array_equal(auto, got)
