@@ -713,7 +713,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
             const f32x4 a = *reinterpret_cast<const f32x4 *>(sp);
             const f32x4 b = *reinterpret_cast<const f32x4 *>(sp + 4);
             const float t = ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
-            const float scale = 1.0f / sqrtf(t / static_cast<float>(L::K) + d.eps);
+            const float scale = __builtin_amdgcn_rsqf(t / static_cast<float>(L::K) + d.eps);  // v_rsq_f32, within 1 ulp
             a1 *= scale;
             a2 *= scale;
         }
@@ -726,7 +726,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
             asm volatile("" : "+v"(braw));
             bias = second ? 0.0f : dec1<WT>(static_cast<uint16_t>(braw));
         }
-        float v = epilogue(a1, a2, bias, L::FLAGS);
+        float v = epilogue_fixed<L::FLAGS>(a1, a2, bias);  // on this op's critical path: hardware SiLU / tanh
         // Wait for a tagged word at byte offset off to carry the run's parity.
         auto await_word = [&](uint32_t &word, uint32_t off) {
             uint32_t spins = 0;
