@@ -189,7 +189,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
     // Softmax numerators and their sum.
     float sum = 0.0f;
     for (int t = tid; t < nk; t += ATT_THREADS) {
-        const float e = expf(sc[t] - mx);
+        const float e = exp_hw(sc[t] - mx);
         sc[t] = e;
         sum += e;
     }
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(ATT_THREADS) void rope_attention_kernel(float *qkv,
 
     float sum = 0.0f;
     for (int t = tid; t < nk; t += ATT_THREADS) {
-        const float e = expf(sc[t] - mx);
+        const float e = exp_hw(sc[t] - mx);
         sc[t] = e;
         sum += e;
     }

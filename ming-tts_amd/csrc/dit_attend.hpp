@@ -81,7 +81,7 @@ __device__ __forceinline__ float2 dit_item_attend(const DitItem &it, uint32_t i,
 #pragma unroll
     for (uint32_t j = 0; j < DIT_MAXS; j++) {
         if (j < S) {
-            const float e = expf(sc[j] - mx);
+            const float e = exp_hw(sc[j] - mx);
             sum += e;
             acc.x = fmaf(e, it.v[j].x, acc.x);
             acc.y = fmaf(e, it.v[j].y, acc.y);

@@ -146,7 +146,7 @@ __device__ __forceinline__ void gemv_feature(const LinearArgs &a, uint32_t n, ui
         acc[m] = group_sum(acc[m], L);
         if constexpr (GATED) acc2[m] = group_sum(acc2[m], L);
         if constexpr (NORM) {
-            const float scale = 1.0f / sqrtf(group_sum(ss[m], L) / static_cast<float>(a.K) + a.eps);
+            const float scale = rsqrt_hw(group_sum(ss[m], L) / static_cast<float>(a.K) + a.eps);
             acc[m] *= scale;
             acc2[m] *= scale;
         }

@@ -430,7 +430,7 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
             float sum = 0.0f, acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (uint32_t j = 0; j < D::S; j++) {
-                const float e = expf(sc[i][j] - mx);
+                const float e = exp_hw(sc[i][j] - mx);
                 sum += e;
 #pragma unroll
                 for (uint32_t d2 = 0; d2 < 8; d2++) acc[d2] = fmaf(e, vv[j][d2], acc[d2]);
@@ -713,7 +713,7 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
             const f32x4 a = *reinterpret_cast<const f32x4 *>(sp);
             const f32x4 b = *reinterpret_cast<const f32x4 *>(sp + 4);
             const float t = ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
-            const float scale = __builtin_amdgcn_rsqf(t / static_cast<float>(L::K) + d.eps);  // v_rsq_f32, within 1 ulp
+            const float scale = rsqrt_hw(t / static_cast<float>(L::K) + d.eps);
             a1 *= scale;
             a2 *= scale;
         }

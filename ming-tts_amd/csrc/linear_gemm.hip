@@ -228,7 +228,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(LinearArgs a) {
             float s = ss[i];
             for (int off = XROW >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
             const int r = (tid + i * NT) / XROW;
-            if ((tid & (XROW - 1)) == 0) row_scale[r] = 1.0f / sqrtf(s / static_cast<float>(K) + a.eps);
+            if ((tid & (XROW - 1)) == 0) row_scale[r] = rsqrt_hw(s / static_cast<float>(K) + a.eps);
         }
         __syncthreads();
     }

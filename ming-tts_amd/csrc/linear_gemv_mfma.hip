@@ -436,7 +436,7 @@ __global__ __launch_bounds__(GM_THREADS, ATT ? 2 : 4) void gemv_mfma_kernel(Line
         if (o < 16 * M && n < a.N) {
             float s1 = tot[f * MM + m], s2 = GATED ? tot[16 * MM + f * MM + m] : 0.0f;
             if constexpr (NORM) {
-                const float scale = 1.0f / sqrtf(tot[NCT * 16 * MM + m] / static_cast<float>(K) + a.eps);
+                const float scale = rsqrt_hw(tot[NCT * 16 * MM + m] / static_cast<float>(K) + a.eps);
                 s1 *= scale;
                 s2 *= scale;
             }

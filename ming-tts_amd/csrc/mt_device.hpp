@@ -55,15 +55,29 @@ __device__ __forceinline__ float dec1(uint16_t v) {
     else return (float)__builtin_bit_cast(_Float16, v);
 }
 
-// Clamped tanh-GELU and SiLU, the reference's epilogue activations (Shaders.swift:21-29).
-// tanh(15) is already 1 in fp32, so the clamp changes no representable result.
-__device__ __forceinline__ float gelu_tanh(float x) {
+// Clamped tanh-GELU and SiLU, the reference's epilogue activations (Shaders.swift:21-29), on
+// the hardware exp2 and reciprocal (each within 1 ulp): silu(v) = v / (1 + 2^(-v log2 e)),
+// tanh(u) = 1 - 2 / (1 + 2^(2 u log2 e)).  A wave issues about one instruction every four
+// cycles, and these sit on the critical path of every persistent op's outputs: they take a few
+// instructions where expf, tanhf and IEEE division take tens (decode step 378 -> 371 us, flow
+// stage 2249 -> 2082 us).  They differ from expf / tanhf and a correctly rounded division by a
+// few ulp.  tanh(15) is already 1 in fp32, so the clamp changes no representable result.
+__device__ __forceinline__ float silu_hw(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
+}
+__device__ __forceinline__ float gelu_hw(float x) {
     const float k = 0.7978845608028654f;
     float u = k * (x + 0.044715f * x * x * x);
     u = fminf(fmaxf(u, -15.0f), 15.0f);
-    return 0.5f * x * (1.0f + tanhf(u));
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * 2.8853900817779268f));
+    return 0.5f * x * (1.0f + t);
 }
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float gelu_tanh(float x) { return gelu_hw(x); }
+__device__ __forceinline__ float silu(float x) { return silu_hw(x); }
+// e^x on the hardware exp2 (softmax weights, x <= 0).
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+// 1 / sqrt(x) on the hardware reciprocal square root (the RMSNorm scale; within 1 ulp).
+__device__ __forceinline__ float rsqrt_hw(float x) { return __builtin_amdgcn_rsqf(x); }
 
 // The epilogue in the reference order (Shaders.swift:92-103): bias, SiLU-gate, GELU, SiLU,
 // then accumulate into the old output.  yp is the output element's address.
@@ -76,20 +90,7 @@ __device__ __forceinline__ float epilogue(float acc, float acc2, float b, uint32
 }
 
 // The epilogue with its flag set FL fixed at compile time, for kernels that branch on the flags
-// once rather than per output.  SiLU and tanh go through the hardware exp2 and reciprocal (each
-// within 1 ulp): silu(v) = v / (1 + 2^(-v log2 e)), tanh(u) = 1 - 2 / (1 + 2^(2 u log2 e)), a
-// few instructions where expf, tanhf and IEEE division take tens.  Their results differ from
-// epilogue()'s by a few ulp.
-__device__ __forceinline__ float silu_hw(float v) {
-    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
-}
-__device__ __forceinline__ float gelu_hw(float x) {
-    const float k = 0.7978845608028654f;
-    float u = k * (x + 0.044715f * x * x * x);
-    u = fminf(fmaxf(u, -15.0f), 15.0f);
-    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * 2.8853900817779268f));
-    return 0.5f * x * (1.0f + t);
-}
+// once rather than per output (the same arithmetic as epilogue()).
 template <uint32_t FL>
 __device__ __forceinline__ float epilogue_fixed(float acc, float acc2, float b) {
     float v = acc;

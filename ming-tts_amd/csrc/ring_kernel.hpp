@@ -496,7 +496,7 @@ __global__ __launch_bounds__(NT) void ring_split_kernel(RingArgs a) {
 #pragma unroll
         for (int j = 0; j < SIA; j++) {
             const float tsum = octet_sum(ss[j]);
-            if (kc == 0) rs[(tid + NT * j) >> 3] = 1.0f / sqrtf(tsum / static_cast<float>(K) + a.eps);
+            if (kc == 0) rs[(tid + NT * j) >> 3] = rsqrt_hw(tsum / static_cast<float>(K) + a.eps);
         }
     }
     // finish's first barrier also publishes the row scales.

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, uint32_t l
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
     ss = group_sum(ss, 64);
-    const float scale = 1.0f / sqrtf(ss / static_cast<float>(width) + eps);
+    const float scale = rsqrt_hw(ss / static_cast<float>(width) + eps);
     float *yr = y + static_cast<size_t>(row) * ldy;
     for (uint32_t k = 4 * lane; k < width; k += 256) {
         const float4 v = *reinterpret_cast<const float4 *>(xr + k);

@@ -535,7 +535,7 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
                 d = octet_sum(d);
                 d *= o.eps;
                 const float mn = fmaxf(m, d);
-                const float a = expf(m - mn), pb = expf(d - mn);
+                const float a = exp_hw(m - mn), pb = exp_hw(d - mn);
                 l = fmaf(l, a, pb);
 #pragma unroll
                 for (int e = 0; e < 8; e++) acc[e] = fmaf(acc[e], a, pb * vf[e]);
@@ -554,7 +554,7 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     mx = red[0];
 #pragma unroll
     for (int ww = 1; ww < NW; ww++) mx = fmaxf(mx, red[ww]);
-    const float f = expf(m - mx);  // 0 for a thread without keys (m = -inf)
+    const float f = exp_hw(m - mx);  // 0 for a thread without keys (m = -inf)
     const float ls = wave_sum_bfly(r == 0 ? l * f : 0.0f);
     if (lane == 0) red[8 + w] = ls;
 #pragma unroll
@@ -928,7 +928,7 @@ __global__ __launch_bounds__(SEQ_THREADS) void seq_kernel(const SeqOp *__restric
                     float t = 0.0f;
 #pragma unroll
                     for (int ww = 0; ww < CW; ww++) t += v[ww];
-                    scale = 1.0f / sqrtf(t / static_cast<float>(o.K) + o.eps);
+                    scale = rsqrt_hw(t / static_cast<float>(o.K) + o.eps);
                 }
                 const float a1 = total(ov);
                 const float a2 = (o.flags & F_SILU_GATE) ? total(ov + s.nr) : 0.0f;

@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
 #pragma unroll
             for (int j = 0; j < IA; j++) {
                 const float t = octet_sum(ss[j]);
-                if (kc == 0) row_ss[(tid + NT * j) >> 3] = a.splits > 1 ? t : 1.0f / sqrtf(t / static_cast<float>(K) + a.eps);
+                if (kc == 0) row_ss[(tid + NT * j) >> 3] = a.splits > 1 ? t : rsqrt_hw(t / static_cast<float>(K) + a.eps);
             }
         }
     } else if constexpr (P == 1) {
@@ -708,7 +708,7 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
                 __syncthreads();  // every thread has read its own row sums
                 if (tid < BM / 4) {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) rsum[e] = 1.0f / sqrtf(rsum[e] / static_cast<float>(K) + a.eps);
+                    for (int e = 0; e < 4; e++) rsum[e] = rsqrt_hw(rsum[e] / static_cast<float>(K) + a.eps);
                     *reinterpret_cast<f32x4t *>(row_ss + 4 * tid) = rsum;  // the rows' scales
                 }
                 __syncthreads();
