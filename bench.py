@@ -1240,7 +1240,7 @@ def main() -> int:
                     help="launch of the persistent sequence kernels: ordinary (the library's default) "
                          "or cooperative (co-residency guaranteed, about 17 us later per launch)")
     ap.add_argument("--only", choices=["decode", "layer", "all", "copy", "gemm", "prefill", "chain", "vae", "attention", "flow",
-                                       "step", "refshapes"],
+                                       "step", "refshapes", "prefill174"],
                     default="all",
                     help="decode: only the linear decode step; layer: it and the decode step with attention; "
                          "copy: only the 1 GiB device copy that calibrates the HBM byte counters; "
@@ -1248,7 +1248,8 @@ def main() -> int:
                          "chain: only the fp32-activation prefill chain at --rows; vae: only the VAE latent "
                          "(graph of launches, then with the persistent stack); attention: only the decode attention; "
                          "step: only one whole generation step, stage by stage; refshapes: only the reference "
-                         "benches' shapes (the 17 GEMV bench shapes, the 174-row prefill per part)")
+                         "benches' shapes (the 17 GEMV bench shapes, the 174-row prefill per part); prefill174: "
+                         "only the 174-row prefill per part")
     ap.add_argument("--rows", type=int, default=512, help="with --only prefill or chain: the prompt rows M")
     ap.add_argument("--vs-blas", action="store_true",
                     help="with --only gemm: also time each prefill linear alone (graph replay) "
@@ -1298,6 +1299,10 @@ def main() -> int:
         log("prefill at the reference bench's 174 prompt rows, whole layers and per part")
         out["prefill_174"] = bench_prefill_parts(torch, mt, dev, ws)
         print(json.dumps(out), flush=True)
+        return 0
+    if args.only == "prefill174":
+        log("prefill at the reference bench's 174 prompt rows, whole layers and per part")
+        print(json.dumps({"prefill_174": bench_prefill_parts(torch, mt, dev, ws)}), flush=True)
         return 0
     if args.only == "step":
         log("one generation step: llm token, VAE latent, flow stage, aggregator")

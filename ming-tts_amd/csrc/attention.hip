@@ -235,6 +235,236 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
     }
 }
 
+// attention_kernel's arithmetic for R consecutive rows of one sequence at a time, for rows whose
+// keys all start at position 0 (no window, or a window longer than every row's span): one
+// 256-thread workgroup per (head, block of R rows), so a block's keys and values are read
+// once for R rows, and the values' loads are in flight while the scores are formed.  Every
+// value is the row kernel's, bit for bit:
+//   - scores: lane r8 of an octet holds dims 8 r8 .. 8 r8 + 7 of all R queries, the octet one
+//     key; the same eight chains and octet_sum per (row, key), then the scale;
+//   - sum: thread t holds keys t, t + 256, ... of each row in order, then the 64-lane tree
+//     and the (w0 + w1) + (w2 + w3) join of the four waves, as the row kernel's 256 threads;
+//   - p.v: thread (ks, d4) folds keys ks, ks + 16, ... of each row in order, and the 16
+//     phases meet in phase order.
+// A block's scores live in LDS as sc[key][row]; the phases' partial sums reuse that space.
+constexpr int AR_ROWS = 4;
+constexpr int AR_MAXKEYS = 1024;  // pos0 + rows the row-block kernel takes
+constexpr uint32_t AR_MIN_ROWS = 8;  // fewer rows go row by row
+
+// The raw load of four cached values (16 bytes of fp32, 8 of fp16) and their decode.
+template <int CT>
+struct Raw4 {
+    uint4 a;  // fp16: a.x, a.y
+};
+template <int CT>
+__device__ __forceinline__ Raw4<CT> load4_raw(const void *base, size_t off) {
+    Raw4<CT> r;
+    if constexpr (CT == DT_F32) {
+        r.a = *reinterpret_cast<const uint4 *>(static_cast<const float *>(base) + off);
+    } else {
+        const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(base) + off);
+        r.a = make_uint4(v.x, v.y, 0u, 0u);
+    }
+    return r;
+}
+template <int CT>
+__device__ __forceinline__ float4 decode4(const Raw4<CT> &r) {
+    if constexpr (CT == DT_F32)
+        return make_float4(__uint_as_float(r.a.x), __uint_as_float(r.a.y), __uint_as_float(r.a.z),
+                           __uint_as_float(r.a.w));
+    else
+        return make_float4(dec_lo<CT>(r.a.x), dec_hi<CT>(r.a.x), dec_lo<CT>(r.a.y), dec_hi<CT>(r.a.y));
+}
+
+template <int CT, int R>
+__global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(const float *q, uint32_t ldq, uint32_t hq,
+                                                                     uint32_t hkv, uint32_t pos0, uint32_t rows,
+                                                                     const void *kc, const void *vc,
+                                                                     uint32_t cache_len, float *out, uint32_t ldo,
+                                                                     float scale) {
+    static_assert(R == 2 || R == 4 || R == 8, "a key's R scores move as whole 8- or 16-byte words");
+    __shared__ __attribute__((aligned(16))) float sc[AR_MAXKEYS * R];  // sc[key * R + row]
+    __shared__ float red[R][ATT_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x, kvh = h / (hq / hkv);
+    const uint32_t m0 = (gridDim.y - 1 - blockIdx.y) * R;  // the longest rows first
+    const int rn = min(R, static_cast<int>(rows - m0));
+    const int p0 = static_cast<int>(pos0 + m0);  // row r attends keys 0 .. p0 + r
+    const int nk = p0 + rn;
+    const size_t kvbase = static_cast<size_t>(kvh) * cache_len * 64;
+
+    // The R queries' dims 8 r8 .. 8 r8 + 7 in registers (rows past the end repeat the last
+    // row and are never stored).
+    const int r8 = tid & 7;
+    float qf[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float4 *qp = reinterpret_cast<const float4 *>(q + static_cast<size_t>(m0 + min(r, rn - 1)) * ldq +
+                                                            h * 64 + 8 * r8);
+        const float4 a = qp[0], b = qp[1];
+        qf[r][0] = a.x; qf[r][1] = a.y; qf[r][2] = a.z; qf[r][3] = a.w;
+        qf[r][4] = b.x; qf[r][5] = b.y; qf[r][6] = b.z; qf[r][7] = b.w;
+    }
+    // p . v's first VU keys of this thread's phase, requested now, used after the softmax
+    // (keys past the end re-read the last key).
+    const int d4 = tid & 15, ks = tid >> 4;
+    constexpr int VU = 16;
+    Raw4<CT> vr[VU];
+#pragma unroll
+    for (int u = 0; u < VU; u++)
+        vr[u] = load4_raw<CT>(vc, kvbase + static_cast<size_t>(min(ks + 16 * u, nk - 1)) * 64 + 4 * d4);
+
+    // Scores: 32 keys per pass, eight passes' keys requested before any is used.  A key up to
+    // p0 belongs to every row; keys p0 + 1 .. nk - 1 only to the rows they precede.
+    float mx[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) mx[r] = -INFINITY;
+    constexpr int KP = ATT_THREADS / 8, KU = 8;
+    for (int t0 = tid >> 3; t0 < nk; t0 += KU * KP) {
+        Raw8<CT> kr[KU];
+#pragma unroll
+        for (int u = 0; u < KU; u++)
+            kr[u] = load8_raw<CT>(kc, kvbase + static_cast<size_t>(min(t0 + u * KP, nk - 1)) * 64 + 8 * r8);
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int t = t0 + u * KP;
+            if (t < nk) {  // the 8 lanes of a key agree
+                float kf[8];
+                decode8<CT>(kr[u], kf);
+                float s[R];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) a = fmaf(qf[r][e], kf[e], a);
+                    s[r] = a;
+                }
+                octet_sums<R>(s);
+#pragma unroll
+                for (int r = 0; r < R; r++) s[r] *= scale;
+                if (r8 == 0) {
+#pragma unroll
+                    for (int r = 0; r < R; r++) sc[t * R + r] = s[r];
+                }
+                if (t <= p0) {
+#pragma unroll
+                    for (int r = 0; r < R; r++) mx[r] = fmaxf(mx[r], s[r]);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+                        if (t <= p0 + r) mx[r] = fmaxf(mx[r], s[r]);
+                }
+            }
+        }
+        // Every key load of this round done (a skipped pass leaves its load outstanding), so
+        // the next round's address arithmetic waits for nothing.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) mx[r] = wave_max(mx[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) red[r][wave] = mx[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; r++) mx[r] = fmaxf(fmaxf(red[r][0], red[r][1]), fmaxf(red[r][2], red[r][3]));
+    __syncthreads();
+
+    // Softmax numerators (a row's keys past its end hold 0) and the rows' sums.
+    float sum[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) sum[r] = 0.0f;
+    for (int t = tid; t < nk; t += ATT_THREADS) {
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) s[r] = sc[t * R + r];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (t <= p0 + r) {
+                s[r] = exp_hw(s[r] - mx[r]);
+                sum[r] += s[r];
+            } else {
+                s[r] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) sc[t * R + r] = s[r];
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) sum[r] = wave_sum(sum[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) red[r][wave] = sum[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; r++) sum[r] = (red[r][0] + red[r][1]) + (red[r][2] + red[r][3]);
+
+    // p . v: 16 lanes per V row (4 dims each), 16 key phases.
+    float4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int t0 = ks; t0 < nk; t0 += 16 * VU) {
+        if (t0 != ks) {
+#pragma unroll
+            for (int u = 0; u < VU; u++)
+                vr[u] = load4_raw<CT>(vc, kvbase + static_cast<size_t>(min(t0 + 16 * u, nk - 1)) * 64 + 4 * d4);
+        }
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int t = t0 + 16 * u;
+            if (t < nk) {
+                const float4 v = decode4<CT>(vr[u]);
+                float p[R];
+#pragma unroll
+                for (int r = 0; r < R; r++) p[r] = sc[t * R + r];
+                if (t <= p0) {
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        acc[r].x = fmaf(p[r], v.x, acc[r].x);
+                        acc[r].y = fmaf(p[r], v.y, acc[r].y);
+                        acc[r].z = fmaf(p[r], v.z, acc[r].z);
+                        acc[r].w = fmaf(p[r], v.w, acc[r].w);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        if (t <= p0 + r) {
+                            acc[r].x = fmaf(p[r], v.x, acc[r].x);
+                            acc[r].y = fmaf(p[r], v.y, acc[r].y);
+                            acc[r].z = fmaf(p[r], v.z, acc[r].z);
+                            acc[r].w = fmaf(p[r], v.w, acc[r].w);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();  // every probability read; the phases' sums take sc's space
+    float4 *part = reinterpret_cast<float4 *>(sc);  // part[(ks * 16 + d4) * R + r]
+#pragma unroll
+    for (int r = 0; r < R; r++) part[(ks * 16 + d4) * R + r] = acc[r];
+    __syncthreads();
+    if (tid < 16 * R) {
+        const int dd = tid & 15, r = tid >> 4;
+        if (r < rn) {
+            float s = sum[0];
+#pragma unroll
+            for (int rr = 1; rr < R; rr++)
+                if (r == rr) s = sum[rr];
+            float4 o = part[dd * R + r];
+            for (int k = 1; k < 16; k++) {
+                const float4 pp = part[(k * 16 + dd) * R + r];
+                o.x += pp.x; o.y += pp.y; o.z += pp.z; o.w += pp.w;
+            }
+            const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+            const float4 res = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+            *reinterpret_cast<float4 *>(out + static_cast<size_t>(m0 + r) * ldo + h * 64 + 4 * dd) = res;
+        }
+    }
+}
+
 // rope_cache then attention over one sequence's M new rows (positions pos0 .. pos0 + M - 1),
 // in one launch: workgroup (row m, head h) rotates its q (and writes it back to qkv), appends
 // row m's rotated k and raw v of kv head h / (hq / hkv) to the caches when h is the first head
@@ -436,6 +666,18 @@ int launch_attention(const float *q, uint32_t ldq, uint32_t rows, uint32_t hq, u
                      const uint32_t *lens, uint32_t window, const void *kc, const void *vc, int ct,
                      uint32_t cache_len, uint64_t cache_stride, float *out, uint32_t ldo, float scale,
                      hipStream_t stream) {
+    // Rows of one sequence whose keys all start at position 0 go by blocks of AR_ROWS rows.
+    if (!lens && rows >= AR_MIN_ROWS && pos0 + rows <= static_cast<uint32_t>(AR_MAXKEYS) &&
+        (window == 0 || pos0 + rows <= window)) {
+        const dim3 g(hq, (rows + AR_ROWS - 1) / AR_ROWS);
+        if (ct == DT_F32)
+            hipLaunchKernelGGL((attention_rows_kernel<DT_F32, AR_ROWS>), g, dim3(ATT_THREADS), 0, stream, q, ldq, hq,
+                               hkv, pos0, rows, kc, vc, cache_len, out, ldo, scale);
+        else
+            hipLaunchKernelGGL((attention_rows_kernel<DT_F16, AR_ROWS>), g, dim3(ATT_THREADS), 0, stream, q, ldq, hq,
+                               hkv, pos0, rows, kc, vc, cache_len, out, ldo, scale);
+        return check_launch("attention");
+    }
     dim3 grid(rows * hq);
     if (ct == DT_F32)
         hipLaunchKernelGGL(attention_kernel<DT_F32>, grid, dim3(ATT_THREADS), 0, stream, q, ldq, hq, hkv, pos0, lens,

@@ -181,6 +181,43 @@ def test_rope_attention_equals_rope_cache_then_attention(gpu, ct, M, pos0, windo
         np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy(), err_msg=what)
 
 
+@pytest.mark.parametrize("ct,M,pos0,window", [
+    (torch.float16, 174, 0, 0),     # the reference's prefill prompt
+    (torch.float32, 174, 0, 0),
+    (torch.float16, 8, 0, 0),       # the fewest rows that go by blocks
+    (torch.float32, 13, 37, 0),     # a ragged last block after cached keys
+    (torch.float16, 301, 700, 0),   # rows of up to 1001 keys: four sum slots a thread
+    (torch.float32, 61, 3, 64),     # a window longer than every row's span
+    (torch.float16, 124, 900, 0),   # pos0 + M = 1024, the most keys that go by blocks
+    (torch.float32, 40, 50, 70),    # a window shorter than the last rows' spans: row by row
+])
+def test_row_blocks_equal_rows_one_at_a_time(gpu, ct, M, pos0, window):
+    """mt_attention over M rows of one sequence (a workgroup per head and block of rows)
+    against the same rows attended one call each (a workgroup per row and head): the same
+    bits; and sampled rows against the fp64 oracle on the stored cache values."""
+    cap = 1024
+    rng = np.random.default_rng(M * 7 + pos0)
+    q = rng.standard_normal((M, HQ * 64)).astype(np.float32)
+    kc = torch.from_numpy(rng.standard_normal((HKV, cap, 64)).astype(np.float32)).to(gpu).to(ct)
+    vc = torch.from_numpy(rng.standard_normal((HKV, cap, 64)).astype(np.float32)).to(gpu).to(ct)
+    qd = torch.from_numpy(q).to(gpu)
+    o1 = torch.full((M, HQ * 64), 7.0, device=gpu)
+    o2 = torch.full((M, HQ * 64), 7.0, device=gpu)
+    say(f"row blocks ct={ct} M={M} pos0={pos0} window={window}")
+    mt.attention(qd, HQ * 64, M, HQ, HKV, pos0, window, kc, vc, cap, o1, HQ * 64, 0.125)
+    for m in range(M):
+        mt.attention(qd[m:], HQ * 64, 1, HQ, HKV, pos0 + m, window, kc, vc, cap, o2[m:], HQ * 64, 0.125)
+    torch.cuda.synchronize()
+    got = o1.cpu().numpy()
+    np.testing.assert_array_equal(got, o2.cpu().numpy())
+    kcg = kc.double().cpu().numpy()
+    vcg = vc.double().cpu().numpy()
+    for m in sorted({0, 1, M // 2, M - 2, M - 1}):
+        want = O.attention_f64(q[m].reshape(HQ, 64), kcg, vcg, pos0 + m, window, 0.125)
+        ex, i, g, w = O.worst_violation(got[m].reshape(HQ, 64), want, 2e-5)
+        assert ex <= 0, f"row {m} index {i} got {g} want {w}"
+
+
 def test_rope_attention_rejects_bad_arguments():
     L = mt.load()
     A = 1 << 20
