@@ -358,7 +358,9 @@ int mt_rope_cache_decode(float *qkv, uint32_t ldq, uint32_t B, uint32_t hq, uint
  * the M query rows at positions pos0 .. pos0 + M - 1 over the cache, keys
  * [max(0, pos + 1 - window), pos] (window 0 = unlimited), scores scaled by `scale`,
  * max-subtracted softmax, out = sum p v.  q rows hold hq heads of 64 (stride ldq),
- * out rows stride ldo.  pos0 + M <= cache_len <= 4096.
+ * out rows stride ldo.  pos0 + M <= cache_len <= 4096.  Rows of a prefill (M >= 8, every
+ * row's keys starting at 0, pos0 + M <= 1024) are attended 4 to a workgroup; the results
+ * are bit-identical to attending the rows one call each.
  */
 int mt_attention(const float *q, uint32_t ldq, uint32_t M, uint32_t hq, uint32_t hkv,
                  uint32_t pos0, uint32_t window, const void *k_cache, const void *v_cache,
