@@ -386,6 +386,8 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     float *part2 = lds + 4608;  // [8][64] sums of eight key groups
     float *kvraw = lds + 5120;  // [8][128] k | v of the rows whose keys come from the activations
     float *skv = lds + 6144;    // [8][128] those keys: k rotated | v, rounded to the cache type
+    float *trig = lds + 512;    // [1 + nnew][cos 32 | sin 32] of the rotation angles (in part's
+                                // space, which the scores' end first writes)
 
     const uint32_t pos = gld(o.pos + b);
     // Keys at positions pos0 .. pos come from rows 0 .. nnew - 1 of the activations: the row
@@ -436,7 +438,25 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
             f[6] = dec_lo<DT_F16>(raw[0].w); f[7] = dec_hi<DT_F16>(raw[0].w);
         }
     };
+    // The last wave (which polls nothing below) requests the inverse frequencies ahead of its
+    // key chunks, so forming the rotation angles' cosines and sines waits for them alone.
+    const bool trig_wave = w == NW - 1 && lane < 32;
+    float invf = 0.0f;
+    if (trig_wave) invf = gld(o.inv_freq + lane);
     chunk_loads(0);
+    // The angles depend on positions only: their cosines and sines are formed while the
+    // other waves poll the activations (q at pos, the activations' keys at pos0 .. pos0 +
+    // nnew - 1).
+    if (trig_wave) {
+        const float aq = static_cast<float>(pos) * invf;
+        trig[lane] = cosf(aq);
+        trig[32 + lane] = sinf(aq);
+        for (uint32_t rr = 0; rr < nnew; rr++) {
+            const float ar = static_cast<float>(pos0 + rr) * invf;
+            trig[64 * (rr + 1) + lane] = cosf(ar);
+            trig[64 * (rr + 1) + 32 + lane] = sinf(ar);
+        }
+    }
 
     // q head h of row b (16 chunks of 4 words), then k and v heads kvh of each row the keys
     // pos0 .. pos come from (32 chunks a row).
@@ -475,14 +495,10 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     __syncthreads();
     if (tid < 32) {
         const uint32_t i = tid;
-        const float f = gld(o.inv_freq + i);
-        const float angle = static_cast<float>(pos) * f;
-        const float c = cosf(angle), s = sinf(angle);
         const float q0 = sraw[i], q1 = sraw[i + 32];
-        rope_rotate(q0, q1, c, s, sq[i], sq[i + 32]);
+        rope_rotate(q0, q1, trig[i], trig[32 + i], sq[i], sq[i + 32]);
         for (uint32_t rr = 0; rr < nnew; rr++) {
-            const float ar = static_cast<float>(pos0 + rr) * f;  // the row's own key: angle
-            const float cr = cosf(ar), sr = sinf(ar);
+            const float cr = trig[64 * (rr + 1) + i], sr = trig[64 * (rr + 1) + 32 + i];
             const float *kr = kvraw + rr * 128;
             const float k0 = kr[i], k1 = kr[32 + i];
             float *d = skv + rr * 128;
