@@ -183,7 +183,9 @@ enum {
                                     M = 384 on) */
     MT_TUNE_GEMM_STAGES = 7,     /* loads of that GEMM for x of the weights' type: 2..4 = direct-to-LDS
                                     stages of 64 k, 1 = two register-staged stages into two LDS
-                                    buffers (0 = auto; fp32 x always takes the latter) */
+                                    buffers (0 = auto); fp32 x always stages through registers,
+                                    its K loop 1 = committing only the split's stages, 2..4 = the
+                                    branch-free loop (64-row tiles; 0 = auto) */
     MT_TUNE_GEMV_MFMA = 8,       /* the MFMA kernel that stages x once per 16 output features: 0 =
                                     for 3..16 rows (default; 3..8 with a fused norm), 1 = never
                                     (lane-group GEMV up to 8 rows, GEMM above), 2 = up to 64 rows of

@@ -80,7 +80,12 @@ TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, in
     S = std::max(1u, std::min(S, KT));
     p.kps = (KT + S - 1) / S;
     p.splits = (KT + p.kps - 1) / p.kps;
-    p.stages = split ? 1 : (s == 0 && tiles > ncu) ? 2 : 4;
+    // fp32 x: the branch-free loop (stages 2) holds more registers, one workgroup a CU at the
+    // 64 x 128 tiles, so those take the other loop when their workgroups outnumber the CUs.
+    if (split)
+        p.stages = p.bm == 128 ? 1 : (p.bn == 64 || tiles * p.splits <= ncu) ? 2 : 1;
+    else
+        p.stages = (s == 0 && tiles > ncu) ? 2 : 4;
     return p;
 }
 
@@ -137,7 +142,7 @@ int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, c
     }
     if (tile == 5) return set_error(MT_EINVAL, "gemm: tile 5 (the gated ring kernel) takes a SiLU-gated linear");
     TiledPlan p = tiled_plan(a.M, a.N, a.K, gated, cus, tile, splitk, split);
-    if (stages_override >= 1 && !split) p.stages = stages_override;
+    if (stages_override >= 1) p.stages = !split ? stages_override : (p.bm == 128 || stages_override == 1) ? 1 : 2;
     if (p.bm == 0) return set_error(MT_EINVAL, "gemm: tile shape %d does not apply to this linear", tile);
     TiledArgs t;
     t.x = a.x;
@@ -165,7 +170,7 @@ int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, c
         t.cnt = cnt;
     }
     const int stages = p.stages;
-    tiled_fn fn = split ? pick_tiled_split(wt, gated, norm, p.shape)
+    tiled_fn fn = split ? pick_tiled_split(wt, gated, norm, p.shape, stages)
                   : wt == DT_BF16
                       ? (gated ? pick_tiled<DT_BF16, true>(p.shape, stages) : pick_tiled<DT_BF16, false>(p.shape, stages))
                       : (gated ? pick_tiled<DT_F16, true>(p.shape, stages) : pick_tiled<DT_F16, false>(p.shape, stages));

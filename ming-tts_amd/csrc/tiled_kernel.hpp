@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
     constexpr int LBYTES = NBUF * SB > XBYTES ? NBUF * SB : XBYTES;
     static_assert(!GATED || BN == 128, "a gated tile is 64 features of W and W2");
     static_assert(LPW * 8 * NW == (SPLIT ? BN : BM + BN) && P >= 1 && P <= 4 && LBYTES <= 160 * 1024, "tile shape");
-    static_assert(!SPLIT || (P == 1 && IA * NT == BM * 8), "split staging: two register-staged LDS buffers");
+    static_assert(!SPLIT || ((P == 1 || P == 2) && IA * NT == BM * 8), "split staging: two register-staged LDS buffers");
     static_assert(NE % (4 * NT) == 0, "partial tiles move as float4 per thread");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LBYTES];
     __shared__ uint32_t last_flag;
@@ -376,7 +376,9 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
             }
             if constexpr (NORM) r.g = ld16(kok ? static_cast<const void *>(a.norm + kx) : zero);
         };
-        auto commit = [&](const Stage &r, uint32_t buf) {
+        // in_range: the stage is one of this split's (a stage past them is staged but never
+        // multiplied, and its x^2 is not summed).
+        auto commit = [&](const Stage &r, uint32_t buf, bool in_range) {
             uint8_t *st = lds + buf * SB;
 #pragma unroll
             for (int i = 0; i < LPW; i++) *reinterpret_cast<u32x4t *>(st + (AR / 8 + wave + NW * i) * 1024 + lane * 16) = r.b[i];
@@ -389,8 +391,10 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
                     x[4 + e] = __uint_as_float(r.x[j][1][e]);
                 }
                 if constexpr (NORM) {
+                    float t = ss[j];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) ss[j] = fmaf(x[e], x[e], ss[j]);
+                    for (int e = 0; e < 8; e++) t = fmaf(x[e], x[e], t);
+                    ss[j] = in_range ? t : ss[j];
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         if constexpr (WT == DT_F16) {  // x times the fp16 gain in one mixed fma each
@@ -415,29 +419,68 @@ __global__ __launch_bounds__(256 * KS) void tiled_kernel(TiledArgs a) {
         Stage r0, r1;
         gload(r0, ks0);
         gload(r1, ks0 + 1);
-        commit(r0, 0);
+        commit(r0, 0, true);
         gload(r0, ks0 + 2);
         __syncthreads();
-        for (uint32_t s = 0; s < nsteps; s += 2) {
-            {  // stage s in buffer 0; r1 holds s + 1, r0 is bound for s + 2
+        if constexpr (P == 2) {
+            // The steady loop has no branch: every step commits the next stage and requests the
+            // one two on (a stage past the split is staged, never multiplied; its loads read the
+            // zero chunk or the next split's rows), so the compiler sees the same loads in flight
+            // on every path and waits for exactly the stage it commits, with the following
+            // stage's loads still in flight.  A scheduling fence after each barrier keeps a
+            // step's conversions in that step: hoisted into the step before, they wait for loads
+            // issued only a step earlier.  An odd last stage runs after the loop.  It holds more
+            // registers than the loop below (one workgroup a CU at the 64 x 128 tiles).
+            uint32_t s = 0;
+            for (; s + 2 <= nsteps; s += 2) {
+                {  // stage s in buffer 0; r1 holds s + 1, r0 is bound for s + 2
+                    Frags f;
+                    load(f, 0);
+                    mma(f);
+                    commit(r1, 1, true);
+                    gload(r1, ks0 + s + 3);
+                    __syncthreads();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                {  // stage s + 1 in buffer 1; r0 holds s + 2
+                    Frags f;
+                    load(f, 1);
+                    mma(f);
+                    commit(r0, 0, s + 2 < nsteps);
+                    gload(r0, ks0 + s + 4);
+                    __syncthreads();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            if (s < nsteps) {  // the odd last stage, in buffer 0
                 Frags f;
                 load(f, 0);
                 mma(f);
-                if (s + 1 < nsteps) {
-                    commit(r1, 1);
-                    gload(r1, ks0 + s + 3);
-                }
-                __syncthreads();
             }
-            if (s + 1 < nsteps) {  // stage s + 1 in buffer 1; r0 holds s + 2
-                Frags f;
-                load(f, 1);
-                mma(f);
-                if (s + 2 < nsteps) {
-                    commit(r0, 0);
-                    gload(r0, ks0 + s + 4);
+        } else {
+            // Commits and requests only within the split: fewer registers, but the compiler's
+            // waits then cover the following stage's loads too.
+            for (uint32_t s = 0; s < nsteps; s += 2) {
+                {  // stage s in buffer 0; r1 holds s + 1, r0 is bound for s + 2
+                    Frags f;
+                    load(f, 0);
+                    mma(f);
+                    if (s + 1 < nsteps) {
+                        commit(r1, 1, true);
+                        gload(r1, ks0 + s + 3);
+                    }
+                    __syncthreads();
                 }
-                __syncthreads();
+                if (s + 1 < nsteps) {  // stage s + 1 in buffer 1; r0 holds s + 2
+                    Frags f;
+                    load(f, 1);
+                    mma(f);
+                    if (s + 2 < nsteps) {
+                        commit(r0, 0, true);
+                        gload(r0, ks0 + s + 4);
+                    }
+                    __syncthreads();
+                }
             }
         }
         if constexpr (NORM) {
@@ -794,7 +837,7 @@ tiled_fn pick_shape(int shape) {
 }  // namespace tiled
 
 // The kernel of an fp32-activation linear (linear_gemm_split.hip): weight type wt, gated,
-// normed, tile shape.
-tiled::tiled_fn pick_tiled_split(int wt, bool gated, bool norm, int shape);
+// normed, tile shape, loop (stages 1: commits only the split's stages; 2: branch-free).
+tiled::tiled_fn pick_tiled_split(int wt, bool gated, bool norm, int shape, int stages);
 
 }  // namespace mt

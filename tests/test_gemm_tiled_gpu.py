@@ -165,6 +165,51 @@ def test_fp32_activations_with_fused_rmsnorm(gpu, shape, tile, wt):
     assert rel <= SPLIT_TOL, f"fp32 x rmsnorm: normwise {rel:.3g} > {SPLIT_TOL}"
 
 
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "rmsnorm"])
+@pytest.mark.parametrize("splits", [0, 3])
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_fp32_activation_loops_agree_bit_for_bit(gpu, shape, tile, splits, norm):
+    """The fp32-x path's two K loops (stages 1: commits only the split's stages; 2: branch-free,
+    the stages past the split staged and never multiplied, their x^2 not summed) multiply the
+    same stages in the same order: the same bits, with and without the fused RMSNorm, and the
+    branch-free loop against fp64."""
+    M, N, K, flags, bias = shape
+    if flags & O.SILU_GATE and tile == 3:
+        pytest.skip("a gated tile always has 128 weight rows")
+    say(f"tiled fp32 x loops tile={tile} splits={splits} norm={norm} {_ids(shape)}")
+    wt = O.F16
+    c = _case(M * 19 + N + K, M, N, K, flags, bias, wt)
+    x = c["x"] * np.float32(3.0)
+    gbits, _ = O.round16(1.0 + 0.1 * O.gaussian(4300 + N, K), wt)
+    gated = bool(flags & O.SILU_GATE)
+    x_d = torch.from_numpy(x).to(gpu)
+    y_d = torch.from_numpy(c["y0"].copy()).to(gpu)
+    g_d = dev16(gbits, wt, gpu)
+    w_d, w2_d = dev16(c["w"], wt, gpu), dev16(c["w2"], wt, gpu) if gated else None
+    b_d = dev16(c["bias"], wt, gpu) if c["bias"] is not None else None
+
+    def go():
+        y_d.copy_(torch.from_numpy(c["y0"]))
+        if norm:
+            rc = mt.linear_rmsnorm_raw(x_d, O.F32, g_d, w_d, w2_d, wt, b_d, y_d, M, N, K, K, N, c["flags"], 1e-6)
+        else:
+            rc = mt.linear_raw(x_d, O.F32, w_d, w2_d, wt, b_d, y_d, M, N, K, K, N, c["flags"])
+        assert rc == 0, mt.last_error()
+        torch.cuda.synchronize()
+        return y_d.cpu().numpy()
+
+    got = {st: _with_tuning(tile, splits, go, stages=st) for st in (1, 2)}
+    np.testing.assert_array_equal(got[2], got[1])
+    xin64 = O.rmsnorm_f64(x, gbits, wt) if norm else x.astype(np.float64)
+    xin32 = O.rmsnorm_f32(x, gbits, wt) if norm else x
+    want64 = O.linear_np64(xin64, c["w"], c["w2"] if gated else None, wt, c["bias"], c["y0"], c["flags"])
+    want32 = O.linear_f32(xin32, c["w"], c["w2"] if gated else None, wt, c["bias"], c["y0"], M, N, K, c["flags"])
+    assert_linear_parity(got[2], want32, want64, K, f"fp32 x loops tile {tile} {_ids(shape)}")
+    rel = O.normwise_rel_err(got[2], want64)
+    assert rel <= SPLIT_TOL, f"fp32 x loops: normwise {rel:.3g} > {SPLIT_TOL}"
+
+
 def test_workspace_grows_and_streams_are_independent(gpu):
     """A small split launch, a much larger one (the workspace grows), then both again on a
     second stream: every result matches the first run of the same case bit for bit."""
