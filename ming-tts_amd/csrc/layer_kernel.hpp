@@ -777,19 +777,32 @@ __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restr
     if constexpr (!EARLY) issue();
 }
 
+// The positions of this workgroup's first attention item of layer op o (its row's and
+// pos[0]), requested before the layer's qkv op so the item's cache reads need not wait for them.
+template <int M>
+__device__ __forceinline__ void lay_attention_pos(const SeqOp &o, uint32_t g, uint32_t (&pos)[2]) {
+    const uint32_t hq = o.heads & 0xFFFFu;
+    if (g < M * hq) {
+        pos[0] = gld(o.pos + g / hq);
+        pos[1] = gld(o.pos);
+    }
+}
+
 // The decode attention item of a layer (the general kernel's attend_item on this kernel's 7
 // waves): its (row, head) pairs, M 14 of them, go to workgroups g, g + G, ...; the x staging
 // is the item's scratch.  Every other workgroup goes straight on to o, whose activations
 // are this item's output.
 template <int WT, int M>
-__device__ __forceinline__ void lay_attention(LayCtx<WT, M> &cx, const SeqOp &o, uint32_t g, uint32_t G) {
+__device__ __forceinline__ void lay_attention(LayCtx<WT, M> &cx, const SeqOp &o, uint32_t g, uint32_t G,
+                                              const uint32_t (&pos)[2]) {
     const uint32_t hq = o.heads & 0xFFFFu, items = M * hq;
     float *scratch = reinterpret_cast<float *>(cx.xs);
     for (uint32_t it = g; it < items; it += G) {
+        const uint32_t *pp = M <= 2 && it == g ? pos : nullptr;
         if (o.cache_t == DT_F32)
-            attend_item<DT_F32, LAY_CW>(o, it / hq, it % hq, cx.rsrc, cx.parity, scratch, cx.gave_up, cx.sync);
+            attend_item<DT_F32, LAY_CW>(o, it / hq, it % hq, cx.rsrc, cx.parity, scratch, cx.gave_up, cx.sync, pp);
         else
-            attend_item<DT_F16, LAY_CW>(o, it / hq, it % hq, cx.rsrc, cx.parity, scratch, cx.gave_up, cx.sync);
+            attend_item<DT_F16, LAY_CW>(o, it / hq, it % hq, cx.rsrc, cx.parity, scratch, cx.gave_up, cx.sync, pp);
     }
 }
 
@@ -903,11 +916,14 @@ __global__ __launch_bounds__(LAY_THREADS) void layer_kernel(const SeqOp *__restr
         const uint32_t i = OPL * l, nx = l + 1 < L ? i + OPL : 0;
         const uint32_t io = i + 1 + A, ig = i + 2 + A, id = i + 3 + A;  // o, gate|up, down
         dn = lops[io];
+        // The M = 4 kernel has no registers to spare for them over the qkv op.
+        uint32_t apos[2] = {0u, 0u};
+        if constexpr (ATT && M <= 2) lay_attention_pos<M>(ops[i + 1], g, apos);
         lay_step<WT, M, LC_QKV, NBQ>(cx, ops, i, dq, PQ, [&]() {
             lay_tiles<WT, M, LC_GU, G1, G2>(cx, lops[ig], PG);
             lay_tiles<WT, M, LC_DOWN, 0, D1>(cx, lops[id], PD);
         });
-        if constexpr (ATT) lay_attention<WT, M>(cx, ops[i + 1], g, G);
+        if constexpr (ATT) lay_attention<WT, M>(cx, ops[i + 1], g, G, apos);
         dq = lops[ig];
         lay_step<WT, M, LC_O, NBO>(cx, ops, io, dn, PO, [&]() {
             lay_tiles<WT, M, LC_GU, G2, LG::TA>(cx, dq, PG);

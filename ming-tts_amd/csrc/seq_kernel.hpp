@@ -366,7 +366,8 @@ __device__ __forceinline__ float wave_sum_bfly(float v) { return group_sum(v, 64
 // NW: the workgroup's waves (8 key groups each).  Uses lds (floats) as scratch: 7168 words.
 template <int CT, int NW = CW>
 __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t h, __amdgpu_buffer_rsrc_t rsrc,
-                                            uint32_t parity, float *lds, bool &gave_up, uint32_t *sync) {
+                                            uint32_t parity, float *lds, bool &gave_up, uint32_t *sync,
+                                            const uint32_t *pos_pre = nullptr) {
     static_assert(NW == 7 || NW == 8, "the final sums are written out for 7 or 8 waves");
     constexpr int KG = 8 * NW;  // key groups of 8 lanes
     // The thread index is made opaque here, so nothing derived from it is hoisted out of
@@ -389,11 +390,12 @@ __device__ __forceinline__ void attend_item(const SeqOp &o, uint32_t b, uint32_t
     float *trig = lds + 512;    // [1 + nnew][cos 32 | sin 32] of the rotation angles (in part's
                                 // space, which the scores' end first writes)
 
-    const uint32_t pos = gld(o.pos + b);
+    // pos_pre: the row's position and pos[0], loaded by the caller ahead of the item.
+    const uint32_t pos = pos_pre ? pos_pre[0] : gld(o.pos + b);
     // Keys at positions pos0 .. pos come from rows 0 .. nnew - 1 of the activations: the row
     // itself, or with a shared cache rows 0 .. b of the sequence.
     const bool shared = o.cache_stride == 0 && o.M > 1;
-    const uint32_t pos0 = shared ? gld(o.pos) : pos;
+    const uint32_t pos0 = shared ? (pos_pre ? pos_pre[1] : gld(o.pos)) : pos;
     const uint32_t nnew = shared ? b + 1 : 1u;
     const bool append = pos < o.cache_len;
     // Keys [j0, len): len = pos + 1 (the new key at pos comes from LDS), or the whole cache
