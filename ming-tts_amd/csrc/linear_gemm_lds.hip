@@ -46,17 +46,20 @@ tiled_fn pick_tiled(int shape, int stages) {
 //     double-buffered ring (68 KB) keeps two 128 x 128 workgroups on a CU.
 //   - fp32 activations (split): staged through registers into two LDS buffers.  K is split
 //     into as many parts as fill the CUs once, or into parts of at most 20 stages, within two
-//     workgroups per CU, parts of at least 4 stages and 8 parts (the last workgroup of a tile
-//     adds the parts); long K (32 stages and more) takes 64 x 128 tiles from 256 rows.  Graph replay at M = 512 (fp32 x): rmsnorm+qkv
-//     13.3 us unsplit against 14.3 in 3 parts, o 11.4 in 2 against 12.6 unsplit, down 24.0 on
-//     64 x 128 tiles in 4 parts against 25.8 on 64 x 64.  Gated: 64 x 128 tiles below the ring
-//     kernel's rows (a 128 x 128 split tile needs 98 KB of LDS, one workgroup per CU).
+//     workgroups per CU, parts of at least 2 stages and 8 parts, 2 parts when gated (the last
+//     workgroup of a tile adds the parts); long K (32 stages and more) takes 64 x 128 tiles
+//     from 384 rows.  Graph replay (fp32 x): at M = 512 rmsnorm+qkv 13.3 us unsplit against
+//     14.3 in 3 parts, o 11.4 in 2 against 12.6 unsplit, down 24.0 on 64 x 128 tiles in 4
+//     parts against 25.8 on 64 x 64; at M = 256 down 16.9 on 64 x 64 against 18.0 on 64 x 128;
+//     at M = 64 o 8.7 in 6-7 parts against 9.5 in 3, rmsnorm+gate|up 13.6 in 2 against 14.1 in
+//     3.  Gated: 64 x 128 tiles below the ring kernel's rows (a 128 x 128 split tile needs 98 KB
+//     of LDS, one workgroup per CU).
 TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, int shape_override, int splitk_override,
                      bool split) {
     TiledPlan p{};
     const uint32_t KT = (K + TBK - 1) / TBK;
     const uint32_t ncu = static_cast<uint32_t>(cus > 0 ? cus : 256);
-    int s = gated ? (M <= 64 || split ? 1 : 0) : (split && KT >= 32 && M >= 256 ? 1 : 2);
+    int s = gated ? (M <= 64 || split ? 1 : 0) : (split && KT >= 32 && M >= 384 ? 1 : 2);
     if (shape_override > 0) s = shape_override - 1;
     if (gated && SHAPE_BN[s] != 128) return p;  // bm == 0: no such tile for a gated linear
     const uint32_t feats = gated ? 64u : static_cast<uint32_t>(SHAPE_BN[s]);
@@ -71,7 +74,8 @@ TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, in
         S = static_cast<uint32_t>(splitk_override);
     } else if (split) {
         const uint32_t t1 = std::max(tiles, 1u);
-        S = std::min({2 * ncu / t1, std::max(ncu / t1, (KT + 19) / 20), std::max(KT / 4, 1u), 8u});
+        S = std::min({2 * ncu / t1, std::max(ncu / t1, (KT + 19) / 20), std::max(KT / 2, 1u), 8u});
+        if (gated) S = std::min(S, 2u);  // a gated part carries two partial tiles
         S = std::max(1u, S);
     } else if (!gated) {
         const uint32_t t1 = std::max(tiles, 1u);
