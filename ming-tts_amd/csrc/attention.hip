@@ -238,7 +238,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const float *q, 
 // attention_kernel's arithmetic for R consecutive rows of one sequence at a time, for rows whose
 // keys all start at position 0 (no window, or a window longer than every row's span): one
 // 256-thread workgroup per (head, block of R rows), so a block's keys and values are read
-// once for R rows, and the values' loads are in flight while the scores are formed.  Every
+// once for R rows, and the values' first loads are in flight during the softmax.  Every
 // value is the row kernel's, bit for bit:
 //   - scores: lane r8 of an octet holds dims 8 r8 .. 8 r8 + 7 of all R queries, the octet one
 //     key; the same eight chains and octet_sum per (row, key), then the scale;
@@ -305,14 +305,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(const float
         qf[r][0] = a.x; qf[r][1] = a.y; qf[r][2] = a.z; qf[r][3] = a.w;
         qf[r][4] = b.x; qf[r][5] = b.y; qf[r][6] = b.z; qf[r][7] = b.w;
     }
-    // p . v's first VU keys of this thread's phase, requested now, used after the softmax
-    // (keys past the end re-read the last key).
-    const int d4 = tid & 15, ks = tid >> 4;
-    constexpr int VU = 16;
-    Raw4<CT> vr[VU];
-#pragma unroll
-    for (int u = 0; u < VU; u++)
-        vr[u] = load4_raw<CT>(vc, kvbase + static_cast<size_t>(min(ks + 16 * u, nk - 1)) * 64 + 4 * d4);
 
     // Scores: 32 keys per pass, eight passes' keys requested before any is used.  A key up to
     // p0 belongs to every row; keys p0 + 1 .. nk - 1 only to the rows they precede.
@@ -360,6 +352,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(const float
         // the next round's address arithmetic waits for nothing.
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
+    // p . v's first VU keys of this thread's phase, requested now (after the keys, so no
+    // score waits for them), used after the softmax (keys past the end re-read the last key).
+    // Few at a time: requested before the scores, or 8-16 at a time, they made the kernel
+    // slower (16 ahead of the keys: 7.9 against 7.0 us at 174 rows).
+    const int d4 = tid & 15, ks = tid >> 4;
+    constexpr int VU = 4;
+    Raw4<CT> vr[VU];
+#pragma unroll
+    for (int u = 0; u < VU; u++)
+        vr[u] = load4_raw<CT>(vc, kvbase + static_cast<size_t>(min(ks + 16 * u, nk - 1)) * 64 + 4 * d4);
 #pragma unroll
     for (int r = 0; r < R; r++) mx[r] = wave_max(mx[r]);
     if (lane == 0) {
