@@ -54,6 +54,16 @@ __device__ __forceinline__ float euler_step(float y, float c, float u, float cfg
 // Row r of the flow input (rows 0-2 the conditional batch, 3-5 the unconditional one):
 // slot r % 3 = 0: t + c (cemb, or the cond embedder's bias for the unconditional rows);
 // 1: emb(history); 2: emb(y), emb(v) = x_b + x_w v.
+// An embedder row's 16-byte chunks d0 / 8 .. d0 / 8 + EMB_CHUNKS - 1, all requested before the
+// first is used (one load round trip for a latent of up to 64); chunks past the row repeat its
+// last one, so every load stays inside the row and none is conditional.
+constexpr uint32_t EMB_CHUNKS = 8;
+__device__ __forceinline__ void emb_chunks(const uint16_t *w, uint32_t d0, uint32_t latent, uint4 *wv) {
+#pragma unroll
+    for (uint32_t i = 0; i < EMB_CHUNKS; i++)
+        wv[i] = *reinterpret_cast<const uint4 *>(w + min(d0 + 8 * i, latent - 8));
+}
+
 template <int WT>
 __global__ __launch_bounds__(256) void flow_assemble_kernel(const float *y, const float *history, const float *cemb,
                                                             const uint16_t *cbias, const float *temb,
@@ -69,12 +79,23 @@ __global__ __launch_bounds__(256) void flow_assemble_kernel(const float *y, cons
         const float *src = s == 1 ? history : y;
         const uint16_t *w = xw + static_cast<size_t>(c) * latent;
         v = dec1<WT>(xb[c]);
-        for (uint32_t d = 0; d < latent; d += 8) {
-            const uint4 wv = *reinterpret_cast<const uint4 *>(w + d);
+        const auto dot = [&](uint4 wv, uint32_t d) {
             float wf[8];
             unpack8<WT>(wv, wf);
 #pragma unroll
             for (int e = 0; e < 8; e++) v = fmaf(wf[e], src[d + e], v);
+        };
+        for (uint32_t d0 = 0; d0 < latent; d0 += 8 * EMB_CHUNKS) {
+            uint4 wv[EMB_CHUNKS];
+            emb_chunks(w, d0, latent, wv);
+            if (d0 + 8 * EMB_CHUNKS <= latent) {
+#pragma unroll
+                for (uint32_t i = 0; i < EMB_CHUNKS; i++) dot(wv[i], d0 + 8 * i);
+            } else {
+#pragma unroll
+                for (uint32_t i = 0; i < EMB_CHUNKS; i++)
+                    if (d0 + 8 * i < latent) dot(wv[i], d0 + 8 * i);
+            }
         }
     }
     x[static_cast<size_t>(r) * ldx + c] = v;
@@ -108,39 +129,68 @@ __global__ __launch_bounds__(1024) void flow_euler_assemble_kernel(float *y, con
                                                                   const uint16_t *xb, float *x, uint32_t ldx,
                                                                   uint32_t hidden, uint32_t latent) {
     __shared__ float ys[FLOW_LATENT_MAX], hs[FLOW_LATENT_MAX];
+    // The inputs of this thread's first column (clamped into the matrix: hidden >= 1) are
+    // requested before the Euler update, so their round trip overlaps the update's.
+    uint32_t c = min(threadIdx.x, hidden - 1);
+    uint4 wv[EMB_CHUNKS];
+    emb_chunks(xw + static_cast<size_t>(c) * latent, 0, latent, wv);
+    float te = temb[c], ce = cemb[c];
+    uint16_t cb = cbias[c], bb = xb[c];
     for (uint32_t d = threadIdx.x; d < latent; d += blockDim.x) {
-        const float c = pred[static_cast<size_t>(pred_row) * ldp + d];
+        const float cv = pred[static_cast<size_t>(pred_row) * ldp + d];
         const float u = pred[static_cast<size_t>(null_row) * ldp + d];
         if (capture) {
-            capture[d] = c;
+            capture[d] = cv;
             capture[latent + d] = u;
         }
-        const float v = euler_step(y[d], c, u, cfg, dt);
+        const float v = euler_step(y[d], cv, u, cfg, dt);
         y[d] = v;
         ys[d] = v;
         hs[d] = history[d];
     }
     __syncthreads();
-    for (uint32_t c = threadIdx.x; c < hidden; c += blockDim.x) {
-        x[c] = temb[c] + cemb[c];
-        x[3 * static_cast<size_t>(ldx) + c] = temb[c] + dec1<WT>(cbias[c]);
+    // Column c's six rows, the first batch of its embedder row's chunks in w0.
+    const auto column = [&](uint32_t c, const uint4 (&w0)[EMB_CHUNKS], float te, float ce, uint16_t cb, uint16_t bb,
+                            uint32_t z) {
+        x[c] = te + ce;
+        x[3 * static_cast<size_t>(ldx) + c] = te + dec1<WT>(cb);
         const uint16_t *w = xw + static_cast<size_t>(c) * latent;
-        const float b = dec1<WT>(xb[c]);
+        const float b = dec1<WT>(bb);
         float vh = b, vy = b;
-        for (uint32_t d = 0; d < latent; d += 8) {
-            const uint4 wv = *reinterpret_cast<const uint4 *>(w + d);
-            float wf[8];
-            unpack8<WT>(wv, wf);
+        const auto batch = [&](const uint4 (&wb)[EMB_CHUNKS], uint32_t d0) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                vh = fmaf(wf[e], hs[d + e], vh);
-                vy = fmaf(wf[e], ys[d + e], vy);
+            for (uint32_t i = 0; i < EMB_CHUNKS; i++) {
+                const uint32_t d = d0 + 8 * i;
+                if (d0 + 8 * EMB_CHUNKS > latent && d >= latent) break;
+                float wf[8];
+                unpack8<WT>(wb[i], wf);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    vh = fmaf(wf[e], hs[z + d + e], vh);
+                    vy = fmaf(wf[e], ys[z + d + e], vy);
+                }
             }
+        };
+        batch(w0, 0);
+        for (uint32_t d0 = 8 * EMB_CHUNKS; d0 < latent; d0 += 8 * EMB_CHUNKS) {
+            uint4 wb[EMB_CHUNKS];
+            emb_chunks(w, d0, latent, wb);
+            batch(wb, d0);
         }
         x[static_cast<size_t>(ldx) + c] = vh;
         x[2 * static_cast<size_t>(ldx) + c] = vy;
         x[4 * static_cast<size_t>(ldx) + c] = vh;
         x[5 * static_cast<size_t>(ldx) + c] = vy;
+    };
+    if (threadIdx.x < hidden) column(threadIdx.x, wv, te, ce, cb, bb, 0);
+    // Columns past the first blockDim.x (hidden above 1024): z is 0 but opaque to the compiler,
+    // which would otherwise keep every LDS value of the first batch in registers across the loop.
+    for (c = threadIdx.x + blockDim.x; c < hidden; c += blockDim.x) {
+        uint32_t z = 0;
+        asm volatile("" : "+v"(z));
+        uint4 w0[EMB_CHUNKS];
+        emb_chunks(xw + static_cast<size_t>(c) * latent, 0, latent, w0);
+        column(c, w0, temb[c], cemb[c], cbias[c], xb[c], z);
     }
 }
 
