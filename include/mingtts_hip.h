@@ -179,8 +179,9 @@ enum {
                                     2 = 64 x 128, 3 = 64 x 64, 4 = the register-staged 64 x 64 kernel
                                     that the other activation types use, for every type, 5 = the
                                     gated ring kernel (128 x rows x 96 features of W and W2; SiLU-gated
-                                    linears of x of the weights' type only: the auto choice from
-                                    M = 384 on) */
+                                    linears only: the auto choice when its tiles fill at least
+                                    3/4 of their last wave on the CUs, e.g. gate|up at 448-640
+                                    rows on 256 CUs) */
     MT_TUNE_GEMM_STAGES = 7,     /* loads of that GEMM for x of the weights' type: 2..4 = direct-to-LDS
                                     stages of 64 k, 1 = two register-staged stages into two LDS
                                     buffers (0 = auto); fp32 x always stages through registers,

@@ -99,11 +99,21 @@ size_t tiled_partial_bytes(const TiledPlan &p, bool gated, bool norm) {
     return static_cast<size_t>(p.tiles_m) * p.tiles_n * p.splits * ne * sizeof(float);
 }
 
-// The gated ring kernel (ring_kernel.hpp) takes a SiLU-gated linear of x of the weights' type
-// from this many rows on (auto tile choice): its 96-feature tiles then fill the chip in one wave
-// (204 tiles at M = 512 on 256 CUs), where the 64-feature tiles need two (gate|up at M = 512:
-// 20.6 against 25.0 us); below it the 64-feature tiles are faster.
-constexpr uint32_t RING_GATED_MIN_M = 384;
+// The gated ring kernel (ring_kernel.hpp, one workgroup a CU) takes a SiLU-gated linear (auto
+// tile choice, x of the weights' type or fp32) when its tiles of 128 rows x 96 features fill at
+// least three quarters of their last wave on the CUs.  Measured on gate|up (2 x 4864 x 896,
+// graph replay, 256 CUs), ring against the best tiled plan, fp16 x / fp32 x with the norm:
+//   M = 384 (153 tiles, 0.60 of a wave)   16.7 / 29.7 us against 14.4 / 26.2 (tiled)
+//   M = 448-640 (204-255 tiles, 0.80-1)   17.4-19.5 / 28.9-30.8 against 19.8-21.0 / 35-36
+//   M = 704-768 (306 tiles, 0.60 of two)  32.3 / 54.6 against 21.9 / 45.3 (tiled)
+//   M = 1024 (408 tiles, 0.80 of two)     33.8 / 56.8 against 36.8 / 59.1
+// Below 384 rows (102 tiles or fewer) the tiled plans are faster as well.
+static bool ring_fills(uint32_t M, uint32_t N, int cus) {
+    const uint64_t t = static_cast<uint64_t>((M + ring::BM - 1) / ring::BM) * ((N + ring::FN - 1) / ring::FN);
+    const uint64_t c = static_cast<uint64_t>(cus > 0 ? cus : 256);
+    const uint64_t waves = (t + c - 1) / c;
+    return t > 0 && 4 * t >= 3 * waves * c;
+}
 
 int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, const FixedWs *fixed) {
     const bool gated = (a.flags & F_SILU_GATE) != 0;
@@ -112,7 +122,7 @@ int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, c
     const int cus = device_cus();
     if (cus <= 0) return set_error(MT_EHIP, "gemm: cannot query the device");
     const int tile = tuning().gemm_tile, splitk = tuning().gemm_splitk, stages_override = tuning().gemm_stages;
-    if (gated && !split && (tile == 5 || (tile == 0 && splitk == 0 && a.M >= RING_GATED_MIN_M))) {
+    if (gated && !split && (tile == 5 || (tile == 0 && splitk == 0 && ring_fills(a.M, a.N, cus)))) {
         ring::RingArgs r{};
         r.x = static_cast<const uint16_t *>(a.x);
         r.w = a.w;
@@ -127,7 +137,7 @@ int launch_gemm_tiled(const LinearArgs &a, int xt, int wt, hipStream_t stream, c
         hipLaunchKernelGGL(pick_ring_gated(wt), dim3(static_cast<uint32_t>(G)), dim3(ring::NT), 0, stream, r);
         return check_launch("gemm (ring)");
     }
-    if (gated && split && (tile == 5 || (tile == 0 && splitk == 0 && a.M >= RING_GATED_MIN_M))) {
+    if (gated && split && (tile == 5 || (tile == 0 && splitk == 0 && ring_fills(a.M, a.N, cus)))) {
         ring::RingArgs r{};
         r.xf = static_cast<const float *>(a.x);
         r.norm = a.norm;

@@ -1,5 +1,6 @@
 // Ring GEMM for the SiLU-gated prefill linear (gate|up) with x of the weights' 16-bit type, at
-// M large enough that its output tiles fill the chip (mt_linear routes M >= 384 here).
+// M large enough that its output tiles fill the chip (mt_linear routes a gated linear here when
+// its tiles fill at least three quarters of their last wave: gate|up at 448-640 rows, 1024).
 //
 // Reference kernel replaced: gemm_kernel<32,64,32,4> with the SiLU-gate epilogue
 // (Shaders.swift:297-410), as QwenForward.dispatches calls it for gate|up (Qwen.swift:90).

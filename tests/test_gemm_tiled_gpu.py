@@ -254,6 +254,15 @@ def test_nan_rows_past_m_are_not_read(gpu):
     assert O.normwise_rel_err(got, want64) <= 1e-5
 
 
+def _ring_auto(M, N, gpu):
+    """Whether the automatic tile choice takes the gated ring kernel: its tiles (128 rows x 96
+    features, one workgroup a CU) fill at least three quarters of their last wave."""
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    t = -(-M // 128) * -(-N // 96)
+    waves = -(-t // cus)
+    return 4 * t >= 3 * waves * cus
+
+
 RING_SHAPES = [  # gated (M, N, K, flags, bias) for the ring kernel of 96-feature tiles
     (512, 4864, 896, O.SILU_GATE, False),             # gate|up at the prefill's 512 rows
     (130, 100, 200, O.SILU_GATE, True),               # ragged: rows, features and K past the tiles
@@ -267,9 +276,10 @@ RING_SHAPES = [  # gated (M, N, K, flags, bias) for the ring kernel of 96-featur
 @pytest.mark.parametrize("wt", [O.F16, O.BF16], ids=["wf16", "wbf16"])
 @pytest.mark.parametrize("shape", RING_SHAPES, ids=_ids)
 def test_gated_ring_kernel(gpu, shape, wt):
-    """The gated ring kernel (MT_TUNE_GEMM_TILE = 5; the auto choice for gated linears of x of
-    the weights' type from 384 rows on) against the oracle's fp32 loop and fp64, re-run
-    bit-identical; at 512 rows the default routing takes it too and gives the same bits."""
+    """The gated ring kernel (MT_TUNE_GEMM_TILE = 5; the auto choice for gated linears whose ring
+    tiles fill at least 3/4 of their last wave) against the oracle's fp32 loop and fp64, re-run
+    bit-identical; where the default routing takes it (gate|up at 512 rows) it gives the same
+    bits."""
     M, N, K, flags, bias = shape
     say(f"ring w{wt} {_ids(shape)}")
     c = _case(M * 19 + N + K + wt, M, N, K, flags, bias, wt)
@@ -277,7 +287,7 @@ def test_gated_ring_kernel(gpu, shape, wt):
     assert_linear_parity(got, *expected(c, xu), K, f"ring w{wt} {_ids(shape)}")
     again, _ = _with_tuning(5, 0, lambda: run_linear(c, wt, gpu))
     np.testing.assert_array_equal(again, got)
-    if M >= 384:
+    if _ring_auto(M, N, gpu):
         auto, _ = _with_tuning(0, 0, lambda: run_linear(c, wt, gpu))
         np.testing.assert_array_equal(auto, got)
 
@@ -301,9 +311,9 @@ def test_ring_tile_refuses_ungated_linears(gpu):
 @pytest.mark.parametrize("shape", RING_SHAPES, ids=_ids)
 def test_gated_ring_kernel_fp32_activations(gpu, shape, wt, norm):
     """The gated ring kernel for fp32 x (hi + lo halves, MT_TUNE_GEMM_TILE = 5; the auto choice
-    for gated linears of fp32 x from 384 rows on), with and without the fused RMSNorm, against
-    the oracle's fp32 loop and fp64 within the split bound; re-run bit-identical, and at 512
-    rows the default routing gives the same bits."""
+    for gated linears whose ring tiles fill at least 3/4 of their last wave), with and without
+    the fused RMSNorm, against the oracle's fp32 loop and fp64 within the split bound; re-run
+    bit-identical, and where the default routing takes it (gate|up at 512 rows) the same bits."""
     M, N, K, flags, bias = shape
     say(f"ring fp32 x w{wt} norm={norm} {_ids(shape)}")
     c = _case(M * 23 + N + K + wt, M, N, K, flags, bias, wt)
@@ -316,7 +326,7 @@ def test_gated_ring_kernel_fp32_activations(gpu, shape, wt, norm):
         assert rel <= SPLIT_TOL, f"ring fp32 x: normwise {rel:.3g} > {SPLIT_TOL}"
         again, _ = _with_tuning(5, 0, lambda: run_linear(c, O.F32, gpu))
         np.testing.assert_array_equal(again, got)
-        if M >= 384:
+        if _ring_auto(M, N, gpu):
             auto, _ = _with_tuning(0, 0, lambda: run_linear(c, O.F32, gpu))
             np.testing.assert_array_equal(auto, got)
         return
@@ -342,7 +352,7 @@ def test_gated_ring_kernel_fp32_activations(gpu, shape, wt, norm):
     assert_linear_parity(got, want32, want64, K, f"ring fp32 x rmsnorm {_ids(shape)}")
     rel = O.normwise_rel_err(got, want64)
     assert rel <= SPLIT_TOL, f"ring fp32 x rmsnorm: normwise {rel:.3g} > {SPLIT_TOL}"
-    if M >= 384:
+    if _ring_auto(M, N, gpu):
         y_d.copy_(torch.from_numpy(c["y0"]))
         auto = _with_tuning(0, 0, go)
         np.testing.assert_array_equal(auto, got)
