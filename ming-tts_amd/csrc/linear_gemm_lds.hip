@@ -54,12 +54,23 @@ tiled_fn pick_tiled(int shape, int stages) {
 //     at M = 64 o 8.7 in 6-7 parts against 9.5 in 3, rmsnorm+gate|up 13.6 in 2 against 14.1 in
 //     3.  Gated: 64 x 128 tiles below the ring kernel's rows (a 128 x 128 split tile needs 98 KB
 //     of LDS, one workgroup per CU).
+//   - 64 x 128 tiles (not gated) hold one workgroup a CU (96 KB of LDS at 4 stages, or the
+//     branch-free fp32-x loop's registers), so their K parts stop at one workgroup per CU; they
+//     take long K from 512 rows for x of the weights' type (down, graph replay: M = 512 15.2 us
+//     in 4 parts against 15.7 on 64 x 64, M = 640 / 768 / 1024 16.5 / 17.4 / 20.5 in 3 / 3 / 2
+//     parts against 18.1 / 18.9 / 23.0), and any K once the 64 x 64 tiles alone outnumber the
+//     CUs (qkv at M = 1024: 15.5 against 18.0 us with fp32 x and the norm, 8.6 against 9.0).
+//     fp32-x down at M = 640 / 768: 26.7 / 27.7 us in 3 parts against 35.6 / 35.5 in 4.
 TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, int shape_override, int splitk_override,
                      bool split) {
     TiledPlan p{};
     const uint32_t KT = (K + TBK - 1) / TBK;
     const uint32_t ncu = static_cast<uint32_t>(cus > 0 ? cus : 256);
-    int s = gated ? (M <= 64 || split ? 1 : 0) : (split && KT >= 32 && M >= 384 ? 1 : 2);
+    int s = gated ? (M <= 64 || split ? 1 : 0) : 2;
+    if (!gated) {
+        const uint64_t t64 = static_cast<uint64_t>((M + 63) / 64) * ((N + 63) / 64);
+        if ((KT >= 32 && M >= (split ? 384u : 512u)) || t64 > ncu) s = 1;
+    }
     if (shape_override > 0) s = shape_override - 1;
     if (gated && SHAPE_BN[s] != 128) return p;  // bm == 0: no such tile for a gated linear
     const uint32_t feats = gated ? 64u : static_cast<uint32_t>(SHAPE_BN[s]);
@@ -74,12 +85,14 @@ TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, in
         S = static_cast<uint32_t>(splitk_override);
     } else if (split) {
         const uint32_t t1 = std::max(tiles, 1u);
-        S = std::min({2 * ncu / t1, std::max(ncu / t1, (KT + 19) / 20), std::max(KT / 2, 1u), 8u});
+        const uint32_t slots = (!gated && p.bn == 128 ? 1 : 2) * ncu;  // workgroups the CUs hold at once
+        S = std::min({slots / t1, std::max(ncu / t1, (KT + 19) / 20), std::max(KT / 2, 1u), 8u});
         if (gated) S = std::min(S, 2u);  // a gated part carries two partial tiles
         S = std::max(1u, S);
     } else if (!gated) {
         const uint32_t t1 = std::max(tiles, 1u);
-        S = std::max(1u, std::min(2 * ncu / t1, std::max(KT / 16, std::min(KT / 8, ncu / (3 * t1)))));
+        const uint32_t slots = (p.bn == 128 ? 1 : 2) * ncu;
+        S = std::max(1u, std::min(slots / t1, std::max(KT / 16, std::min(KT / 8, ncu / (3 * t1)))));
     }
     S = std::max(1u, std::min(S, KT));
     p.kps = (KT + S - 1) / S;
