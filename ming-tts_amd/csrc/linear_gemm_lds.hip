@@ -42,17 +42,19 @@ tiled_fn pick_tiled(int shape, int stages) {
 //     CUs, and at most two workgroups per CU (down, 896 x 4864, graph replay: at M = 256 4 parts
 //     take 12.5 us against 14.7 for 9, at M = 512 4 parts 16.0 against 16.9 for 2; at M = 64 6
 //     parts 11.0 against 11.3 for 4 and 11.7 for 9).
-//   - Gated: 64 x 128 tiles while M <= 64, else 128 x 128; with more tiles than CUs the
-//     double-buffered ring (68 KB) keeps two 128 x 128 workgroups on a CU.
+//   - Gated: 64 x 128 tiles while they fit the CUs in one wave (gate|up up to 192 rows: at
+//     M = 96 / 128 10.9 / 11.3 us against 13.6 / 13.7 on 128 x 128), else 128 x 128; with more
+//     tiles than CUs the double-buffered ring (68 KB) keeps two 128 x 128 workgroups on a CU.
 //   - fp32 activations (split): staged through registers into two LDS buffers.  K is split
 //     into as many parts as fill the CUs once, or into parts of at most 20 stages, within two
-//     workgroups per CU, parts of at least 2 stages and 8 parts, 2 parts when gated (the last
+//     workgroups per CU, parts of at least 3 stages and 8 parts, 2 parts when gated (the last
 //     workgroup of a tile adds the parts); long K (32 stages and more) takes 64 x 128 tiles
 //     from 384 rows.  Graph replay (fp32 x): at M = 512 rmsnorm+qkv 13.3 us unsplit against
 //     14.3 in 3 parts, o 11.4 in 2 against 12.6 unsplit, down 24.0 on 64 x 128 tiles in 4
 //     parts against 25.8 on 64 x 64; at M = 256 down 16.9 on 64 x 64 against 18.0 on 64 x 128;
 //     at M = 64 o 8.7 in 6-7 parts against 9.5 in 3, rmsnorm+gate|up 13.6 in 2 against 14.1 in
-//     3.  Gated: 64 x 128 tiles below the ring kernel's rows (a 128 x 128 split tile needs 98 KB
+//     3; rmsnorm+qkv and o (14 stages) at M = 24-128 0.2-1 us faster in 5 parts of 3 stages
+//     than in 7 of 2.  Gated: 64 x 128 tiles below the ring kernel's rows (a 128 x 128 split tile needs 98 KB
 //     of LDS, one workgroup per CU).
 //   - 64 x 128 tiles (not gated) hold one workgroup a CU (96 KB of LDS at 4 stages, or the
 //     branch-free fp32-x loop's registers), so their K parts stop at one workgroup per CU; they
@@ -66,7 +68,7 @@ TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, in
     TiledPlan p{};
     const uint32_t KT = (K + TBK - 1) / TBK;
     const uint32_t ncu = static_cast<uint32_t>(cus > 0 ? cus : 256);
-    int s = gated ? (M <= 64 || split ? 1 : 0) : 2;
+    int s = gated ? (split || M <= 64 || static_cast<uint64_t>((M + 63) / 64) * ((N + 63) / 64) <= ncu ? 1 : 0) : 2;
     if (!gated) {
         const uint64_t t64 = static_cast<uint64_t>((M + 63) / 64) * ((N + 63) / 64);
         if ((KT >= 32 && M >= (split ? 384u : 512u)) || t64 > ncu) s = 1;
@@ -86,7 +88,7 @@ TiledPlan tiled_plan(uint32_t M, uint32_t N, uint32_t K, bool gated, int cus, in
     } else if (split) {
         const uint32_t t1 = std::max(tiles, 1u);
         const uint32_t slots = (!gated && p.bn == 128 ? 1 : 2) * ncu;  // workgroups the CUs hold at once
-        S = std::min({slots / t1, std::max(ncu / t1, (KT + 19) / 20), std::max(KT / 2, 1u), 8u});
+        S = std::min({slots / t1, std::max(ncu / t1, (KT + 19) / 20), std::max((KT + 2) / 3, 1u), 8u});
         if (gated) S = std::min(S, 2u);  // a gated part carries two partial tiles
         S = std::max(1u, S);
     } else if (!gated) {
