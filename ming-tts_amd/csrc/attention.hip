@@ -59,11 +59,25 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(float *qkv, uint32_t ld
     // A device-side position past the cache (only possible through pos_arr, which the host
     // cannot see) appends nothing; the query heads are still rotated.
     const bool append = pos < cache_len;
+    float *row = qkv + static_cast<size_t>(m) * ldq;
+    // The group's first RC_SLOTS slots are requested together (clamped to the row's last slot,
+    // so every load stays in the row) before the angle's cosine and sine are computed, then
+    // rotated and stored: one load round trip, overlapping the trigonometry, for the 18 slots
+    // of a Qwen2-0.5B row instead of one per slot.
+    constexpr uint32_t RC_SLOTS = 3;
+    const uint32_t nslot = hq + 2 * hkv;
+    float x0s[RC_SLOTS], x1s[RC_SLOTS];
+#pragma unroll
+    for (uint32_t u = 0; u < RC_SLOTS; u++) {
+        const uint32_t sl = min(grp + 8 * u, nslot - 1);
+        x0s[u] = row[sl * 64 + i];
+        x1s[u] = row[sl * 64 + i + 32];
+    }
     const float angle = static_cast<float>(pos) * inv_freq[i];
     const float c = cosf(angle), s = sinf(angle);
-    float *row = qkv + static_cast<size_t>(m) * ldq;
-    for (uint32_t slot = grp; slot < hq + 2 * hkv; slot += 8) {
-        const float x0 = row[slot * 64 + i], x1 = row[slot * 64 + i + 32];
+    for (uint32_t slot = grp, u = 0; slot < nslot; slot += 8, u++) {
+        const float x0 = u < RC_SLOTS ? x0s[u] : row[slot * 64 + i];
+        const float x1 = u < RC_SLOTS ? x1s[u] : row[slot * 64 + i + 32];
         float r0, r1;
         rope_rotate(x0, x1, c, s, r0, r1);
         if (slot < hq) {
