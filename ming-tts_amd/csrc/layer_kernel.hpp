@@ -468,15 +468,16 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
 // normed ops (qkv, gate|up) at M <= 2 issue theirs early: the norm's reductions give them
 // the longest window (decode step at M = 2: 421 -> 395.5 us; M = 1: 389 -> 341 us, A/B on
 // one box).  down, split over K, does too in plans without attention items (ATTK false; M =
-// 2: 370 -> 367 us; with them 490 -> 498 us, so not there).  Early batches from o or
-// at M = 4 measured slower (o: +28 us at M = 2; M = 4: +40 to +110 us), so they stay behind
+// 2: 370 -> 367 us), and with them at M = 1 (the whole layer 410.6 -> 401.5 us; at M = 2
+// 439.4 -> 440.4, so not there).  Early batches from o or at M = 4 measured slower (o: +27
+// us at M = 2 linear-only, +35 with attention; M = 4: +40 to +110 us), so they stay behind
 // the stores.
 template <int WT, int M, int C, uint32_t NB, bool ATTK = false, int NA, class ISSUE>
 __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restrict__ ops, uint32_t i, const LayOp &d,
                                          const u32x4 (&A)[NA], ISSUE &&issue) {
     typedef LCls<C, M> L;
     static_assert(M * L::KX <= LayCtx<WT, M>::PLANE, "x staging");
-    constexpr bool EARLY = (L::NORM || (C == LC_DOWN && !ATTK)) && M <= 2;
+    constexpr bool EARLY = (L::NORM || (C == LC_DOWN && (!ATTK || M == 1))) && M <= 2;
     static_assert(NB < 16, "a batch fits the explicit wait below");
     const uint32_t tid = cx.tid, lane = cx.lane;
     const uint32_t r0 = cx.r0[L::SLOT], nr = cx.nr[L::SLOT];
