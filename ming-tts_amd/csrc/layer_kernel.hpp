@@ -469,15 +469,17 @@ __device__ __forceinline__ void dit_att_stage(LayCtx<WT, M> &cx, const LayOp &d,
 // the longest window (decode step at M = 2: 421 -> 395.5 us; M = 1: 389 -> 341 us, A/B on
 // one box).  down, split over K, does too in plans without attention items (ATTK false; M =
 // 2: 370 -> 367 us), and with them at M = 1 (the whole layer 410.6 -> 401.5 us; at M = 2
-// 439.4 -> 440.4, so not there).  Early batches from o or at M = 4 measured slower (o: +27
-// us at M = 2 linear-only, +35 with attention; M = 4: +40 to +110 us), so they stay behind
-// the stores.
+// 439.4 -> 440.4, so not there).  At M = 4 the normed ops and down all go early (linear-only
+// step 486.4 -> 462.8 us, the VAE latent's stack with attention items 580.0 -> 543.1 us; the
+// normed ops alone 551.9, down alone 578.4).  Early batches from o measured slower (+27 us at
+// M = 2 linear-only, +35 with attention), so o's stay behind the stores.
 template <int WT, int M, int C, uint32_t NB, bool ATTK = false, int NA, class ISSUE>
 __device__ __forceinline__ void lay_step(LayCtx<WT, M> &cx, const SeqOp *__restrict__ ops, uint32_t i, const LayOp &d,
                                          const u32x4 (&A)[NA], ISSUE &&issue) {
     typedef LCls<C, M> L;
     static_assert(M * L::KX <= LayCtx<WT, M>::PLANE, "x staging");
-    constexpr bool EARLY = (L::NORM || (C == LC_DOWN && (!ATTK || M == 1))) && M <= 2;
+    constexpr bool EARLY = ((L::NORM || (C == LC_DOWN && (!ATTK || M == 1))) && M <= 2) ||
+                           ((L::NORM || C == LC_DOWN) && M == 4);
     static_assert(NB < 16, "a batch fits the explicit wait below");
     const uint32_t tid = cx.tid, lane = cx.lane;
     const uint32_t r0 = cx.r0[L::SLOT], nr = cx.nr[L::SLOT];
